@@ -1,0 +1,410 @@
+// C-ABI entry points: argument checks (all before the first launch), launch planning and workspace layout.
+#include <algorithm>
+#include <cstring>
+
+#include "../../include/mi355moe.h"
+#include "common.cuh"
+#include "mi355moe_internal.h"
+
+using namespace mi355moe;
+
+namespace {
+
+constexpr int64_t MAX_PAIRS = 65536;
+constexpr int64_t MAX_EXPERTS = 4096;
+constexpr int64_t MAX_TOPK = 32;
+constexpr size_t ALIGN = 256;
+
+inline size_t align_up(size_t v) { return (v + ALIGN - 1) / ALIGN * ALIGN; }
+
+int hip_rc(hipError_t e) { return e == hipSuccess ? 0 : -(int)e; }
+
+int rc_launch(int r) {
+    if (r == 0) return 0;
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? -1 : -(int)e;
+}
+
+// Bump allocator over the caller's workspace (or a dry run that only measures).
+struct Carve {
+    char* base;
+    size_t off = 0;
+    explicit Carve(void* b) : base(static_cast<char*>(b)) {}
+    template <typename T>
+    T* take(size_t count) {
+        T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+        off = align_up(off + count * sizeof(T));
+        return p;
+    }
+};
+
+// The decode plan for P pairs.
+struct DecodePlan {
+    int rmax, seg, S_cap, sk_gu, sk_dn;
+};
+
+int pow2ceil(int64_t v) {
+    int p = 1;
+    while (p < v && p < (1 << 30)) p <<= 1;
+    return p;
+}
+
+DecodePlan plan_decode(int64_t P, int64_t rows_bound, int64_t n, int64_t K, int64_t N) {
+    DecodePlan d;
+    d.rmax = (int)std::min<int64_t>(16, pow2ceil(std::max<int64_t>(1, rows_bound)));
+    d.seg = d.rmax;
+    d.S_cap = (int)(std::min(P, n) + (P + d.seg - 1) / d.seg);
+    const int64_t s_est = std::max<int64_t>(1, std::min(P, n));
+    const int64_t target = 2048;
+    // K range per gate/up workgroup: largest of {1024, 512, 256, 128} that divides K and still gives ~target
+    // workgroups (the input-row buffer 2 * rmax * KR fp16 stays <= 64 KiB)
+    int64_t kr = 128;
+    for (int64_t c : {1024, 512, 256, 128}) {
+        if (K % c || 2 * d.rmax * c * 2 > 65536) continue;
+        if (s_est * (N / 128) * (K / c) >= target || c == 128) { kr = c; break; }
+    }
+    d.sk_gu = (int)(K / kr);
+    int64_t nr = 128;
+    for (int64_t c : {1024, 512, 256, 128}) {
+        if (N % c || d.rmax * c * 2 > 65536) continue;
+        if (s_est * (K / 128) * (N / c) >= target || c == 128) { nr = c; break; }
+    }
+    d.sk_dn = (int)(N / nr);
+    return d;
+}
+
+struct DecodeWs {
+    RouteArgs ra;
+    DecodeArgs da;
+    size_t bytes;
+};
+
+// Layout of the workspace for P pairs (route tables first, then the GEMV scratch).
+void carve_decode(void* ws, int64_t P, int64_t n, int64_t K, int64_t N, const DecodePlan& p, bool with_contrib,
+                  DecodeWs& w) {
+    Carve c(ws);
+    RouteArgs& r = w.ra;
+    DecodeArgs& d = w.da;
+    memset(&r, 0, sizeof(r));
+    memset(&d, 0, sizeof(d));
+    r.tok = c.take<int>(P);
+    r.w16 = c.take<uint16_t>(P);
+    r.pe = c.take<int>(P);
+    r.inv = c.take<int>(P);
+    r.seg_expert = c.take<int>(p.S_cap);
+    r.seg_row0 = c.take<int>(p.S_cap);
+    r.seg_rows = c.take<int>(p.S_cap);
+    r.nseg = c.take<int>(1);
+    r.counts = c.take<int>(n + 1);
+    r.loc = c.take<int>(P);
+    r.blk_cnt = c.take<int>(((P + 1023) / 1024) * (n + 1));
+    r.cnt_out = c.take<int>(n + 1);
+    d.cnt_gu = c.take<unsigned>((size_t)p.S_cap * (N / 128));
+    d.cnt_dn = c.take<unsigned>((size_t)p.S_cap * (K / 128));
+    r.zero = d.cnt_gu;                                               // both counter arrays, zeroed per call
+    r.zero_words = (int64_t)((c.off - ((char*)d.cnt_gu - c.base)) / sizeof(unsigned));
+    d.zg = c.take<float>((size_t)p.sk_gu * 2 * P * N);
+    d.zd = c.take<float>((size_t)p.sk_dn * P * K);
+    d.xd = c.take<uint16_t>((size_t)P * N);
+    d.contrib = with_contrib ? c.take<float>((size_t)P * K) : nullptr;
+    w.bytes = c.off;
+}
+
+bool layer_ok(const mi355moe_exl3_layer* L) {
+    return L && L->gate_trellis && L->gate_suh && L->gate_svh && L->up_trellis && L->up_suh && L->up_svh &&
+           L->down_trellis && L->down_suh && L->down_svh;
+}
+
+int layer_shape_ok(const mi355moe_exl3_layer* L) {
+    if (!layer_ok(L)) return MI355MOE_EINVAL;
+    if (L->n < 1 || L->n > MAX_EXPERTS) return MI355MOE_ELIMIT;
+    if (L->hidden < 256 || L->hidden % 256 || L->intermediate < 128 || L->intermediate % 128)
+        return MI355MOE_ESHAPE;
+    return 0;
+}
+
+Exl3Tables tables(const mi355moe_exl3_layer* L) {
+    Exl3Tables t;
+    t.g_tr = L->gate_trellis;
+    t.g_suh = L->gate_suh;
+    t.g_svh = L->gate_svh;
+    t.u_tr = L->up_trellis;
+    t.u_suh = L->up_suh;
+    t.u_svh = L->up_svh;
+    t.d_tr = L->down_trellis;
+    t.d_suh = L->down_suh;
+    t.d_svh = L->down_svh;
+    return t;
+}
+
+int dt_act(int dt) { return dt == MI355MOE_F16 ? DT_F16 : dt == MI355MOE_BF16 ? DT_BF16 : -1; }
+int dt_w(int dt) {
+    return dt == MI355MOE_F32 ? DT_F32 : dt == MI355MOE_F16 ? DT_F16 : dt == MI355MOE_BF16 ? DT_BF16 : -1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi355moe_abi_version(void) { return MI355MOE_ABI_VERSION; }
+
+const char* mi355moe_strerror(int code) {
+    switch (code) {
+        case MI355MOE_OK: return "ok";
+        case MI355MOE_EINVAL: return "invalid argument (null pointer or bad flag)";
+        case MI355MOE_ESHAPE: return "unsupported shape";
+        case MI355MOE_ELIMIT: return "beyond a documented limit";
+        case MI355MOE_EWORKSPACE: return "workspace too small";
+        case MI355MOE_EDTYPE: return "unsupported dtype";
+        case MI355MOE_EUNSUPPORTED: return "unsupported format variant";
+        default: return code < 0 ? "HIP launch error" : "unknown error";
+    }
+}
+
+int mi355moe_exl3_dequant(const void* trellis, int64_t k_tiles, int64_t n_tiles, void* wq, hipStream_t stream) {
+    if (!trellis || !wq) return MI355MOE_EINVAL;
+    if (k_tiles < 1 || n_tiles < 8 || n_tiles % 8 || k_tiles > 65535 || n_tiles > (1 << 20)) return MI355MOE_ESHAPE;
+    return rc_launch(launch_dequant(static_cast<const uint16_t*>(trellis), (int)k_tiles, (int)n_tiles,
+                                    static_cast<uint16_t*>(wq), stream));
+}
+
+int mi355moe_router_logits(const void* x, int64_t T, int64_t K, int64_t x_stride, const void* w, int64_t E,
+                           float* logits, hipStream_t stream) {
+    if (!x || !w || !logits) return MI355MOE_EINVAL;
+    if (T < 0 || E < 1 || K < 512 || K % 512 || x_stride < K || x_stride % 8) return MI355MOE_ESHAPE;
+    if (T == 0) return 0;
+    return rc_launch(launch_router_logits(static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(w),
+                                          (int)T, (int)K, (int)E, logits, stream));
+}
+
+int mi355moe_router_topk(const float* logits, int64_t T, int64_t E, const float* bias, int64_t topk,
+                         float routed_scale, int renormalize, int32_t* topk_ids, float* topk_weights,
+                         hipStream_t stream) {
+    if (!logits || !topk_ids || !topk_weights) return MI355MOE_EINVAL;
+    if (E < 1 || E > 1024 || topk < 1 || topk > MAX_TOPK || topk > E || T < 0) return MI355MOE_ELIMIT;
+    if (T == 0) return 0;
+    return rc_launch(launch_router_topk(logits, (int)T, (int)E, bias, (int)topk, routed_scale, renormalize ? 1 : 0,
+                                        topk_ids, topk_weights, stream));
+}
+
+int64_t mi355moe_route_workspace_bytes(int64_t P, int64_t n) {
+    if (P < 0 || n < 0) return -1;
+    return (int64_t)(align_up((size_t)P * 4) + align_up(((size_t)(P + 1023) / 1024) * (n + 1) * 4) +
+                     align_up((size_t)(n + 1) * 4));
+}
+
+int mi355moe_route(const void* ids, int ids_dtype, const void* weights, int weights_dtype, int64_t T, int64_t topk,
+                   const int64_t* expert_map, int64_t n_global, int64_t n, int64_t R, int64_t seg_rows,
+                   int32_t* tok, uint16_t* w16, int32_t* pe, int32_t* inv, int32_t* seg_expert, int32_t* seg_row0,
+                   int32_t* seg_rows_out, int64_t s_cap, int32_t* nseg, int32_t* counts, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
+    if (!ids || !weights || !tok || !w16 || !pe || !inv || !seg_expert || !seg_row0 || !seg_rows_out || !nseg)
+        return MI355MOE_EINVAL;
+    if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
+    if (dt_w(weights_dtype) < 0) return MI355MOE_EDTYPE;
+    if (T < 0 || topk < 1 || topk > MAX_TOPK || n < 1 || n > MAX_EXPERTS || R < 1 || seg_rows < 1 ||
+        seg_rows > 4096)
+        return MI355MOE_ELIMIT;
+    if (expert_map && n_global < 0) return MI355MOE_EINVAL;
+    const int64_t P = T * topk;
+    if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (P == 0) return 0;
+    if (s_cap < std::min(P, n) + (P + seg_rows - 1) / seg_rows) return MI355MOE_ESHAPE;
+    const int64_t need = mi355moe_route_workspace_bytes(P, n);
+    if (P > ROUTE_SMALL_MAX_P && (!workspace || (int64_t)workspace_bytes < need)) return MI355MOE_EWORKSPACE;
+    RouteArgs a;
+    memset(&a, 0, sizeof(a));
+    a.ids = ids;
+    a.ids64 = ids_dtype == MI355MOE_I64;
+    a.w = weights;
+    a.wdt = dt_w(weights_dtype);
+    a.emap = expert_map;
+    a.n_global = expert_map ? n_global : 0;
+    a.P = (int)P;
+    a.topk = (int)topk;
+    a.n = (int)n;
+    a.R = (int)std::min<int64_t>(R, 1 << 30);
+    a.seg = (int)seg_rows;
+    a.S_cap = (int)s_cap;
+    a.tok = tok;
+    a.w16 = w16;
+    a.pe = pe;
+    a.inv = inv;
+    a.seg_expert = seg_expert;
+    a.seg_row0 = seg_row0;
+    a.seg_rows = seg_rows_out;
+    a.nseg = nseg;
+    a.counts = counts;
+    if (workspace) {
+        Carve c(workspace);
+        a.loc = c.take<int>(P);
+        a.blk_cnt = c.take<int>(((P + 1023) / 1024) * (n + 1));
+        a.cnt_out = c.take<int>(n + 1);
+    }
+    return rc_launch(launch_route(a, stream));
+}
+
+int mi355moe_rot_in(const void* x, int x_dtype, int64_t x_stride, int64_t K, const int32_t* tok, const int32_t* pe,
+                    int64_t P, const int64_t* suh_table, void* out, hipStream_t stream) {
+    if (!x || !tok || !pe || !suh_table || !out) return MI355MOE_EINVAL;
+    if (dt_act(x_dtype) < 0) return MI355MOE_EDTYPE;
+    if (K < 128 || K % 128 || x_stride < K || x_stride % 2 || P < 0 || P > (1 << 24)) return MI355MOE_ESHAPE;
+    if (P == 0) return 0;
+    return rc_launch(launch_rot_in(x, dt_act(x_dtype), x_stride, tok, pe, suh_table, (int)P, (int)K,
+                                   static_cast<uint16_t*>(out), stream));
+}
+
+int64_t mi355moe_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk) {
+    if (layer_shape_ok(layer) || T < 0 || topk < 1 || topk > MAX_TOPK) return -1;
+    const int64_t P = std::max<int64_t>(1, T * topk);
+    const DecodePlan p = plan_decode(P, P, layer->n, layer->hidden, layer->intermediate);
+    DecodeWs w;
+    carve_decode(nullptr, P, layer->n, layer->hidden, layer->intermediate, p, true, w);
+    return (int64_t)w.bytes;
+}
+
+int mi355moe_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                             int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                             int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                             int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+    return mi355moe_moe_forward_ids_stages(layer, x, x_dtype, x_stride, T, ids, ids_dtype, weights, weights_dtype,
+                                           topk, expert_map, n_global, limit, out, out_dtype, out_stride, workspace,
+                                           workspace_bytes, MI355MOE_STAGE_ALL, stream);
+}
+
+int mi355moe_moe_forward_ids_stages(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                    int64_t T, const void* ids, int ids_dtype, const void* weights,
+                                    int weights_dtype, int64_t topk, const int64_t* expert_map, int64_t n_global,
+                                    float limit, void* out, int out_dtype, int64_t out_stride, void* workspace,
+                                    size_t workspace_bytes, int stages, hipStream_t stream) {
+    if (stages <= 0 || stages > MI355MOE_STAGE_ALL) return MI355MOE_EINVAL;
+    if (int r = layer_shape_ok(layer)) return r;
+    if (!x || !ids || !weights || !out || !workspace) return MI355MOE_EINVAL;
+    if (dt_act(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;
+    if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
+    const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n;
+    if (T < 0 || topk < 1 || topk > MAX_TOPK) return MI355MOE_ELIMIT;
+    if (x_stride < K || x_stride % 2 || out_stride < K || out_stride % 2) return MI355MOE_ESHAPE;
+    if (expert_map && n_global < 0) return MI355MOE_EINVAL;
+    const int64_t P = T * topk;
+    if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (P == 0) return 0;
+    const DecodePlan p = plan_decode(P, P, n, K, N);
+    if (p.S_cap > 65535) return MI355MOE_ELIMIT;
+    DecodeWs w;
+    carve_decode(workspace, P, n, K, N, p, true, w);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    RouteArgs& r = w.ra;
+    r.ids = ids;
+    r.ids64 = ids_dtype == MI355MOE_I64;
+    r.w = weights;
+    r.wdt = dt_w(weights_dtype);
+    r.emap = expert_map;
+    r.n_global = expert_map ? n_global : 0;
+    r.P = (int)P;
+    r.topk = (int)topk;
+    r.n = (int)n;
+    r.R = 1 << 30;
+    r.seg = p.seg;
+    r.S_cap = p.S_cap;
+    DecodeArgs& d = w.da;
+    d.wt = tables(layer);
+    d.n = (int)n;
+    d.K = (int)K;
+    d.N = (int)N;
+    d.P = (int)P;
+    d.T = (int)T;
+    d.x = x;
+    d.xdt = dt_act(x_dtype);
+    d.x_stride = x_stride;
+    d.tok = r.tok;
+    d.w16 = r.w16;
+    d.pe = r.pe;
+    d.inv = r.inv;
+    d.seg_expert = r.seg_expert;
+    d.seg_row0 = r.seg_row0;
+    d.seg_rows = r.seg_rows;
+    d.nseg = r.nseg;
+    d.S_cap = p.S_cap;
+    d.sk_gu = p.sk_gu;
+    d.sk_dn = p.sk_dn;
+    d.limit = limit;
+    d.out = out;
+    d.odt = dt_w(out_dtype);
+    d.out_stride = out_stride;
+    d.accumulate = 0;
+    d.topk = (int)topk;
+    if (stages & MI355MOE_STAGE_ROUTE)
+        if (int rc = launch_route(r, stream)) return rc_launch(rc);
+    return rc_launch(launch_decode(d, p.rmax, stream, stages >> 1));
+}
+
+int64_t mi355moe_exl3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t P) {
+    if (layer_shape_ok(layer) || P < 0) return -1;
+    const int64_t Pp = std::max<int64_t>(1, P);
+    const DecodePlan p = plan_decode(Pp, Pp, layer->n, layer->hidden, layer->intermediate);
+    DecodeWs w;
+    carve_decode(nullptr, Pp, layer->n, layer->hidden, layer->intermediate, p, false, w);
+    return (int64_t)w.bytes;
+}
+
+int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int64_t B, float* out,
+                      const int64_t* expert_count, const int64_t* token_sorted, const void* weight_sorted, int64_t P,
+                      int64_t max_rows, int act_function, int k_gate, int k_up, int k_down, int gate_mcg,
+                      int gate_mul1, int up_mcg, int up_mul1, int down_mcg, int down_mul1, float act_limit,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (int r = layer_shape_ok(layer)) return r;
+    if (!hidden || !out || !expert_count || !token_sorted || !weight_sorted || !workspace) return MI355MOE_EINVAL;
+    if (act_function != 0) return MI355MOE_EUNSUPPORTED;
+    if (k_gate != 4 || k_up != 4 || k_down != 4) return MI355MOE_EUNSUPPORTED;
+    if (!gate_mcg || !up_mcg || !down_mcg || gate_mul1 || up_mul1 || down_mul1) return MI355MOE_EUNSUPPORTED;
+    if (B < 1 || max_rows < 1) return MI355MOE_ESHAPE;
+    if (P < 0 || P > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (P == 0) return 0;
+    const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n;
+    const DecodePlan p = plan_decode(P, std::min(P, max_rows), n, K, N);
+    if (p.S_cap > 65535) return MI355MOE_ELIMIT;
+    DecodeWs w;
+    carve_decode(workspace, P, n, K, N, p, false, w);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    RouteArgs& r = w.ra;
+    r.P = (int)P;
+    r.n = (int)n;
+    r.R = (int)std::min<int64_t>(max_rows, 1 << 30);
+    r.seg = p.seg;
+    r.S_cap = p.S_cap;
+    DecodeArgs& d = w.da;
+    d.wt = tables(layer);
+    d.n = (int)n;
+    d.K = (int)K;
+    d.N = (int)N;
+    d.P = (int)P;
+    d.T = (int)B;
+    d.x = hidden;
+    d.xdt = DT_F16;
+    d.x_stride = K;
+    d.tok = r.tok;
+    d.w16 = r.w16;
+    d.pe = r.pe;
+    d.inv = nullptr;
+    d.seg_expert = r.seg_expert;
+    d.seg_row0 = r.seg_row0;
+    d.seg_rows = r.seg_rows;
+    d.nseg = r.nseg;
+    d.S_cap = p.S_cap;
+    d.sk_gu = p.sk_gu;
+    d.sk_dn = p.sk_dn;
+    d.limit = act_limit;
+    d.out = out;
+    d.odt = DT_F32;
+    d.out_stride = K;
+    d.accumulate = 1;
+    d.topk = 1;
+    if (int rc = launch_route_counts(expert_count, token_sorted, static_cast<const uint16_t*>(weight_sorted), (int)B,
+                                     r, stream))
+        return rc_launch(rc);
+    return rc_launch(launch_decode(d, p.rmax, stream, 7));
+}
+
+}  // extern "C"

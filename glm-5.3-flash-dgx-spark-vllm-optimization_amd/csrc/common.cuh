@@ -1,0 +1,114 @@
+// Shared device helpers for the routed-MoE kernels on gfx950 (CDNA4, wave64).
+//
+// EXL3 4-bit trellis tiles (code/fork/kernels/exl3_format_ref.py:13-27): a 16x16 tile is 32 little-endian
+// 32-bit words; value p of the tile is the 16-bit state s ending at stream bit 4p+4, decoded as
+//   x = s * 0xCBAC1FED (mod 2^32); x = (x & 0x8FFF8FFF) ^ 0x3B603B60; v = fp16(x.lo) + fp16(x.hi) (one rounding)
+// and placed at row 2(l%4) + (j&1) + 8((j>>1)&1), column l/4 + 8(j>>2) with l = p/8, j = p%8.
+//
+// Lane mapping used by every decode kernel here: eight consecutive lanes own one tile; lane q (0..7) of the tile
+// loads words 4q..4q+3 with one 16-byte load and needs word 4q-1 (held by lane q-1, or by lane 7 of the same
+// tile for q = 0). Word 4q+i holds column q and column q+8 at rows 2i, 2i+1, 2i+8, 2i+9, so a lane owns two whole
+// columns of the tile (all 16 k rows) and a GEMV needs no cross-lane reduction inside a tile.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi355moe {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float HAD_R = 0.088388347648f;   // 1/sqrt(128) as fp32 (ExLlamaV3's r_scale, exl3.cu:37-39)
+constexpr uint32_t MCG_MUL = 0xCBAC1FEDu, MCG_MASK = 0x8FFF8FFFu, MCG_FLIP = 0x3B603B60u;
+
+__device__ __forceinline__ _Float16 u16_as_h(uint32_t v) { return __builtin_bit_cast(_Float16, (uint16_t)v); }
+__device__ __forceinline__ uint32_t h_as_u16(_Float16 h) { return (uint32_t)__builtin_bit_cast(uint16_t, h); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs; NaN kept quiet)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7F800000u) == 0x7F800000u) return (uint16_t)((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// The codebook value of one 16-bit state (s < 2^16).
+__device__ __forceinline__ _Float16 mcg_value(uint32_t s) {
+    const uint32_t x = ((s * MCG_MUL) & MCG_MASK) ^ MCG_FLIP;
+    return u16_as_h(x & 0xFFFFu) + u16_as_h(x >> 16);
+}
+
+// Decode one trellis word w (its predecessor pw) into the four fp16 pairs of this lane's two columns:
+//   d[0] = (k 2i, 2i+1) and d[1] = (k 2i+8, 2i+9) of column q; d[2], d[3] the same rows of column q+8,
+// where i = the word's index inside the lane's four words (word 4q+i). State j of the word is
+// bits 28-4j .. 43-4j of the 64-bit pair (pw, w).
+__device__ __forceinline__ void decode_word(uint32_t pw, uint32_t w, h2 (&d)[4]) {
+    const uint32_t D = __builtin_amdgcn_alignbit(pw, w, 20);        // (pw:w) >> 20
+    const _Float16 v0 = mcg_value(__builtin_amdgcn_ubfe(D, 8, 16));
+    const _Float16 v1 = mcg_value(__builtin_amdgcn_ubfe(D, 4, 16));
+    const _Float16 v2 = mcg_value(D & 0xFFFFu);
+    const _Float16 v3 = mcg_value(w >> 16);
+    const _Float16 v4 = mcg_value(__builtin_amdgcn_ubfe(w, 12, 16));
+    const _Float16 v5 = mcg_value(__builtin_amdgcn_ubfe(w, 8, 16));
+    const _Float16 v6 = mcg_value(__builtin_amdgcn_ubfe(w, 4, 16));
+    const _Float16 v7 = mcg_value(w & 0xFFFFu);
+    d[0] = h2{v0, v1};
+    d[1] = h2{v2, v3};
+    d[2] = h2{v4, v5};
+    d[3] = h2{v6, v7};
+}
+
+// Word 4q-1 for this lane: lane q-1's last word, or lane 7's of the same tile for q = 0.
+__device__ __forceinline__ uint32_t prev_word(uint32_t w3, int lane) {
+    return (uint32_t)__shfl((int)w3, (lane & ~7) | ((lane + 7) & 7), 64);
+}
+
+// 128-point Walsh-Hadamard of one row held as two values per lane (lane l: elements 2l, 2l+1) of a wave:
+// butterfly strides 1 (in registers), then 2, 4, ..., 64 across lanes xor 1, 2, ..., 32; the lower element of
+// every pair keeps a + b, the upper a - b (the fixed fp32 order of exl3.cu:273-284).
+__device__ __forceinline__ void fwht128_w64(float& a, float& b, int lane) {
+    const float s = a + b, d = a - b;
+    a = s;
+    b = d;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const float pa = __shfl_xor(a, m, 64), pb = __shfl_xor(b, m, 64);
+        const bool up = (lane & m) != 0;
+        a = up ? pa - a : a + pa;
+        b = up ? pb - b : b + pb;
+    }
+}
+
+// 128-point Walsh-Hadamard of a row held as four values per lane by 32 lanes (lane l of the half-wave:
+// elements 4l..4l+3); strides 1, 2 in registers, 4..64 across lanes xor 1..16 (same order as above).
+__device__ __forceinline__ void fwht128_h32(float (&v)[4], int lane) {
+    const float a = v[0] + v[1], b = v[0] - v[1], c = v[2] + v[3], d = v[2] - v[3];
+    v[0] = a + c;
+    v[1] = b + d;
+    v[2] = a - c;
+    v[3] = b - d;
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) {
+        const bool up = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float p = __shfl_xor(v[i], m, 64);
+            v[i] = up ? p - v[i] : v[i] + p;
+        }
+    }
+}
+
+// sigmoid as the oracle defines it: 1 / (1 + (float)exp(-(double)g)) with IEEE fp32 division
+__device__ __forceinline__ float sigmoid_dexp(float g) {
+    const float e = (float)exp(-(double)g);
+    return __fdiv_rn(1.0f, 1.0f + e);
+}
+
+// Release / acquire around the split-K arrival counters: stores before the release are visible at device
+// scope to a workgroup that observes the counter value after its acquire.
+__device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+}  // namespace mi355moe

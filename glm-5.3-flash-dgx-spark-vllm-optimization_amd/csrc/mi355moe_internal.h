@@ -1,0 +1,101 @@
+// Internal launch descriptors shared by the kernel files and the C-ABI layer (host and device visible).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi355moe {
+
+enum DType { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+
+constexpr int ROUTE_SMALL_MAX_P = 1024;   // pairs the one-block permutation handles
+
+// Permutation of P = T * topk routed pairs into expert order.
+struct RouteArgs {
+    const void* ids;        // [P] int32 or int64 router ids
+    int ids64;
+    const void* w;          // [P] router weights (wdt)
+    int wdt;
+    const int64_t* emap;    // optional expert map [n_global] (global id -> local id or -1)
+    int64_t n_global;
+    int P, topk, n, R, seg, S_cap;
+    // outputs (sorted position order unless noted)
+    int* tok;               // [P] token of the pair at pos
+    uint16_t* w16;          // [P] fp16 weight bits
+    int* pe;                // [P] local expert, -1 = skipped (sentinel or more than R rows)
+    int* inv;               // [P] pair j -> pos
+    int* seg_expert;        // [S_cap]
+    int* seg_row0;          // [S_cap]
+    int* seg_rows;          // [S_cap]
+    int* nseg;              // [1]
+    int* counts;            // optional [n + 1] pairs per local id (last = sentinel)
+    // multi-block scratch
+    int* loc;               // [P]
+    int* blk_cnt;           // [ceil(P / 1024) * (n + 1)]
+    int* cnt_out;           // [n + 1]
+    // split-K arrival counters of the kernels that follow, zeroed by the first route kernel of the call
+    unsigned* zero;
+    int64_t zero_words;
+};
+
+// Pointer tables of one layer's experts: device arrays of n int64 device addresses.
+struct Exl3Tables {
+    const int64_t* g_tr;    // gate trellis int16 [K/16][N/16][64]
+    const int64_t* g_suh;   // fp16 [K]
+    const int64_t* g_svh;   // fp16 [N]
+    const int64_t* u_tr;
+    const int64_t* u_suh;
+    const int64_t* u_svh;
+    const int64_t* d_tr;    // down trellis int16 [N/16][K/16][64]
+    const int64_t* d_suh;   // fp16 [N]
+    const int64_t* d_svh;   // fp16 [K]
+};
+
+// The decode-path kernels (grouped trellis GEMV with fused epilogues).
+struct DecodeArgs {
+    Exl3Tables wt;
+    int n, K, N, P, T;
+    // activations
+    const void* x;
+    int xdt;                // DT_F16 or DT_BF16
+    int64_t x_stride;       // elements
+    // routing tables (sorted position order)
+    const int* tok;
+    const uint16_t* w16;
+    const int* pe;
+    const int* inv;         // pair j -> pos (slot-order combine); nullptr when pairs have no slots
+    const int* seg_expert;
+    const int* seg_row0;
+    const int* seg_rows;
+    const int* nseg;
+    int S_cap;
+    int sk_gu, sk_dn;       // K splits of the gate/up GEMV (over K) and the down GEMV (over N)
+    float limit;
+    // workspace
+    float* zg;              // [sk_gu][2][P][N]
+    float* zd;              // [sk_dn][P][K]
+    uint16_t* xd;           // [P][N] fp16 bits
+    float* contrib;         // [P][K] per-pair contribution (slot-order combine)
+    unsigned* cnt_gu;       // [S_cap][N/128], zero between calls
+    unsigned* cnt_dn;       // [S_cap][K/128], zero between calls
+    // output
+    void* out;
+    int odt;                // output dtype
+    int64_t out_stride;
+    int accumulate;         // 1: out (fp32) += contributions with atomics; 0: out = slot-order sum
+    int topk;
+};
+
+int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w, int T, int K, int E, float* logits,
+                         hipStream_t st);
+int launch_router_topk(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
+                       int32_t* ids, float* wts, hipStream_t st);
+int launch_route(const RouteArgs& a, hipStream_t st);
+int launch_route_counts(const int64_t* counts64, const int64_t* token_sorted, const uint16_t* weight_sorted, int B,
+                        const RouteArgs& a, hipStream_t st);
+// kernels: bit 0 gate/up, bit 1 down, bit 2 combine
+int launch_decode(const DecodeArgs& a, int rmax, hipStream_t st, int kernels = 7);
+int launch_dequant(const uint16_t* trellis, int kt, int nt, uint16_t* wq, hipStream_t st);
+int launch_rot_in(const void* x, int xdt, int64_t x_stride, const int* tok, const int* pe, const int64_t* suh_tab,
+                  int P, int K, uint16_t* out, hipStream_t st);
+
+}  // namespace mi355moe

@@ -1,0 +1,423 @@
+// Router and token->expert permutation kernels.
+//
+// router_logits  logits[t][e] = x[t] . W[e] (bf16 operands, fp32), one wave per expert: lane l accumulates
+//                k = 512c + 8l + i (c ascending, i = 0..7) sequentially, then the 64 lane partials are combined by
+//                the xor butterfly m = 32, 16, ..., 1 (a fixed order, so results are reproducible bit for bit).
+//                Replaces F.linear(x, W).to(float32) (code/fork/docs/BF16_GEMV.md:27,38).
+// router_topk    vLLM grouped_topk with n_group = topk_group = 1 as restated by code/fork/docs/ref/tf_glue.py:371-401:
+//                score = sigmoid(logit), pick the topk largest score + bias (lower id first among equals),
+//                w = score / (sum of picked scores + 1e-20) * scale, one wave per token.
+// route_*        map_topk_to_local (code/fork/docs/prod_exl3_reference.py:936-958), counts, exclusive scan, and the
+//                stable sorted position of every pair (pairs grouped by local id, the sentinel group last, inside a
+//                group by pair index; code/fork/kernels/exl3.cu:742-775), plus the row-segment table
+//                (code/fork/kernels/exl3.cu:529-566) with a caller-chosen segment height.
+#include "common.cuh"
+#include "mi355moe_internal.h"
+
+namespace mi355moe {
+
+// ------------------------------------------------------------------------------------------------ router GEMV
+
+constexpr int RL_TCHUNK = 8;   // tokens per pass of a wave
+
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                            const uint16_t* __restrict__ w, int T, int K, int E,
+                                                            float* __restrict__ logits) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (e >= E) return;
+    const uint16_t* wr = w + (size_t)e * K;
+    const int chunks = K / 512;
+    for (int t0 = 0; t0 < T; t0 += RL_TCHUNK) {
+        float acc[RL_TCHUNK];
+#pragma unroll
+        for (int i = 0; i < RL_TCHUNK; ++i) acc[i] = 0.f;
+        for (int c = 0; c < chunks; ++c) {
+            const int k0 = c * 512 + lane * 8;
+            const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + k0);
+            float wf[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                wf[2 * i] = __builtin_bit_cast(float, wv[i] << 16);
+                wf[2 * i + 1] = __builtin_bit_cast(float, wv[i] & 0xFFFF0000u);
+            }
+#pragma unroll
+            for (int tt = 0; tt < RL_TCHUNK; ++tt) {
+                if (t0 + tt < T) {
+                    const u32x4 xv = *reinterpret_cast<const u32x4*>(x + (size_t)(t0 + tt) * x_stride + k0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc[tt] = __builtin_fmaf(__builtin_bit_cast(float, xv[i] << 16), wf[2 * i], acc[tt]);
+                        acc[tt] = __builtin_fmaf(__builtin_bit_cast(float, xv[i] & 0xFFFF0000u), wf[2 * i + 1],
+                                                 acc[tt]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < RL_TCHUNK; ++tt) {
+            float v = acc[tt];
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
+            if (lane == 0 && t0 + tt < T) logits[(size_t)(t0 + tt) * E + e] = v;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ router top-k
+
+constexpr int TOPK_MAX_E = 1024;   // experts per token row (16 per lane)
+constexpr int TOPK_MAX_K = 32;
+
+__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T, int E,
+                                                          const float* __restrict__ bias, int topk, float scale,
+                                                          int renorm, int32_t* __restrict__ ids,
+                                                          float* __restrict__ wts) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    constexpr int PER = TOPK_MAX_E / 64;
+    float sc[PER], ch[PER];
+    const int per = (E + 63) / 64;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = i * 64 + lane;
+        sc[i] = 0.f;
+        ch[i] = -__builtin_inff();
+        if (i < per && e < E) {
+            const float lg = logits[(size_t)t * E + e];
+            sc[i] = (float)(1.0 / (1.0 + exp(-(double)lg)));
+            ch[i] = sc[i] + (bias ? bias[e] : 0.f);
+        }
+    }
+    float total = 0.f;
+    float picked_s = 0.f;
+    int picked_e = 0;
+    for (int k = 0; k < topk; ++k) {
+        float bv = -__builtin_inff();
+        int be = 0x7FFFFFFF;
+        float bs = 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int e = i * 64 + lane;
+            if (i < per && e < E && (ch[i] > bv || (ch[i] == bv && e < be))) {
+                bv = ch[i];
+                be = e;
+                bs = sc[i];
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ov = __shfl_xor(bv, m, 64);
+            const int oe = __shfl_xor(be, m, 64);
+            const float os = __shfl_xor(bs, m, 64);
+            if (ov > bv || (ov == bv && oe < be)) {
+                bv = ov;
+                be = oe;
+                bs = os;
+            }
+        }
+        // be is the same on every lane; the owner drops it from the candidates
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (i * 64 + lane == be) ch[i] = -__builtin_inff();
+        total = total + bs;
+        if (lane == k) {
+            picked_s = bs;
+            picked_e = be;
+        }
+    }
+    if (lane < topk) {
+        float wv = picked_s;
+        if (renorm) wv = __fdiv_rn(wv, total + 1e-20f);
+        wv = wv * scale;
+        ids[(size_t)t * topk + lane] = picked_e;
+        wts[(size_t)t * topk + lane] = wv;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ permutation
+
+template <typename IT>
+__device__ __forceinline__ int local_id(IT raw, const int64_t* __restrict__ emap, int64_t n_global, int n) {
+    const int64_t id = (int64_t)raw;
+    if (!emap) return (id < 0 || id >= n) ? n : (int)id;
+    const int64_t hi = n_global > 0 ? n_global - 1 : 0;
+    const int64_t safe = id < 0 ? 0 : (id > hi ? hi : id);
+    const int64_t mapped = n_global ? emap[safe] : (int64_t)n;
+    return (id < 0 || id >= n_global || mapped < 0 || mapped >= n) ? n : (int)mapped;
+}
+
+__device__ __forceinline__ uint16_t weight_f16(const void* w, int wdt, int j) {
+    float f;
+    if (wdt == DT_F32) f = reinterpret_cast<const float*>(w)[j];
+    else if (wdt == DT_BF16) f = bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[j]);
+    else return reinterpret_cast<const uint16_t*>(w)[j];
+    return (uint16_t)h_as_u16((_Float16)f);
+}
+
+// block-wide inclusive scan of one int per thread (blockDim.x a multiple of 64, <= 1024)
+__device__ __forceinline__ int block_scan_incl(int v, int* tot, int& total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(v, o, 64);
+        if (lane >= o) v += y;
+    }
+    if (lane == 63) tot[wv] = v;
+    __syncthreads();
+    if (wv == 0) {
+        int s = lane < nw ? tot[lane] : 0;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(s, o, 64);
+            if (lane >= o) s += y;
+        }
+        if (lane < nw) tot[lane] = s;
+    }
+    __syncthreads();
+    const int pre = wv ? tot[wv - 1] : 0;
+    total = tot[nw - 1];
+    __syncthreads();
+    return v + pre;
+}
+
+// Segment table from per-expert counts held in `cnt` (shared, [n]) and their starts: every expert with
+// 0 < c <= R gets ceil(c / seg) segments (expert, first row, rows). Called by every thread of the block.
+__device__ void build_segments(const int* cnt, const int* start, int n, int R, int seg, int S_cap,
+                               int* __restrict__ seg_expert, int* __restrict__ seg_row0, int* __restrict__ seg_rows,
+                               int* __restrict__ nseg_out, int* tot) {
+    int run = 0;
+    for (int base = 0; base < n; base += blockDim.x) {
+        const int e = base + threadIdx.x;
+        const int c = e < n ? cnt[e] : 0;
+        const bool elig = e < n && c > 0 && c <= R;
+        const int ns = elig ? (c + seg - 1) / seg : 0;
+        int stot;
+        const int sinc = block_scan_incl(ns, tot, stot);
+        const int soff = run + sinc - ns;
+        if (elig)
+            for (int q = 0; q < ns; ++q) {
+                const int s = soff + q;
+                if (s < S_cap) {
+                    seg_expert[s] = e;
+                    seg_row0[s] = start[e] + seg * q;
+                    seg_rows[s] = min(seg, c - seg * q);
+                }
+            }
+        run += stot;
+    }
+    if (threadIdx.x == 0) nseg_out[0] = run < S_cap ? run : S_cap;
+}
+
+// Zeroes this call's split-K arrival counters (a grid-stride fill by the first kernel of the call).
+__device__ __forceinline__ void zero_counters(const RouteArgs& a) {
+    if (!a.zero) return;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.zero_words;
+         i += (int64_t)gridDim.x * blockDim.x)
+        a.zero[i] = 0u;
+}
+
+// One block does the whole permutation (P <= ROUTE_SMALL_MAX_P). Shared memory: local[P], cnt[n+1], start[n+1].
+template <typename IT>
+__global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
+    extern __shared__ int sh[];
+    __shared__ int tot[16];
+    int* loc = sh;
+    int* cnt = sh + a.P;
+    int* start = cnt + (a.n + 1);
+    const IT* ids = reinterpret_cast<const IT*>(a.ids);
+    zero_counters(a);
+    for (int e = threadIdx.x; e <= a.n; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int j = threadIdx.x; j < a.P; j += blockDim.x) {
+        const int l = local_id<IT>(ids[j], a.emap, a.n_global, a.n);
+        loc[j] = l;
+        atomicAdd(&cnt[l], 1);
+    }
+    __syncthreads();
+    int run = 0;
+    for (int base = 0; base <= a.n; base += blockDim.x) {
+        const int e = base + threadIdx.x;
+        const int c = e <= a.n ? cnt[e] : 0;
+        int ctot;
+        const int cinc = block_scan_incl(c, tot, ctot);
+        if (e <= a.n) start[e] = run + cinc - c;
+        run += ctot;
+    }
+    __syncthreads();
+    if (a.counts)
+        for (int e = threadIdx.x; e <= a.n; e += blockDim.x) a.counts[e] = cnt[e];
+    build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot);
+    for (int j = threadIdx.x; j < a.P; j += blockDim.x) {
+        const int l = loc[j];
+        int rank = 0;
+        for (int i = 0; i < j; ++i) rank += loc[i] == l;
+        const int pos = start[l] + rank;
+        a.tok[pos] = j / a.topk;
+        a.w16[pos] = weight_f16(a.w, a.wdt, j);
+        a.pe[pos] = (l < a.n && cnt[l] <= a.R) ? l : -1;
+        a.inv[j] = pos;
+    }
+}
+
+// Tables from pre-sorted pairs (the exl3_moe contract): counts [n+1] int64 give each expert's span of the sorted
+// arrays; experts with 0 < count <= R get segments and pe = e on their span, every other row pe = -1; token ids
+// outside [0, B) are skipped (pe = -1). code/fork/kernels/exl3.cu:529-566 (route_prep).
+__global__ __launch_bounds__(1024) void route_counts_kernel(const int64_t* __restrict__ counts64,
+                                                            const int64_t* __restrict__ token_sorted,
+                                                            const uint16_t* __restrict__ weight_sorted, int B,
+                                                            RouteArgs a) {
+    extern __shared__ int sh[];
+    __shared__ int tot[16];
+    int* cnt = sh;
+    int* start = sh + a.n;
+    zero_counters(a);
+    for (int j = threadIdx.x; j < a.P; j += blockDim.x) a.pe[j] = -1;
+    int run = 0;
+    for (int base = 0; base < a.n; base += blockDim.x) {
+        const int e = base + threadIdx.x;
+        const int64_t c64 = e < a.n ? counts64[e] : 0;
+        const int c = c64 < 0 ? 0 : (c64 > a.P ? a.P + 1 : (int)c64);
+        int ctot;
+        const int cinc = block_scan_incl(c, tot, ctot);
+        if (e < a.n) {
+            const int st = run + cinc - c;
+            start[e] = st;
+            cnt[e] = (c > 0 && c <= a.R && st + c <= a.P) ? c : 0;    // ineligible experts: no rows, no segments
+        }
+        run += ctot;
+    }
+    __syncthreads();
+    build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot);
+    __syncthreads();
+    for (int e = 0; e < a.n; ++e) {
+        const int c = cnt[e], st = start[e];
+        for (int i = threadIdx.x; i < c; i += blockDim.x) a.pe[st + i] = e;
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < a.P; j += blockDim.x) {
+        const int64_t t = token_sorted[j];
+        if (t < 0 || t >= B) {
+            a.pe[j] = -1;
+            a.tok[j] = 0;
+        } else {
+            a.tok[j] = (int)t;
+        }
+        a.w16[j] = weight_sorted[j];
+    }
+}
+
+// Multi-block permutation for large P: (1) per-block counts, (2) one block scans them into per-block offsets
+// and builds the segments, (3) every block places its pairs (rank inside the block by pair index).
+constexpr int ROUTE_BLK = 1024;
+
+template <typename IT>
+__global__ __launch_bounds__(ROUTE_BLK) void route_hist_kernel(RouteArgs a) {
+    extern __shared__ int cnt[];
+    const IT* ids = reinterpret_cast<const IT*>(a.ids);
+    zero_counters(a);
+    for (int e = threadIdx.x; e <= a.n; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    const int j = blockIdx.x * ROUTE_BLK + threadIdx.x;
+    if (j < a.P) {
+        const int l = local_id<IT>(ids[j], a.emap, a.n_global, a.n);
+        a.loc[j] = l;
+        atomicAdd(&cnt[l], 1);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e <= a.n; e += blockDim.x) a.blk_cnt[(size_t)blockIdx.x * (a.n + 1) + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(1024) void route_scan_kernel(RouteArgs a, int nblk) {
+    extern __shared__ int sh[];
+    __shared__ int tot[16];
+    int* cnt = sh;
+    int* start = sh + (a.n + 1);
+    for (int e = threadIdx.x; e <= a.n; e += blockDim.x) {
+        int c = 0;
+        for (int b = 0; b < nblk; ++b) c += a.blk_cnt[(size_t)b * (a.n + 1) + e];
+        cnt[e] = c;
+    }
+    __syncthreads();
+    int run = 0;
+    for (int base = 0; base <= a.n; base += blockDim.x) {
+        const int e = base + threadIdx.x;
+        const int c = e <= a.n ? cnt[e] : 0;
+        int ctot;
+        const int cinc = block_scan_incl(c, tot, ctot);
+        if (e <= a.n) start[e] = run + cinc - c;
+        run += ctot;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e <= a.n; e += blockDim.x) {
+        int off = start[e];
+        for (int b = 0; b < nblk; ++b) {
+            const size_t i = (size_t)b * (a.n + 1) + e;
+            const int c = a.blk_cnt[i];
+            a.blk_cnt[i] = off;
+            off += c;
+        }
+        if (a.counts) a.counts[e] = cnt[e];
+        a.cnt_out[e] = cnt[e];
+    }
+    build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot);
+}
+
+__global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
+    __shared__ int loc[ROUTE_BLK];
+    const int j0 = blockIdx.x * ROUTE_BLK;
+    const int j = j0 + threadIdx.x;
+    const int nj = min(ROUTE_BLK, a.P - j0);
+    if (threadIdx.x < nj) loc[threadIdx.x] = a.loc[j];
+    __syncthreads();
+    if (threadIdx.x >= nj) return;
+    const int l = loc[threadIdx.x];
+    int rank = 0;
+    for (int i = 0; i < (int)threadIdx.x; ++i) rank += loc[i] == l;
+    const int pos = a.blk_cnt[(size_t)blockIdx.x * (a.n + 1) + l] + rank;
+    a.tok[pos] = j / a.topk;
+    a.w16[pos] = weight_f16(a.w, a.wdt, j);
+    a.pe[pos] = (l < a.n && a.cnt_out[l] <= a.R) ? l : -1;
+    a.inv[j] = pos;
+}
+
+// ------------------------------------------------------------------------------------------------ launchers
+
+int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w, int T, int K, int E, float* logits,
+                         hipStream_t st) {
+    hipLaunchKernelGGL(router_logits_kernel, dim3((E + 3) / 4), dim3(256), 0, st, x, x_stride, w, T, K, E, logits);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_router_topk(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
+                       int32_t* ids, float* wts, hipStream_t st) {
+    hipLaunchKernelGGL(router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, st, logits, T, E, bias, topk, scale,
+                       renorm, ids, wts);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_route_counts(const int64_t* counts64, const int64_t* token_sorted, const uint16_t* weight_sorted, int B,
+                        const RouteArgs& a, hipStream_t st) {
+    const size_t shm = (size_t)2 * a.n * sizeof(int);
+    hipLaunchKernelGGL(route_counts_kernel, dim3(1), dim3(1024), shm, st, counts64, token_sorted, weight_sorted, B, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_route(const RouteArgs& a, hipStream_t st) {
+    if (a.P <= ROUTE_SMALL_MAX_P) {
+        const size_t shm = (size_t)(a.P + 2 * (a.n + 1)) * sizeof(int);
+        if (a.ids64) hipLaunchKernelGGL(route_small_kernel<int64_t>, dim3(1), dim3(1024), shm, st, a);
+        else hipLaunchKernelGGL(route_small_kernel<int32_t>, dim3(1), dim3(1024), shm, st, a);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    const int nblk = (a.P + ROUTE_BLK - 1) / ROUTE_BLK;
+    const size_t shm1 = (size_t)(a.n + 1) * sizeof(int);
+    if (a.ids64) hipLaunchKernelGGL(route_hist_kernel<int64_t>, dim3(nblk), dim3(ROUTE_BLK), shm1, st, a);
+    else hipLaunchKernelGGL(route_hist_kernel<int32_t>, dim3(nblk), dim3(ROUTE_BLK), shm1, st, a);
+    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 2 * shm1, st, a, nblk);
+    hipLaunchKernelGGL(route_place_kernel, dim3(nblk), dim3(ROUTE_BLK), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace mi355moe

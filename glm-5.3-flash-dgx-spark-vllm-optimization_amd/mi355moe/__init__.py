@@ -1,0 +1,14 @@
+"""mi355moe: the routed-MoE layer hot path of GLM-style EXL3 models on AMD MI355X (gfx950).
+
+Python host code over libmi355moe.so (hand-written HIP kernels behind the C ABI of include/mi355moe.h):
+  ops        torch-level wrappers of every entry point (dequant, router, permutation, rotation, decode forward)
+  method     the reference's call contracts: Exl3MoEMethod.apply, apply_exl3_experts, fused_experts, exl3_moe
+  layer      production's stacked EXL3 layout and its pointer tables
+  synthetic  seeded synthetic layers / routings of the benchmark configurations
+  build      in-tree hipcc build of the library
+"""
+from . import _lib, layer, ops, synthetic  # noqa: F401
+from .layer import Exl3Experts  # noqa: F401
+from .method import Exl3MoEMethod, apply_exl3_experts, exl3_moe, fused_experts  # noqa: F401
+
+__all__ = ["Exl3Experts", "Exl3MoEMethod", "apply_exl3_experts", "exl3_moe", "fused_experts", "ops", "synthetic"]

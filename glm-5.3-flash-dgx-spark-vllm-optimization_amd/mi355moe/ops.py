@@ -1,0 +1,186 @@
+"""Torch-level wrappers of the C ABI (device tensors in, device tensors out, current stream).
+
+Every function validates its tensors on the host, then calls one C entry point, which checks its arguments again
+before enqueuing anything. No function synchronizes with the host or allocates per call except for its outputs
+(the persistent workspace is allocated once per device and grown when a larger call needs it).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .layer import Exl3Experts
+
+_WS: dict = {}
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _p(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _need_cuda(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("mi355moe: every tensor must be on the GPU")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"mi355moe: tensors on {t.device} and {dev}")
+    return dev
+
+
+def act_dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float16:
+        return _lib.F16
+    if dt == torch.bfloat16:
+        return _lib.BF16
+    raise ValueError(f"activations must be fp16 or bf16, got {dt}")
+
+
+def weight_dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return _lib.F32
+    return act_dtype_code(dt)
+
+
+def ids_dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.int32:
+        return _lib.I32
+    if dt == torch.int64:
+        return _lib.I64
+    raise ValueError(f"router ids must be int32 or int64, got {dt}")
+
+
+def workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """The persistent zero-initialised workspace of `dev`, at least `nbytes` (grown, never shrunk). Calls keep
+    its counters at zero; calls that share it must be stream-ordered."""
+    key = (dev.type, dev.index)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=dev)
+        _WS[key] = ws
+    return ws
+
+
+def dequant(trellis: torch.Tensor) -> torch.Tensor:
+    """W_q fp16 [K, N] from a 4-bit trellis int16 [K/16, N/16, 64] (exl3_format_ref.py:88-97)."""
+    dev = _need_cuda(trellis)
+    if trellis.dtype != torch.int16 or trellis.dim() != 3 or trellis.shape[-1] != 64:
+        raise ValueError("trellis must be int16 [K/16, N/16, 64]")
+    t = trellis.contiguous()
+    kt, nt = t.shape[0], t.shape[1]
+    out = torch.empty(kt * 16, nt * 16, dtype=torch.float16, device=dev)
+    _lib.check("mi355moe_exl3_dequant", _lib.lib().mi355moe_exl3_dequant(_p(t), kt, nt, _p(out), _stream(dev)))
+    return out
+
+
+def router_logits(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """fp32 [T, E] = x bf16 [T, K] @ w bf16 [E, K]^T in the library's fixed summation order."""
+    dev = _need_cuda(x, w)
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
+        raise ValueError("router_logits: bf16 x [T, K] and bf16 W [E, K]")
+    if x.stride(1) != 1:
+        raise ValueError("router_logits: x needs unit column stride")
+    w = w.contiguous()
+    T, K = x.shape
+    E = w.shape[0]
+    out = torch.empty(T, E, dtype=torch.float32, device=dev)
+    _lib.check("mi355moe_router_logits", _lib.lib().mi355moe_router_logits(_p(x), T, K, x.stride(0), _p(w), E,
+                                                                           _p(out), _stream(dev)))
+    return out
+
+
+def router_topk(logits: torch.Tensor, topk: int, bias: torch.Tensor | None = None, routed_scale: float = 1.0,
+                renormalize: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """(ids int32 [T, topk], weights fp32 [T, topk]) of vLLM grouped_topk with sigmoid scoring and one group."""
+    dev = _need_cuda(logits, bias)
+    lg = logits.float().contiguous()
+    T, E = lg.shape
+    b = None if bias is None else bias.float().contiguous()
+    if b is not None and b.numel() != E:
+        raise ValueError("bias must have one entry per expert")
+    ids = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    wts = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    _lib.check("mi355moe_router_topk", _lib.lib().mi355moe_router_topk(
+        _p(lg), T, E, _p(b), topk, float(routed_scale), int(bool(renormalize)), _p(ids), _p(wts), _stream(dev)))
+    return ids, wts
+
+
+def route(ids: torch.Tensor, weights: torch.Tensor, n: int, R: int = 1 << 30, seg_rows: int = 16,
+          expert_map: torch.Tensor | None = None) -> dict:
+    """The token -> expert permutation tables (stage entry; see mi355moe_route in include/mi355moe.h)."""
+    dev = _need_cuda(ids, weights, expert_map)
+    T, topk = ids.shape
+    P = T * topk
+    ids_c, w_c = ids.contiguous(), weights.contiguous()
+    s_cap = min(P, n) + (P + seg_rows - 1) // seg_rows
+    i32 = dict(dtype=torch.int32, device=dev)
+    out = {"tok": torch.empty(P, **i32), "w16": torch.empty(P, dtype=torch.float16, device=dev),
+           "pe": torch.empty(P, **i32), "inv": torch.empty(P, **i32), "seg_expert": torch.full((s_cap,), -1, **i32),
+           "seg_row0": torch.zeros(s_cap, **i32), "seg_rows": torch.zeros(s_cap, **i32),
+           "nseg": torch.zeros(1, **i32), "counts": torch.zeros(n + 1, **i32)}
+    L = _lib.lib()
+    ws = workspace(dev, L.mi355moe_route_workspace_bytes(P, n))
+    em = None
+    if expert_map is not None:
+        em = expert_map.to(torch.int64).contiguous()
+    _lib.check("mi355moe_route", L.mi355moe_route(
+        _p(ids_c), ids_dtype_code(ids.dtype), _p(w_c), weight_dtype_code(weights.dtype), T, topk, _p(em),
+        0 if em is None else em.numel(), n, R, seg_rows, _p(out["tok"]), _p(out["w16"]), _p(out["pe"]),
+        _p(out["inv"]), _p(out["seg_expert"]), _p(out["seg_row0"]), _p(out["seg_rows"]), s_cap, _p(out["nseg"]),
+        _p(out["counts"]), _p(ws), ws.numel(), _stream(dev)))
+    return out
+
+
+def rot_in(x: torch.Tensor, tok: torch.Tensor, pe: torch.Tensor, suh_table: torch.Tensor) -> torch.Tensor:
+    """fp16 [P, K]: row pos = fp16(H(fp16(x[tok[pos]] * suh[pe[pos]])) * r) (rows with pe < 0 are NaN)."""
+    dev = _need_cuda(x, tok, pe, suh_table)
+    if x.stride(1) != 1:
+        raise ValueError("rot_in: x needs unit column stride")
+    P, K = tok.numel(), x.shape[1]
+    out = torch.full((P, K), float("nan"), dtype=torch.float16, device=dev)
+    _lib.check("mi355moe_rot_in", _lib.lib().mi355moe_rot_in(
+        _p(x), act_dtype_code(x.dtype), x.stride(0), K, _p(tok.int().contiguous()), _p(pe.int().contiguous()), P,
+        _p(suh_table.contiguous()), _p(out), _stream(dev)))
+    return out
+
+
+def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                    limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                    out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Routed-expert output [T, K] (x's dtype unless out/out_dtype say otherwise), written (not accumulated)."""
+    dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
+    if dev != experts.device:
+        raise ValueError(f"activations on {dev}, experts on {experts.device}")
+    if x.dim() != 2 or x.shape[1] != experts.K or x.stride(1) != 1:
+        raise ValueError(f"x must be [T, {experts.K}] with unit column stride")
+    T = x.shape[0]
+    ids = topk_ids.reshape(T, -1).contiguous()
+    w = topk_weights.reshape(T, -1).contiguous()
+    topk = ids.shape[1]
+    if w.shape != ids.shape:
+        raise ValueError("topk_weights must be shaped like topk_ids")
+    if out is None:
+        out = torch.empty(T, experts.K, dtype=out_dtype or x.dtype, device=dev)
+    if out.shape != (T, experts.K) or out.stride(1) != 1:
+        raise ValueError("out must be [T, K] with unit column stride")
+    L = _lib.lib()
+    nb = L.mi355moe_moe_workspace_bytes(ctypes.byref(experts.desc), T, topk)
+    if nb < 0:
+        raise ValueError("mi355moe_moe_workspace_bytes rejected the shape")
+    ws = workspace(dev, nb)
+    em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
+    _lib.check("mi355moe_moe_forward_ids", L.mi355moe_moe_forward_ids(
+        ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
+        ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em), 0 if em is None else em.numel(),
+        float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), _stream(dev)))
+    return out

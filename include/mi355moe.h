@@ -1,0 +1,140 @@
+/*
+ * mi355moe: the routed-MoE layer hot path of GLM-style EXL3 models on one AMD MI355X (gfx950), as a C ABI.
+ *
+ * Conventions (every entry point):
+ *   - all tensor arguments are device pointers (hipMalloc'd or torch CUDA tensors); sizes are element counts;
+ *   - work is enqueued on `stream` in order; nothing is allocated, nothing synchronizes with the host, so every
+ *     call can be captured into a HIP graph;
+ *   - return 0 on success, a positive MI355MOE_E* code when an argument is rejected (checked before anything is
+ *     enqueued, so outputs are untouched), or a negative value when a launch failed (the HIP error, negated);
+ *   - `workspace` is caller-owned device memory of at least the size the matching *_workspace_bytes function
+ *     reports, zero-filled once before its first use; calls keep it in that state (counters return to zero).
+ *     Calls that share one workspace must be stream-ordered (not concurrent).
+ *
+ * EXL3 weights of one layer (code/fork/docs/prod_exl3_reference.py:2048-2162): per expert e, gate/up
+ * trellis int16 [K/16][N/16][64], suh fp16 [K], svh fp16 [N]; down trellis int16 [N/16][K/16][64], suh fp16 [N],
+ * svh fp16 [K]. The kernels reach them through nine int64 pointer tables of n device addresses each, the same
+ * tables production builds (prod_exl3_reference.py:1438-1487).
+ */
+#ifndef MI355MOE_H
+#define MI355MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI355MOE_ABI_VERSION 1
+
+enum {
+    MI355MOE_OK = 0,
+    MI355MOE_EINVAL = 1,       /* null pointer or bad flag */
+    MI355MOE_ESHAPE = 2,       /* unsupported shape */
+    MI355MOE_ELIMIT = 3,       /* beyond a documented limit (pairs, experts, topk) */
+    MI355MOE_EWORKSPACE = 4,   /* workspace too small */
+    MI355MOE_EDTYPE = 5,       /* unsupported dtype code */
+    MI355MOE_EUNSUPPORTED = 6  /* a format variant this library does not implement (e.g. bits != 4) */
+};
+
+/* dtype codes */
+enum { MI355MOE_F32 = 0, MI355MOE_F16 = 1, MI355MOE_BF16 = 2, MI355MOE_I32 = 3, MI355MOE_I64 = 4 };
+
+typedef struct mi355moe_exl3_layer {
+    int64_t n;              /* local experts */
+    int64_t hidden;         /* K, multiple of 256 */
+    int64_t intermediate;   /* N, multiple of 128 */
+    const int64_t* gate_trellis;   /* device int64 [n] each */
+    const int64_t* gate_suh;
+    const int64_t* gate_svh;
+    const int64_t* up_trellis;
+    const int64_t* up_suh;
+    const int64_t* up_svh;
+    const int64_t* down_trellis;
+    const int64_t* down_suh;
+    const int64_t* down_svh;
+} mi355moe_exl3_layer;
+
+int mi355moe_abi_version(void);
+const char* mi355moe_strerror(int code);
+
+/* W_q fp16 [k_tiles*16][n_tiles*16] from one 4-bit trellis int16 [k_tiles][n_tiles][64], bit for bit the
+ * reference decode (replaces code/fork/kernels/exl3_format_ref.py:88-97 `unpack` and ExLlamaV3's `reconstruct`,
+ * code/fork/tests/test_layout_equiv.py:1-46). n_tiles must be a multiple of 8. */
+int mi355moe_exl3_dequant(const void* trellis, int64_t k_tiles, int64_t n_tiles, void* wq, hipStream_t stream);
+
+/* Router logits fp32 [T][E] = x bf16 [T][K] (row stride x_stride) times W bf16 [E][K]^T, in a fixed summation
+ * order (replaces F.linear(x, W).to(torch.float32), code/fork/docs/BF16_GEMV.md:27,38). K % 512 == 0. */
+int mi355moe_router_logits(const void* x, int64_t T, int64_t K, int64_t x_stride, const void* w, int64_t E,
+                           float* logits, hipStream_t stream);
+
+/* Sigmoid + bias top-k with renormalisation and routed scale: vLLM grouped_topk(logits, num_expert_group=1,
+ * topk_group=1, topk, renormalize, routed_scaling_factor, e_score_correction_bias, scoring="sigmoid")
+ * (code/fork/tests/router_topk_agreement.py:58-61; semantics code/fork/docs/ref/tf_glue.py:371-401).
+ * ids int32 [T][topk], weights fp32 [T][topk]. bias may be NULL. E <= 1024, topk <= 32. */
+int mi355moe_router_topk(const float* logits, int64_t T, int64_t E, const float* bias, int64_t topk,
+                         float routed_scale, int renormalize, int32_t* topk_ids, float* topk_weights,
+                         hipStream_t stream);
+
+/* Token -> expert permutation of P = T*topk pairs (stage entry). Local ids by map_topk_to_local
+ * (prod_exl3_reference.py:936-958, expert_map optional, NULL = identity), stable sorted position per pair
+ * (code/fork/kernels/exl3.cu:742-775), counts and the row-segment table of eligible experts (0 < count <= R,
+ * ceil(count/seg_rows) segments each, code/fork/kernels/exl3.cu:529-566).
+ * Outputs: tok/pe/w16 indexed by sorted position, inv[j] = position of pair j, seg_* [s_cap], nseg [1],
+ * counts [n+1] (last = sentinel). ids dtype I32/I64, weights F32/F16/BF16. */
+int64_t mi355moe_route_workspace_bytes(int64_t P, int64_t n);
+int mi355moe_route(const void* ids, int ids_dtype, const void* weights, int weights_dtype, int64_t T, int64_t topk,
+                   const int64_t* expert_map, int64_t n_global, int64_t n, int64_t R, int64_t seg_rows,
+                   int32_t* tok, uint16_t* w16, int32_t* pe, int32_t* inv, int32_t* seg_expert, int32_t* seg_row0,
+                   int32_t* seg_rows_out, int64_t s_cap, int32_t* nseg, int32_t* counts, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream);
+
+/* Input rotation (stage entry): out[pos] = fp16(H(fp16(x[tok[pos]] * suh[pe[pos]])) * r) for rows with pe >= 0
+ * (code/fork/kernels/exl3.cu:321-349; E3 gather code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu:95-126).
+ * x dtype F16 or BF16 [*, K] (row stride x_stride); out fp16 [P][K]. */
+int mi355moe_rot_in(const void* x, int x_dtype, int64_t x_stride, int64_t K, const int32_t* tok, const int32_t* pe,
+                    int64_t P, const int64_t* suh_table, void* out, hipStream_t stream);
+
+/* Routed experts from router ids: the decode apply (code/fork/kernels/exl3.cpp:307-391 moe_forward_ids,
+ * exl3.cpp:409-503 moe_forward_glue). x F16/BF16 [T][K] (row stride x_stride), ids I32/I64 [T][topk],
+ * weights F32/F16/BF16 [T][topk], out [T][K] of out_dtype (row stride out_stride) is WRITTEN with the
+ * routed sum over each token's slots in slot order (deterministic). limit = the SwiGLU limit (0 = none).
+ * Pairs P = T*topk <= 65536. */
+int64_t mi355moe_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk);
+
+/* Stage mask of mi355moe_moe_forward_ids_stages: the same call split into its launches, so a caller can time or
+ * test one of them (the reference's stage entry points, code/fork/kernels/exl3.cpp:130-220: route_prep, grouped,
+ * gateup_epilogue, down_epilogue). A stage reads what the earlier stages of a call with the same arguments left in
+ * the workspace. */
+enum { MI355MOE_STAGE_ROUTE = 1, MI355MOE_STAGE_GATEUP = 2, MI355MOE_STAGE_DOWN = 4, MI355MOE_STAGE_COMBINE = 8,
+       MI355MOE_STAGE_ALL = 15 };
+int mi355moe_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                             int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                             int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                             int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+int mi355moe_moe_forward_ids_stages(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                    int64_t T, const void* ids, int ids_dtype, const void* weights,
+                                    int weights_dtype, int64_t topk, const int64_t* expert_map, int64_t n_global,
+                                    float limit, void* out, int out_dtype, int64_t out_stride, void* workspace,
+                                    size_t workspace_bytes, int stages, hipStream_t stream);
+
+/* The fused-experts op exllamav3_ext.exl3_moe (code/fork/docs/ref/xl_exl3_moe.cu:93-130, called by
+ * prod_exl3_reference.py:1490-1537): hidden fp16 [B][K]; out fp32 [B][K] ACCUMULATED into; expert_count int64
+ * [n+1] (last = sentinel bucket, ignored); token_sorted int64 [P]; weight_sorted fp16 [P]; experts with more
+ * than max_rows (the temps' second dimension) rows are skipped, as the original kernel does; act_function 0
+ * (SiLU) only; k_gate/k_up/k_down = 4 (bits) only; mcg flags must be 1 and mul1 flags 0 (the formats this
+ * library decodes). P = 0 is a no-op. */
+int64_t mi355moe_exl3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t P);
+int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int64_t B, float* out,
+                      const int64_t* expert_count, const int64_t* token_sorted, const void* weight_sorted, int64_t P,
+                      int64_t max_rows, int act_function, int k_gate, int k_up, int k_down, int gate_mcg,
+                      int gate_mul1, int up_mcg, int up_mul1, int down_mcg, int down_mul1, float act_limit,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MI355MOE_H */

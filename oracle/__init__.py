@@ -1,0 +1,15 @@
+"""CPU oracle for the routed-MoE hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package is the checker that the HIP kernels are measured against. Only ``tests/``,
+``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import it, and only as the checker or as
+the timed CPU baseline, never as a product code path. The shipped package (``mi355moe``) never imports it and
+fails loudly when its HIP library is missing.
+
+Contents (each function cites the reference file:line it restates):
+  exl3.py     EXL3 4-bit trellis format: codebook, tile order, states, unpack, Hadamard (numpy)
+  routing.py  router (sigmoid + bias top-k, softmax top-k), map_topk_to_local, stable permutation, segment tables
+  moe.py      routed-MoE forward: float64 reference and the rounding-faithful kernel paths (C, via ctypes)
+  e4m3.py     e4m3 quantisation (RN, saturating), per-token activation quant, block-scaled expert FFN
+  dense.py    the bf16 dense CPU MoE block (softmax top-4 router, SwiGLU experts)
+  csrc/       the C restatement (oracle.c) behind moe.py, built by oracle/Makefile into oracle/_build/
+"""

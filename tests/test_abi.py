@@ -1,0 +1,84 @@
+"""The C-ABI library loads and exports every entry point include/mi355moe.h declares; host-side planning entry
+points (no device work) answer; the Python layer rejects bad arguments before any device call. No GPU needed."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "mi355moe.h")
+
+
+def _declared() -> set[str]:
+    src = open(HEADER).read()
+    return set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(mi355moe_\w+)\s*\(", src, re.M))
+
+
+def test_header_declarations_match_binding():
+    from mi355moe import _lib
+    assert _declared() == set(_lib.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    from mi355moe import _lib
+    L = _lib.lib()
+    for name in sorted(_declared()):
+        assert getattr(L, name) is not None, name
+    assert L.mi355moe_abi_version() == _lib.ABI_VERSION
+    assert L.mi355moe_strerror(2) == b"unsupported shape"
+
+
+def _fake_desc(n=288, K=4096, N=1024):
+    from mi355moe import _lib
+    d = _lib.Exl3LayerDesc()
+    d.n, d.hidden, d.intermediate = n, K, N
+    for f, _ in d._fields_[3:]:
+        setattr(d, f, ctypes.c_void_p(0x1000))      # never dereferenced by the host-side planners
+    return d
+
+
+def test_workspace_planners_answer_without_a_gpu():
+    from mi355moe import _lib
+    L = _lib.lib()
+    d = _fake_desc()
+    b8 = L.mi355moe_moe_workspace_bytes(ctypes.byref(d), 8, 8)
+    b64 = L.mi355moe_moe_workspace_bytes(ctypes.byref(d), 64, 8)
+    assert 0 < b8 < b64 < 1 << 31
+    assert L.mi355moe_exl3_moe_workspace_bytes(ctypes.byref(d), 64) > 0
+    bad = _fake_desc(K=4000)
+    assert L.mi355moe_moe_workspace_bytes(ctypes.byref(bad), 8, 8) == -1
+    assert L.mi355moe_route_workspace_bytes(65536, 288) > 0
+
+
+def test_argument_errors_before_any_launch():
+    from mi355moe import _lib
+    L = _lib.lib()
+    null = ctypes.c_void_p(0)
+    assert L.mi355moe_exl3_dequant(null, 16, 8, null, null) == 1                     # EINVAL
+    assert L.mi355moe_exl3_dequant(ctypes.c_void_p(0x1000), 16, 7, ctypes.c_void_p(0x1000), null) == 2
+    assert L.mi355moe_router_topk(ctypes.c_void_p(8), 1, 2000, null, 8, 2.5, 1, ctypes.c_void_p(8),
+                                  ctypes.c_void_p(8), null) == 3                       # E > 1024
+    d = _fake_desc()
+    p = ctypes.c_void_p(0x1000)
+    # exl3_moe contract: only SiLU, 4 bits, mcg codebook
+    args = [ctypes.byref(d), p, 4, p, p, p, p, 32, 128]
+    tail = [0, 0, 0, 0.0, p, 1 << 30, null]
+    assert L.mi355moe_exl3_moe(*args, 1, 4, 4, 4, 1, 0, 1, 0, 1, 0, *tail[3:]) == 6   # act_function 1
+    assert L.mi355moe_exl3_moe(*args, 0, 3, 4, 4, 1, 0, 1, 0, 1, 0, *tail[3:]) == 6   # 3 bits
+    assert L.mi355moe_exl3_moe(*args, 0, 4, 4, 4, 1, 1, 1, 0, 1, 0, *tail[3:]) == 6   # mul1 codebook
+
+
+def test_python_layer_rejects_cpu_tensors_and_bad_shapes():
+    from mi355moe import ops
+    with pytest.raises(ValueError):
+        ops.dequant(torch.zeros(4, 8, 64, dtype=torch.int16))
+    with pytest.raises(ValueError):
+        ops.router_topk(torch.zeros(2, 8), 2)
+    from mi355moe.layer import Exl3Experts
+    with pytest.raises(ValueError):
+        Exl3Experts(torch.zeros(2, 2, 4, 4, 48, dtype=torch.int16), *[torch.zeros(1)] * 5)

@@ -1,0 +1,118 @@
+"""GPU parity of the bit-exact stages against the oracle: trellis dequant, input rotation, router logits and top-k,
+and the token -> expert permutation (single-block and multi-block)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exl3, routing
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+@pytest.mark.parametrize("kt,nt", [(1, 8), (16, 64), (256, 64), (64, 256)])
+def test_dequant_bit_exact(cuda, kt, nt):
+    from mi355moe import ops
+    _say(f"dequant kt={kt} nt={nt}")
+    g = torch.Generator().manual_seed(kt * 1000 + nt)
+    t = torch.randint(-32768, 32768, (kt, nt, 64), generator=g, dtype=torch.int32).to(torch.int16)
+    got = ops.dequant(t.to(cuda)).cpu().numpy()
+    ref = exl3.unpack(t.numpy())
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+def test_dequant_every_state(cuda):
+    """Tiles whose words make every 16-bit state occur: state 8l+j of a tile reads bits of words l-1, l; tiles
+    of constant words w repeat the states of (w:w); 65536 such words cover all states at offset 16."""
+    from mi355moe import ops
+    w = np.arange(65536, dtype=np.uint32) * 0x10001                 # word = s:s
+    tiles = np.repeat(w[:, None], 32, axis=1).view(np.int16).reshape(65536 // 8, 8, 64)
+    got = ops.dequant(torch.from_numpy(tiles.copy()).to(cuda)).cpu().numpy()
+    ref = exl3.unpack(tiles)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    states = exl3.states(tiles)
+    assert len(np.unique(states)) == 65536
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16])
+def test_rot_in_bit_exact(cuda, xdt):
+    from mi355moe import ops
+    from mi355moe.layer import _table
+    _say(f"rot_in {xdt}")
+    g = torch.Generator().manual_seed(5)
+    n, K, P, T = 6, 1024, 40, 7
+    x = (torch.randn(T, K, generator=g) * 3).to(xdt)
+    suh = (torch.randn(n, K, generator=g)).to(torch.float16)
+    tok = torch.randint(0, T, (P,), generator=g, dtype=torch.int32)
+    pe = torch.randint(0, n, (P,), generator=g, dtype=torch.int32)
+    pe[3] = -1
+    suh_d = suh.to(cuda)
+    got = ops.rot_in(x.to(cuda), tok.to(cuda), pe.to(cuda), _table(suh_d, ())).cpu()
+    x16 = x.to(torch.float16).numpy()
+    for j in range(P):
+        if pe[j] < 0:
+            assert torch.isnan(got[j]).all()
+            continue
+        ref = exl3.rot_in(x16[tok[j]][None], suh[pe[j]].numpy())[0]
+        assert np.array_equal(got[j].numpy().view(np.uint16), ref.view(np.uint16)), j
+
+
+def test_router_logits_bit_exact(cuda):
+    from mi355moe import ops, synthetic
+    _say("router_logits T=8 E=288 K=4096")
+    w, _ = synthetic.router(288, 4096, seed=1, device="cpu")
+    x = synthetic.activations(8, 4096, seed=2, device="cpu")
+    got = ops.router_logits(x.to(cuda), w.to(cuda)).cpu().numpy()
+    ref = routing.router_logits(x.float().numpy(), w.float().numpy())
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("T,E,topk", [(64, 288, 8), (5, 32, 4), (3, 1024, 32)])
+def test_router_topk_bit_exact(cuda, T, E, topk):
+    from mi355moe import ops
+    _say(f"router_topk T={T} E={E} topk={topk}")
+    g = torch.Generator().manual_seed(T + E)
+    lg = torch.randn(T, E, generator=g) * 2
+    b = torch.randn(E, generator=g) * 0.01
+    lg[0, 7] = lg[0, 9]
+    b[7] = b[9]                                   # an exact tie
+    ids, w = ops.router_topk(lg.to(cuda), topk, b.to(cuda), routed_scale=2.5)
+    rid, rw = routing.topk_sigmoid_bias(lg.numpy(), b.numpy(), topk, 2.5)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert np.array_equal(w.cpu().numpy(), rw)
+
+
+@pytest.mark.parametrize("T,topk,n,seg,ids64,emap", [(8, 8, 288, 8, False, False), (1, 8, 288, 1, True, False),
+                                                     (64, 8, 288, 16, False, True), (2048, 8, 288, 256, False, False),
+                                                     (8192, 8, 288, 256, True, False), (130, 8, 64, 16, True, True)])
+def test_route_bit_exact(cuda, T, topk, n, seg, ids64, emap):
+    from mi355moe import ops
+    _say(f"route T={T} topk={topk} n={n} seg={seg}")
+    g = torch.Generator().manual_seed(T)
+    ids = torch.randint(-1, n + 2, (T, topk), generator=g)
+    ids = ids.to(torch.int64 if ids64 else torch.int32)
+    w = torch.rand(T, topk, generator=g)
+    em = None
+    if emap:
+        em = torch.randint(-1, n, (n + 2,), generator=g, dtype=torch.int64)
+    r = ops.route(ids.to(cuda), w.to(cuda), n, R=1 << 30, seg_rows=seg, expert_map=None if em is None else em.to(cuda))
+    local = routing.map_topk_to_local(ids.numpy(), n, None if em is None else em.numpy())
+    o = routing.permutation(local, n, topk, 1 << 30, seg)
+    P = T * topk
+    assert np.array_equal(r["inv"].cpu().numpy(), o["inv"])
+    assert np.array_equal(r["tok"].cpu().numpy(), o["token"])
+    assert np.array_equal(r["pe"].cpu().numpy(), o["pair_expert"])
+    assert np.array_equal(r["counts"].cpu().numpy(), o["counts"])
+    ns = int(r["nseg"].item())
+    assert ns == len(o["seg_expert"])
+    assert np.array_equal(r["seg_expert"][:ns].cpu().numpy(), o["seg_expert"])
+    assert np.array_equal(r["seg_row0"][:ns].cpu().numpy(), o["seg_row0"])
+    assert np.array_equal(r["seg_rows"][:ns].cpu().numpy(), o["seg_rows"])
+    w16 = w.numpy().reshape(-1).astype(np.float16)[o["order"]]
+    assert np.array_equal(r["w16"].cpu().numpy().view(np.uint16), w16.view(np.uint16))
+    assert P == o["order"].size
