@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark of the routed-MoE layer hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill]
+
+Default workload (one "step" = one MoE layer call): the decode MoE layer, T=8 tokens, hidden 4096, 288 experts,
+sigmoid router + bias, top-8, routed scale 2.5, intermediate 1024 (one tensor-parallel rank's shard), EXL3 4-bit
+synthetic experts. A step runs the router GEMM, the sigmoid/bias top-k, the permutation, the grouped gate/up and
+down trellis GEMVs and the combine, replayed from HIP graphs captured per (layer, input) pair. Steps cycle over
+several distinct layers so every step streams cold expert weights (the set exceeds the 256 MiB last-level cache).
+
+Printed (one JSON line): value = achieved HBM GB/s over the timed steps, counting per step the bytes a layer call
+must read: D distinct routed experts x (6,291,456 B trellis + 30,720 B fp16 scales) + router weight and bias +
+activations in and out. The roofline entry times the dominant kernel (the grouped gate/up GEMV) alone with HIP
+events on the launch stream. cpu_baseline times the oracle's C port of the same layer call on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "glm-5.3-flash-dgx-spark-vllm-optimization_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MoE layer µs @T=8 + achieved HBM GB/s; prefill MoE tokens/s @T=8192"
+HBM_PEAK_GBS = 8000.0
+K, N, E, TOPK, SCALE, LIMIT = 4096, 1024, 288, 8, 2.5, 10.0
+EXPERT_TRELLIS = 3 * K * N // 2            # 6,291,456
+EXPERT_SCALES = 2 * (3 * K + 3 * N)        # 30,720
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_problem(torch, synthetic, ops, dev, T, n_layers, n_inputs):
+    layers, routers, xs = [], [], []
+    for l in range(n_layers):
+        w, b = synthetic.router(E, K, seed=100 + l, device=dev)
+        routers.append((w, b))
+        layers.append(synthetic.exl3_layer(E, K, N, seed=200 + l, device=dev))
+    for i in range(n_inputs):
+        xs.append(synthetic.activations(T, K, seed=300 + i, device=dev))
+    return layers, routers, xs
+
+
+def step_fn(ops, layer, router, x, bufs):
+    w, b = router
+    logits = ops.router_logits(x, w)
+    ids, wts = ops.router_topk(logits, TOPK, b, routed_scale=SCALE)
+    ops.moe_forward_ids(layer, x, ids, wts, limit=LIMIT, out=bufs["out"])
+    return ids, wts
+
+
+def cpu_baseline(torch, layer, x, ids, wts, threads, min_seconds=10.0):
+    """The oracle's C port of one full layer call (decode rounding points) on the host, repeated >= min_seconds."""
+    import numpy as np
+    from oracle import moe, routing
+    ids_np = ids.cpu().numpy()
+    used = np.unique(ids_np[ids_np >= 0])
+    remap = {int(e): i for i, e in enumerate(used)}
+    sel = torch.as_tensor(used, dtype=torch.long, device=layer.device)
+    lay = {k: getattr(layer, k).index_select(0, sel).cpu().numpy() for k in
+           ("w13_trellis", "w13_suh", "w13_svh", "w2_trellis", "w2_suh", "w2_svh")}
+    local = np.vectorize(lambda e: remap.get(int(e), len(used)))(ids_np)
+    tok, ex, w16 = moe.pairs_from_routing(local, wts.cpu().numpy(), len(used), ids_np.shape[1])
+    x16 = x.to(torch.float16).cpu().numpy()
+    moe.lib()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        moe.forward(lay, x16, tok, ex, w16, LIMIT, "decode", threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= min_seconds and reps >= 2:
+            break
+    del routing
+    return el / reps, reps, len(used)
+
+
+def run_decode(args, torch, mi355moe, dev):
+    from mi355moe import _lib, ops, synthetic
+    T = args.tokens
+    n_layers, n_inputs = args.layers, 4
+    log(f"[bench] building {n_layers} layers x {E} experts ({n_layers * E * (EXPERT_TRELLIS + EXPERT_SCALES) / 1e9:.1f}"
+        " GB) ...")
+    layers, routers, xs = build_problem(torch, synthetic, ops, dev, T, n_layers, n_inputs)
+    combos = [(l, i) for i in range(n_inputs) for l in range(n_layers)]
+    bufs = {c: {"out": torch.empty(T, K, dtype=torch.bfloat16, device=dev)} for c in combos}
+    # eager pass: routing of every combo (distinct experts per call) and workspace sizing before capture
+    info = {}
+    for c in combos:
+        ids, wts = step_fn(ops, layers[c[0]], routers[c[0]], xs[c[1]], bufs[c])
+        torch.cuda.synchronize()
+        d = int(torch.unique(ids).numel())
+        info[c] = (d, ids.clone(), wts.clone())
+    graphs = {}
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for c in combos:
+            step_fn(ops, layers[c[0]], routers[c[0]], xs[c[1]], bufs[c])
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    for c in combos:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step_fn(ops, layers[c[0]], routers[c[0]], xs[c[1]], bufs[c])
+        graphs[c] = g
+    torch.cuda.synchronize()
+    # correctness guard: a replay equals the eager result
+    ref = bufs[combos[0]]["out"].clone()
+    graphs[combos[0]].replay()
+    torch.cuda.synchronize()
+    if not torch.equal(ref, bufs[combos[0]]["out"]):
+        raise RuntimeError("graph replay differs from the eager step")
+
+    def step_bytes(c):
+        d = info[c][0]
+        return d * (EXPERT_TRELLIS + EXPERT_SCALES) + E * K * 2 + E * 4 + 2 * T * K * 2
+
+    for w in range(args.warmup):
+        graphs[combos[w % len(combos)]].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    total_bytes = 0
+    dsum = 0
+    for k in range(args.steps):
+        c = combos[k % len(combos)]
+        graphs[c].replay()
+        total_bytes += step_bytes(c)
+        dsum += info[c][0]
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = ev0.elapsed_time(ev1)
+    us_per_step = ms * 1000.0 / args.steps
+    gbs = total_bytes / (ms / 1000.0) / 1e9
+
+    # dominant kernel alone (grouped gate/up GEMV): route staged untimed, then event-bracketed gate/up launches
+    gu_us, gu_bytes = [], []
+    for k in range(args.steps):
+        c = combos[k % len(combos)]
+        d, ids, wts = info[c]
+        lay, x = layers[c[0]], xs[c[1]]
+        ops.moe_forward_ids(lay, x, ids, wts, limit=LIMIT, out=bufs[c]["out"], stages=_lib.STAGE_ROUTE)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        ops.moe_forward_ids(lay, x, ids, wts, limit=LIMIT, out=bufs[c]["out"], stages=_lib.STAGE_GATEUP)
+        b.record()
+        ops.moe_forward_ids(lay, x, ids, wts, limit=LIMIT, out=bufs[c]["out"],
+                            stages=_lib.STAGE_DOWN | _lib.STAGE_COMBINE)
+        gu_us.append((a, b))
+        gu_bytes.append(d * (2 * K * N // 2 + 2 * (2 * K + 3 * N)) + T * TOPK * 0 + T * K * 2)
+    torch.cuda.synchronize()
+    gu_t = [a.elapsed_time(b) * 1000.0 for a, b in gu_us]
+    gu_avg_us = sum(gu_t) / len(gu_t)
+    gu_gbs = (sum(gu_bytes) / len(gu_bytes)) / (gu_avg_us * 1e-6) / 1e9
+
+    res = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"decode MoE layer T={T}: hidden {K}, {E} experts, sigmoid+bias top-{TOPK} x{SCALE}, "
+                               f"intermediate {N}, EXL3 4-bit synthetic experts, {n_layers} layers cycled (cold)",
+                   "tokens": T, "hidden": K, "experts": E, "topk": TOPK, "intermediate": N,
+                   "graph": "one HIP graph per (layer, input)"},
+        "decode_us_per_layer": round(us_per_step, 2),
+        "distinct_experts_mean": round(dsum / args.steps, 2),
+        "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "dec_gateup_kernel", "achieved": round(gu_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "avg_launch_us": round(gu_avg_us, 2)},
+        "wall_s": round(wall, 3),
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        c = combos[0]
+        sec, reps, d = cpu_baseline(torch, layers[c[0]], xs[c[1]], info[c][1], info[c][2], threads)
+        res["cpu_baseline"] = {"value": round(step_bytes(c) / sec / 1e9, 4), "unit": "GB/s", "cores": threads,
+                               "kind": "port", "seconds_per_call": round(sec, 4),
+                               "sample": f"{reps} repetitions of one full T={T} layer call ({d} distinct experts) "
+                                         "through the oracle's C port (oracle/csrc/oracle.c, decode rounding "
+                                         f"points, OpenMP {threads} threads)"}
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--tokens", type=int, default=8)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    import mi355moe
+    mi355moe._lib.lib()
+    dev = torch.device("cuda", 0)
+    res = run_decode(args, torch, mi355moe, dev)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

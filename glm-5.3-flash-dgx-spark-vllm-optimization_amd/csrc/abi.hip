@@ -58,15 +58,16 @@ DecodePlan plan_decode(int64_t P, int64_t rows_bound, int64_t n, int64_t K, int6
     const int64_t target = 2048;
     // K range per gate/up workgroup: largest of {1024, 512, 256, 128} that divides K and still gives ~target
     // workgroups (the input-row buffer 2 * rmax * KR fp16 stays <= 64 KiB)
+    // (the input rows staged in LDS stay <= 16 KiB per workgroup so occupancy is set by registers, not LDS)
     int64_t kr = 128;
     for (int64_t c : {1024, 512, 256, 128}) {
-        if (K % c || 2 * d.rmax * c * 2 > 65536) continue;
+        if (K % c || 2 * d.rmax * c * 2 > 16384) continue;
         if (s_est * (N / 128) * (K / c) >= target || c == 128) { kr = c; break; }
     }
     d.sk_gu = (int)(K / kr);
     int64_t nr = 128;
     for (int64_t c : {1024, 512, 256, 128}) {
-        if (N % c || d.rmax * c * 2 > 65536) continue;
+        if (N % c || d.rmax * c * 2 > 16384) continue;
         if (s_est * (K / 128) * (N / c) >= target || c == 128) { nr = c; break; }
     }
     d.sk_dn = (int)(N / nr);
@@ -171,7 +172,7 @@ int mi355moe_exl3_dequant(const void* trellis, int64_t k_tiles, int64_t n_tiles,
 int mi355moe_router_logits(const void* x, int64_t T, int64_t K, int64_t x_stride, const void* w, int64_t E,
                            float* logits, hipStream_t stream) {
     if (!x || !w || !logits) return MI355MOE_EINVAL;
-    if (T < 0 || E < 1 || K < 512 || K % 512 || x_stride < K || x_stride % 8) return MI355MOE_ESHAPE;
+    if (T < 0 || E < 1 || K < 512 || K % 512 || K > 8192 || x_stride < K || x_stride % 8) return MI355MOE_ESHAPE;
     if (T == 0) return 0;
     return rc_launch(launch_router_logits(static_cast<const uint16_t*>(x), x_stride, static_cast<const uint16_t*>(w),
                                           (int)T, (int)K, (int)E, logits, stream));
@@ -257,7 +258,7 @@ int mi355moe_rot_in(const void* x, int x_dtype, int64_t x_stride, int64_t K, con
 int64_t mi355moe_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk) {
     if (layer_shape_ok(layer) || T < 0 || topk < 1 || topk > MAX_TOPK) return -1;
     const int64_t P = std::max<int64_t>(1, T * topk);
-    const DecodePlan p = plan_decode(P, P, layer->n, layer->hidden, layer->intermediate);
+    const DecodePlan p = plan_decode(P, std::max<int64_t>(1, T), layer->n, layer->hidden, layer->intermediate);
     DecodeWs w;
     carve_decode(nullptr, P, layer->n, layer->hidden, layer->intermediate, p, true, w);
     return (int64_t)w.bytes;
@@ -290,7 +291,7 @@ int mi355moe_moe_forward_ids_stages(const mi355moe_exl3_layer* layer, const void
     const int64_t P = T * topk;
     if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
     if (P == 0) return 0;
-    const DecodePlan p = plan_decode(P, P, n, K, N);
+    const DecodePlan p = plan_decode(P, T, n, K, N);
     if (p.S_cap > 65535) return MI355MOE_ELIMIT;
     DecodeWs w;
     carve_decode(workspace, P, n, K, N, p, true, w);
@@ -343,10 +344,14 @@ int mi355moe_moe_forward_ids_stages(const mi355moe_exl3_layer* layer, const void
 int64_t mi355moe_exl3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t P) {
     if (layer_shape_ok(layer) || P < 0) return -1;
     const int64_t Pp = std::max<int64_t>(1, P);
-    const DecodePlan p = plan_decode(Pp, Pp, layer->n, layer->hidden, layer->intermediate);
-    DecodeWs w;
-    carve_decode(nullptr, Pp, layer->n, layer->hidden, layer->intermediate, p, false, w);
-    return (int64_t)w.bytes;
+    size_t most = 0;                                  // the plan depends on the row cap: take the largest layout
+    for (int64_t rows = 1; rows <= 16; rows *= 2) {
+        const DecodePlan p = plan_decode(Pp, std::min(Pp, rows), layer->n, layer->hidden, layer->intermediate);
+        DecodeWs w;
+        carve_decode(nullptr, Pp, layer->n, layer->hidden, layer->intermediate, p, false, w);
+        most = std::max(most, w.bytes);
+    }
+    return (int64_t)most;
 }
 
 int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int64_t B, float* out,

@@ -106,9 +106,26 @@ __device__ __forceinline__ float sigmoid_dexp(float g) {
     return __fdiv_rn(1.0f, 1.0f + e);
 }
 
-// Release / acquire around the split-K arrival counters: stores before the release are visible at device
-// scope to a workgroup that observes the counter value after its acquire.
-__device__ __forceinline__ void fence_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-__device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+// Split-K partials cross workgroups (and XCDs, each with its own L2) through device-coherent accesses instead of
+// L2 write-back / invalidate fences: partials are stored and re-loaded as relaxed agent-scope atomics (stores write
+// through to the device coherence point, loads do not hit stale lines), and the arrival counter is bumped only
+// after every store of the workgroup has completed (s_waitcnt + barrier).
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Returns true in the workgroup that completes counter `c` (the `total`-th arrival); it then resets the counter.
+// Every thread's coherent stores are complete before its workgroup arrives.
+__device__ __forceinline__ bool arrive_last(unsigned* c, unsigned total, int* flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *flag = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+    __syncthreads();
+    return *flag != 0;
+}
 
 }  // namespace mi355moe

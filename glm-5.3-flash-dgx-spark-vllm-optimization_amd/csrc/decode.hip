@@ -143,21 +143,11 @@ __device__ __forceinline__ void reduce_store(float (&acc)[RMAX][2], float* red, 
         float s = red[r * 128 + c];
 #pragma unroll
         for (int w2 = 1; w2 < DEC_WAVES; ++w2) s += red[(w2 * RMAX + r) * 128 + c];
-        dst[(size_t)r * ld + c] = s;
+        st_coherent(dst + (size_t)r * ld + c, s);
     }
     __syncthreads();
 }
 
-// Split-K arrival: returns true in the workgroup that completes counter `c` (after all `total` splits arrived).
-__device__ __forceinline__ bool arrive_last(unsigned* c, unsigned total, int* flag) {
-    fence_release();
-    __syncthreads();
-    if (threadIdx.x == 0) *flag = atomicAdd(c, 1u) == total - 1;
-    __syncthreads();
-    if (!*flag) return false;
-    fence_acquire();
-    return true;
-}
 
 template <int RMAX>
 __global__ __launch_bounds__(DEC_WAVES * 64) void dec_gateup_kernel(DecodeArgs a) {
@@ -193,15 +183,27 @@ __global__ __launch_bounds__(DEC_WAVES * 64) void dec_gateup_kernel(DecodeArgs a
     float ag[RMAX][2], au[RMAX][2];
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) ag[r][0] = ag[r][1] = au[r][0] = au[r][1] = 0.f;
+    // software pipeline: the next two k tiles of both matrices are in flight while the current two are decoded
+    u32x4 g0 = ld_stream(G + idx), u0 = ld_stream(U + idx);
+    u32x4 g1 = ld_stream(G + idx + kstr), u1 = ld_stream(U + idx + kstr);
     for (int kk = 0; kk < KTw; kk += 2) {
-        const u32x4 g0 = ld_stream(G + idx), u0 = ld_stream(U + idx);
-        const u32x4 g1 = ld_stream(G + idx + kstr), u1 = ld_stream(U + idx + kstr);
         idx += 2 * kstr;
+        u32x4 ng0 = g0, nu0 = u0, ng1 = g1, nu1 = u1;
+        if (kk + 2 < KTw) {
+            ng0 = ld_stream(G + idx);
+            nu0 = ld_stream(U + idx);
+            ng1 = ld_stream(G + idx + kstr);
+            nu1 = ld_stream(U + idx + kstr);
+        }
         const int koff = (ktl0 + kk) * 16;
         tile_fma<RMAX>(g0, lane, xs, KR, koff, rn, ag);
         tile_fma<RMAX>(u0, lane, xs + (size_t)RMAX * KR, KR, koff, rn, au);
         tile_fma<RMAX>(g1, lane, xs, KR, koff + 16, rn, ag);
         tile_fma<RMAX>(u1, lane, xs + (size_t)RMAX * KR, KR, koff + 16, rn, au);
+        g0 = ng0;
+        u0 = nu0;
+        g1 = ng1;
+        u1 = nu1;
     }
     __syncthreads();                                                 // xs is reused for the reduction
 
@@ -225,10 +227,10 @@ __global__ __launch_bounds__(DEC_WAVES * 64) void dec_gateup_kernel(DecodeArgs a
         for (int k = 0; k < a.sk_gu; ++k) {
             const float* zg = a.zg + ((size_t)(k * 2) * P + row) * N + col;
             const float* zu = a.zg + ((size_t)(k * 2 + 1) * P + row) * N + col;
-            g[0] += zg[0];
-            g[1] += zg[1];
-            u[0] += zu[0];
-            u[1] += zu[1];
+            g[0] += ld_coherent(zg);
+            g[1] += ld_coherent(zg + 1);
+            u[0] += ld_coherent(zu);
+            u[1] += ld_coherent(zu + 1);
         }
         fwht128_w64(g[0], g[1], lane);
         fwht128_w64(u[0], u[1], lane);
@@ -279,12 +281,19 @@ __global__ __launch_bounds__(DEC_WAVES * 64) void dec_down_kernel(DecodeArgs a) 
     float ad[RMAX][2];
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) ad[r][0] = ad[r][1] = 0.f;
+    u32x4 d0 = ld_stream(D + idx), d1 = ld_stream(D + idx + nstr);
     for (int kk = 0; kk < NTw; kk += 2) {
-        const u32x4 d0 = ld_stream(D + idx), d1 = ld_stream(D + idx + nstr);
         idx += 2 * nstr;
+        u32x4 n0 = d0, n1 = d1;
+        if (kk + 2 < NTw) {
+            n0 = ld_stream(D + idx);
+            n1 = ld_stream(D + idx + nstr);
+        }
         const int koff = (ntl0 + kk) * 16;
         tile_fma<RMAX>(d0, lane, xs, NR, koff, rn, ad);
         tile_fma<RMAX>(d1, lane, xs, NR, koff + 16, rn, ad);
+        d0 = n0;
+        d1 = n1;
     }
     __syncthreads();
     float* red = reinterpret_cast<float*>(smem);
@@ -302,8 +311,8 @@ __global__ __launch_bounds__(DEC_WAVES * 64) void dec_down_kernel(DecodeArgs a) 
         float v[2] = {0.f, 0.f};
         for (int k = 0; k < a.sk_dn; ++k) {
             const float* z = a.zd + ((size_t)k * P + row) * K + col;
-            v[0] += z[0];
-            v[1] += z[1];
+            v[0] += ld_coherent(z);
+            v[1] += ld_coherent(z + 1);
         }
         fwht128_w64(v[0], v[1], lane);
         const float rs = HAD_R * (float)u16_as_h(a.w16[row]);

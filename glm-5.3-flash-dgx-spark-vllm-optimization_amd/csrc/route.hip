@@ -1,8 +1,7 @@
 // Router and token->expert permutation kernels.
 //
-// router_logits  logits[t][e] = x[t] . W[e] (bf16 operands, fp32), one wave per expert: lane l accumulates
-//                k = 512c + 8l + i (c ascending, i = 0..7) sequentially, then the 64 lane partials are combined by
-//                the xor butterfly m = 32, 16, ..., 1 (a fixed order, so results are reproducible bit for bit).
+// router_logits  logits[t][e] = x[t] . W[e] (bf16 operands, fp32) in a fixed order (reproducible bit for bit):
+//                per 512-wide chunk, lane sums of 8 products, a lane butterfly, then the chunks in order.
 //                Replaces F.linear(x, W).to(float32) (code/fork/docs/BF16_GEMV.md:27,38).
 // router_topk    vLLM grouped_topk with n_group = topk_group = 1 as restated by code/fork/docs/ref/tf_glue.py:371-401:
 //                score = sigmoid(logit), pick the topk largest score + bias (lower id first among equals),
@@ -18,49 +17,55 @@ namespace mi355moe {
 
 // ------------------------------------------------------------------------------------------------ router GEMV
 
-constexpr int RL_TCHUNK = 8;   // tokens per pass of a wave
+constexpr int RL_TCHUNK = 8;   // tokens per pass
+constexpr int RL_MAXC = 16;    // K chunks of 512 (K <= 8192)
 
-__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
-                                                            const uint16_t* __restrict__ w, int T, int K, int E,
-                                                            float* __restrict__ logits) {
+// One workgroup per expert, one wave per 512-wide chunk c of K. Lane l of chunk c accumulates k = 512c + 8l + i,
+// i = 0..7, sequentially in fp32 (bf16 x bf16 products are exact in fp32, so the fused multiply-add rounds like
+// an add); the 64 lane partials are combined by the xor butterfly m = 32, 16, ..., 1; the chunk sums are then added
+// in chunk order c = 0, 1, ... (wave 0 adds them from LDS).
+__global__ __launch_bounds__(1024) void router_logits_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                             const uint16_t* __restrict__ w, int T, int K, int E,
+                                                             float* __restrict__ logits) {
+    __shared__ float part[RL_MAXC][RL_TCHUNK];
     const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (e >= E) return;
-    const uint16_t* wr = w + (size_t)e * K;
+    const int c = threadIdx.x >> 6;                 // chunk of this wave
     const int chunks = K / 512;
+    const int e = blockIdx.x;
+    const int k0 = c * 512 + lane * 8;
+    u32x4 wv = {0u, 0u, 0u, 0u};
+    if (c < chunks) wv = *reinterpret_cast<const u32x4*>(w + (size_t)e * K + k0);
+    float wf[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        wf[2 * i] = __builtin_bit_cast(float, wv[i] << 16);
+        wf[2 * i + 1] = __builtin_bit_cast(float, wv[i] & 0xFFFF0000u);
+    }
     for (int t0 = 0; t0 < T; t0 += RL_TCHUNK) {
-        float acc[RL_TCHUNK];
-#pragma unroll
-        for (int i = 0; i < RL_TCHUNK; ++i) acc[i] = 0.f;
-        for (int c = 0; c < chunks; ++c) {
-            const int k0 = c * 512 + lane * 8;
-            const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + k0);
-            float wf[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                wf[2 * i] = __builtin_bit_cast(float, wv[i] << 16);
-                wf[2 * i + 1] = __builtin_bit_cast(float, wv[i] & 0xFFFF0000u);
-            }
+        if (c < chunks) {
 #pragma unroll
             for (int tt = 0; tt < RL_TCHUNK; ++tt) {
+                float acc = 0.f;
                 if (t0 + tt < T) {
                     const u32x4 xv = *reinterpret_cast<const u32x4*>(x + (size_t)(t0 + tt) * x_stride + k0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        acc[tt] = __builtin_fmaf(__builtin_bit_cast(float, xv[i] << 16), wf[2 * i], acc[tt]);
-                        acc[tt] = __builtin_fmaf(__builtin_bit_cast(float, xv[i] & 0xFFFF0000u), wf[2 * i + 1],
-                                                 acc[tt]);
+                        acc = __builtin_fmaf(__builtin_bit_cast(float, xv[i] << 16), wf[2 * i], acc);
+                        acc = __builtin_fmaf(__builtin_bit_cast(float, xv[i] & 0xFFFF0000u), wf[2 * i + 1], acc);
                     }
                 }
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m, 64);
+                if (lane == 0) part[c][tt] = acc;
             }
         }
-#pragma unroll
-        for (int tt = 0; tt < RL_TCHUNK; ++tt) {
-            float v = acc[tt];
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, 64);
-            if (lane == 0 && t0 + tt < T) logits[(size_t)(t0 + tt) * E + e] = v;
+        __syncthreads();
+        if (threadIdx.x < RL_TCHUNK && t0 + (int)threadIdx.x < T) {
+            float s = part[0][threadIdx.x];
+            for (int cc = 1; cc < chunks; ++cc) s = s + part[cc][threadIdx.x];
+            logits[(size_t)(t0 + threadIdx.x) * E + e] = s;
         }
+        __syncthreads();
     }
 }
 
@@ -386,7 +391,7 @@ __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
 
 int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w, int T, int K, int E, float* logits,
                          hipStream_t st) {
-    hipLaunchKernelGGL(router_logits_kernel, dim3((E + 3) / 4), dim3(256), 0, st, x, x_stride, w, T, K, E, logits);
+    hipLaunchKernelGGL(router_logits_kernel, dim3(E), dim3(64 * (K / 512)), 0, st, x, x_stride, w, T, K, E, logits);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

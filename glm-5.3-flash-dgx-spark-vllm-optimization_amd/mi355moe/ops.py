@@ -156,8 +156,9 @@ def rot_in(x: torch.Tensor, tok: torch.Tensor, pe: torch.Tensor, suh_table: torc
 
 def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                     limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                    out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """Routed-expert output [T, K] (x's dtype unless out/out_dtype say otherwise), written (not accumulated)."""
+                    out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL) -> torch.Tensor:
+    """Routed-expert output [T, K] (x's dtype unless out/out_dtype say otherwise), written (not accumulated).
+    stages: a subset of the call's launches (_lib.STAGE_*), for timing one kernel; the default runs them all."""
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
     if dev != experts.device:
         raise ValueError(f"activations on {dev}, experts on {experts.device}")
@@ -179,8 +180,9 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
         raise ValueError("mi355moe_moe_workspace_bytes rejected the shape")
     ws = workspace(dev, nb)
     em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
-    _lib.check("mi355moe_moe_forward_ids", L.mi355moe_moe_forward_ids(
+    _lib.check("mi355moe_moe_forward_ids", L.mi355moe_moe_forward_ids_stages(
         ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
         ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em), 0 if em is None else em.numel(),
-        float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), _stream(dev)))
+        float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), int(stages),
+        _stream(dev)))
     return out

@@ -66,7 +66,8 @@ const char* mi355moe_strerror(int code);
 int mi355moe_exl3_dequant(const void* trellis, int64_t k_tiles, int64_t n_tiles, void* wq, hipStream_t stream);
 
 /* Router logits fp32 [T][E] = x bf16 [T][K] (row stride x_stride) times W bf16 [E][K]^T, in a fixed summation
- * order (replaces F.linear(x, W).to(torch.float32), code/fork/docs/BF16_GEMV.md:27,38). K % 512 == 0. */
+ * order (replaces F.linear(x, W).to(torch.float32), code/fork/docs/BF16_GEMV.md:27,38). K % 512 == 0,
+ * K <= 8192. */
 int mi355moe_router_logits(const void* x, int64_t T, int64_t K, int64_t x_stride, const void* w, int64_t E,
                            float* logits, hipStream_t stream);
 

@@ -30,27 +30,31 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 
 def router_logits(x: np.ndarray, w: np.ndarray) -> np.ndarray:
     """fp32 logits [T, E] of bf16 x [T, K] and bf16 W [E, K] (given as float32 arrays holding bf16 values), in the
-    summation order of this build's router kernel: lane l (of 64) accumulates k = c*512 + 8l + i for c = 0..K/512-1,
-    i = 0..7 sequentially in fp32 (each bf16 x bf16 product is exact in fp32, so a fused multiply-add rounds like
-    an add); the 64 lane partials are then combined by the xor butterfly p[l] += p[l ^ m], m = 32, 16, ..., 1."""
+    summation order of this build's router kernel: for every 512-wide chunk c of K, lane l (of 64) adds
+    k = 512c + 8l + i for i = 0..7 sequentially in fp32 from 0 (each bf16 x bf16 product is exact in fp32, so a
+    fused multiply-add rounds like an add); the 64 lane sums are combined by the xor butterfly p[l] += p[l ^ m],
+    m = 32, 16, ..., 1; the chunk sums are then added in chunk order."""
     x = np.asarray(x, np.float32)
     w = np.asarray(w, np.float32)
     T, K = x.shape
     E = w.shape[0]
     if K % ROUTER_CHUNK:
         raise ValueError("K must be a multiple of 512")
-    xc = x.reshape(T, K // ROUTER_CHUNK, 64, 8)
-    wc = w.reshape(E, K // ROUTER_CHUNK, 64, 8)
-    acc = np.zeros((T, E, 64), np.float32)
-    for c in range(K // ROUTER_CHUNK):
-        for i in range(8):
-            acc = acc + xc[:, None, c, :, i] * wc[None, :, c, :, i]
+    C = K // ROUTER_CHUNK
+    xc = x.reshape(T, C, 64, 8)
+    wc = w.reshape(E, C, 64, 8)
+    acc = np.zeros((T, E, C, 64), np.float32)
+    for i in range(8):
+        acc = acc + xc[:, None, :, :, i] * wc[None, :, :, :, i]
     m = 32
     lanes = np.arange(64)
     while m:
-        acc = acc + acc[:, :, lanes ^ m]
+        acc = acc + acc[..., lanes ^ m]
         m >>= 1
-    return acc[:, :, 0]
+    tot = acc[..., 0, 0].copy()
+    for c in range(1, C):
+        tot = tot + acc[..., c, 0]
+    return tot
 
 
 def sigmoid_f32(logits: np.ndarray) -> np.ndarray:

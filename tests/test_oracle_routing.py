@@ -30,19 +30,24 @@ def test_router_logits_order_by_explicit_loops():
     got = routing.router_logits(x, w)
     for t in range(T):
         for e in range(E):
-            part = []
-            for lane in range(64):
-                acc = np.float32(0)
-                for c in range(K // 512):
+            chunk_sums = []
+            for c in range(K // 512):
+                part = []
+                for lane in range(64):
+                    acc = np.float32(0)
                     for i in range(8):
                         k = c * 512 + lane * 8 + i
                         acc = np.float32(acc + np.float32(x[t, k] * w[e, k]))
-                part.append(acc)
-            m = 32
-            while m:
-                part = [np.float32(part[l] + part[l ^ m]) for l in range(64)]
-                m //= 2
-            assert got[t, e] == part[0]
+                    part.append(acc)
+                m = 32
+                while m:
+                    part = [np.float32(part[l] + part[l ^ m]) for l in range(64)]
+                    m //= 2
+                chunk_sums.append(part[0])
+            tot = chunk_sums[0]
+            for s in chunk_sums[1:]:
+                tot = np.float32(tot + s)
+            assert got[t, e] == tot
 
 
 def test_router_logits_close_to_f64():
