@@ -30,6 +30,7 @@ for _p in (ROOT, PKG):
 
 METRIC = "MoE layer µs @T=8 + achieved HBM GB/s; prefill MoE tokens/s @T=8192"
 HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
 K, N, E, TOPK, SCALE, LIMIT = 4096, 1024, 288, 8, 2.5, 10.0
 EXPERT_TRELLIS = 3 * K * N // 2            # 6,291,456
 EXPERT_SCALES = 2 * (3 * K + 3 * N)        # 30,720
@@ -192,12 +193,73 @@ def run_decode(args, torch, mi355moe, dev):
     return res
 
 
+def run_prefill(args, torch, dev):
+    """Prefill MoE chunk, T=8192 (same layer shapes), uniform-random router logits; the grouped MFMA path."""
+    from mi355moe import _lib, ops, synthetic
+    T = args.prefill_tokens
+    n_layers = 2
+    layers = [synthetic.exl3_layer(E, K, N, seed=400 + l, device=dev) for l in range(n_layers)]
+    x = synthetic.activations(T, K, seed=500, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(501)
+    logits = [torch.rand(T, E, generator=g, device=dev) * 4 - 2 for _ in range(n_layers)]
+    outs = [torch.empty(T, K, dtype=torch.bfloat16, device=dev) for _ in range(n_layers)]
+
+    def step(l):
+        ids, wts = ops.router_topk(logits[l], TOPK, None, routed_scale=SCALE)
+        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l])
+        return ids, wts
+
+    info = [step(l) for l in range(n_layers)]
+    torch.cuda.synchronize()
+    pairs = [int((i >= 0).sum().item()) for i, _ in info]
+    for w in range(max(2, args.warmup // 4)):
+        step(w % n_layers)
+    torch.cuda.synchronize()
+    steps = max(4, args.steps // 4)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for k in range(steps):
+        step(k % n_layers)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    # the gate/up grouped GEMM alone (route + gather staged before the bracketed launch)
+    gu = []
+    for k in range(steps):
+        l = k % n_layers
+        ids, wts = info[l]
+        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], stages=_lib.STAGE_ROUTE)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], stages=_lib.STAGE_GATEUP)
+        b.record()
+        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l],
+                            stages=_lib.STAGE_DOWN | _lib.STAGE_COMBINE)
+        gu.append((a, b))
+    torch.cuda.synchronize()
+    gu_ms = sum(a.elapsed_time(b) for a, b in gu) / len(gu)
+    P = sum(pairs) / len(pairs)
+    flops = 2.0 * P * (K * 2 * N + N * K)
+    gu_flops = 2.0 * P * K * 2 * N
+    return {"prefill_tokens_per_s": round(T / (ms / 1000.0), 1), "prefill_ms_per_layer": round(ms, 4),
+            "prefill_tflops": round(flops / (ms / 1000.0) / 1e12, 2),
+            "roofline_prefill": {"bound": "mfma", "kernel": "pf_gateup_kernel (includes the gather launch)",
+                                 "achieved": round(gu_flops / (gu_ms / 1000.0) / 1e12, 2),
+                                 "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(gu_flops / (gu_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+                                 "avg_launch_us": round(gu_ms * 1000.0, 1)},
+            "prefill_config": f"T={T}, {E} experts, top-{TOPK}, uniform-random router logits, EXL3 4-bit synthetic "
+                              f"experts, {n_layers} layers alternated, {steps} timed steps"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill"])
+    ap.add_argument("--prefill-tokens", type=int, default=8192)
     ap.add_argument("--tokens", type=int, default=8)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -213,7 +275,14 @@ def main():
     import mi355moe
     mi355moe._lib.lib()
     dev = torch.device("cuda", 0)
-    res = run_decode(args, torch, mi355moe, dev)
+    if args.workload == "prefill":
+        args.no_cpu_baseline = True
+        res = run_decode(argparse.Namespace(**{**vars(args), "steps": 8, "warmup": 2}), torch, mi355moe, dev)
+    else:
+        res = run_decode(args, torch, mi355moe, dev)
+    if args.workload in ("all", "prefill"):
+        log("[bench] prefill ...")
+        res.update(run_prefill(args, torch, dev))
     print(json.dumps(res), flush=True)
 
 

@@ -255,13 +255,68 @@ int mi355moe_rot_in(const void* x, int x_dtype, int64_t x_stride, int64_t K, con
                                    static_cast<uint16_t*>(out), stream));
 }
 
-int64_t mi355moe_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk) {
+// ---- routed experts from router ids: decode path or grouped prefill path
+
+namespace {
+
+struct PrefillWs {
+    RouteArgs ra;
+    PrefillArgs pa;
+    size_t bytes;
+};
+
+void carve_prefill(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t N, PrefillWs& w, int& S_cap) {
+    Carve c(ws);
+    RouteArgs& r = w.ra;
+    PrefillArgs& d = w.pa;
+    memset(&r, 0, sizeof(r));
+    memset(&d, 0, sizeof(d));
+    S_cap = (int)(std::min(P, n) + (P + PREFILL_TM - 1) / PREFILL_TM);
+    r.tok = c.take<int>(P);
+    r.w16 = c.take<uint16_t>(P);
+    r.pe = c.take<int>(P);
+    r.inv = c.take<int>(P);
+    r.seg_expert = c.take<int>(S_cap);
+    r.seg_row0 = c.take<int>(S_cap);
+    r.seg_rows = c.take<int>(S_cap);
+    r.nseg = c.take<int>(1);
+    r.counts = c.take<int>(n + 1);
+    r.loc = c.take<int>(P);
+    r.blk_cnt = c.take<int>(((P + 1023) / 1024) * (n + 1));
+    r.cnt_out = c.take<int>(n + 1);
+    d.h13 = c.take<uint16_t>((size_t)P * K);
+    d.h2 = c.take<uint16_t>((size_t)P * N);
+    d.out32 = c.take<float>((size_t)T * K);
+    w.bytes = c.off;
+}
+
+int choose_path(const mi355moe_exl3_layer* L, int64_t P, int path) {
+    if (path == MI355MOE_PATH_AUTO)
+        return (P >= MI355MOE_PREFILL_MIN_PAIRS && (L->flags & MI355MOE_LAYER_SHARED_W13_SUH)) ? MI355MOE_PATH_PREFILL
+                                                                                                 : MI355MOE_PATH_DECODE;
+    return path;
+}
+
+}  // namespace
+
+int64_t mi355moe_moe_workspace_bytes_path(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk, int path) {
     if (layer_shape_ok(layer) || T < 0 || topk < 1 || topk > MAX_TOPK) return -1;
+    if (path < MI355MOE_PATH_AUTO || path > MI355MOE_PATH_PREFILL) return -1;
     const int64_t P = std::max<int64_t>(1, T * topk);
+    if (choose_path(layer, P, path) == MI355MOE_PATH_PREFILL) {
+        PrefillWs w;
+        int sc;
+        carve_prefill(nullptr, P, std::max<int64_t>(1, T), layer->n, layer->hidden, layer->intermediate, w, sc);
+        return (int64_t)w.bytes;
+    }
     const DecodePlan p = plan_decode(P, std::max<int64_t>(1, T), layer->n, layer->hidden, layer->intermediate);
     DecodeWs w;
     carve_decode(nullptr, P, layer->n, layer->hidden, layer->intermediate, p, true, w);
     return (int64_t)w.bytes;
+}
+
+int64_t mi355moe_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk) {
+    return mi355moe_moe_workspace_bytes_path(layer, T, topk, MI355MOE_PATH_AUTO);
 }
 
 int mi355moe_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
@@ -269,19 +324,20 @@ int mi355moe_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* x, in
                              int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
                              int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
                              hipStream_t stream) {
-    return mi355moe_moe_forward_ids_stages(layer, x, x_dtype, x_stride, T, ids, ids_dtype, weights, weights_dtype,
-                                           topk, expert_map, n_global, limit, out, out_dtype, out_stride, workspace,
-                                           workspace_bytes, MI355MOE_STAGE_ALL, stream);
+    return mi355moe_moe_forward_ids_ex(layer, x, x_dtype, x_stride, T, ids, ids_dtype, weights, weights_dtype, topk,
+                                       expert_map, n_global, limit, out, out_dtype, out_stride, workspace,
+                                       workspace_bytes, MI355MOE_PATH_AUTO, MI355MOE_STAGE_ALL, stream);
 }
 
-int mi355moe_moe_forward_ids_stages(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
-                                    int64_t T, const void* ids, int ids_dtype, const void* weights,
-                                    int weights_dtype, int64_t topk, const int64_t* expert_map, int64_t n_global,
-                                    float limit, void* out, int out_dtype, int64_t out_stride, void* workspace,
-                                    size_t workspace_bytes, int stages, hipStream_t stream) {
-    if (stages <= 0 || stages > MI355MOE_STAGE_ALL) return MI355MOE_EINVAL;
+int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, int path,
+                                int stages, hipStream_t stream) {
     if (int r = layer_shape_ok(layer)) return r;
     if (!x || !ids || !weights || !out || !workspace) return MI355MOE_EINVAL;
+    if (stages <= 0 || stages > MI355MOE_STAGE_ALL) return MI355MOE_EINVAL;
+    if (path < MI355MOE_PATH_AUTO || path > MI355MOE_PATH_PREFILL) return MI355MOE_EINVAL;
     if (dt_act(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;
     if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
     const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n;
@@ -291,12 +347,65 @@ int mi355moe_moe_forward_ids_stages(const mi355moe_exl3_layer* layer, const void
     const int64_t P = T * topk;
     if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
     if (P == 0) return 0;
+    const int use = choose_path(layer, P, path);
+    if (use == MI355MOE_PATH_PREFILL && !(layer->flags & MI355MOE_LAYER_SHARED_W13_SUH))
+        return MI355MOE_EUNSUPPORTED;                   // the grouped tier gathers once with the gate's suh
+    RouteArgs r;
+    if (use == MI355MOE_PATH_PREFILL) {
+        PrefillWs w;
+        int S_cap;
+        carve_prefill(workspace, P, T, n, K, N, w, S_cap);
+        if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+        r = w.ra;
+        r.seg = PREFILL_TM;
+        r.S_cap = S_cap;
+        PrefillArgs& d = w.pa;
+        d.wt = tables(layer);
+        d.n = (int)n;
+        d.K = (int)K;
+        d.N = (int)N;
+        d.P = (int)P;
+        d.T = (int)T;
+        d.x = x;
+        d.xdt = dt_act(x_dtype);
+        d.x_stride = x_stride;
+        d.tok = r.tok;
+        d.w16 = r.w16;
+        d.pe = r.pe;
+        d.seg_expert = r.seg_expert;
+        d.seg_row0 = r.seg_row0;
+        d.seg_rows = r.seg_rows;
+        d.nseg = r.nseg;
+        d.S_cap = S_cap;
+        d.limit = limit;
+        d.out = out;
+        d.odt = dt_w(out_dtype);
+        d.out_stride = out_stride;
+        if (prefill_setup()) return rc_launch(-1);
+        r.ids = ids;
+        r.ids64 = ids_dtype == MI355MOE_I64;
+        r.w = weights;
+        r.wdt = dt_w(weights_dtype);
+        r.emap = expert_map;
+        r.n_global = expert_map ? n_global : 0;
+        r.P = (int)P;
+        r.topk = (int)topk;
+        r.n = (int)n;
+        r.R = 1 << 30;
+        if (stages & MI355MOE_STAGE_ROUTE)
+            if (int rc = launch_route(r, stream)) return rc_launch(rc);
+        int kernels = 0;
+        if (stages & MI355MOE_STAGE_GATEUP) kernels |= 1 | 2;
+        if (stages & MI355MOE_STAGE_DOWN) kernels |= 4;
+        if (stages & MI355MOE_STAGE_COMBINE) kernels |= 8;
+        return rc_launch(launch_prefill(d, stream, kernels));
+    }
     const DecodePlan p = plan_decode(P, T, n, K, N);
     if (p.S_cap > 65535) return MI355MOE_ELIMIT;
     DecodeWs w;
     carve_decode(workspace, P, n, K, N, p, true, w);
     if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
-    RouteArgs& r = w.ra;
+    r = w.ra;
     r.ids = ids;
     r.ids64 = ids_dtype == MI355MOE_I64;
     r.w = weights;

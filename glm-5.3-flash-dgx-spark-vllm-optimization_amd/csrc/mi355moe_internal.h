@@ -85,6 +85,35 @@ struct DecodeArgs {
     int topk;
 };
 
+// The prefill-path kernels (gather, fp16 MFMA grouped GEMMs over 256-row expert tiles).
+struct PrefillArgs {
+    Exl3Tables wt;
+    int n, K, N, P, T;
+    const void* x;
+    int xdt;
+    int64_t x_stride;
+    const int* tok;
+    const uint16_t* w16;
+    const int* pe;
+    const int* seg_expert;
+    const int* seg_row0;
+    const int* seg_rows;
+    const int* nseg;
+    int S_cap;
+    float limit;
+    uint16_t* h13;          // [P][K] rotated gate/up inputs
+    uint16_t* h2;           // [P][N] rotated down inputs
+    float* out32;           // [T][K] fp32 accumulation
+    void* out;
+    int odt;
+    int64_t out_stride;
+};
+constexpr int PREFILL_TM = 256;
+
+// kernels: bit 0 zero + gather, bit 1 gate/up, bit 2 down, bit 3 convert to the output dtype
+int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels);
+int prefill_setup();
+
 int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w, int T, int K, int E, float* logits,
                          hipStream_t st);
 int launch_router_topk(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,

@@ -1,0 +1,343 @@
+// Prefill-path kernels (many rows per expert, the E3 grouped tier): gather + input rotation, the gate/up grouped
+// GEMM and the down grouped GEMM on fp16 MFMA (v_mfma_f32_32x32x16_f16) with the EXL3 trellis decoded into LDS.
+//
+// Tiles: a workgroup of 8 waves owns a 256-row segment of one expert (rows sorted by expert) and one column block:
+//   gate/up: 128 columns of gate and the same 128 of up (waves 2g and 2g+1: rows 64g..64g+63 of gate / of up);
+//   down:    256 output columns (two 128-column halves).
+// Per K step of 32: every thread loads 8 bytes of trellis (two words of one 16x16 tile) and 32 bytes of the A rows
+// for the next step while the MFMAs of the current step run; the decoded B step (32 k x 256 columns fp16) and the A
+// step (256 rows x 32 k fp16) are double-buffered in LDS. Each weight value is decoded once per 256-row tile.
+// Numerics (oracle/csrc/oracle.c mode 1 = the E3 kernels, code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu):
+//   gather   h13 = fp16(H(fp16(x * suh_g)) * r)                                         (exl3_fat_moe.cu:95-126)
+//   gate/up  g = (H(acc_g) * r) * svh_g, u likewise; iff L != 0: g = min(g, L), u = clamp(u, -L, L);
+//            a = (1 / (1 + (float)exp(-(double)g))) * g * u; h2 = fp16(H(fp16(fp16(a) * suh_d)) * r)  (:340-378)
+//   down     out[token] += ((H(acc_d) * r) * svh_d) * w16                                (:443-457)
+#include <algorithm>
+
+#include "common.cuh"
+#include "mi355moe_internal.h"
+
+namespace mi355moe {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int PF_TM = PREFILL_TM;   // rows per tile (segment height)
+constexpr int PF_THREADS = 512;     // 8 waves
+constexpr int PF_LD = 40;           // halves per LDS row of a 32-k step (32 + 8 padding)
+constexpr int PF_AS = PF_TM * PF_LD;            // one A stage (halves)
+constexpr int PF_BS = 2 * 128 * PF_LD;          // one B stage: 2 x 128 columns (halves)
+constexpr size_t PF_LDS = (size_t)(2 * PF_AS + 2 * PF_BS) * 2;   // 81,920 bytes
+
+// ------------------------------------------------------------------------------------------------ gather
+
+// h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0; one wave per
+// (row, 128-block) task, grid-stride.
+__global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int nb = a.K >> 7;
+    const int64_t tasks = (int64_t)a.P * nb;
+    for (int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); task < tasks; task += (int64_t)gridDim.x * 4) {
+        const int pos = (int)(task / nb), blk = (int)(task - (int64_t)pos * nb);
+        const int e = a.pe[pos];
+        if (e < 0) continue;
+        const _Float16* suh = reinterpret_cast<const _Float16*>(a.wt.g_suh[e]) + blk * 128;
+        const size_t xoff = (size_t)a.tok[pos] * a.x_stride + blk * 128;
+        _Float16 h0, h1;
+        if (a.xdt == DT_BF16) {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(a.x) + xoff +
+                                                                   2 * lane);
+            h0 = (_Float16)__builtin_bit_cast(float, v << 16);
+            h1 = (_Float16)__builtin_bit_cast(float, v & 0xFFFF0000u);
+        } else {
+            const h2 v = *reinterpret_cast<const h2*>(reinterpret_cast<const uint16_t*>(a.x) + xoff + 2 * lane);
+            h0 = v.x;
+            h1 = v.y;
+        }
+        const h2 s = *reinterpret_cast<const h2*>(suh + 2 * lane);
+        float p0 = (float)(_Float16)(h0 * s.x), p1 = (float)(_Float16)(h1 * s.y);
+        fwht128_w64(p0, p1, lane);
+        *reinterpret_cast<h2*>(reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + blk * 128 + 2 * lane) =
+            h2{(_Float16)(p0 * HAD_R), (_Float16)(p1 * HAD_R)};
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ GEMM core
+
+// Decode this thread's two trellis words (words 2wp, 2wp+1 of one tile; the tile's 16 threads are 16 consecutive
+// lanes) into the B stage: column-major [col][k] with the k of the 32-step contiguous.
+__device__ __forceinline__ void pf_store_b(uint2 bw, int lane, int wp, _Float16* B, int col_base, int krow) {
+    const uint32_t prev = (uint32_t)__shfl((int)bw.y, (lane & ~15) | ((lane + 15) & 15), 64);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t w = i ? bw.y : bw.x;
+        const uint32_t pw = i ? bw.x : prev;
+        const int l = 2 * wp + i;
+        h2 d[4];
+        decode_word(pw, w, d);
+        const int c0 = col_base + (l >> 2), r0 = krow + 2 * (l & 3);
+        *reinterpret_cast<h2*>(B + c0 * PF_LD + r0) = d[0];
+        *reinterpret_cast<h2*>(B + c0 * PF_LD + r0 + 8) = d[1];
+        *reinterpret_cast<h2*>(B + (c0 + 8) * PF_LD + r0) = d[2];
+        *reinterpret_cast<h2*>(B + (c0 + 8) * PF_LD + r0 + 8) = d[3];
+    }
+}
+
+// The tile GEMM: acc[rb][c4] (32x32 blocks) of rows 64*rg + 32*rb, columns 32*c4 of B half `half` (128 columns),
+// over kdim. A rows come from `a_rows` (row stride kdim), clamped to rn - 1. B tiles: (k tile, column tile) ->
+// trellis words of matrix `bmat[half]` at ((kt * btiles_n) + bcol0[half] + ct) * 32.
+struct PfTile {
+    const uint16_t* a_rows;       // first row of the segment
+    int rn, kdim;
+    const uint32_t* btr[2];       // trellis of half 0 / 1
+    int btiles_n;                 // tiles per trellis row (the matrix's column tiles)
+    int bcol0[2];                 // first column tile of half 0 / 1
+};
+
+__device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[2][4]) {
+    _Float16* As = reinterpret_cast<_Float16*>(smem);
+    _Float16* Bs = As + 2 * PF_AS;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rg = wv >> 1, half = wv & 1;
+    // A loader: rows ar and ar + 128, 16-byte chunk ac of the 64-byte step slice
+    const int ar = tid >> 2, ac = tid & 3;
+    const int ra0 = min(ar, t.rn - 1), ra1 = min(ar + 128, t.rn - 1);
+    const u32x4* A0 = reinterpret_cast<const u32x4*>(t.a_rows + (size_t)ra0 * t.kdim) + ac;
+    const u32x4* A1 = reinterpret_cast<const u32x4*>(t.a_rows + (size_t)ra1 * t.kdim) + ac;
+    // B loader: half bm, tile bt (k tile bkt, column tile bct), word pair wp
+    const int bm = tid >> 8, bt = (tid >> 4) & 15, bkt = bt >> 3, bct = bt & 7, wp = tid & 15;
+    const uint32_t* Bg = t.btr[bm] + ((size_t)bkt * t.btiles_n + t.bcol0[bm] + bct) * 32 + 2 * wp;
+    const size_t bstep = (size_t)2 * t.btiles_n * 32;      // two k tiles
+    const int steps = t.kdim / 32;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[rb][c][r] = 0.f;
+
+    u32x4 a0 = A0[0], a1 = A1[0];
+    uint2 bw = *reinterpret_cast<const uint2*>(Bg);
+    *reinterpret_cast<u32x4*>(As + ar * PF_LD + ac * 8) = a0;
+    *reinterpret_cast<u32x4*>(As + (ar + 128) * PF_LD + ac * 8) = a1;
+    pf_store_b(bw, lane, wp, Bs + bm * 128 * PF_LD, bct * 16, bkt * 16);
+    __syncthreads();
+    for (int it = 0; it < steps; ++it) {
+        const int st = it & 1;
+        const bool more = it + 1 < steps;
+        if (more) {
+            a0 = A0[(it + 1) * 4];
+            a1 = A1[(it + 1) * 4];
+            bw = *reinterpret_cast<const uint2*>(Bg + (size_t)(it + 1) * bstep);
+        }
+        const _Float16* as = As + st * PF_AS;
+        const _Float16* bs = Bs + st * PF_BS + half * 128 * PF_LD;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            const int k = 16 * kh + 8 * (lane >> 5);
+            h8 af[2], bf[4];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+                af[rb] = *reinterpret_cast<const h8*>(as + (64 * rg + 32 * rb + (lane & 31)) * PF_LD + k);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) bf[c] = *reinterpret_cast<const h8*>(bs + (32 * c + (lane & 31)) * PF_LD + k);
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    acc[rb][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], bf[c], acc[rb][c], 0, 0, 0);
+        }
+        if (more) {
+            _Float16* an = As + (st ^ 1) * PF_AS;
+            *reinterpret_cast<u32x4*>(an + ar * PF_LD + ac * 8) = a0;
+            *reinterpret_cast<u32x4*>(an + (ar + 128) * PF_LD + ac * 8) = a1;
+            pf_store_b(bw, lane, wp, Bs + (st ^ 1) * PF_BS + bm * 128 * PF_LD, bct * 16, bkt * 16);
+        }
+        __syncthreads();
+    }
+}
+
+// Stage the accumulators of row block (rg2, rb) (32 rows x 256 columns) into Cs [32][256] fp32.
+__device__ __forceinline__ void pf_stage_rows(const f16v (&acc)[2][4], float* Cs, int rg2, int rb) {
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if ((wv >> 1) != rg2) return;
+    const int half = wv & 1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            Cs[row * 256 + half * 128 + 32 * c + (lane & 31)] = acc[rb][c][r];
+        }
+}
+
+// ------------------------------------------------------------------------------------------------ gate/up
+
+__global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int cb = blockIdx.x, s = blockIdx.y;
+    if (s >= a.nseg[0]) return;
+    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
+    const int K = a.K, N = a.N;
+    PfTile t;
+    t.a_rows = a.h13 + (size_t)row0 * K;
+    t.rn = rn;
+    t.kdim = K;
+    t.btr[0] = reinterpret_cast<const uint32_t*>(a.wt.g_tr[e]);
+    t.btr[1] = reinterpret_cast<const uint32_t*>(a.wt.u_tr[e]);
+    t.btiles_n = N >> 4;
+    t.bcol0[0] = t.bcol0[1] = cb * 8;
+    f16v acc[2][4];
+    pf_gemm(t, smem, acc);
+
+    float* Cs = reinterpret_cast<float*>(smem);
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = cb * 128 + 2 * lane;
+    const h2 svg = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + col);
+    const h2 svu = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + col);
+    const h2 sud = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + col);
+    const float L = a.limit;
+    for (int rg2 = 0; rg2 < 4; ++rg2)
+        for (int rb = 0; rb < 2; ++rb) {
+            if (64 * rg2 + 32 * rb >= rn) continue;                 // uniform over the workgroup
+            pf_stage_rows(acc, Cs, rg2, rb);
+            __syncthreads();
+            for (int rr = 0; rr < 4; ++rr) {
+                const int rl = wv * 4 + rr;
+                const int trow = 64 * rg2 + 32 * rb + rl;
+                if (trow < rn) {
+                    float g[2] = {Cs[rl * 256 + 2 * lane], Cs[rl * 256 + 2 * lane + 1]};
+                    float u[2] = {Cs[rl * 256 + 128 + 2 * lane], Cs[rl * 256 + 128 + 2 * lane + 1]};
+                    fwht128_w64(g[0], g[1], lane);
+                    fwht128_w64(u[0], u[1], lane);
+                    float b[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        float gv = g[i] * HAD_R * (float)(i ? svg.y : svg.x);
+                        float uv = u[i] * HAD_R * (float)(i ? svu.y : svu.x);
+                        if (L != 0.0f) {
+                            gv = fminf(gv, L);
+                            uv = fminf(fmaxf(uv, -L), L);
+                        }
+                        const float act = sigmoid_dexp(gv) * gv * uv;
+                        b[i] = (float)(_Float16)((_Float16)act * (i ? sud.y : sud.x));
+                    }
+                    fwht128_w64(b[0], b[1], lane);
+                    *reinterpret_cast<h2*>(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow) * N + col) =
+                        h2{(_Float16)(b[0] * HAD_R), (_Float16)(b[1] * HAD_R)};
+                }
+            }
+            __syncthreads();
+        }
+}
+
+// ------------------------------------------------------------------------------------------------ down
+
+__global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int cb = blockIdx.x, s = blockIdx.y;
+    if (s >= a.nseg[0]) return;
+    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
+    const int K = a.K, N = a.N;
+    PfTile t;
+    t.a_rows = a.h2 + (size_t)row0 * N;
+    t.rn = rn;
+    t.kdim = N;
+    t.btr[0] = t.btr[1] = reinterpret_cast<const uint32_t*>(a.wt.d_tr[e]);
+    t.btiles_n = K >> 4;
+    t.bcol0[0] = cb * 16;
+    t.bcol0[1] = cb * 16 + 8;
+    f16v acc[2][4];
+    pf_gemm(t, smem, acc);
+
+    float* Cs = reinterpret_cast<float*>(smem);
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const _Float16* svd = reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + cb * 256;
+    const h2 sv0 = *reinterpret_cast<const h2*>(svd + 2 * lane);
+    const h2 sv1 = *reinterpret_cast<const h2*>(svd + 128 + 2 * lane);
+    for (int rg2 = 0; rg2 < 4; ++rg2)
+        for (int rb = 0; rb < 2; ++rb) {
+            if (64 * rg2 + 32 * rb >= rn) continue;
+            pf_stage_rows(acc, Cs, rg2, rb);
+            __syncthreads();
+            for (int rr = 0; rr < 4; ++rr) {
+                const int rl = wv * 4 + rr;
+                const int trow = 64 * rg2 + 32 * rb + rl;
+                if (trow < rn) {
+                    const int row = row0 + trow;
+                    const float w = (float)u16_as_h(a.w16[row]);
+                    float* o = a.out32 + (size_t)a.tok[row] * K + cb * 256 + 2 * lane;
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        float v0 = Cs[rl * 256 + hf * 128 + 2 * lane], v1 = Cs[rl * 256 + hf * 128 + 2 * lane + 1];
+                        fwht128_w64(v0, v1, lane);
+                        const h2 sv = hf ? sv1 : sv0;
+                        v0 = v0 * HAD_R * (float)sv.x * w;
+                        v1 = v1 * HAD_R * (float)sv.y * w;
+                        atomicAdd(o + hf * 128, v0);
+                        atomicAdd(o + hf * 128 + 1, v1);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+}
+
+// ------------------------------------------------------------------------------------------------ out buffers
+
+__global__ __launch_bounds__(256) void pf_zero_kernel(float* __restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.f;
+}
+
+__global__ __launch_bounds__(256) void pf_convert_kernel(const float* __restrict__ src, int T, int K, void* dst,
+                                                         int odt, int64_t stride) {
+    const int64_t n = (int64_t)T * K;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const int64_t t = i / K, c = i - t * K;
+        const float v = src[i];
+        if (odt == DT_F32) reinterpret_cast<float*>(dst)[t * stride + c] = v;
+        else if (odt == DT_BF16) reinterpret_cast<uint16_t*>(dst)[t * stride + c] = f32_to_bf16(v);
+        else reinterpret_cast<_Float16*>(dst)[t * stride + c] = (_Float16)v;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ launchers
+
+static bool g_pf_attr = false;
+
+int prefill_setup() {
+    if (g_pf_attr) return 0;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(pf_gateup_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS) != hipSuccess)
+        return -1;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(pf_down_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)PF_LDS) != hipSuccess)
+        return -1;
+    g_pf_attr = true;
+    return 0;
+}
+
+int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
+    if (prefill_setup()) return -1;
+    if (kernels & 1) {
+        const int64_t n = (int64_t)a.T * a.K;
+        hipLaunchKernelGGL(pf_zero_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0,
+                           st, a.out32, n);
+        hipLaunchKernelGGL(pf_gather_kernel, dim3(4096), dim3(256), 0, st, a);
+    }
+    if (kernels & 2)
+        hipLaunchKernelGGL(pf_gateup_kernel, dim3(a.N / 128, a.S_cap), dim3(PF_THREADS), PF_LDS, st, a);
+    if (kernels & 4) hipLaunchKernelGGL(pf_down_kernel, dim3(a.K / 256, a.S_cap), dim3(PF_THREADS), PF_LDS, st, a);
+    if (kernels & 8) {
+        const int64_t n = (int64_t)a.T * a.K;
+        hipLaunchKernelGGL(pf_convert_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0,
+                           st, a.out32, a.T, a.K, a.out, a.odt, a.out_stride);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace mi355moe

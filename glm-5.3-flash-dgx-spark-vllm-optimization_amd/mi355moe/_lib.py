@@ -14,6 +14,9 @@ ABI_VERSION = 1
 
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
 STAGE_ROUTE, STAGE_GATEUP, STAGE_DOWN, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 8, 15
+PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
+LAYER_SHARED_W13_SUH = 1
+PREFILL_MIN_PAIRS = 4096
 
 _c_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -27,7 +30,7 @@ class Exl3LayerDesc(ctypes.Structure):
     _fields_ = [("n", _i64), ("hidden", _i64), ("intermediate", _i64),
                 ("gate_trellis", _c_p), ("gate_suh", _c_p), ("gate_svh", _c_p),
                 ("up_trellis", _c_p), ("up_suh", _c_p), ("up_svh", _c_p),
-                ("down_trellis", _c_p), ("down_suh", _c_p), ("down_svh", _c_p)]
+                ("down_trellis", _c_p), ("down_suh", _c_p), ("down_svh", _c_p), ("flags", _i64)]
 
 
 class MoeError(RuntimeError):
@@ -54,9 +57,10 @@ _SIGS = {
     "mi355moe_moe_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64, _i64]),
     "mi355moe_moe_forward_ids": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int, _c_p,
                                         _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _c_p]),
-    "mi355moe_moe_forward_ids_stages": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int,
-                                               _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int,
-                                               _c_p]),
+    "mi355moe_moe_workspace_bytes_path": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64, _i64, _int]),
+    "mi355moe_moe_forward_ids_ex": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int,
+                                           _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int, _int,
+                                           _c_p]),
     "mi355moe_exl3_moe_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64]),
     "mi355moe_exl3_moe": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _i64,
                                  _int, _int, _int, _int, _int, _int, _int, _int, _int, _int, _f, _c_p, _sz, _c_p]),

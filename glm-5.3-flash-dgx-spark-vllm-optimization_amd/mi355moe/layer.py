@@ -74,6 +74,8 @@ class Exl3Experts:
             "down_trellis": _table(self.w2_trellis, ()), "down_suh": _table(self.w2_suh, ()),
             "down_svh": _table(self.w2_svh, ()),
         }
+        # gate and up share one input rotation (production's _exl3_shared_w13_suh, prod_exl3_reference.py:2243-2245)
+        self.shared_suh = bool(torch.equal(self.w13_suh[:, 0], self.w13_suh[:, 1]))
         self.desc = self.make_desc(self.tables)
 
     def make_desc(self, tables: dict) -> _lib.Exl3LayerDesc:
@@ -81,6 +83,7 @@ class Exl3Experts:
         d.n, d.hidden, d.intermediate = self.n, self.K, self.N
         for k, v in tables.items():
             setattr(d, k, ctypes.c_void_p(v.data_ptr()))
+        d.flags = _lib.LAYER_SHARED_W13_SUH if self.shared_suh else 0
         return d
 
     @property
@@ -97,10 +100,11 @@ class Exl3Experts:
                            layer.w2_suh.data, layer.w2_svh.data)
 
 
-def tables_desc(n: int, K: int, N: int, tables: dict) -> _lib.Exl3LayerDesc:
+def tables_desc(n: int, K: int, N: int, tables: dict, shared_suh: bool = False) -> _lib.Exl3LayerDesc:
     """Descriptor from caller-built pointer tables (the exl3_moe contract passes them directly)."""
     d = _lib.Exl3LayerDesc()
     d.n, d.hidden, d.intermediate = n, K, N
+    d.flags = _lib.LAYER_SHARED_W13_SUH if shared_suh else 0
     for k in ("gate_trellis", "gate_suh", "gate_svh", "up_trellis", "up_suh", "up_svh", "down_trellis", "down_suh",
               "down_svh"):
         t = tables[k]

@@ -156,8 +156,10 @@ def rot_in(x: torch.Tensor, tok: torch.Tensor, pe: torch.Tensor, suh_table: torc
 
 def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                     limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                    out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL) -> torch.Tensor:
+                    out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL,
+                    path: int = _lib.PATH_AUTO) -> torch.Tensor:
     """Routed-expert output [T, K] (x's dtype unless out/out_dtype say otherwise), written (not accumulated).
+    path: _lib.PATH_AUTO (decode kernels for few pairs, the grouped MFMA prefill kernels for many), or forced.
     stages: a subset of the call's launches (_lib.STAGE_*), for timing one kernel; the default runs them all."""
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
     if dev != experts.device:
@@ -175,14 +177,14 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
     if out.shape != (T, experts.K) or out.stride(1) != 1:
         raise ValueError("out must be [T, K] with unit column stride")
     L = _lib.lib()
-    nb = L.mi355moe_moe_workspace_bytes(ctypes.byref(experts.desc), T, topk)
+    nb = L.mi355moe_moe_workspace_bytes_path(ctypes.byref(experts.desc), T, topk, int(path))
     if nb < 0:
         raise ValueError("mi355moe_moe_workspace_bytes rejected the shape")
     ws = workspace(dev, nb)
     em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
-    _lib.check("mi355moe_moe_forward_ids", L.mi355moe_moe_forward_ids_stages(
+    _lib.check("mi355moe_moe_forward_ids", L.mi355moe_moe_forward_ids_ex(
         ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
         ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em), 0 if em is None else em.numel(),
-        float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), int(stages),
-        _stream(dev)))
+        float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), int(path),
+        int(stages), _stream(dev)))
     return out

@@ -55,7 +55,12 @@ typedef struct mi355moe_exl3_layer {
     const int64_t* down_trellis;
     const int64_t* down_suh;
     const int64_t* down_svh;
+    int64_t flags;          /* MI355MOE_LAYER_* bits */
 } mi355moe_exl3_layer;
+
+/* gate and up share one input rotation (w13_suh[:, 0] == w13_suh[:, 1], production's _exl3_shared_w13_suh,
+ * code/fork/docs/prod_exl3_reference.py:2243-2245); the grouped prefill path requires it (:376) */
+#define MI355MOE_LAYER_SHARED_W13_SUH 1
 
 int mi355moe_abi_version(void);
 const char* mi355moe_strerror(int code);
@@ -99,13 +104,20 @@ int mi355moe_rot_in(const void* x, int x_dtype, int64_t x_stride, int64_t K, con
                     int64_t P, const int64_t* suh_table, void* out, hipStream_t stream);
 
 /* Routed experts from router ids: the decode apply (code/fork/kernels/exl3.cpp:307-391 moe_forward_ids,
- * exl3.cpp:409-503 moe_forward_glue). x F16/BF16 [T][K] (row stride x_stride), ids I32/I64 [T][topk],
- * weights F32/F16/BF16 [T][topk], out [T][K] of out_dtype (row stride out_stride) is WRITTEN with the
- * routed sum over each token's slots in slot order (deterministic). limit = the SwiGLU limit (0 = none).
- * Pairs P = T*topk <= 65536. */
+ * exl3.cpp:409-503 moe_forward_glue) and, for many pairs, the grouped prefill tier (E3,
+ * code/fork/docs/prod_exl3_reference.py:1364-1435, code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu).
+ * x F16/BF16 [T][K] (row stride x_stride), ids I32/I64 [T][topk], weights F32/F16/BF16 [T][topk], out [T][K] of
+ * out_dtype (row stride out_stride) is WRITTEN (not accumulated). limit = the SwiGLU limit (0 = none).
+ * Decode path: per-token slot-order sum (deterministic). Prefill path: fp32 atomic scatter-add, then the
+ * conversion to out_dtype. Pairs P = T*topk <= 65536. */
+enum { MI355MOE_PATH_AUTO = 0, MI355MOE_PATH_DECODE = 1, MI355MOE_PATH_PREFILL = 2 };
+/* The automatic choice: the prefill path when P >= MI355MOE_PREFILL_MIN_PAIRS and the layer has
+ * MI355MOE_LAYER_SHARED_W13_SUH, else the decode path. */
+#define MI355MOE_PREFILL_MIN_PAIRS 4096
 int64_t mi355moe_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk);
+int64_t mi355moe_moe_workspace_bytes_path(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk, int path);
 
-/* Stage mask of mi355moe_moe_forward_ids_stages: the same call split into its launches, so a caller can time or
+/* Stage mask of mi355moe_moe_forward_ids_ex: the same call split into its launches, so a caller can time or
  * test one of them (the reference's stage entry points, code/fork/kernels/exl3.cpp:130-220: route_prep, grouped,
  * gateup_epilogue, down_epilogue). A stage reads what the earlier stages of a call with the same arguments left in
  * the workspace. */
@@ -116,11 +128,11 @@ int mi355moe_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* x, in
                              int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
                              int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
                              hipStream_t stream);
-int mi355moe_moe_forward_ids_stages(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
-                                    int64_t T, const void* ids, int ids_dtype, const void* weights,
-                                    int weights_dtype, int64_t topk, const int64_t* expert_map, int64_t n_global,
-                                    float limit, void* out, int out_dtype, int64_t out_stride, void* workspace,
-                                    size_t workspace_bytes, int stages, hipStream_t stream);
+int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, int path,
+                                int stages, hipStream_t stream);
 
 /* The fused-experts op exllamav3_ext.exl3_moe (code/fork/docs/ref/xl_exl3_moe.cu:93-130, called by
  * prod_exl3_reference.py:1490-1537): hidden fp16 [B][K]; out fp32 [B][K] ACCUMULATED into; expert_count int64

@@ -213,10 +213,10 @@ typedef struct {
  * Routed MoE of one layer. pairs: P (token, local expert, fp16 weight) entries, expert < 0 or >= n skipped.
  * mode 0: decode path (exl3_moe semantics: s = silu(g), limit after SiLU: min(s, L), u in [-L, L], iff L != 0;
  *         fp32 epilogues; fp16 at the GEMV inputs xg/xu/xd and at the activation a16).
- * mode 1: E3 prefill path (limit before SiLU: g = min(g, L), u in [-L, L]; sigmoid via double exp).
+ * mode 1: E3 prefill path (limit before SiLU: g = min(g, L), u in [-L, L], iff L != 0; sigmoid via double exp).
  * mode 2: float64 reference (test_e2e_vs_f64.py:52-75: double everywhere, exl3_moe's post-SiLU clamp,
  *         weights rounded to fp16 as production passes them).
- * mode 3: float64 reference with the limit before SiLU (production's python loop, prod:961-1006).
+ * mode 3: float64 reference with the limit before SiLU iff L != 0 (production's python loop, prod:961-1006).
  * out[T][K] (fp32, or double for modes 2/3 through out64) is accumulated into in pair order per token.
  * Returns 0, or -1 on a bad argument.
  */
@@ -288,8 +288,10 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
                             float u = zu[b0 + i] * HAD_R * orc_h2f(svh_u[b0 + i]);
                             float a;
                             if (mode == 1) {
-                                g = fminf(g, limit);
-                                u = fminf(fmaxf(u, -limit), limit);
+                                if (limit != 0.0f) {
+                                    g = fminf(g, limit);
+                                    u = fminf(fmaxf(u, -limit), limit);
+                                }
                                 a = sigm(g) * g * u;
                             } else {
                                 float s = g * sigm(g);
@@ -348,8 +350,10 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
                         double uv = u[c] * rr * (double)orc_h2f(svh_u[c]);
                         double s;
                         if (mode == 3) {
-                            gv = fmin(gv, (double)limit);
-                            uv = fmin(fmax(uv, -(double)limit), (double)limit);
+                            if (limit != 0.0f) {
+                                gv = fmin(gv, (double)limit);
+                                uv = fmin(fmax(uv, -(double)limit), (double)limit);
+                            }
                             s = gv / (1.0 + exp(-gv));
                         } else {
                             s = gv / (1.0 + exp(-gv));

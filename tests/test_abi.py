@@ -37,8 +37,10 @@ def _fake_desc(n=288, K=4096, N=1024):
     from mi355moe import _lib
     d = _lib.Exl3LayerDesc()
     d.n, d.hidden, d.intermediate = n, K, N
-    for f, _ in d._fields_[3:]:
-        setattr(d, f, ctypes.c_void_p(0x1000))      # never dereferenced by the host-side planners
+    for f, t in d._fields_[3:]:
+        if t is ctypes.c_void_p:
+            setattr(d, f, ctypes.c_void_p(0x1000))  # never dereferenced by the host-side planners
+    d.flags = 1
     return d
 
 
@@ -53,6 +55,11 @@ def test_workspace_planners_answer_without_a_gpu():
     bad = _fake_desc(K=4000)
     assert L.mi355moe_moe_workspace_bytes(ctypes.byref(bad), 8, 8) == -1
     assert L.mi355moe_route_workspace_bytes(65536, 288) > 0
+    # the automatic choice: prefill layout (rotated rows + fp32 accumulator) above 4096 pairs with shared suh
+    big = L.mi355moe_moe_workspace_bytes(ctypes.byref(d), 8192, 8)
+    assert big >= 8192 * 8 * (4096 + 1024) * 2 + 8192 * 4096 * 4
+    assert L.mi355moe_moe_workspace_bytes_path(ctypes.byref(d), 8192, 8, 1) != big      # forced decode layout
+    assert L.mi355moe_moe_workspace_bytes_path(ctypes.byref(d), 8, 8, 3) == -1         # bad path
 
 
 def test_argument_errors_before_any_launch():

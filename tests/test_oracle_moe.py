@@ -35,8 +35,9 @@ def _numpy_f64(layer, x16, tok, ex, w16, L, pre):
         g = exl3.linear_f64(xs, layer["w13_trellis"][e, 0], layer["w13_suh"][e, 0], layer["w13_svh"][e, 0])
         u = exl3.linear_f64(xs, layer["w13_trellis"][e, 1], layer["w13_suh"][e, 1], layer["w13_svh"][e, 1])
         if pre:
-            g = np.minimum(g, L)
-            u = np.clip(u, -L, L)
+            if L:
+                g = np.minimum(g, L)
+                u = np.clip(u, -L, L)
             a = g / (1 + np.exp(-g)) * u
         else:
             s = g / (1 + np.exp(-g))
