@@ -39,6 +39,8 @@ struct Carve {
 };
 
 // The decode plan for P pairs.
+int shared_flag(const mi355moe_exl3_layer* L) { return (L->flags & MI355MOE_LAYER_SHARED_W13_SUH) ? 1 : 0; }
+
 struct DecodePlan {
     int rmax, seg, S_cap, sk_gu, sk_dn;
 };
@@ -49,26 +51,27 @@ int pow2ceil(int64_t v) {
     return p;
 }
 
-DecodePlan plan_decode(int64_t P, int64_t rows_bound, int64_t n, int64_t K, int64_t N) {
+DecodePlan plan_decode(int64_t P, int64_t rows_bound, int64_t n, int64_t K, int64_t N, int shared_suh) {
     DecodePlan d;
     d.rmax = (int)std::min<int64_t>(16, pow2ceil(std::max<int64_t>(1, rows_bound)));
     d.seg = d.rmax;
     d.S_cap = (int)(std::min(P, n) + (P + d.seg - 1) / d.seg);
     const int64_t s_est = std::max<int64_t>(1, std::min(P, n));
-    const int64_t target = 2048;
-    // K range per gate/up workgroup: largest of {1024, 512, 256, 128} that divides K and still gives ~target
-    // workgroups (the input-row buffer 2 * rmax * KR fp16 stays <= 64 KiB)
-    // (the input rows staged in LDS stay <= 16 KiB per workgroup so occupancy is set by registers, not LDS)
-    int64_t kr = 128;
-    for (int64_t c : {1024, 512, 256, 128}) {
-        if (K % c || 2 * d.rmax * c * 2 > 16384) continue;
-        if (s_est * (N / 128) * (K / c) >= target || c == 128) { kr = c; break; }
+    // K splits: the fewest that keep the staged input rows within DECODE_LDS_MAX and still give ~target 512-thread
+    // workgroups (one split needs no cross-workgroup reduction); each half of a split spans a multiple of 128
+    const int64_t target = 400;
+    int64_t sk = 0;
+    for (int64_t c : {1, 2, 4, 8, 16}) {
+        if (K % c || (K / c) % 256 || decode_lds_gateup(d.rmax, (int)K, (int)c, shared_suh) > DECODE_LDS_MAX) continue;
+        sk = c;
+        if (s_est * (N / 128) * c >= target) break;
     }
-    d.sk_gu = (int)(K / kr);
-    int64_t nr = 128;
-    for (int64_t c : {1024, 512, 256, 128}) {
-        if (N % c || d.rmax * c * 2 > 16384) continue;
-        if (s_est * (K / 128) * (N / c) >= target || c == 128) { nr = c; break; }
+    d.sk_gu = (int)std::max<int64_t>(1, sk);
+    int64_t nr = N;
+    for (int64_t c : {1, 2, 4, 8}) {
+        if (N % c || (N / c) % 128 || decode_lds_down(d.rmax, (int)N, (int)c) > DECODE_LDS_MAX) continue;
+        nr = N / c;
+        if (s_est * (K / 256) * c >= target) break;
     }
     d.sk_dn = (int)(N / nr);
     return d;
@@ -101,7 +104,7 @@ void carve_decode(void* ws, int64_t P, int64_t n, int64_t K, int64_t N, const De
     r.blk_cnt = c.take<int>(((P + 1023) / 1024) * (n + 1));
     r.cnt_out = c.take<int>(n + 1);
     d.cnt_gu = c.take<unsigned>((size_t)p.S_cap * (N / 128));
-    d.cnt_dn = c.take<unsigned>((size_t)p.S_cap * (K / 128));
+    d.cnt_dn = c.take<unsigned>((size_t)p.S_cap * (K / 256));
     r.zero = d.cnt_gu;                                               // both counter arrays, zeroed per call
     r.zero_words = (int64_t)((c.off - ((char*)d.cnt_gu - c.base)) / sizeof(unsigned));
     d.zg = c.take<float>((size_t)p.sk_gu * 2 * P * N);
@@ -309,7 +312,8 @@ int64_t mi355moe_moe_workspace_bytes_path(const mi355moe_exl3_layer* layer, int6
         carve_prefill(nullptr, P, std::max<int64_t>(1, T), layer->n, layer->hidden, layer->intermediate, w, sc);
         return (int64_t)w.bytes;
     }
-    const DecodePlan p = plan_decode(P, std::max<int64_t>(1, T), layer->n, layer->hidden, layer->intermediate);
+    const DecodePlan p = plan_decode(P, std::max<int64_t>(1, T), layer->n, layer->hidden, layer->intermediate,
+                                     shared_flag(layer));
     DecodeWs w;
     carve_decode(nullptr, P, layer->n, layer->hidden, layer->intermediate, p, true, w);
     return (int64_t)w.bytes;
@@ -400,7 +404,7 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
         if (stages & MI355MOE_STAGE_COMBINE) kernels |= 8;
         return rc_launch(launch_prefill(d, stream, kernels));
     }
-    const DecodePlan p = plan_decode(P, T, n, K, N);
+    const DecodePlan p = plan_decode(P, T, n, K, N, shared_flag(layer));
     if (p.S_cap > 65535) return MI355MOE_ELIMIT;
     DecodeWs w;
     carve_decode(workspace, P, n, K, N, p, true, w);
@@ -439,6 +443,7 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
     d.S_cap = p.S_cap;
     d.sk_gu = p.sk_gu;
     d.sk_dn = p.sk_dn;
+    d.shared_suh = shared_flag(layer);
     d.limit = limit;
     d.out = out;
     d.odt = dt_w(out_dtype);
@@ -455,7 +460,8 @@ int64_t mi355moe_exl3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int6
     const int64_t Pp = std::max<int64_t>(1, P);
     size_t most = 0;                                  // the plan depends on the row cap: take the largest layout
     for (int64_t rows = 1; rows <= 16; rows *= 2) {
-        const DecodePlan p = plan_decode(Pp, std::min(Pp, rows), layer->n, layer->hidden, layer->intermediate);
+        const DecodePlan p = plan_decode(Pp, std::min(Pp, rows), layer->n, layer->hidden, layer->intermediate,
+                                         shared_flag(layer));
         DecodeWs w;
         carve_decode(nullptr, Pp, layer->n, layer->hidden, layer->intermediate, p, false, w);
         most = std::max(most, w.bytes);
@@ -477,7 +483,7 @@ int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int6
     if (P < 0 || P > MAX_PAIRS) return MI355MOE_ELIMIT;
     if (P == 0) return 0;
     const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n;
-    const DecodePlan p = plan_decode(P, std::min(P, max_rows), n, K, N);
+    const DecodePlan p = plan_decode(P, std::min(P, max_rows), n, K, N, shared_flag(layer));
     if (p.S_cap > 65535) return MI355MOE_ELIMIT;
     DecodeWs w;
     carve_decode(workspace, P, n, K, N, p, false, w);
@@ -509,6 +515,7 @@ int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int6
     d.S_cap = p.S_cap;
     d.sk_gu = p.sk_gu;
     d.sk_dn = p.sk_dn;
+    d.shared_suh = shared_flag(layer);
     d.limit = act_limit;
     d.out = out;
     d.odt = DT_F32;

@@ -1,14 +1,18 @@
 // Decode-path kernels (few rows per expert): trellis dequant, input rotation, the grouped gate/up and down trellis
 // GEMVs with their epilogues fused through split-K arrival counters, and the slot-order combine.
 //
-// Work decomposition of the grouped GEMVs (no MFMA: at a few rows per expert the work is a stream of 4-bit codes):
-//   workgroup (128-column block cb, K split ks, row segment s): 4 waves split the split's k tiles; lane (t, q) of a
-//   wave owns columns q and q+8 of tile cb*8 + t, loads 16 bytes of trellis per k tile and matrix, decodes 32
-//   values in registers and accumulates them against the segment's rows with v_dot2_f32_f16. Waves reduce in
-//   fixed order through LDS; each split writes its fp32 partial; the workgroup that arrives last for (s, cb) adds
-//   the splits in split order and runs the epilogue. Every result is therefore independent of scheduling.
-// Numerics (oracle/csrc/oracle.c mode 0):
+// Work decomposition of the grouped GEMVs (a few rows per expert: the work is a stream of 4-bit codes):
+//   workgroup (128-column block cb, K split ks, row segment s) of 4 waves; wave w owns 32 columns over the split's
+//   K range and steps through it four k tiles at a time. Each lane loads 16 bytes of trellis per step and matrix
+//   (a quarter of one 16x16 tile), decodes its 32 states to raw codebook words, and hands each word's (lo, hi)
+//   fp16 halves to v_mfma_f32_16x16x32_f16 as the B operand, with the rows' inputs duplicated per k as the A
+//   operand (staged in LDS in that order). The matrix core therefore performs the codebook's lo + hi sum and the
+//   dot product for up to 16 rows at once; the VALU only extracts states, multiplies and masks. Each split stores
+//   its fp32 partial; the workgroup that arrives last for (s, cb) adds the splits in split order and runs the
+//   epilogue, so every result is independent of scheduling.
+// Numerics (oracle/csrc/oracle.c mode 4 = mode 0 with unrounded codebook sums):
 //   rot_in   xg = fp16(H(fp16(x * suh_g)) * r)                       (exl3.cu:321-349)
+//   GEMV     z = sum_k xg[k] * (fp16(lo) + fp16(hi)) in fp32 (the reference rounds lo + hi to fp16 first)
 //   gate/up  g = H(sum_k xg Wq_g) * r * svh_g, u likewise (fp32); s = silu(g); s = min(s, L), u = clamp(u, -L, L)
 //            iff L != 0 (exl3_moe's order, xl_hadamard_inner.cuh:280-400); a16 = fp16(s*u); xd = fp16(H(fp16(a16 *
 //            suh_d)) * r)
@@ -91,32 +95,99 @@ __global__ __launch_bounds__(64) void rot_in_kernel(const void* __restrict__ x, 
 
 // ------------------------------------------------------------------------------------------------ grouped GEMV
 
-// acc[r][0..1] += the decoded tile (two columns per lane) times rows r < rn of xs (16 k values at koff)
-template <int RMAX>
-__device__ __forceinline__ void tile_fma(const u32x4& w, int lane, const _Float16* xs, int ldx, int koff, int rn,
-                                         float (&acc)[RMAX][2]) {
-    const uint32_t pw0 = prev_word(w[3], lane);
-    h2 d[4][4];
+// Staged GEMV inputs in LDS (fp16), in the matrix-core operand order: a row holds its k range as 16-half groups per
+// k tile, half 4i + m of a group = k 2i + (m & 1) + 8 (m >> 1) of the tile. Word i of a trellis tile holds exactly
+// those four k rows (per column), so halves 4i..4i+3, each duplicated into both halves of a dword, form the A
+// operand that matches the decoded word. Rows are padded by XPAD halves against bank conflicts.
+constexpr int XPAD = 8;
+__device__ __forceinline__ int xa_pos(int k) {
+    const int kk = k & 15;
+    return 16 * (k >> 4) + 4 * ((kk & 7) >> 1) + (kk & 1) + 2 * (kk >> 3);
+}
+
+// rot_in_block in two phases so a wave can have several blocks' loads in flight: rot_load fetches this lane's two
+// inputs and two suh values, rot_store rotates them and writes them into a staged row (dst = the row, k0 = local k
+// of the block, a multiple of 128).
+struct RotIn {
+    uint32_t x2, s2;
+};
+__device__ __forceinline__ RotIn rot_load(const void* x, size_t xoff, const _Float16* suh, int lane) {
+    return RotIn{*reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + xoff + 2 * lane),
+                 *reinterpret_cast<const uint32_t*>(suh + 2 * lane)};
+}
+__device__ __forceinline__ void rot_store(const RotIn& v, int xdt, uint16_t* dst, int k0, int lane) {
+    _Float16 h0, h1;
+    if (xdt == DT_BF16) {
+        h0 = (_Float16)__builtin_bit_cast(float, v.x2 << 16);
+        h1 = (_Float16)__builtin_bit_cast(float, v.x2 & 0xFFFF0000u);
+    } else {
+        h0 = u16_as_h(v.x2 & 0xFFFFu);
+        h1 = u16_as_h(v.x2 >> 16);
+    }
+    const h2 s = __builtin_bit_cast(h2, v.s2);
+    float p0 = (float)(_Float16)(h0 * s.x), p1 = (float)(_Float16)(h1 * s.y);
+    fwht128_w64(p0, p1, lane);
+    *reinterpret_cast<h2*>(dst + xa_pos(k0 + 2 * lane)) = h2{(_Float16)(p0 * HAD_R), (_Float16)(p1 * HAD_R)};
+}
+
+// The raw codebook word of a state: its two fp16 halves sum to the weight.
+__device__ __forceinline__ uint32_t mcg_word(uint32_t s) { return ((s * MCG_MUL) & MCG_MASK) ^ MCG_FLIP; }
+
+// Decode trellis word w (predecessor pw) into matrix-core B operands: b0 = column q, b1 = column q + 8, dword m
+// holding the (lo, hi) halves of k row 2i + (m & 1) + 8 (m >> 1) (i = the word's index in the lane's four).
+__device__ __forceinline__ void decode_word_b(uint32_t pw, uint32_t w, u32x4& b0, u32x4& b1) {
+    const uint32_t D = __builtin_amdgcn_alignbit(pw, w, 20);        // (pw:w) >> 20
+    b0[0] = mcg_word(__builtin_amdgcn_ubfe(D, 8, 16));
+    b0[1] = mcg_word(__builtin_amdgcn_ubfe(D, 4, 16));
+    b0[2] = mcg_word(D & 0xFFFFu);
+    b0[3] = mcg_word(w >> 16);
+    b1[0] = mcg_word(__builtin_amdgcn_ubfe(w, 12, 16));
+    b1[1] = mcg_word(__builtin_amdgcn_ubfe(w, 8, 16));
+    b1[2] = mcg_word(__builtin_amdgcn_ubfe(w, 4, 16));
+    b1[3] = mcg_word(w & 0xFFFFu);
+}
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+
+// A operand of word i: staged halves 4i..4i+3 (dwords 2i, 2i + 1 of the step's eight), each duplicated.
+__device__ __forceinline__ u32x4 a_operand(const u32x4& x0, const u32x4& x1, int i) {
+    const uint32_t d0 = i < 2 ? x0[2 * i] : x1[2 * i - 4], d1 = i < 2 ? x0[2 * i + 1] : x1[2 * i - 3];
+    return u32x4{__builtin_amdgcn_perm(d0, d0, 0x01000100u), __builtin_amdgcn_perm(d0, d0, 0x03020302u),
+                 __builtin_amdgcn_perm(d1, d1, 0x01000100u), __builtin_amdgcn_perm(d1, d1, 0x03020302u)};
+}
+
+// One step of a wave over one matrix: lane (t, q) holds words 4q..4q+3 of the tile (pw0 = word 4q - 1) (k tile t/2 of the step, column
+// tile t%2); for word i the matrix core takes A = the rows' staged inputs of that word's four k rows (lane group
+// t/2 = lane/16 supplies k tile t/2) and B = the decoded halves of column q (acc[0]) or q + 8 (acc[1]): the MFMA
+// adds lo and hi exactly in fp32 together with the products.
+__device__ __forceinline__ void step_mfma(const u32x4& w, uint32_t pw0, const u32x4& x0, const u32x4& x1,
+                                          f32x4 (&acc)[2]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) decode_word(i ? w[i - 1] : pw0, w[i], d[i]);
+    for (int i = 0; i < 4; ++i) {
+        const u32x4 av = a_operand(x0, x1, i);
+        u32x4 b0, b1;
+        decode_word_b(i ? w[i - 1] : pw0, w[i], b0, b1);
+        acc[0] = mfma16(av, b0, acc[0]);
+        acc[1] = mfma16(av, b1, acc[1]);
+    }
+}
+
+// The same step for gate and up with one shared staged input (one A operand per word for both matrices).
+__device__ __forceinline__ void step_mfma2(const u32x4& wg, uint32_t pwg, const u32x4& wu, uint32_t pwu,
+                                           const u32x4& x0, const u32x4& x1, f32x4 (&ag)[2], f32x4 (&au)[2]) {
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-        if (r < rn) {
-            const h2* xp = reinterpret_cast<const h2*>(xs + (size_t)r * ldx + koff);
-            h2 xv[8];
-#pragma unroll
-            for (int m = 0; m < 8; ++m) xv[m] = xp[m];
-            float a0 = acc[r][0], a1 = acc[r][1];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a0 = __builtin_amdgcn_fdot2(d[i][0], xv[i], a0, false);
-                a0 = __builtin_amdgcn_fdot2(d[i][1], xv[4 + i], a0, false);
-                a1 = __builtin_amdgcn_fdot2(d[i][2], xv[i], a1, false);
-                a1 = __builtin_amdgcn_fdot2(d[i][3], xv[4 + i], a1, false);
-            }
-            acc[r][0] = a0;
-            acc[r][1] = a1;
-        }
+    for (int i = 0; i < 4; ++i) {
+        const u32x4 av = a_operand(x0, x1, i);
+        u32x4 b0, b1;
+        decode_word_b(i ? wg[i - 1] : pwg, wg[i], b0, b1);
+        ag[0] = mfma16(av, b0, ag[0]);
+        ag[1] = mfma16(av, b1, ag[1]);
+        decode_word_b(i ? wu[i - 1] : pwu, wu[i], b0, b1);
+        au[0] = mfma16(av, b0, au[0]);
+        au[1] = mfma16(av, b1, au[1]);
     }
 }
 
@@ -126,31 +197,21 @@ __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
     return __builtin_nontemporal_load(reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(p)));
 }
 
-// Cross-wave reduction of acc (fixed order w = 0..3) and store of this split's partial rows into dst (row stride ld).
-template <int RMAX>
-__device__ __forceinline__ void reduce_store(float (&acc)[RMAX][2], float* red, int wv, int lane, int rn, float* dst,
-                                             size_t ld) {
-    const int t = lane >> 3, q = lane & 7;
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r)
-        if (r < rn) {
-            red[(wv * RMAX + r) * 128 + t * 16 + q] = acc[r][0];
-            red[(wv * RMAX + r) * 128 + t * 16 + q + 8] = acc[r][1];
-        }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < rn * 128; idx += DEC_WAVES * 64) {
-        const int r = idx >> 7, c = idx & 127;
-        float s = red[r * 128 + c];
-#pragma unroll
-        for (int w2 = 1; w2 < DEC_WAVES; ++w2) s += red[(w2 * RMAX + r) * 128 + c];
-        st_coherent(dst + (size_t)r * ld + c, s);
-    }
-    __syncthreads();
-}
+// Accumulator layout of a wave (two 16x16 tiles): lane column c = lane % 16 is output column (c/8)*16 + c%8 (acc[0])
+// and that + 8 (acc[1]) of the wave's 32; rows 4 (lane/16) + r.
+__device__ __forceinline__ int acc_col(int lane) { return ((lane & 15) >> 3) * 16 + (lane & 7); }
 
+constexpr int GU_WAVES = 8;      // gate/up workgroup: 4 column groups of 32 x 2 halves of the K range
+constexpr int DN_WAVES = 8;      // down workgroup: 8 column groups of 32 (256 output columns) over the N range
+constexpr int ZS_ROWS = 16;
 
-template <int RMAX>
-__global__ __launch_bounds__(DEC_WAVES * 64) void dec_gateup_kernel(DecodeArgs a) {
+// grid (N/128, K splits, segments), 512 threads: workgroup = 128 gate and up columns of one segment over one K range
+// (all of K unless small segment counts call for splits); wave (cg, kh) = columns 32cg..32cg+31 over half kh of the
+// range, DEPTH steps of loads in flight. The halves are added in LDS; with one split the epilogue follows directly,
+// with several each split stores its partial and the workgroup that arrives last adds them in split order.
+template <int DEPTH, bool SHARED>
+__global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_gateup_kernel(
+    DecodeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int last_flag;
     const int cb = blockIdx.x, ks = blockIdx.y, s = blockIdx.z;
@@ -158,80 +219,150 @@ __global__ __launch_bounds__(DEC_WAVES * 64) void dec_gateup_kernel(DecodeArgs a
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cg = wv & 3, kh = wv >> 2;
     const int K = a.K, N = a.N, NT = N >> 4;
-    const int KR = K / a.sk_gu, kbase = ks * KR;
-    _Float16* xs = reinterpret_cast<_Float16*>(smem);              // [2][RMAX][KR]
+    const int KR = K / a.sk_gu, KH = KR >> 1, kbase = ks * KR, RSH = KR + XPAD;
+    constexpr int NMAT = SHARED ? 1 : 2;
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);              // [NMAT][rn][RSH]
 
-    // prologue: the segment's rotated gate and up inputs for this K range
-    const int nb = KR >> 7;
-    for (int task = wv; task < rn * 2 * nb; task += DEC_WAVES) {
-        const int r = task / (2 * nb), rem = task - r * 2 * nb, mat = rem / nb, b = rem - mat * nb;
-        const _Float16* suh = reinterpret_cast<const _Float16*>((mat ? a.wt.u_suh : a.wt.g_suh)[e]) + kbase + b * 128;
-        rot_in_block(a.x, a.xdt, (size_t)a.tok[row0 + r] * a.x_stride + kbase + b * 128, suh,
-                     xs + (size_t)(mat * RMAX + r) * KR + b * 128, lane);
+    // first weight loads are issued before the prologue so their latency overlaps it
+    const int t = lane >> 3, q = lane & 7;
+    const int ct = cb * 8 + cg * 2 + (t & 1);
+    const u32x4* G = reinterpret_cast<const u32x4*>(a.wt.g_tr[e]);
+    const u32x4* U = reinterpret_cast<const u32x4*>(a.wt.u_tr[e]);
+    const size_t sstr = (size_t)NT * 8 * 4;                         // one step = four k tiles
+    const size_t idx0 = ((size_t)(((kbase + kh * KH) >> 4) + (t >> 1)) * NT + ct) * 8 + q;
+    const int steps = KH >> 6;                                       // a multiple of DEPTH
+    // buffer j is refilled right after use with step st + DEPTH + j; refills past the last step re-read the last
+    // step, so every load is unconditional and in bounds
+    u32x4 gb[DEPTH], ub[DEPTH];
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) {
+        gb[j] = ld_stream(G + idx0 + j * sstr);
+        ub[j] = ld_stream(U + idx0 + j * sstr);
+    }
+
+    // prologue: the segment's rotated inputs for this K range, four blocks per wave per round (loads first)
+    const int nb = KR >> 7, ntask = rn * NMAT * nb;
+    for (int t0 = wv; t0 < ntask; t0 += 4 * GU_WAVES) {
+        RotIn v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int task = t0 + c * GU_WAVES;
+            if (task < ntask) {
+                const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
+                const _Float16* suh =
+                    reinterpret_cast<const _Float16*>((mat ? a.wt.u_suh : a.wt.g_suh)[e]) + kbase + b * 128;
+                v[c] = rot_load(a.x, (size_t)a.tok[row0 + r] * a.x_stride + kbase + b * 128, suh, lane);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int task = t0 + c * GU_WAVES;
+            if (task < ntask) {
+                const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
+                rot_store(v[c], a.xdt, xs + (size_t)(mat * rn + r) * RSH, b * 128, lane);
+            }
+        }
     }
     __syncthreads();
 
-    // main loop: this wave's k tiles of gate and up
-    const int t = lane >> 3, q = lane & 7;
-    const int KTw = (KR >> 4) / DEC_WAVES;
-    const int ktl0 = wv * KTw;                                       // local k tile (within KR)
-    const u32x4* G = reinterpret_cast<const u32x4*>(a.wt.g_tr[e]);
-    const u32x4* U = reinterpret_cast<const u32x4*>(a.wt.u_tr[e]);
-    const size_t kstr = (size_t)NT * 8;
-    size_t idx = ((size_t)((kbase >> 4) + ktl0) * NT + cb * 8 + t) * 8 + q;
-    float ag[RMAX][2], au[RMAX][2];
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r) ag[r][0] = ag[r][1] = au[r][0] = au[r][1] = 0.f;
-    // software pipeline: the next two k tiles of both matrices are in flight while the current two are decoded
-    u32x4 g0 = ld_stream(G + idx), u0 = ld_stream(U + idx);
-    u32x4 g1 = ld_stream(G + idx + kstr), u1 = ld_stream(U + idx + kstr);
-    for (int kk = 0; kk < KTw; kk += 2) {
-        idx += 2 * kstr;
-        u32x4 ng0 = g0, nu0 = u0, ng1 = g1, nu1 = u1;
-        if (kk + 2 < KTw) {
-            ng0 = ld_stream(G + idx);
-            nu0 = ld_stream(U + idx);
-            ng1 = ld_stream(G + idx + kstr);
-            nu1 = ld_stream(U + idx + kstr);
-        }
-        const int koff = (ktl0 + kk) * 16;
-        tile_fma<RMAX>(g0, lane, xs, KR, koff, rn, ag);
-        tile_fma<RMAX>(u0, lane, xs + (size_t)RMAX * KR, KR, koff, rn, au);
-        tile_fma<RMAX>(g1, lane, xs, KR, koff + 16, rn, ag);
-        tile_fma<RMAX>(u1, lane, xs + (size_t)RMAX * KR, KR, koff + 16, rn, au);
-        g0 = ng0;
-        u0 = nu0;
-        g1 = ng1;
-        u1 = nu1;
+    const int arow = min(lane & 15, rn - 1);                         // rows >= rn repeat the last row (dropped)
+    const uint16_t* xg = xs + (size_t)arow * RSH + kh * KH + (t >> 1) * 16;
+    const uint16_t* xu = xs + (size_t)((NMAT - 1) * rn + arow) * RSH + kh * KH + (t >> 1) * 16;
+    f32x4 ag[2], au[2];
+    ag[0] = ag[1] = au[0] = au[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // staged inputs are read one step ahead (xc = this step's, xn = the next step's)
+    u32x4 xc[2][2], xn[2][2];
+    xc[0][0] = reinterpret_cast<const u32x4*>(xg)[0];
+    xc[0][1] = reinterpret_cast<const u32x4*>(xg)[1];
+    if (!SHARED) {
+        xc[1][0] = reinterpret_cast<const u32x4*>(xu)[0];
+        xc[1][1] = reinterpret_cast<const u32x4*>(xu)[1];
     }
-    __syncthreads();                                                 // xs is reused for the reduction
+    for (int st = 0; st < steps; st += DEPTH) {
+#pragma unroll
+        for (int j = 0; j < DEPTH; ++j) {
+            const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
+            const int sn = min(st + j + 1, steps - 1);
+            xn[0][0] = reinterpret_cast<const u32x4*>(xg + sn * 64)[0];
+            xn[0][1] = reinterpret_cast<const u32x4*>(xg + sn * 64)[1];
+            if (SHARED) {
+                step_mfma2(gb[j], prev_word(gb[j][3], lane), ub[j], prev_word(ub[j][3], lane), xc[0][0], xc[0][1], ag,
+                           au);
+            } else {
+                xn[1][0] = reinterpret_cast<const u32x4*>(xu + sn * 64)[0];
+                xn[1][1] = reinterpret_cast<const u32x4*>(xu + sn * 64)[1];
+                step_mfma(gb[j], prev_word(gb[j][3], lane), xc[0][0], xc[0][1], ag);
+                step_mfma(ub[j], prev_word(ub[j][3], lane), xc[1][0], xc[1][1], au);
+            }
+            gb[j] = ld_stream(G + nx);
+            ub[j] = ld_stream(U + nx);
+            __builtin_amdgcn_sched_barrier(0);                      // keep the refill here, not sunk to the end
+            xc[0][0] = xn[0][0];
+            xc[0][1] = xn[0][1];
+            if (!SHARED) {
+                xc[1][0] = xn[1][0];
+                xc[1][1] = xn[1][1];
+            }
+        }
+    }
 
-    float* red = reinterpret_cast<float*>(smem);                    // [DEC_WAVES][RMAX][128]
+    // the two K halves: kh = 1 hands its accumulators to kh = 0 through LDS, which writes the row sums
+    __syncthreads();                                                 // the staged inputs are no longer read
+    float* red = reinterpret_cast<float*>(smem);                    // [4][64][16]
+    float* zs = red + 4 * 64 * 16;                                   // [2][ZS_ROWS][128]
+    if (kh == 1) {
+        f32x4* rp = reinterpret_cast<f32x4*>(red + (cg * 64 + lane) * 16);
+        rp[0] = ag[0];
+        rp[1] = ag[1];
+        rp[2] = au[0];
+        rp[3] = au[1];
+    }
+    __syncthreads();
+    if (kh == 0) {
+        const f32x4* rp = reinterpret_cast<const f32x4*>(red + (cg * 64 + lane) * 16);
+        const int col = cg * 32 + acc_col(lane), rb = 4 * (lane >> 4);
+        const f32x4 g0 = rp[0], g1 = rp[1], u0 = rp[2], u1 = rp[3];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (rb + r < rn) {
+                zs[(rb + r) * 128 + col] = ag[0][r] + g0[r];
+                zs[(rb + r) * 128 + col + 8] = ag[1][r] + g1[r];
+                zs[(ZS_ROWS + rb + r) * 128 + col] = au[0][r] + u0[r];
+                zs[(ZS_ROWS + rb + r) * 128 + col + 8] = au[1][r] + u1[r];
+            }
+    }
+    __syncthreads();
+
     const size_t P = a.P;
-    reduce_store<RMAX>(ag, red, wv, lane, rn, a.zg + ((size_t)(ks * 2 + 0) * P + row0) * N + cb * 128, N);
-    reduce_store<RMAX>(au, red, wv, lane, rn, a.zg + ((size_t)(ks * 2 + 1) * P + row0) * N + cb * 128, N);
-
     unsigned* cnt = a.cnt_gu + (size_t)s * (N >> 7) + cb;
-    if (!arrive_last(cnt, (unsigned)a.sk_gu, &last_flag)) return;
+    if (a.sk_gu > 1) {
+        for (int i = tid; i < 2 * rn * 128; i += GU_WAVES * 64) {
+            const int mat = i / (rn * 128), rem = i - mat * rn * 128, r = rem >> 7, c = rem & 127;
+            st_coherent(a.zg + ((size_t)(ks * 2 + mat) * P + row0 + r) * N + cb * 128 + c,
+                        zs[(mat * ZS_ROWS + r) * 128 + c]);
+        }
+        if (!arrive_last(cnt, (unsigned)a.sk_gu, &last_flag)) return;
+        for (int i = tid; i < 2 * rn * 128; i += GU_WAVES * 64) {
+            const int mat = i / (rn * 128), rem = i - mat * rn * 128, r = rem >> 7, c = rem & 127;
+            float v = 0.f;
+            for (int k = 0; k < a.sk_gu; ++k) v += ld_coherent(a.zg + ((size_t)(k * 2 + mat) * P + row0 + r) * N + cb * 128 + c);
+            zs[(mat * ZS_ROWS + r) * 128 + c] = v;
+        }
+        __syncthreads();
+    }
 
-    // epilogue (last split): sum the splits in order, output Hadamard, SwiGLU, down-input rotation
+    // epilogue: output Hadamard, SwiGLU, down-input rotation; wave w takes rows w, w + 8
     const int col = cb * 128 + 2 * lane;
     const h2 svg = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + col);
     const h2 svu = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + col);
     const h2 sud = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + col);
     const float L = a.limit;
-    for (int r = wv; r < rn; r += DEC_WAVES) {
+    for (int r = wv; r < rn; r += GU_WAVES) {
         const size_t row = row0 + r;
-        float g[2] = {0.f, 0.f}, u[2] = {0.f, 0.f};
-        for (int k = 0; k < a.sk_gu; ++k) {
-            const float* zg = a.zg + ((size_t)(k * 2) * P + row) * N + col;
-            const float* zu = a.zg + ((size_t)(k * 2 + 1) * P + row) * N + col;
-            g[0] += ld_coherent(zg);
-            g[1] += ld_coherent(zg + 1);
-            u[0] += ld_coherent(zu);
-            u[1] += ld_coherent(zu + 1);
-        }
+        float g[2] = {zs[r * 128 + 2 * lane], zs[r * 128 + 2 * lane + 1]};
+        float u[2] = {zs[(ZS_ROWS + r) * 128 + 2 * lane], zs[(ZS_ROWS + r) * 128 + 2 * lane + 1]};
         fwht128_w64(g[0], g[1], lane);
         fwht128_w64(u[0], u[1], lane);
         float b[2];
@@ -250,11 +381,14 @@ __global__ __launch_bounds__(DEC_WAVES * 64) void dec_gateup_kernel(DecodeArgs a
         fwht128_w64(b[0], b[1], lane);
         *reinterpret_cast<h2*>(a.xd + row * N + col) = h2{(_Float16)(b[0] * HAD_R), (_Float16)(b[1] * HAD_R)};
     }
-    if (tid == 0) *cnt = 0u;
+    if (a.sk_gu > 1 && tid == 0) *cnt = 0u;
 }
 
-template <int RMAX>
-__global__ __launch_bounds__(DEC_WAVES * 64) void dec_down_kernel(DecodeArgs a) {
+// grid (K/256, N splits, segments), 512 threads: workgroup = 256 output columns of one segment over one N range;
+// wave w = columns 32w..32w+31 over the whole range.
+template <int DEPTH>
+__global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_down_kernel(
+    DecodeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int last_flag;
     const int cb = blockIdx.x, ks = blockIdx.y, s = blockIdx.z;
@@ -263,57 +397,84 @@ __global__ __launch_bounds__(DEC_WAVES * 64) void dec_down_kernel(DecodeArgs a) 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, N = a.N, KT = K >> 4;
-    const int NR = N / a.sk_dn, nbase = ks * NR;
-    _Float16* xs = reinterpret_cast<_Float16*>(smem);              // [RMAX][NR]
-    for (int i = tid; i < rn * (NR >> 3); i += DEC_WAVES * 64) {
-        const int r = i / (NR >> 3), c8 = i - r * (NR >> 3);
-        *reinterpret_cast<u32x4*>(xs + (size_t)r * NR + c8 * 8) =
-            *reinterpret_cast<const u32x4*>(a.xd + (size_t)(row0 + r) * N + nbase + c8 * 8);
-    }
-    __syncthreads();
+    const int NR = N / a.sk_dn, nbase = ks * NR, RSH = NR + XPAD;
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);              // [rn][RSH]
 
     const int t = lane >> 3, q = lane & 7;
-    const int NTw = (NR >> 4) / DEC_WAVES;
-    const int ntl0 = wv * NTw;
+    const int ct = cb * 16 + wv * 2 + (t & 1);
     const u32x4* D = reinterpret_cast<const u32x4*>(a.wt.d_tr[e]);
-    const size_t nstr = (size_t)KT * 8;
-    size_t idx = ((size_t)((nbase >> 4) + ntl0) * KT + cb * 8 + t) * 8 + q;
-    float ad[RMAX][2];
+    const size_t sstr = (size_t)KT * 8 * 4;
+    const size_t idx0 = ((size_t)((nbase >> 4) + (t >> 1)) * KT + ct) * 8 + q;
+    const int steps = NR >> 6;                                       // a multiple of DEPTH
+    u32x4 db[DEPTH];
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) ad[r][0] = ad[r][1] = 0.f;
-    u32x4 d0 = ld_stream(D + idx), d1 = ld_stream(D + idx + nstr);
-    for (int kk = 0; kk < NTw; kk += 2) {
-        idx += 2 * nstr;
-        u32x4 n0 = d0, n1 = d1;
-        if (kk + 2 < NTw) {
-            n0 = ld_stream(D + idx);
-            n1 = ld_stream(D + idx + nstr);
-        }
-        const int koff = (ntl0 + kk) * 16;
-        tile_fma<RMAX>(d0, lane, xs, NR, koff, rn, ad);
-        tile_fma<RMAX>(d1, lane, xs, NR, koff + 16, rn, ad);
-        d0 = n0;
-        d1 = n1;
+    for (int j = 0; j < DEPTH; ++j) db[j] = ld_stream(D + idx0 + j * sstr);
+
+    // prologue: the segment's down inputs (already rotated) for this N range, into the staged layout
+    for (int i = tid; i < rn * (NR >> 1); i += DN_WAVES * 64) {
+        const int r = i / (NR >> 1), k = 2 * (i - r * (NR >> 1));
+        *reinterpret_cast<uint32_t*>(xs + (size_t)r * RSH + xa_pos(k)) =
+            *reinterpret_cast<const uint32_t*>(a.xd + (size_t)(row0 + r) * N + nbase + k);
     }
     __syncthreads();
-    float* red = reinterpret_cast<float*>(smem);
+
+    const int arow = min(lane & 15, rn - 1);
+    const uint16_t* xr = xs + (size_t)arow * RSH + (t >> 1) * 16;
+    f32x4 ad[2];
+    ad[0] = ad[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 xc0 = reinterpret_cast<const u32x4*>(xr)[0], xc1 = reinterpret_cast<const u32x4*>(xr)[1];
+    for (int st = 0; st < steps; st += DEPTH) {
+#pragma unroll
+        for (int j = 0; j < DEPTH; ++j) {
+            const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
+            const int sn = min(st + j + 1, steps - 1);
+            const u32x4 xn0 = reinterpret_cast<const u32x4*>(xr + sn * 64)[0];
+            const u32x4 xn1 = reinterpret_cast<const u32x4*>(xr + sn * 64)[1];
+            step_mfma(db[j], prev_word(db[j][3], lane), xc0, xc1, ad);
+            db[j] = ld_stream(D + nx);
+            __builtin_amdgcn_sched_barrier(0);
+            xc0 = xn0;
+            xc1 = xn1;
+        }
+    }
+    __syncthreads();                                                 // the staged inputs are no longer read
+    float* zs = reinterpret_cast<float*>(smem);                     // [ZS_ROWS][256]
+    {
+        const int col = wv * 32 + acc_col(lane), rb = 4 * (lane >> 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (rb + r < rn) {
+                zs[(rb + r) * 256 + col] = ad[0][r];
+                zs[(rb + r) * 256 + col + 8] = ad[1][r];
+            }
+    }
+    __syncthreads();
+
     const size_t P = a.P;
-    reduce_store<RMAX>(ad, red, wv, lane, rn, a.zd + ((size_t)ks * P + row0) * K + cb * 128, K);
+    unsigned* cnt = a.cnt_dn + (size_t)s * (K >> 8) + cb;
+    if (a.sk_dn > 1) {
+        for (int i = tid; i < rn * 256; i += DN_WAVES * 64) {
+            const int r = i >> 8, c = i & 255;
+            st_coherent(a.zd + ((size_t)ks * P + row0 + r) * K + cb * 256 + c, zs[r * 256 + c]);
+        }
+        if (!arrive_last(cnt, (unsigned)a.sk_dn, &last_flag)) return;
+        for (int i = tid; i < rn * 256; i += DN_WAVES * 64) {
+            const int r = i >> 8, c = i & 255;
+            float v = 0.f;
+            for (int k = 0; k < a.sk_dn; ++k) v += ld_coherent(a.zd + ((size_t)k * P + row0 + r) * K + cb * 256 + c);
+            zs[r * 256 + c] = v;
+        }
+        __syncthreads();
+    }
 
-    unsigned* cnt = a.cnt_dn + (size_t)s * (K >> 7) + cb;
-    if (!arrive_last(cnt, (unsigned)a.sk_dn, &last_flag)) return;
-
-    const int col = cb * 128 + 2 * lane;
-    const h2 svd = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + col);
-    for (int r = wv; r < rn; r += DEC_WAVES) {
+    // epilogue: (row, 128-column half) tasks; output Hadamard, scale, then atomics or the per-pair contribution
+    for (int task = wv; task < rn * 2; task += DN_WAVES) {
+        const int r = task >> 1, hb = task & 1;
         const size_t row = row0 + r;
         if (a.pe[row] < 0) continue;                                 // a row whose token id was out of range
-        float v[2] = {0.f, 0.f};
-        for (int k = 0; k < a.sk_dn; ++k) {
-            const float* z = a.zd + ((size_t)k * P + row) * K + col;
-            v[0] += ld_coherent(z);
-            v[1] += ld_coherent(z + 1);
-        }
+        const int col = cb * 256 + hb * 128 + 2 * lane;
+        const h2 svd = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + col);
+        float v[2] = {zs[r * 256 + hb * 128 + 2 * lane], zs[r * 256 + hb * 128 + 2 * lane + 1]};
         fwht128_w64(v[0], v[1], lane);
         const float rs = HAD_R * (float)u16_as_h(a.w16[row]);
         v[0] = v[0] * rs * (float)svd.x;
@@ -326,7 +487,7 @@ __global__ __launch_bounds__(DEC_WAVES * 64) void dec_down_kernel(DecodeArgs a) 
             *reinterpret_cast<float2*>(a.contrib + row * K + col) = make_float2(v[0], v[1]);
         }
     }
-    if (tid == 0) *cnt = 0u;
+    if (a.sk_dn > 1 && tid == 0) *cnt = 0u;
 }
 
 // grid (T, K/256), 128 threads x 2 columns: out[t] = sum over slots k (in order) of the valid pairs' contributions
@@ -366,30 +527,59 @@ int launch_rot_in(const void* x, int xdt, int64_t x_stride, const int* tok, cons
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int RMAX>
-static void launch_decode_r(const DecodeArgs& a, hipStream_t st, int kernels) {
-    const int KR = a.K / a.sk_gu, NR = a.N / a.sk_dn;
-    const size_t red = (size_t)DEC_WAVES * RMAX * 128 * sizeof(float);
-    const size_t shm_gu = std::max((size_t)2 * RMAX * KR * 2, red);
-    const size_t shm_dn = std::max((size_t)RMAX * NR * 2, red);
-    if (kernels & 1)
-        hipLaunchKernelGGL(dec_gateup_kernel<RMAX>, dim3(a.N / 128, a.sk_gu, a.S_cap), dim3(DEC_WAVES * 64), shm_gu,
-                           st, a);
-    if (kernels & 2)
-        hipLaunchKernelGGL(dec_down_kernel<RMAX>, dim3(a.K / 128, a.sk_dn, a.S_cap), dim3(DEC_WAVES * 64), shm_dn, st,
-                           a);
-    if ((kernels & 4) && !a.accumulate) hipLaunchKernelGGL(combine_kernel, dim3(a.T, a.K / 256), dim3(128), 0, st, a);
+size_t decode_lds_gateup(int rmax, int K, int sk_gu, int shared_suh) {
+    const size_t staged = (size_t)(shared_suh ? 1 : 2) * rmax * (K / sk_gu + XPAD) * 2;
+    const size_t reduce = (size_t)(4 * 64 * 16 + 2 * ZS_ROWS * 128) * 4;
+    return std::max(staged, reduce);
+}
+size_t decode_lds_down(int rmax, int N, int sk_dn) {
+    return std::max((size_t)rmax * (N / sk_dn + XPAD) * 2, (size_t)ZS_ROWS * 256 * 4);
 }
 
-int launch_decode(const DecodeArgs& a, int rmax, hipStream_t st, int kernels) {
-    switch (rmax) {
-        case 1: launch_decode_r<1>(a, st, kernels); break;
-        case 2: launch_decode_r<2>(a, st, kernels); break;
-        case 4: launch_decode_r<4>(a, st, kernels); break;
-        case 8: launch_decode_r<8>(a, st, kernels); break;
-        case 16: launch_decode_r<16>(a, st, kernels); break;
-        default: return 1;
+template <typename F>
+static int allow_lds(F* f) {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)DECODE_LDS_MAX) == hipSuccess ? 0 : -1;
+}
+
+static int decode_setup() {
+    static bool done = false;
+    if (done) return 0;
+    if (allow_lds(dec_gateup_kernel<4, true>) || allow_lds(dec_gateup_kernel<2, true>) ||
+        allow_lds(dec_gateup_kernel<4, false>) || allow_lds(dec_gateup_kernel<2, false>) ||
+        allow_lds(dec_down_kernel<4>) || allow_lds(dec_down_kernel<2>))
+        return -1;
+    done = true;
+    return 0;
+}
+
+int launch_decode(const DecodeArgs& a0, int rmax, hipStream_t st, int kernels) {
+    if (rmax < 1 || rmax > ZS_ROWS) return 1;
+    if (decode_setup()) return -1;
+    DecodeArgs a = a0;
+    a.rmax = rmax;
+    // load depth: four steps (of 64 k) when each wave's range holds a multiple of four, else two
+    if (kernels & 1) {
+        const dim3 grid(a.N / 128, a.sk_gu, a.S_cap);
+        const size_t lds = decode_lds_gateup(rmax, a.K, a.sk_gu, a.shared_suh);
+        const bool d4 = ((a.K / a.sk_gu / 2) >> 6) % 4 == 0;
+        if (a.shared_suh) {
+            if (d4) hipLaunchKernelGGL((dec_gateup_kernel<4, true>), grid, dim3(GU_WAVES * 64), lds, st, a);
+            else hipLaunchKernelGGL((dec_gateup_kernel<2, true>), grid, dim3(GU_WAVES * 64), lds, st, a);
+        } else {
+            if (d4) hipLaunchKernelGGL((dec_gateup_kernel<4, false>), grid, dim3(GU_WAVES * 64), lds, st, a);
+            else hipLaunchKernelGGL((dec_gateup_kernel<2, false>), grid, dim3(GU_WAVES * 64), lds, st, a);
+        }
     }
+    if (kernels & 2) {
+        const dim3 grid(a.K / 256, a.sk_dn, a.S_cap);
+        const size_t lds = decode_lds_down(rmax, a.N, a.sk_dn);
+        if (((a.N / a.sk_dn) >> 6) % 4 == 0)
+            hipLaunchKernelGGL(dec_down_kernel<4>, grid, dim3(DN_WAVES * 64), lds, st, a);
+        else
+            hipLaunchKernelGGL(dec_down_kernel<2>, grid, dim3(DN_WAVES * 64), lds, st, a);
+    }
+    if ((kernels & 4) && !a.accumulate) hipLaunchKernelGGL(combine_kernel, dim3(a.T, a.K / 256), dim3(128), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -69,6 +69,8 @@ struct DecodeArgs {
     const int* nseg;
     int S_cap;
     int sk_gu, sk_dn;       // K splits of the gate/up GEMV (over K) and the down GEMV (over N)
+    int rmax;               // rows per segment (<= 16)
+    int shared_suh;         // gate and up share one input rotation (one staged copy)
     float limit;
     // workspace
     float* zg;              // [sk_gu][2][P][N]
@@ -76,7 +78,7 @@ struct DecodeArgs {
     uint16_t* xd;           // [P][N] fp16 bits
     float* contrib;         // [P][K] per-pair contribution (slot-order combine)
     unsigned* cnt_gu;       // [S_cap][N/128], zero between calls
-    unsigned* cnt_dn;       // [S_cap][K/128], zero between calls
+    unsigned* cnt_dn;       // [S_cap][K/256], zero between calls
     // output
     void* out;
     int odt;                // output dtype
@@ -123,6 +125,10 @@ int launch_route_counts(const int64_t* counts64, const int64_t* token_sorted, co
                         const RouteArgs& a, hipStream_t st);
 // kernels: bit 0 gate/up, bit 1 down, bit 2 combine
 int launch_decode(const DecodeArgs& a, int rmax, hipStream_t st, int kernels = 7);
+// LDS bytes of the decode GEMV workgroups (staged inputs)
+size_t decode_lds_gateup(int rmax, int K, int sk_gu, int shared_suh);
+size_t decode_lds_down(int rmax, int N, int sk_dn);
+constexpr size_t DECODE_LDS_MAX = 81920;   // two 512-thread workgroups per CU
 int launch_dequant(const uint16_t* trellis, int kt, int nt, uint16_t* wq, hipStream_t st);
 int launch_rot_in(const void* x, int xdt, int64_t x_stride, const int* tok, const int* pe, const int64_t* suh_tab,
                   int P, int K, uint16_t* out, hipStream_t st);

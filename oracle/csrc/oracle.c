@@ -112,14 +112,26 @@ static inline uint32_t tile_state(const uint32_t* words, int p) {
 /* trellis int16 [kt][nt][64] -> W_q fp16 bits [kt*16][nt*16] (row-major, K rows, N columns) */
 static uint16_t g_cb[65536];
 static float g_cbf[65536];
+static float g_cbx[65536];         /* fp16(lo) + fp16(hi) without the final fp16 rounding (exact in fp32) */
 static int g_cb_ready = 0;
 
 /* fills the codebook tables once; called before any parallel region */
 void orc_init(void) {
     if (g_cb_ready) return;
     orc_codebook(g_cb);
-    for (uint32_t s = 0; s < 65536u; ++s) g_cbf[s] = orc_h2f(g_cb[s]);
+    for (uint32_t s = 0; s < 65536u; ++s) {
+        g_cbf[s] = orc_h2f(g_cb[s]);
+        uint32_t x = s * MCG_MUL;
+        x = (x & MCG_MASK) ^ MCG_FLIP;
+        g_cbx[s] = (float)((double)orc_h2f((uint16_t)(x & 0xFFFFu)) + (double)orc_h2f((uint16_t)(x >> 16)));
+    }
     g_cb_ready = 1;
+}
+
+/* fp16(lo) + fp16(hi) of every state without the final rounding (exact in fp32) */
+void orc_codebook_exact(float* cb) {
+    orc_init();
+    for (uint32_t s = 0; s < 65536u; ++s) cb[s] = g_cbx[s];
 }
 
 void orc_unpack(const uint16_t* trellis, int kt, int nt, uint16_t* wq) {
@@ -141,8 +153,7 @@ void orc_unpack(const uint16_t* trellis, int kt, int nt, uint16_t* wq) {
     }
 }
 
-static void unpack_f32(const uint16_t* trellis, int kt, int nt, float* w) {
-    const float* cbf = g_cbf;
+static void unpack_f32(const uint16_t* trellis, int kt, int nt, float* w, const float* cbf) {
     const int ncol = nt * 16;
     uint32_t words[32];
     for (int a = 0; a < kt; ++a)
@@ -217,6 +228,8 @@ typedef struct {
  * mode 2: float64 reference (test_e2e_vs_f64.py:52-75: double everywhere, exl3_moe's post-SiLU clamp,
  *         weights rounded to fp16 as production passes them).
  * mode 3: float64 reference with the limit before SiLU iff L != 0 (production's python loop, prod:961-1006).
+ * mode 4: mode 0 with every weight taken as fp16(lo) + fp16(hi) of its codebook word without the final fp16
+ *         rounding (the decode GEMV feeds both halves to the matrix cores, whose fp32 sum is exact).
  * out[T][K] (fp32, or double for modes 2/3 through out64) is accumulated into in pair order per token.
  * Returns 0, or -1 on a bad argument.
  */
@@ -226,8 +239,10 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
     const int n = L->n, K = L->K, N = L->N;
     if (K % 128 || N % 128 || T < 0 || P < 0) return -1;
     const int KT = K / 16, NT = N / 16;
-    const int f64 = mode >= 2;
+    const int f64 = mode == 2 || mode == 3;
+    if (mode < 0 || mode > 4) return -1;
     orc_init();
+    const float* cbt = mode == 4 ? g_cbx : g_cbf;
     /* per-pair contribution rows, summed per token in pair order afterwards (deterministic) */
     float* c32 = f64 ? NULL : (float*)calloc((size_t)P * K, sizeof(float));
     double* c64 = f64 ? (double*)calloc((size_t)P * K, sizeof(double)) : NULL;
@@ -249,9 +264,9 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
             int any = 0;
             for (int j = 0; j < P; ++j) any |= pair_expert[j] == e;
             if (!any) continue;
-            unpack_f32(L->w13_trellis + ((size_t)e * 2 + 0) * KT * NT * 64, KT, NT, wg);
-            unpack_f32(L->w13_trellis + ((size_t)e * 2 + 1) * KT * NT * 64, KT, NT, wu);
-            unpack_f32(L->w2_trellis + (size_t)e * NT * KT * 64, NT, KT, wd);
+            unpack_f32(L->w13_trellis + ((size_t)e * 2 + 0) * KT * NT * 64, KT, NT, wg, cbt);
+            unpack_f32(L->w13_trellis + ((size_t)e * 2 + 1) * KT * NT * 64, KT, NT, wu, cbt);
+            unpack_f32(L->w2_trellis + (size_t)e * NT * KT * 64, NT, KT, wd, cbt);
             const uint16_t* suh_g = L->w13_suh + ((size_t)e * 2 + 0) * K;
             const uint16_t* suh_u = L->w13_suh + ((size_t)e * 2 + 1) * K;
             const uint16_t* svh_g = L->w13_svh + ((size_t)e * 2 + 0) * N;

@@ -32,6 +32,18 @@ def codebook() -> np.ndarray:
 
 
 @functools.lru_cache(maxsize=1)
+def codebook_exact() -> np.ndarray:
+    """fp16(lo) + fp16(hi) of every state as float64 without the final fp16 rounding: the weight the decode GEMV's
+    matrix cores see when they take both halves as operands (exactly representable in float32)."""
+    s = np.arange(1 << 16, dtype=np.uint64)
+    x = ((s * np.uint64(MCG)) & np.uint64(0xFFFFFFFF))
+    x = (x & np.uint64(MASK)) ^ np.uint64(FLIP)
+    lo = (x & np.uint64(0xFFFF)).astype(np.uint16).view(np.float16).astype(np.float64)
+    hi = (x >> np.uint64(16)).astype(np.uint16).view(np.float16).astype(np.float64)
+    return lo + hi
+
+
+@functools.lru_cache(maxsize=1)
 def tile_order() -> tuple[np.ndarray, np.ndarray]:
     """(row, col) inside its 16x16 tile of stream value p = 0..255 (exl3_format_ref.py:22-23, :59-67)."""
     p = np.arange(256)

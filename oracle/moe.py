@@ -7,6 +7,8 @@ module loads it with ctypes and exposes:
                           mode "e3"      : the E3 prefill kernels' rounding points (limit before SiLU)
                           mode "f64"     : float64 reference, limit after SiLU (code/fork/tests/test_e2e_vs_f64.py:52-75)
                           mode "f64_pre" : float64 reference, limit before SiLU (code/fork/docs/prod_exl3_reference.py:961-1006)
+                          mode "decode_x": "decode" with every weight fp16(lo) + fp16(hi) unrounded (the decode GEMV
+                                           feeds both codebook halves to the matrix cores)
   pairs_from_routing      (token, local expert, fp16 weight) per routed pair, invalid ids skipped
 """
 from __future__ import annotations
@@ -20,7 +22,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _SO = os.path.join(_HERE, "_build", "liboracle.so")
 _LIB = None
-MODES = {"decode": 0, "e3": 1, "f64": 2, "f64_pre": 3}
+MODES = {"decode": 0, "e3": 1, "f64": 2, "f64_pre": 3, "decode_x": 4}
 
 
 class _Layer(ctypes.Structure):
@@ -48,6 +50,7 @@ def lib() -> ctypes.CDLL:
         L.orc_d2h.restype = ctypes.c_uint16
         L.orc_d2h.argtypes = [ctypes.c_double]
         L.orc_codebook.argtypes = [ctypes.c_void_p]
+        L.orc_codebook_exact.argtypes = [ctypes.c_void_p]
         L.orc_unpack.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
         L.orc_fwht128.argtypes = [ctypes.c_void_p]
         L.orc_rot_in.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
@@ -69,6 +72,12 @@ def codebook_c() -> np.ndarray:
     out = np.empty(65536, np.uint16)
     lib().orc_codebook(_p(out))
     return out.view(np.float16)
+
+
+def codebook_exact_c() -> np.ndarray:
+    out = np.empty(65536, np.float32)
+    lib().orc_codebook_exact(_p(out))
+    return out
 
 
 def unpack_c(trellis: np.ndarray) -> np.ndarray:
@@ -127,7 +136,7 @@ def forward(layer: dict, x16: np.ndarray, pair_token: np.ndarray, pair_expert: n
     ex = np.ascontiguousarray(pair_expert, np.int32)
     w = np.ascontiguousarray(pair_w16, np.float16)
     m = MODES[mode]
-    if m >= 2:
+    if m in (2, 3):
         out = np.zeros((T, K), np.float64)
         rc = lib().orc_moe_forward(ctypes.byref(L), T, _p(x), tok.size, _p(tok), _p(ex), _p(w), float(limit), m,
                                    None, _p(out), int(threads))

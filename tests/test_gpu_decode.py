@@ -1,8 +1,8 @@
 """GPU parity of the decode path (grouped trellis GEMVs with fused epilogues) against the oracle.
 
 Two references per case (oracle/moe.py):
-  - "decode" mode: the same rounding points as the kernels; only the fp32 summation order of the GEMVs differs, so
-    the fp32 outputs agree to rel_l2 <= 5e-4;
+  - "decode_x" mode: the same rounding points as the kernels (weights as the unrounded codebook sums the matrix
+    cores add); only the fp32 summation order of the GEMVs differs, so the fp32 outputs agree to rel_l2 <= 5e-4;
   - float64: the layer definition (code/fork/tests/test_e2e_vs_f64.py:52-75); outputs within rel_l2 <= 5e-3 (the
     reference's E.2 bound) and elementwise rtol 2e-2 / atol 1e-3 on the bf16 output.
 """
@@ -59,7 +59,7 @@ def test_moe_forward_ids_vs_oracle(cuda, layer32, T, topk, xdt, limit):
     out32 = ops.moe_forward_ids(ex, x, ids, w, limit=limit, out_dtype=torch.float32)
     out_bf = ops.moe_forward_ids(ex, x, ids, w, limit=limit, out_dtype=torch.bfloat16)
     torch.cuda.synchronize()
-    ref_k = _oracle(lay, x, ids, w, n, limit, "decode")
+    ref_k = _oracle(lay, x, ids, w, n, limit, "decode_x")
     ref64 = _oracle(lay, x, ids, w, n, limit, "f64")
     got = out32.cpu().numpy()
     assert np.isfinite(got).all()
@@ -83,14 +83,14 @@ def test_sentinels_map_and_duplicates(cuda, layer32):
     ids[2, 5] = n + 7                   # beyond the local experts
     w = synthetic.softmax_weights(T, topk, seed=79, device=cuda)
     got = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32).cpu().numpy()
-    ref = _oracle(lay, x, ids, w, n, 10.0, "decode")
+    ref = _oracle(lay, x, ids, w, n, 10.0, "decode_x")
     assert _rel(got, ref) <= 5e-4
     # an expert map: global ids 0..2n-1, every other one local
     emap = torch.full((2 * n,), -1, dtype=torch.int64)
     emap[0::2] = torch.arange(n)
     ids2 = synthetic.random_ids(T, 2 * n, topk, seed=80, device=cuda)
     got2 = ops.moe_forward_ids(ex, x, ids2, w, expert_map=emap.to(cuda), out_dtype=torch.float32).cpu().numpy()
-    ref2 = _oracle(lay, x, ids2, w, n, 10.0, "decode", emap=emap)
+    ref2 = _oracle(lay, x, ids2, w, n, 10.0, "decode_x", emap=emap)
     assert _rel(got2, ref2) <= 5e-4
     none = torch.full((T, topk), -1, dtype=torch.int32, device=cuda)
     z = ops.moe_forward_ids(ex, x, none, w, out_dtype=torch.float32)
@@ -161,7 +161,7 @@ def test_exl3_moe_contract(cuda, layer32):
     keep = np.array([e < n and cnt[e] <= R for e in ex_sorted])
     tok = token_sorted.cpu().numpy().astype(np.int32)
     exs = np.where(keep, ex_sorted, -1).astype(np.int32)
-    ref = moe.forward(lay, x.cpu().numpy(), tok, exs, weight_sorted.cpu().numpy(), 10.0, "decode") + 1.0
+    ref = moe.forward(lay, x.cpu().numpy(), tok, exs, weight_sorted.cpu().numpy(), 10.0, "decode_x") + 1.0
     assert _rel(out.cpu().numpy() - 1.0, ref - 1.0) <= 5e-4
     assert (cnt[:n] > R).any() and (cnt[:n] <= R).any()
 

@@ -37,6 +37,21 @@ def test_codebook_c_equals_numpy_and_known_answers():
     assert abs(cbf.mean()) < 0.05 and 0.5 < cbf.std() < 2.0
 
 
+def test_exact_codebook_sums_vs_python_integers():
+    """The unrounded lo + hi sums (what the decode GEMV's matrix cores add): equal in C and numpy, exactly
+    representable in float32, every one rounding to the pinned fp16 codebook, and equal to Python's own sums."""
+    ex = exl3.codebook_exact()
+    exc = moe.codebook_exact_c()
+    assert np.array_equal(exc.astype(np.float64), ex)
+    assert np.array_equal(ex.astype(np.float32).astype(np.float64), ex)
+    assert np.array_equal(ex.astype(np.float16).view(np.uint16), exl3.codebook().view(np.uint16))
+    for s in list(range(0, 65536, 97)) + [0, 1, 0x7FFF, 0x8000, 0xFFFF]:
+        x = (s * 0xCBAC1FED) & 0xFFFFFFFF
+        x = (x & 0x8FFF8FFF) ^ 0x3B603B60
+        assert ex[s] == _half_value_py(x & 0xFFFF) + _half_value_py(x >> 16), s
+    assert np.any(ex != exl3.codebook().astype(np.float64))          # the rounding is not a no-op
+
+
 def test_tile_order_is_the_ptx_b_fragment_layout():
     # PTX ISA, mma.m16n8k16 (.f16): B is 16x8; lane L holds b0,b1 at rows 2*(L%4)+{0,1} and b2,b3 at rows
     # 2*(L%4)+8+{0,1}, column L/4. A tile's lane decodes two n8 halves: values j=0..3 -> first half,

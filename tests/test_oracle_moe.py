@@ -65,7 +65,7 @@ def test_c_f64_equals_numpy_f64(L, pre):
     assert np.all(got[1, :] == got[1, :])
 
 
-@pytest.mark.parametrize("mode,ref_mode", [("decode", "f64"), ("e3", "f64_pre")])
+@pytest.mark.parametrize("mode,ref_mode", [("decode", "f64"), ("decode_x", "f64"), ("e3", "f64_pre")])
 def test_kernel_modes_within_e2e_tolerance_of_f64(mode, ref_mode):
     rng = np.random.default_rng(1)
     n, K, N, T, topk = 8, 512, 256, 4, 4
@@ -81,6 +81,37 @@ def test_kernel_modes_within_e2e_tolerance_of_f64(mode, ref_mode):
     rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert rel < 5e-3, rel
     assert np.allclose(got, ref, rtol=2e-2, atol=1e-3 * np.abs(ref).max())
+
+
+def _constant_tiles(rng, shape, patterns):
+    """int16 trellis whose every 16x16 tile repeats one nibble (all 256 states of the tile equal n * 0x1111)."""
+    pick = rng.choice(np.asarray(patterns, np.int64), size=shape[:-1])
+    return np.repeat(pick[..., None], 64, axis=-1).astype(np.uint16).view(np.int16)
+
+
+def test_decode_x_changes_only_the_weight_rounding():
+    """decode_x differs from decode only in the codebook sums' final fp16 rounding: on tiles whose states all have
+    fp16-exact sums the two modes agree bit for bit, and one tile of an inexact state makes them differ."""
+    ex, cb = exl3.codebook_exact(), exl3.codebook().astype(np.float64)
+    exact = [n * 0x1111 for n in range(16) if ex[n * 0x1111] == cb[n * 0x1111]]
+    inexact = [n * 0x1111 for n in range(16) if ex[n * 0x1111] != cb[n * 0x1111]]
+    assert len(exact) >= 8 and len(inexact) >= 3
+    rng = np.random.default_rng(5)
+    n, K, N, T = 4, 256, 128, 3
+    layer = _layer(rng, n, K, N)
+    layer["w13_trellis"] = _constant_tiles(rng, layer["w13_trellis"].shape, exact)
+    layer["w2_trellis"] = _constant_tiles(rng, layer["w2_trellis"].shape, exact)
+    x16 = rng.standard_normal((T, K)).astype(np.float16)
+    tok = np.array([0, 1, 2, 2], np.int32)
+    exs = np.array([0, 1, 2, 3], np.int32)
+    w16 = np.array([1.0, 0.5, 0.25, 2.0], np.float16)
+    a = moe.forward(layer, x16, tok, exs, w16, 10.0, "decode")
+    b = moe.forward(layer, x16, tok, exs, w16, 10.0, "decode_x")
+    assert np.array_equal(a, b) and np.any(a != 0)
+    layer["w2_trellis"][1, :, 0, :] = np.uint16(inexact[0]).view(np.int16)
+    a = moe.forward(layer, x16, tok, exs, w16, 10.0, "decode")
+    b = moe.forward(layer, x16, tok, exs, w16, 10.0, "decode_x")
+    assert not np.array_equal(a[1], b[1]) and np.array_equal(a[[0, 2]], b[[0, 2]])
 
 
 def test_sentinel_pairs_contribute_nothing():
