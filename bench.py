@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the routed-MoE layer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|prefill]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|prefill|fp8]
 
 Default workload (one "step" = one MoE layer call): the decode MoE layer, T=8 tokens, hidden 4096, 288 experts,
 sigmoid router + bias, top-8, routed scale 2.5, intermediate 1024 (one tensor-parallel rank's shard), EXL3 4-bit
@@ -253,13 +253,78 @@ def run_prefill(args, torch, dev):
                               f"experts, {n_layers} layers alternated, {steps} timed steps"}
 
 
+def run_fp8(args, torch, dev):
+    """e4m3 expert variant, T=2048 (hidden 4096, 288 experts, top-8, intermediate 1024): block-scaled e4m3 experts
+    (N(0, 0.02) weights, fp32 scale per 128x128 block), bf16 activations quantised per token, the router of the
+    decode configuration (sigmoid + bias top-8 x2.5). HBM-bound: bytes = distinct experts x 3 x K x N + scales."""
+    from mi355moe import _lib, fp8, ops, synthetic
+    T = args.fp8_tokens
+    n_layers = 2
+    layers = [synthetic.fp8_layer(E, K, N, seed=600 + l, device=dev) for l in range(n_layers)]
+    routers = [synthetic.router(E, K, seed=610 + l, device=dev) for l in range(n_layers)]
+    x = synthetic.activations(T, K, seed=620, device=dev)
+    outs = [torch.empty(T, K, dtype=torch.bfloat16, device=dev) for _ in range(n_layers)]
+
+    def step(l):
+        w, b = routers[l]
+        ids, wts = ops.router_topk(ops.router_logits(x, w), TOPK, b, routed_scale=SCALE)
+        fp8.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l])
+        return ids, wts
+
+    info = [step(l) for l in range(n_layers)]
+    torch.cuda.synchronize()
+    distinct = [int(torch.unique(i).numel()) for i, _ in info]
+    for w in range(max(2, args.warmup // 4)):
+        step(w % n_layers)
+    torch.cuda.synchronize()
+    steps = max(4, args.steps // 4)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for k in range(steps):
+        step(k % n_layers)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    gu = []
+    for k in range(steps):
+        l = k % n_layers
+        ids, wts = info[l]
+        fp8.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], stages=_lib.STAGE_ROUTE)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fp8.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], stages=_lib.STAGE_GATEUP)
+        b.record()
+        fp8.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l],
+                            stages=_lib.STAGE_DOWN | _lib.STAGE_COMBINE)
+        gu.append((a, b))
+    torch.cuda.synchronize()
+    gu_ms = sum(a.elapsed_time(b) for a, b in gu) / len(gu)
+    D = sum(distinct) / len(distinct)
+    scales = 4 * 3 * (K // 128) * (N // 128)
+    layer_bytes = D * (3 * K * N + scales) + E * K * 2 + T * K * 2 * 2
+    gu_bytes = D * (2 * K * N + 4 * 2 * (K // 128) * (N // 128))
+    P = T * TOPK
+    return {"fp8_tokens_per_s": round(T / (ms / 1000.0), 1), "fp8_ms_per_layer": round(ms, 4),
+            "fp8_gbs": round(layer_bytes / (ms / 1000.0) / 1e9, 1),
+            "fp8_tflops": round(2.0 * P * 3 * K * N / (ms / 1000.0) / 1e12, 2),
+            "fp8_distinct_experts": D,
+            "roofline_fp8": {"bound": "hbm", "kernel": "fp8_gateup_kernel",
+                             "achieved": round(gu_bytes / (gu_ms / 1000.0) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(gu_bytes / (gu_ms / 1000.0) / 1e9 / HBM_PEAK_GBS, 4),
+                             "avg_launch_us": round(gu_ms * 1000.0, 1)},
+            "fp8_config": f"T={T}, {E} experts, top-{TOPK}, sigmoid+bias router x{SCALE}, block-scaled e4m3 experts "
+                          f"(128x128 fp32 scales), per-token e4m3 activations, {n_layers} layers alternated, "
+                          f"{steps} timed steps"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill"])
+    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill", "fp8"])
     ap.add_argument("--prefill-tokens", type=int, default=8192)
+    ap.add_argument("--fp8-tokens", type=int, default=2048)
     ap.add_argument("--tokens", type=int, default=8)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -275,7 +340,7 @@ def main():
     import mi355moe
     mi355moe._lib.lib()
     dev = torch.device("cuda", 0)
-    if args.workload == "prefill":
+    if args.workload in ("prefill", "fp8"):
         args.no_cpu_baseline = True
         res = run_decode(argparse.Namespace(**{**vars(args), "steps": 8, "warmup": 2}), torch, mi355moe, dev)
     else:
@@ -283,6 +348,9 @@ def main():
     if args.workload in ("all", "prefill"):
         log("[bench] prefill ...")
         res.update(run_prefill(args, torch, dev))
+    if args.workload in ("all", "fp8"):
+        log("[bench] fp8 ...")
+        res.update(run_fp8(args, torch, dev))
     print(json.dumps(res), flush=True)
 
 

@@ -142,6 +142,51 @@ Exl3Tables tables(const mi355moe_exl3_layer* L) {
 }
 
 int dt_act(int dt) { return dt == MI355MOE_F16 ? DT_F16 : dt == MI355MOE_BF16 ? DT_BF16 : -1; }
+
+int fp8_layer_ok(const mi355moe_fp8_layer* L) {
+    if (!L || !L->w13 || !L->w13_scale || !L->w2 || !L->w2_scale) return MI355MOE_EINVAL;
+    if (L->n < 1 || L->n > MAX_EXPERTS) return MI355MOE_ELIMIT;
+    if (L->hidden < 256 || L->hidden % 256 || L->intermediate < 128 || L->intermediate % 128)
+        return MI355MOE_ESHAPE;
+    return 0;
+}
+
+struct Fp8Ws {
+    RouteArgs ra;
+    Fp8Args fa;
+    size_t bytes;
+};
+
+// Layout of the e4m3 path's workspace: route tables (64-row segments), quantised activations, SwiGLU output and
+// its quantisation, the fp32 accumulator.
+void carve_fp8(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t N, Fp8Ws& w, int& S_cap) {
+    Carve c(ws);
+    RouteArgs& r = w.ra;
+    Fp8Args& f = w.fa;
+    memset(&r, 0, sizeof(r));
+    memset(&f, 0, sizeof(f));
+    S_cap = (int)(std::min(P, n) + (P + FP8_TM - 1) / FP8_TM);
+    r.tok = c.take<int>(P);
+    r.w16 = c.take<uint16_t>(P);
+    r.w32 = c.take<float>(P);
+    r.pe = c.take<int>(P);
+    r.inv = c.take<int>(P);
+    r.seg_expert = c.take<int>(S_cap);
+    r.seg_row0 = c.take<int>(S_cap);
+    r.seg_rows = c.take<int>(S_cap);
+    r.nseg = c.take<int>(1);
+    r.counts = c.take<int>(n + 1);
+    r.loc = c.take<int>(P);
+    r.blk_cnt = c.take<int>(((P + 1023) / 1024) * (n + 1));
+    r.cnt_out = c.take<int>(n + 1);
+    f.qx = c.take<uint8_t>((size_t)T * K);
+    f.sx = c.take<float>(T);
+    f.a16 = c.take<uint16_t>((size_t)P * N);
+    f.qa = c.take<uint8_t>((size_t)P * N);
+    f.sa = c.take<float>(P);
+    f.out32 = c.take<float>((size_t)T * K);
+    w.bytes = c.off;
+}
 int dt_w(int dt) {
     return dt == MI355MOE_F32 ? DT_F32 : dt == MI355MOE_F16 ? DT_F16 : dt == MI355MOE_BF16 ? DT_BF16 : -1;
 }
@@ -528,4 +573,94 @@ int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int6
     return rc_launch(launch_decode(d, p.rmax, stream, 7));
 }
 
+int mi355moe_fp8_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t K, int64_t x_stride, void* q,
+                            float* scale, hipStream_t stream) {
+    if (!x || !q || !scale) return MI355MOE_EINVAL;
+    if (dt_w(x_dtype) < 0) return MI355MOE_EDTYPE;
+    if (rows < 0 || rows > (1 << 30) || K < 4 || K % 4 || x_stride < K) return MI355MOE_ESHAPE;
+    return rc_launch(launch_quant_rows(x, dt_w(x_dtype), x_stride, (int)rows, (int)K, static_cast<uint8_t*>(q), scale,
+                                       stream));
+}
+
+int64_t mi355moe_fp8_moe_workspace_bytes(const mi355moe_fp8_layer* layer, int64_t T, int64_t topk) {
+    if (fp8_layer_ok(layer) || T < 0 || topk < 1 || topk > MAX_TOPK) return -1;
+    const int64_t P = std::max<int64_t>(1, T * topk);
+    Fp8Ws w;
+    int sc;
+    carve_fp8(nullptr, P, std::max<int64_t>(1, T), layer->n, layer->hidden, layer->intermediate, w, sc);
+    return (int64_t)w.bytes;
+}
+
+int mi355moe_fp8_moe_forward_ids(const mi355moe_fp8_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                 int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                 int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                 int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                 int stages, hipStream_t stream) {
+    if (int r = fp8_layer_ok(layer)) return r;
+    if (!x || !ids || !weights || !out || !workspace) return MI355MOE_EINVAL;
+    if (stages <= 0 || stages > MI355MOE_STAGE_ALL) return MI355MOE_EINVAL;
+    if (dt_w(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;
+    if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
+    const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n;
+    if (T < 0 || topk < 1 || topk > MAX_TOPK) return MI355MOE_ELIMIT;
+    if (x_stride < K || out_stride < K) return MI355MOE_ESHAPE;
+    if (expert_map && n_global < 0) return MI355MOE_EINVAL;
+    const int64_t P = T * topk;
+    if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (T == 0) return 0;
+    Fp8Ws w;
+    int S_cap;
+    carve_fp8(workspace, P, T, n, K, N, w, S_cap);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    if (S_cap > 65535) return MI355MOE_ELIMIT;
+    RouteArgs& r = w.ra;
+    r.ids = ids;
+    r.ids64 = ids_dtype == MI355MOE_I64;
+    r.w = weights;
+    r.wdt = dt_w(weights_dtype);
+    r.emap = expert_map;
+    r.n_global = expert_map ? n_global : 0;
+    r.P = (int)P;
+    r.topk = (int)topk;
+    r.n = (int)n;
+    r.R = 1 << 30;
+    r.seg = FP8_TM;
+    r.S_cap = S_cap;
+    Fp8Args& f = w.fa;
+    f.n = (int)n;
+    f.K = (int)K;
+    f.N = (int)N;
+    f.P = (int)P;
+    f.T = (int)T;
+    f.w13 = static_cast<const uint8_t*>(layer->w13);
+    f.w13s = layer->w13_scale;
+    f.w2 = static_cast<const uint8_t*>(layer->w2);
+    f.w2s = layer->w2_scale;
+    f.x = x;
+    f.xdt = dt_w(x_dtype);
+    f.x_stride = x_stride;
+    f.tok = r.tok;
+    f.w32 = r.w32;
+    f.pe = r.pe;
+    f.seg_expert = r.seg_expert;
+    f.seg_row0 = r.seg_row0;
+    f.seg_rows = r.seg_rows;
+    f.nseg = r.nseg;
+    f.S_cap = S_cap;
+    f.limit = limit;
+    f.out = out;
+    f.odt = dt_w(out_dtype);
+    f.out_stride = out_stride;
+    int kernels = 0;
+    if (stages & MI355MOE_STAGE_ROUTE) {
+        if (int rc = launch_route(r, stream)) return rc_launch(rc);
+        kernels |= 1;
+    }
+    if (stages & MI355MOE_STAGE_GATEUP) kernels |= 2;
+    if (stages & MI355MOE_STAGE_DOWN) kernels |= 4;
+    if (stages & MI355MOE_STAGE_COMBINE) kernels |= 8;
+    return rc_launch(launch_fp8(f, stream, kernels));
+}
+
 }  // extern "C"
+

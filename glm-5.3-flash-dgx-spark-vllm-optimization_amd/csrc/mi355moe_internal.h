@@ -21,6 +21,7 @@ struct RouteArgs {
     // outputs (sorted position order unless noted)
     int* tok;               // [P] token of the pair at pos
     uint16_t* w16;          // [P] fp16 weight bits
+    float* w32;             // optional [P] fp32 weight
     int* pe;                // [P] local expert, -1 = skipped (sentinel or more than R rows)
     int* inv;               // [P] pair j -> pos
     int* seg_expert;        // [S_cap]
@@ -115,6 +116,40 @@ constexpr int PREFILL_TM = 256;
 // kernels: bit 0 zero + gather, bit 1 gate/up, bit 2 down, bit 3 convert to the output dtype
 int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels);
 int prefill_setup();
+
+// The block-scaled e4m3 expert path: per-token e4m3 activations, grouped fp8 MFMA GEMMs over 64-row segments.
+struct Fp8Args {
+    int n, K, N, P, T;
+    const uint8_t* w13;     // [n][2N][K] e4m3, gate rows then up rows
+    const float* w13s;      // [n][2N/128][K/128]
+    const uint8_t* w2;      // [n][K][N] e4m3
+    const float* w2s;       // [n][K/128][N/128]
+    const void* x;
+    int xdt;                // DT_F32, DT_F16 or DT_BF16
+    int64_t x_stride;
+    const int* tok;
+    const float* w32;
+    const int* pe;
+    const int* seg_expert;
+    const int* seg_row0;
+    const int* seg_rows;
+    const int* nseg;
+    int S_cap;
+    float limit;
+    uint8_t* qx;            // [T][K] e4m3 activations
+    float* sx;              // [T] their scales
+    uint16_t* a16;          // [P][N] fp16 SwiGLU output (sorted position order)
+    uint8_t* qa;            // [P][N] e4m3 down inputs
+    float* sa;              // [P]
+    float* out32;           // [T][K] fp32 accumulation
+    void* out;
+    int odt;
+    int64_t out_stride;
+};
+constexpr int FP8_TM = 64;   // rows per segment (two 32-row MFMA tiles)
+// kernels: bit 0 zero + quantize inputs, bit 1 gate/up, bit 2 down-input quantization + down, bit 3 convert
+int launch_fp8(const Fp8Args& a, hipStream_t st, int kernels);
+int launch_quant_rows(const void* x, int xdt, int64_t stride, int rows, int K, uint8_t* q, float* s, hipStream_t st);
 
 int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w, int T, int K, int E, float* logits,
                          hipStream_t st);

@@ -161,6 +161,12 @@ __device__ __forceinline__ uint16_t weight_f16(const void* w, int wdt, int j) {
     return (uint16_t)h_as_u16((_Float16)f);
 }
 
+__device__ __forceinline__ float weight_f32(const void* w, int wdt, int j) {
+    if (wdt == DT_F32) return reinterpret_cast<const float*>(w)[j];
+    if (wdt == DT_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(w)[j]);
+    return (float)u16_as_h(reinterpret_cast<const uint16_t*>(w)[j]);
+}
+
 // block-wide inclusive scan of one int per thread (blockDim.x a multiple of 64, <= 1024)
 __device__ __forceinline__ int block_scan_incl(int v, int* tot, int& total) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -261,6 +267,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
         const int pos = start[l] + rank;
         a.tok[pos] = j / a.topk;
         a.w16[pos] = weight_f16(a.w, a.wdt, j);
+        if (a.w32) a.w32[pos] = weight_f32(a.w, a.wdt, j);
         a.pe[pos] = (l < a.n && cnt[l] <= a.R) ? l : -1;
         a.inv[j] = pos;
     }
@@ -383,6 +390,7 @@ __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
     const int pos = a.blk_cnt[(size_t)blockIdx.x * (a.n + 1) + l] + rank;
     a.tok[pos] = j / a.topk;
     a.w16[pos] = weight_f16(a.w, a.wdt, j);
+    if (a.w32) a.w32[pos] = weight_f32(a.w, a.wdt, j);
     a.pe[pos] = (l < a.n && a.cnt_out[l] <= a.R) ? l : -1;
     a.inv[j] = pos;
 }

@@ -33,6 +33,12 @@ class Exl3LayerDesc(ctypes.Structure):
                 ("down_trellis", _c_p), ("down_suh", _c_p), ("down_svh", _c_p), ("flags", _i64)]
 
 
+class Fp8LayerDesc(ctypes.Structure):
+    """mi355moe_fp8_layer: shape + the block-scaled e4m3 weights and their scales (device pointers)."""
+    _fields_ = [("n", _i64), ("hidden", _i64), ("intermediate", _i64),
+                ("w13", _c_p), ("w13_scale", _c_p), ("w2", _c_p), ("w2_scale", _c_p)]
+
+
 class MoeError(RuntimeError):
     """A call into libmi355moe.so was rejected (argument check) or failed to launch."""
 
@@ -62,6 +68,10 @@ _SIGS = {
                                            _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int, _int,
                                            _c_p]),
     "mi355moe_exl3_moe_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64]),
+    "mi355moe_fp8_quant_rows": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _c_p]),
+    "mi355moe_fp8_moe_workspace_bytes": (_i64, [ctypes.POINTER(Fp8LayerDesc), _i64, _i64]),
+    "mi355moe_fp8_moe_forward_ids": (_int, [ctypes.POINTER(Fp8LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int, _c_p,
+                                            _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int, _c_p]),
     "mi355moe_exl3_moe": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _i64,
                                  _int, _int, _int, _int, _int, _int, _int, _int, _int, _int, _f, _c_p, _sz, _c_p]),
 }

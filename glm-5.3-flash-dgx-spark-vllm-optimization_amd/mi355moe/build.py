@@ -16,7 +16,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _PKG_ROOT = os.path.dirname(_HERE)
 CSRC = os.path.join(_PKG_ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(_PKG_ROOT), "include")
-SOURCES = ["abi.hip", "route.hip", "decode.hip", "prefill.hip", "e4m3.hip"]
+SOURCES = ["abi.hip", "route.hip", "decode.hip", "prefill.hip", "fp8.hip"]
 OUT = os.path.join(_HERE, "libmi355moe.so")
 ARCH = "gfx950"
 

@@ -47,6 +47,39 @@ def exl3_layer(n: int, K: int, N: int, seed: int, device="cuda", svh_scale: floa
     return Exl3Experts(w13_trellis, w13_suh, w13_svh, w2_trellis, w2_suh, w2_svh)
 
 
+def block_quant_e4m3(w: torch.Tensor, block: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
+    """e4m3 codes (uint8) and fp32 scales of float32 matrices [..., R, C] with one scale per block x block tile:
+    s = amax(tile) / 448 (1 if 0), codes = e4m3(clamp(w / s, -448, 448))."""
+    *lead, R, C = w.shape
+    wb = w.reshape(*lead, R // block, block, C // block, block)
+    s = wb.abs().amax(dim=(-3, -1)) / 448.0
+    s = torch.where(s > 0, s, torch.ones_like(s))
+    q = (wb / s[..., :, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.view(torch.uint8).reshape(w.shape), s.to(torch.float32).contiguous()
+
+
+def fp8_layer(n: int, K: int, N: int, seed: int, device="cuda", std: float = 0.02):
+    """One layer of n block-scaled e4m3 experts (the e4m3 expert configuration): weights N(0, std), quantised per
+    128x128 block (fp32 scale = block amax / 448). Returns mi355moe.fp8.Fp8Experts."""
+    from .fp8 import Fp8Experts
+    device = torch.device(device)
+    g = _gen(seed, device)
+    w13 = torch.empty(n, 2 * N, K, dtype=torch.uint8, device=device)
+    w2 = torch.empty(n, K, N, dtype=torch.uint8, device=device)
+    s13 = torch.empty(n, 2 * N // 128, K // 128, dtype=torch.float32, device=device)
+    s2 = torch.empty(n, K // 128, N // 128, dtype=torch.float32, device=device)
+    step = max(1, min(n, 16))
+    for e0 in range(0, n, step):
+        e1 = min(n, e0 + step)
+        q, s = block_quant_e4m3(torch.randn(e1 - e0, 2 * N, K, generator=g, device=device) * std)
+        w13[e0:e1].copy_(q)
+        s13[e0:e1].copy_(s)
+        q, s = block_quant_e4m3(torch.randn(e1 - e0, K, N, generator=g, device=device) * std)
+        w2[e0:e1].copy_(q)
+        s2[e0:e1].copy_(s)
+    return Fp8Experts(w13, s13, w2, s2)
+
+
 def router(E: int, K: int, seed: int, device="cuda") -> tuple[torch.Tensor, torch.Tensor]:
     """(W bf16 [E, K] ~ N(0, 0.02), e_score_correction_bias fp32 [E] ~ N(0, 0.01))."""
     device = torch.device(device)

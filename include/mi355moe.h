@@ -147,6 +147,38 @@ int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int6
                       int gate_mul1, int up_mcg, int up_mul1, int down_mcg, int down_mul1, float act_limit,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---------------------------------------------------------------- e4m3 expert variant */
+
+/* One layer of block-scaled e4m3 routed experts in vLLM's fp8 w8a8 block-quantised MoE layout (128x128 blocks):
+ * the weight the GEMM sees is e4m3(w) * scale[block]. */
+typedef struct mi355moe_fp8_layer {
+    int64_t n, hidden, intermediate;
+    const void* w13;        /* e4m3 [n][2*intermediate][hidden]: rows 0..I-1 gate, I..2I-1 up */
+    const float* w13_scale; /* [n][2*intermediate/128][hidden/128] */
+    const void* w2;         /* e4m3 [n][hidden][intermediate] */
+    const float* w2_scale;  /* [n][hidden/128][intermediate/128] */
+} mi355moe_fp8_layer;
+
+/* Per-row dynamic e4m3 quantisation: s[r] = amax(|x[r]|) / 448 (1 if 0), q[r] = e4m3_rn(clamp(x[r] / s[r],
+ * -448, 448)), IEEE divisions. Replaces the reference's activation quantisers gather_tok / actq
+ * (code/fork/kernels/moe_e4m3.cu:152-176, :245-310, :440-488; spec glm53_moe_e4m3.py:648-652). x: F32, F16 or
+ * BF16 [rows][x_stride]; q uint8 [rows][K]; K % 4 == 0. */
+int mi355moe_fp8_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t K, int64_t x_stride, void* q,
+                            float* scale, hipStream_t stream);
+
+/* Routed-expert output of a block-scaled e4m3 layer from router ids and weights (the e4m3 expert path,
+ * code/fork/overlay/glm53_moe_e4m3.py:484-592 -> moe_e4m3.cu fused, :3081-3096): activations quantised per
+ * token, SwiGLU a16 = fp16(silu(min(g, L)) * clamp(u, -L, L)) (iff L != 0), a16 requantised per row, down GEMM,
+ * fp32 scatter-add of w * y, out in out_dtype. hidden % 256 == 0, intermediate % 128 == 0; T * topk <= 65536.
+ * stages: the MI355MOE_STAGE_* mask (ROUTE = permutation and input quantisation, GATEUP, DOWN = requantisation and
+ * down GEMM, COMBINE = output conversion). */
+int64_t mi355moe_fp8_moe_workspace_bytes(const mi355moe_fp8_layer* layer, int64_t T, int64_t topk);
+int mi355moe_fp8_moe_forward_ids(const mi355moe_fp8_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                 int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                 int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                 int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                 int stages, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
