@@ -71,73 +71,75 @@ __global__ __launch_bounds__(1024) void router_logits_kernel(const uint16_t* __r
 
 // ------------------------------------------------------------------------------------------------ router top-k
 
-constexpr int TOPK_MAX_E = 1024;   // experts per token row (16 per lane)
+constexpr int TOPK_MAX_E = 1024;   // experts per token row
 constexpr int TOPK_MAX_K = 32;
 
-__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T, int E,
-                                                          const float* __restrict__ bias, int topk, float scale,
-                                                          int renorm, int32_t* __restrict__ ids,
-                                                          float* __restrict__ wts) {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T) return;
-    constexpr int PER = TOPK_MAX_E / 64;
-    float sc[PER], ch[PER];
-    const int per = (E + 63) / 64;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int e = i * 64 + lane;
-        sc[i] = 0.f;
-        ch[i] = -__builtin_inff();
-        if (i < per && e < E) {
+// grid T, 1024 threads per token: scores s = sigmoid(logit) (through double exp) and choice keys s + bias go to
+// LDS; every candidate's rank = the number of candidates with a larger key, or an equal key and a lower id (ranks
+// are distinct and follow the reference's order: largest first, lower id on ties). Q = 1024 / E16 threads share a
+// candidate, each counting over a slice of the keys; the topk lowest ranks write themselves to their slot and the
+// renormalising total is summed sequentially in pick order.
+__global__ __launch_bounds__(1024) void router_topk_kernel(const float* __restrict__ logits, int T, int E,
+                                                           const float* __restrict__ bias, int topk, float scale,
+                                                           int renorm, int32_t* __restrict__ ids,
+                                                           float* __restrict__ wts) {
+    __shared__ __align__(16) float key[TOPK_MAX_E];
+    __shared__ float sco[TOPK_MAX_E];
+    __shared__ int part[1024];
+    __shared__ int pick_e[TOPK_MAX_K];
+    __shared__ float pick_s[TOPK_MAX_K];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int E16 = (E + 15) & ~15;                                  // keys padded with -inf (never ahead of a key)
+    for (int e = tid; e < E16; e += 1024) {
+        float sv = 0.f, kv = -__builtin_inff();
+        if (e < E) {
             const float lg = logits[(size_t)t * E + e];
-            sc[i] = (float)(1.0 / (1.0 + exp(-(double)lg)));
-            ch[i] = sc[i] + (bias ? bias[e] : 0.f);
+            sv = (float)(1.0 / (1.0 + exp(-(double)lg)));
+            kv = sv + (bias ? bias[e] : 0.f);
         }
+        sco[e] = sv;
+        key[e] = kv;
     }
-    float total = 0.f;
-    float picked_s = 0.f;
-    int picked_e = 0;
-    for (int k = 0; k < topk; ++k) {
-        float bv = -__builtin_inff();
-        int be = 0x7FFFFFFF;
-        float bs = 0.f;
+    __syncthreads();
+    const int Q = E16 <= 256 ? 4 : (E16 <= 512 ? 2 : 1);
+    const int c = tid / Q, p = tid - c * Q;
+    const int slice = E16 / Q;                                       // a multiple of 4 (E16 % 16 == 0)
+    int greater = 0, tie = 0;
+    if (c < E) {
+        const float v = key[c];
+        const f32x4* k4 = reinterpret_cast<const f32x4*>(key + p * slice);
+        int equal = 0;
+        for (int j4 = 0; j4 < slice / 4; ++j4) {
+            const f32x4 u = k4[j4];
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int e = i * 64 + lane;
-            if (i < per && e < E && (ch[i] > bv || (ch[i] == bv && e < be))) {
-                bv = ch[i];
-                be = e;
-                bs = sc[i];
+            for (int i = 0; i < 4; ++i) {
+                greater += u[i] > v;
+                equal += u[i] == v;
             }
         }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = __shfl_xor(bv, m, 64);
-            const int oe = __shfl_xor(be, m, 64);
-            const float os = __shfl_xor(bs, m, 64);
-            if (ov > bv || (ov == bv && oe < be)) {
-                bv = ov;
-                be = oe;
-                bs = os;
-            }
-        }
-        // be is the same on every lane; the owner drops it from the candidates
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (i * 64 + lane == be) ch[i] = -__builtin_inff();
-        total = total + bs;
-        if (lane == k) {
-            picked_s = bs;
-            picked_e = be;
+        if (c >= p * slice && c < p * slice + slice) --equal;       // the candidate itself
+        if (equal)                                                   // rare: equal keys, lower ids come first
+            for (int j = p * slice; j < p * slice + slice && j < c; ++j) tie += key[j] == v;
+    }
+    part[tid] = greater + tie;
+    __syncthreads();
+    if (p == 0 && c < E) {
+        int rank = 0;
+        for (int i = 0; i < Q; ++i) rank += part[tid + i];
+        if (rank < topk) {
+            pick_e[rank] = c;
+            pick_s[rank] = sco[c];
         }
     }
-    if (lane < topk) {
-        float wv = picked_s;
+    __syncthreads();
+    if (tid < topk) {
+        float total = 0.f;
+        for (int k = 0; k < topk; ++k) total = total + pick_s[k];
+        float wv = pick_s[tid];
         if (renorm) wv = __fdiv_rn(wv, total + 1e-20f);
         wv = wv * scale;
-        ids[(size_t)t * topk + lane] = picked_e;
-        wts[(size_t)t * topk + lane] = wv;
+        ids[(size_t)t * topk + tid] = pick_e[tid];
+        wts[(size_t)t * topk + tid] = wv;
     }
 }
 
@@ -405,8 +407,9 @@ int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w,
 
 int launch_router_topk(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
                        int32_t* ids, float* wts, hipStream_t st) {
-    hipLaunchKernelGGL(router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, st, logits, T, E, bias, topk, scale,
-                       renorm, ids, wts);
+    if (T > 0)
+        hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(1024), 0, st, logits, T, E, bias, topk, scale, renorm,
+                           ids, wts);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
