@@ -148,6 +148,7 @@ int fp8_layer_ok(const mi355moe_fp8_layer* L) {
     if (L->n < 1 || L->n > MAX_EXPERTS) return MI355MOE_ELIMIT;
     if (L->hidden < 256 || L->hidden % 256 || L->intermediate < 128 || L->intermediate % 128)
         return MI355MOE_ESHAPE;
+    if (L->hidden > 16384 || L->intermediate > 16384) return MI355MOE_ELIMIT;
     return 0;
 }
 
@@ -158,7 +159,7 @@ struct Fp8Ws {
 };
 
 // Layout of the e4m3 path's workspace: route tables (64-row segments), quantised activations, SwiGLU output and
-// its quantisation, the fp32 accumulator.
+// its quantisation, the per-pair fp32 contributions.
 void carve_fp8(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t N, Fp8Ws& w, int& S_cap) {
     Carve c(ws);
     RouteArgs& r = w.ra;
@@ -184,7 +185,7 @@ void carve_fp8(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t N, 
     f.a16 = c.take<uint16_t>((size_t)P * N);
     f.qa = c.take<uint8_t>((size_t)P * N);
     f.sa = c.take<float>(P);
-    f.out32 = c.take<float>((size_t)T * K);
+    f.contrib = c.take<float>((size_t)P * K);
     w.bytes = c.off;
 }
 int dt_w(int dt) {
@@ -334,7 +335,7 @@ void carve_prefill(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t
     r.cnt_out = c.take<int>(n + 1);
     d.h13 = c.take<uint16_t>((size_t)P * K);
     d.h2 = c.take<uint16_t>((size_t)P * N);
-    d.out32 = c.take<float>((size_t)T * K);
+    d.contrib = c.take<float>((size_t)P * K);
     w.bytes = c.off;
 }
 
@@ -421,6 +422,8 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
         d.tok = r.tok;
         d.w16 = r.w16;
         d.pe = r.pe;
+        d.inv = r.inv;
+        d.topk = (int)topk;
         d.seg_expert = r.seg_expert;
         d.seg_row0 = r.seg_row0;
         d.seg_rows = r.seg_rows;
@@ -603,7 +606,7 @@ int mi355moe_fp8_moe_forward_ids(const mi355moe_fp8_layer* layer, const void* x,
     if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
     const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n;
     if (T < 0 || topk < 1 || topk > MAX_TOPK) return MI355MOE_ELIMIT;
-    if (x_stride < K || out_stride < K) return MI355MOE_ESHAPE;
+    if (x_stride < K || out_stride < K || out_stride % 2) return MI355MOE_ESHAPE;
     if (expert_map && n_global < 0) return MI355MOE_EINVAL;
     const int64_t P = T * topk;
     if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
@@ -642,6 +645,8 @@ int mi355moe_fp8_moe_forward_ids(const mi355moe_fp8_layer* layer, const void* x,
     f.tok = r.tok;
     f.w32 = r.w32;
     f.pe = r.pe;
+    f.inv = r.inv;
+    f.topk = (int)topk;
     f.seg_expert = r.seg_expert;
     f.seg_row0 = r.seg_row0;
     f.seg_rows = r.seg_rows;

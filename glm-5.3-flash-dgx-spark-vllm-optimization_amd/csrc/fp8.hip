@@ -8,14 +8,16 @@
 //   gate/up  acc = sum over 128-k blocks b of (sum_{k in b} q_x[k] * W8[n][k]) * ws[n/128][b]  (fp8 MFMA, fp32
 //            accumulate); g = acc * s_x, u likewise; a16 = fp16(silu(min(g, L)) * clamp(u, -L, L)) (iff L != 0),
 //            silu(v) = v / (1 + (float)exp(-(double)v))
-//   down     q_a, s_a = quant(a16 row); y = (same GEMM with the down scales) * s_a; out[token] += w * y (fp32 atomics)
+//   down     q_a, s_a = quant(a16 row); y = (same GEMM with the down scales) * s_a; contribution w * y per pair;
+//            out[token] = the token's contributions summed in slot order (fp32), then the output dtype
 //
 // Work decomposition: a workgroup (4 waves) owns one 64-row segment of one expert and 128 output columns; wave w
 // owns 32 of them for both 32-row tiles (and, in gate/up, for gate and up, so the SwiGLU is local to the lane).
-// Per 128-k block every lane loads 64 contiguous bytes of its weight row and of each of its two activation rows:
-// lane half h = lane/32 holds k 64h..64h+63, and v_mfma_scale_f32_32x32x64_f8f6f4 #1 takes the first 32 of those
-// bytes, #2 the last 32 (the same k assignment for both operands, so the dot products are the block's). The block
-// sum is scaled by its weight scale in fp32 before it joins the accumulator. Loads run one block ahead.
+// Per 128-k block the workgroup stages its weight rows and activation rows in LDS with asynchronous
+// global-to-LDS loads (three stages, two blocks in flight), each wave instruction reading whole 128-byte lines;
+// lane half h = lane/32 then takes k 64h..64h+63 of its row from LDS, and v_mfma_scale_f32_32x32x64_f8f6f4 #1
+// multiplies the first 32 of those bytes, #2 the last 32 (the same k assignment for both operands, so the dot
+// products are the block's). The block sum is scaled by its weight scale in fp32 before it joins the accumulator.
 #include "common.cuh"
 #include "mi355moe_internal.h"
 
@@ -78,7 +80,32 @@ __device__ __forceinline__ f32x16 mfma_fp8(const u32x4& a0, const u32x4& a1, con
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
-// The 128-k block sum of one 32x32 tile from 64-byte chunks (A rows, B columns), times its block scale, added to acc.
+// Staging of one 128-k block of a workgroup tile in LDS: row R of the tile holds its 128 bytes as eight 16-byte
+// chunks, chunk g at slot g ^ swz(R). The swizzle is applied through the load addresses (global_load_lds writes
+// lane l of a wave instruction to slot l % 8 of row l / 8), so every wave instruction reads eight whole 128-byte
+// lines, and the fragment reads below (32 consecutive rows, one chunk each) are free of bank conflicts.
+__device__ __forceinline__ int swz(int R) { return (R >> 1) & 7; }
+
+// Wave instruction: 64 lanes x 16 bytes, lane l -> LDS bytes lds_wave + 16 l (rows of 128 bytes: row l / 8, slot
+// l % 8). Written as inline assembly so the compiler adds no wait of its own for these loads: the kernels wait for
+// them explicitly (WAIT_VM) before the barrier that publishes a stage, and issue no other global loads while any
+// are in flight.
+__device__ __forceinline__ void dma16(const uint8_t* src_lane, unsigned char* lds_wave) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src_lane)
+                 : "memory", "m0");
+}
+
+// The 64 bytes of row R at k half h (chunks 4h..4h+3) as four 16-byte LDS reads.
+__device__ __forceinline__ void frag64(const unsigned char* st, int R, int h, u32x4 (&v)[4]) {
+    const unsigned char* row = st + R * 128;
+    const int sw = swz(R);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const u32x4*>(row + (((4 * h + i) ^ sw) << 4));
+}
+
+// The 128-k block sum of one 32x32 tile from 64-byte fragments (A rows, B columns), times its block scale, added
+// to acc. MFMA #1 takes each lane's first 32 bytes, #2 the last 32: the same k assignment for both operands.
 __device__ __forceinline__ void block_acc(const u32x4 (&xa)[4], const u32x4 (&wb)[4], float ws, f32x16& acc) {
     f32x16 p = {};
     p = mfma_fp8(xa[0], xa[1], wb[0], wb[1], p);
@@ -87,71 +114,90 @@ __device__ __forceinline__ void block_acc(const u32x4 (&xa)[4], const u32x4 (&wb
     for (int i = 0; i < 16; ++i) acc[i] += p[i] * ws;
 }
 
-typedef __attribute__((address_space(1))) const u32x4 gu32x4_f8;
-__device__ __forceinline__ void ld64_stream(const uint8_t* p, u32x4 (&v)[4]) {
-    const gu32x4_f8* q = reinterpret_cast<gu32x4_f8*>(reinterpret_cast<uintptr_t>(p));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __builtin_nontemporal_load(q + i);
-}
-__device__ __forceinline__ void ld64(const uint8_t* p, u32x4 (&v)[4]) {
-    const u32x4* q = reinterpret_cast<const u32x4*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = q[i];
-}
-
 // Accumulator layout of a 32x32 tile: lane l holds column l % 32, register r row 8 (r / 4) + 4 (l / 32) + r % 4.
 __device__ __forceinline__ int tile_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
+// s_waitcnt vmcnt(n) lgkmcnt(0) (n <= 15): this wave's staged loads up to the one n before the last have landed in
+// LDS, and its LDS reads of the buffer about to be refilled have returned
+#define WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0070 | (n))
+#define LDS_BARRIER() asm volatile("s_barrier" ::: "memory")
+
+constexpr int FP8_MAX_KB = 128;           // 128-k blocks per row (hidden and intermediate <= 16384)
+constexpr int GU_ROWS = 320;              // 128 gate + 128 up weight rows + 64 activation rows per stage
+constexpr int GU_INST = GU_ROWS / 8 / 4;  // wave instructions per stage per wave (10)
+constexpr int DN_ROWS = 192;              // 128 weight rows + 64 activation rows
+constexpr int DN_INST = DN_ROWS / 8 / 4;  // 6
+
 // grid (N/128, segments), 256 threads: the 64-row segment's gate and up outputs of 128 columns, SwiGLU -> a16.
+// Three LDS stages of 40 KB; the loads for block kb + 2 are issued while block kb is multiplied.
 __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
+    __shared__ __align__(16) unsigned char st0[GU_ROWS * 128];
+    __shared__ __align__(16) unsigned char st1[GU_ROWS * 128];
+    __shared__ __align__(16) unsigned char st2[GU_ROWS * 128];
+    __shared__ float scl[2 * FP8_MAX_KB];
     const int cb = blockIdx.x, s = blockIdx.y;
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int K = a.K, N = a.N, h = lane >> 5, c = lane & 31;
-    const int col = cb * 128 + wv * 32 + c;
-    const uint8_t* wg = a.w13 + ((size_t)e * 2 * N + col) * K + 64 * h;
-    const uint8_t* wu = wg + (size_t)N * K;
-    const uint8_t* x0 = a.qx + (size_t)a.tok[row0 + min(c, rn - 1)] * K + 64 * h;
-    const uint8_t* x1 = a.qx + (size_t)a.tok[row0 + min(32 + c, rn - 1)] * K + 64 * h;
+    const int K = a.K, N = a.N;
     const int nkb = K >> 7;
-    const float* sg = a.w13s + ((size_t)e * (2 * N / 128) + cb) * nkb;
-    const float* su = a.w13s + ((size_t)e * (2 * N / 128) + N / 128 + cb) * nkb;
 
+    // this lane's source rows for its ten stage instructions (swizzled chunk offset included)
+    const uint8_t* src[GU_INST];
+#pragma unroll
+    for (int j = 0; j < GU_INST; ++j) {
+        const int R = wv * (GU_INST * 8) + j * 8 + (lane >> 3);
+        const uint8_t* rowp;
+        if (R < 128) rowp = a.w13 + ((size_t)e * 2 * N + cb * 128 + R) * K;
+        else if (R < 256) rowp = a.w13 + ((size_t)e * 2 * N + N + cb * 128 + (R - 128)) * K;
+        else rowp = a.qx + (size_t)a.tok[row0 + min(R - 256, rn - 1)] * K;
+        src[j] = rowp + (((lane & 7) ^ swz(R)) << 4);
+    }
+    const int ldsw = wv * (GU_INST * 8) * 128;                       // this wave's first stage row
+    auto issue = [&](unsigned char* st, int kb) {
+#pragma unroll
+        for (int j = 0; j < GU_INST; ++j) dma16(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+    };
+
+    // the block scales of this column block (gate then up) go to LDS before any staged load is issued, so the
+    // loop reads no global memory of its own
+    for (int i = threadIdx.x; i < 2 * nkb; i += 256)
+        scl[i] = a.w13s[((size_t)e * (2 * N / 128) + (i < nkb ? 0 : N / 128) + cb) * nkb + (i < nkb ? i : i - nkb)];
+    __syncthreads();
+    const int h = lane >> 5, c = lane & 31;
     f32x16 g0 = {}, g1 = {}, u0 = {}, u1 = {};
-    u32x4 Ag[4], Au[4], Ax0[4], Ax1[4], Bg[4], Bu[4], Bx0[4], Bx1[4];
-    ld64_stream(wg, Ag);
-    ld64_stream(wu, Au);
-    ld64(x0, Ax0);
-    ld64(x1, Ax1);
-    for (int kb = 0; kb < nkb; kb += 2) {
-        const size_t o1 = (size_t)min(kb + 1, nkb - 1) * 128, o2 = (size_t)min(kb + 2, nkb - 1) * 128;
-        ld64_stream(wg + o1, Bg);
-        ld64_stream(wu + o1, Bu);
-        ld64(x0 + o1, Bx0);
-        ld64(x1 + o1, Bx1);
-        __builtin_amdgcn_sched_barrier(0);
-        block_acc(Ax0, Ag, sg[kb], g0);
-        block_acc(Ax1, Ag, sg[kb], g1);
-        block_acc(Ax0, Au, su[kb], u0);
-        block_acc(Ax1, Au, su[kb], u1);
-        __builtin_amdgcn_sched_barrier(0);
-        ld64_stream(wg + o2, Ag);
-        ld64_stream(wu + o2, Au);
-        ld64(x0 + o2, Ax0);
-        ld64(x1 + o2, Ax1);
-        __builtin_amdgcn_sched_barrier(0);
-        if (kb + 1 < nkb) {
-            block_acc(Bx0, Bg, sg[kb + 1], g0);
-            block_acc(Bx1, Bg, sg[kb + 1], g1);
-            block_acc(Bx0, Bu, su[kb + 1], u0);
-            block_acc(Bx1, Bu, su[kb + 1], u1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+    auto compute = [&](const unsigned char* st, int kb) {
+        u32x4 wg[4], wu[4], x0[4], x1[4];
+        frag64(st, wv * 32 + c, h, wg);
+        frag64(st, 128 + wv * 32 + c, h, wu);
+        frag64(st, 256 + c, h, x0);
+        frag64(st, 288 + c, h, x1);
+        const float fg = scl[kb], fu = scl[nkb + kb];
+        block_acc(x0, wg, fg, g0);
+        block_acc(x1, wg, fg, g1);
+        block_acc(x0, wu, fu, u0);
+        block_acc(x1, wu, fu, u1);
+    };
+    // one pipeline step on stage buffer `cur` (block kb): wait for it, barrier, refill `nxt` (the buffer read in
+    // the previous step) with block kb + 2, multiply
+    auto step = [&](unsigned char* cur, unsigned char* nxt, int kb) {
+        if (kb + 1 < nkb) WAIT_VM(GU_INST);
+        else WAIT_VM(0);
+        LDS_BARRIER();
+        if (kb + 2 < nkb) issue(nxt, kb + 2);
+        compute(cur, kb);
+    };
+    issue(st0, 0);
+    if (nkb > 1) issue(st1, 1);
+    for (int kb = 0; kb < nkb; kb += 3) {
+        step(st0, st2, kb);
+        if (kb + 1 < nkb) step(st1, st0, kb + 1);
+        if (kb + 2 < nkb) step(st2, st1, kb + 2);
     }
 
     const float L = a.limit;
+    const int col = cb * 128 + wv * 32 + c;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -172,46 +218,65 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     }
 }
 
-// grid (K/128, segments), 256 threads: the segment's down outputs of 128 columns, scattered with fp32 atomics.
+// grid (K/128, segments), 256 threads: the segment's down outputs of 128 columns, stored as each pair's weighted
+// contribution (the combine adds a token's contributions in slot order).
+// Three LDS stages of 24 KB.
 __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
+    __shared__ __align__(16) unsigned char st0[DN_ROWS * 128];
+    __shared__ __align__(16) unsigned char st1[DN_ROWS * 128];
+    __shared__ __align__(16) unsigned char st2[DN_ROWS * 128];
+    __shared__ float scl[FP8_MAX_KB];
     const int cb = blockIdx.x, s = blockIdx.y;
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int K = a.K, N = a.N, h = lane >> 5, c = lane & 31;
-    const int col = cb * 128 + wv * 32 + c;
-    const uint8_t* wd = a.w2 + ((size_t)e * K + col) * N + 64 * h;
-    const uint8_t* x0 = a.qa + (size_t)(row0 + min(c, rn - 1)) * N + 64 * h;
-    const uint8_t* x1 = a.qa + (size_t)(row0 + min(32 + c, rn - 1)) * N + 64 * h;
+    const int K = a.K, N = a.N;
     const int nkb = N >> 7;
-    const float* sd = a.w2s + ((size_t)e * (K / 128) + cb) * nkb;
 
+    const uint8_t* src[DN_INST];
+#pragma unroll
+    for (int j = 0; j < DN_INST; ++j) {
+        const int R = wv * (DN_INST * 8) + j * 8 + (lane >> 3);
+        const uint8_t* rowp;
+        if (R < 128) rowp = a.w2 + ((size_t)e * K + cb * 128 + R) * N;
+        else rowp = a.qa + (size_t)(row0 + min(R - 128, rn - 1)) * N;
+        src[j] = rowp + (((lane & 7) ^ swz(R)) << 4);
+    }
+    const int ldsw = wv * (DN_INST * 8) * 128;
+    auto issue = [&](unsigned char* st, int kb) {
+#pragma unroll
+        for (int j = 0; j < DN_INST; ++j) dma16(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+    };
+    for (int i = threadIdx.x; i < nkb; i += 256) scl[i] = a.w2s[((size_t)e * (K / 128) + cb) * nkb + i];
+    __syncthreads();
+    const int h = lane >> 5, c = lane & 31;
     f32x16 d0 = {}, d1 = {};
-    u32x4 Aw[4], Ax0[4], Ax1[4], Bw[4], Bx0[4], Bx1[4];
-    ld64_stream(wd, Aw);
-    ld64(x0, Ax0);
-    ld64(x1, Ax1);
-    for (int kb = 0; kb < nkb; kb += 2) {
-        const size_t o1 = (size_t)min(kb + 1, nkb - 1) * 128, o2 = (size_t)min(kb + 2, nkb - 1) * 128;
-        ld64_stream(wd + o1, Bw);
-        ld64(x0 + o1, Bx0);
-        ld64(x1 + o1, Bx1);
-        __builtin_amdgcn_sched_barrier(0);
-        block_acc(Ax0, Aw, sd[kb], d0);
-        block_acc(Ax1, Aw, sd[kb], d1);
-        __builtin_amdgcn_sched_barrier(0);
-        ld64_stream(wd + o2, Aw);
-        ld64(x0 + o2, Ax0);
-        ld64(x1 + o2, Ax1);
-        __builtin_amdgcn_sched_barrier(0);
-        if (kb + 1 < nkb) {
-            block_acc(Bx0, Bw, sd[kb + 1], d0);
-            block_acc(Bx1, Bw, sd[kb + 1], d1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+    auto compute = [&](const unsigned char* st, int kb) {
+        u32x4 wd[4], x0[4], x1[4];
+        frag64(st, wv * 32 + c, h, wd);
+        frag64(st, 128 + c, h, x0);
+        frag64(st, 160 + c, h, x1);
+        const float fd = scl[kb];
+        block_acc(x0, wd, fd, d0);
+        block_acc(x1, wd, fd, d1);
+    };
+    auto step = [&](unsigned char* cur, unsigned char* nxt, int kb) {
+        if (kb + 1 < nkb) WAIT_VM(DN_INST);
+        else WAIT_VM(0);
+        LDS_BARRIER();
+        if (kb + 2 < nkb) issue(nxt, kb + 2);
+        compute(cur, kb);
+    };
+    issue(st0, 0);
+    if (nkb > 1) issue(st1, 1);
+    for (int kb = 0; kb < nkb; kb += 3) {
+        step(st0, st2, kb);
+        if (kb + 1 < nkb) step(st1, st0, kb + 1);
+        if (kb + 2 < nkb) step(st2, st1, kb + 2);
     }
 
+    const int col = cb * 128 + wv * 32 + c;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -221,25 +286,33 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
                 const int pos = row0 + row;
                 if (a.pe[pos] < 0) continue;                         // a row whose token id was out of range
                 const float y = (t ? d1[r] : d0[r]) * a.sa[pos];
-                atomicAdd(a.out32 + (size_t)a.tok[pos] * K + col, a.w32[pos] * y);
+                a.contrib[(size_t)pos * K + col] = a.w32[pos] * y;
             }
         }
     }
 }
 
-__global__ __launch_bounds__(256) void fp8_zero_kernel(float* __restrict__ p, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.f;
-}
-
-__global__ __launch_bounds__(256) void fp8_convert_kernel(const float* __restrict__ src, int T, int K, void* dst,
-                                                          int odt, int64_t stride) {
-    const int64_t n = (int64_t)T * K;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-        const int64_t t = i / K, c = i - t * K;
-        const float v = src[i];
-        if (odt == DT_F32) reinterpret_cast<float*>(dst)[t * stride + c] = v;
-        else if (odt == DT_BF16) reinterpret_cast<uint16_t*>(dst)[t * stride + c] = f32_to_bf16(v);
-        else reinterpret_cast<_Float16*>(dst)[t * stride + c] = (_Float16)v;
+// grid (T, K/256), 128 threads x 2 columns: out[t] = sum over the token's slots k (in order) of the valid pairs'
+// contributions, converted to the output dtype (deterministic: no atomics).
+__global__ __launch_bounds__(128) void fp8_combine_kernel(Fp8Args a) {
+    const int t = blockIdx.x;
+    const int col = blockIdx.y * 256 + 2 * threadIdx.x;
+    float s0 = 0.f, s1 = 0.f;
+    for (int k = 0; k < a.topk; ++k) {
+        const int pos = a.inv[t * a.topk + k];
+        if (a.pe[pos] < 0) continue;
+        const float2 c = *reinterpret_cast<const float2*>(a.contrib + (size_t)pos * a.K + col);
+        s0 += c.x;
+        s1 += c.y;
+    }
+    const size_t o = (size_t)t * a.out_stride + col;
+    if (a.odt == DT_F32) {
+        *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.out) + o) = make_float2(s0, s1);
+    } else if (a.odt == DT_BF16) {
+        const uint32_t v = (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + o) = v;
+    } else {
+        *reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o) = h2{(_Float16)s0, (_Float16)s1};
     }
 }
 
@@ -251,21 +324,16 @@ int launch_quant_rows(const void* x, int xdt, int64_t stride, int rows, int K, u
 }
 
 int launch_fp8(const Fp8Args& a, hipStream_t st, int kernels) {
-    const int64_t tk = (int64_t)a.T * a.K;
-    const unsigned gz = (unsigned)std::max<int64_t>(1, std::min<int64_t>((tk + 255) / 256, 8192));
-    if (kernels & 1) {
-        hipLaunchKernelGGL(fp8_zero_kernel, dim3(gz), dim3(256), 0, st, a.out32, tk);
+    if (kernels & 1)
         if (a.T > 0) hipLaunchKernelGGL(quant_rows_kernel, dim3(a.T), dim3(256), 0, st, a.x, a.xdt, a.x_stride, a.K,
                                         a.qx, a.sx);
-    }
     if (kernels & 2) hipLaunchKernelGGL(fp8_gateup_kernel, dim3(a.N / 128, a.S_cap), dim3(256), 0, st, a);
     if (kernels & 4) {
         hipLaunchKernelGGL(quant_rows_kernel, dim3(a.P), dim3(256), 0, st, (const void*)a.a16, (int)DT_F16,
                            (int64_t)a.N, a.N, a.qa, a.sa);
         hipLaunchKernelGGL(fp8_down_kernel, dim3(a.K / 128, a.S_cap), dim3(256), 0, st, a);
     }
-    if (kernels & 8) hipLaunchKernelGGL(fp8_convert_kernel, dim3(gz), dim3(256), 0, st, a.out32, a.T, a.K, a.out,
-                                        a.odt, a.out_stride);
+    if (kernels & 8) hipLaunchKernelGGL(fp8_combine_kernel, dim3(a.T, a.K / 256), dim3(128), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -106,14 +106,16 @@ struct PrefillArgs {
     float limit;
     uint16_t* h13;          // [P][K] rotated gate/up inputs
     uint16_t* h2;           // [P][N] rotated down inputs
-    float* out32;           // [T][K] fp32 accumulation
+    float* contrib;         // [P][K] per-pair weighted contribution (sorted position order)
+    const int* inv;         // [P] pair j -> sorted position
+    int topk;
     void* out;
     int odt;
     int64_t out_stride;
 };
 constexpr int PREFILL_TM = 256;
 
-// kernels: bit 0 zero + gather, bit 1 gate/up, bit 2 down, bit 3 convert to the output dtype
+// kernels: bit 0 gather, bit 1 gate/up, bit 2 down, bit 3 slot-order combine into the output dtype
 int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels);
 int prefill_setup();
 
@@ -141,13 +143,15 @@ struct Fp8Args {
     uint16_t* a16;          // [P][N] fp16 SwiGLU output (sorted position order)
     uint8_t* qa;            // [P][N] e4m3 down inputs
     float* sa;              // [P]
-    float* out32;           // [T][K] fp32 accumulation
+    float* contrib;         // [P][K] per-pair weighted contribution (sorted position order)
+    const int* inv;         // [P] pair j -> sorted position
+    int topk;
     void* out;
     int odt;
     int64_t out_stride;
 };
 constexpr int FP8_TM = 64;   // rows per segment (two 32-row MFMA tiles)
-// kernels: bit 0 zero + quantize inputs, bit 1 gate/up, bit 2 down-input quantization + down, bit 3 convert
+// kernels: bit 0 quantize inputs, bit 1 gate/up, bit 2 down-input quantization + down, bit 3 slot-order combine
 int launch_fp8(const Fp8Args& a, hipStream_t st, int kernels);
 int launch_quant_rows(const void* x, int xdt, int64_t stride, int rows, int K, uint8_t* q, float* s, hipStream_t st);
 

@@ -11,7 +11,8 @@
 //   gather   h13 = fp16(H(fp16(x * suh_g)) * r)                                         (exl3_fat_moe.cu:95-126)
 //   gate/up  g = (H(acc_g) * r) * svh_g, u likewise; iff L != 0: g = min(g, L), u = clamp(u, -L, L);
 //            a = (1 / (1 + (float)exp(-(double)g))) * g * u; h2 = fp16(H(fp16(fp16(a) * suh_d)) * r)  (:340-378)
-//   down     out[token] += ((H(acc_d) * r) * svh_d) * w16                                (:443-457)
+//   down     contribution ((H(acc_d) * r) * svh_d) * w16 per pair                       (:443-457); out[token] =
+//            the token's contributions summed in slot order (fp32), then the output dtype
 #include <algorithm>
 
 #include "common.cuh"
@@ -270,7 +271,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
                 if (trow < rn) {
                     const int row = row0 + trow;
                     const float w = (float)u16_as_h(a.w16[row]);
-                    float* o = a.out32 + (size_t)a.tok[row] * K + cb * 256 + 2 * lane;
+                    float* o = a.contrib + (size_t)row * K + cb * 256 + 2 * lane;
 #pragma unroll
                     for (int hf = 0; hf < 2; ++hf) {
                         float v0 = Cs[rl * 256 + hf * 128 + 2 * lane], v1 = Cs[rl * 256 + hf * 128 + 2 * lane + 1];
@@ -278,8 +279,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
                         const h2 sv = hf ? sv1 : sv0;
                         v0 = v0 * HAD_R * (float)sv.x * w;
                         v1 = v1 * HAD_R * (float)sv.y * w;
-                        atomicAdd(o + hf * 128, v0);
-                        atomicAdd(o + hf * 128 + 1, v1);
+                        *reinterpret_cast<float2*>(o + hf * 128) = make_float2(v0, v1);
                     }
                 }
             }
@@ -287,21 +287,29 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
         }
 }
 
-// ------------------------------------------------------------------------------------------------ out buffers
+// ------------------------------------------------------------------------------------------------ combine
 
-__global__ __launch_bounds__(256) void pf_zero_kernel(float* __restrict__ p, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.f;
-}
-
-__global__ __launch_bounds__(256) void pf_convert_kernel(const float* __restrict__ src, int T, int K, void* dst,
-                                                         int odt, int64_t stride) {
-    const int64_t n = (int64_t)T * K;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-        const int64_t t = i / K, c = i - t * K;
-        const float v = src[i];
-        if (odt == DT_F32) reinterpret_cast<float*>(dst)[t * stride + c] = v;
-        else if (odt == DT_BF16) reinterpret_cast<uint16_t*>(dst)[t * stride + c] = f32_to_bf16(v);
-        else reinterpret_cast<_Float16*>(dst)[t * stride + c] = (_Float16)v;
+// grid (T, K/256), 128 threads x 2 columns: out[t] = sum over the token's slots k (in order) of the valid pairs'
+// contributions, in the output dtype (deterministic: no atomics).
+__global__ __launch_bounds__(128) void pf_combine_kernel(PrefillArgs a) {
+    const int t = blockIdx.x;
+    const int col = blockIdx.y * 256 + 2 * threadIdx.x;
+    float s0 = 0.f, s1 = 0.f;
+    for (int k = 0; k < a.topk; ++k) {
+        const int pos = a.inv[t * a.topk + k];
+        if (a.pe[pos] < 0) continue;
+        const float2 c = *reinterpret_cast<const float2*>(a.contrib + (size_t)pos * a.K + col);
+        s0 += c.x;
+        s1 += c.y;
+    }
+    const size_t o = (size_t)t * a.out_stride + col;
+    if (a.odt == DT_F32) {
+        *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.out) + o) = make_float2(s0, s1);
+    } else if (a.odt == DT_BF16) {
+        const uint32_t v = (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + o) = v;
+    } else {
+        *reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o) = h2{(_Float16)s0, (_Float16)s1};
     }
 }
 
@@ -323,20 +331,11 @@ int prefill_setup() {
 
 int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
     if (prefill_setup()) return -1;
-    if (kernels & 1) {
-        const int64_t n = (int64_t)a.T * a.K;
-        hipLaunchKernelGGL(pf_zero_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0,
-                           st, a.out32, n);
-        hipLaunchKernelGGL(pf_gather_kernel, dim3(4096), dim3(256), 0, st, a);
-    }
+    if (kernels & 1) hipLaunchKernelGGL(pf_gather_kernel, dim3(4096), dim3(256), 0, st, a);
     if (kernels & 2)
         hipLaunchKernelGGL(pf_gateup_kernel, dim3(a.N / 128, a.S_cap), dim3(PF_THREADS), PF_LDS, st, a);
     if (kernels & 4) hipLaunchKernelGGL(pf_down_kernel, dim3(a.K / 256, a.S_cap), dim3(PF_THREADS), PF_LDS, st, a);
-    if (kernels & 8) {
-        const int64_t n = (int64_t)a.T * a.K;
-        hipLaunchKernelGGL(pf_convert_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0,
-                           st, a.out32, a.T, a.K, a.out, a.odt, a.out_stride);
-    }
+    if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3(a.T, a.K / 256), dim3(128), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

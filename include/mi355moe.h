@@ -108,8 +108,8 @@ int mi355moe_rot_in(const void* x, int x_dtype, int64_t x_stride, int64_t K, con
  * code/fork/docs/prod_exl3_reference.py:1364-1435, code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu).
  * x F16/BF16 [T][K] (row stride x_stride), ids I32/I64 [T][topk], weights F32/F16/BF16 [T][topk], out [T][K] of
  * out_dtype (row stride out_stride) is WRITTEN (not accumulated). limit = the SwiGLU limit (0 = none).
- * Decode path: per-token slot-order sum (deterministic). Prefill path: fp32 atomic scatter-add, then the
- * conversion to out_dtype. Pairs P = T*topk <= 65536. */
+ * Both paths add a token's per-pair contributions in slot order (fp32, deterministic) and write out_dtype.
+ * Pairs P = T*topk <= 65536. */
 enum { MI355MOE_PATH_AUTO = 0, MI355MOE_PATH_DECODE = 1, MI355MOE_PATH_PREFILL = 2 };
 /* The automatic choice: the prefill path when P >= MI355MOE_PREFILL_MIN_PAIRS and the layer has
  * MI355MOE_LAYER_SHARED_W13_SUH, else the decode path. */
@@ -169,9 +169,11 @@ int mi355moe_fp8_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t K,
 /* Routed-expert output of a block-scaled e4m3 layer from router ids and weights (the e4m3 expert path,
  * code/fork/overlay/glm53_moe_e4m3.py:484-592 -> moe_e4m3.cu fused, :3081-3096): activations quantised per
  * token, SwiGLU a16 = fp16(silu(min(g, L)) * clamp(u, -L, L)) (iff L != 0), a16 requantised per row, down GEMM,
- * fp32 scatter-add of w * y, out in out_dtype. hidden % 256 == 0, intermediate % 128 == 0; T * topk <= 65536.
+ * per-pair contributions w * y summed per token in slot order (fp32, deterministic), out WRITTEN in out_dtype
+ * (out_stride even). hidden % 256 == 0, intermediate % 128 == 0, both <= 16384;
+ * T * topk <= 65536.
  * stages: the MI355MOE_STAGE_* mask (ROUTE = permutation and input quantisation, GATEUP, DOWN = requantisation and
- * down GEMM, COMBINE = output conversion). */
+ * down GEMM, COMBINE = the slot-order sum into out). */
 int64_t mi355moe_fp8_moe_workspace_bytes(const mi355moe_fp8_layer* layer, int64_t T, int64_t topk);
 int mi355moe_fp8_moe_forward_ids(const mi355moe_fp8_layer* layer, const void* x, int x_dtype, int64_t x_stride,
                                  int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
