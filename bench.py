@@ -178,7 +178,7 @@ def run_decode(args, torch, mi355moe, dev):
         "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "kernel": "dec_gateup_kernel", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_launch_us": round(gu_avg_us, 2)},
+                     "traffic": _traffic(dsum / args.steps), "avg_launch_us": round(gu_avg_us, 2)},
         "wall_s": round(wall, 3),
     }
     if not args.no_cpu_baseline:
@@ -319,6 +319,28 @@ def run_fp8(args, torch, dev):
                           f"{steps} timed steps"}
 
 
+def _traffic(distinct: float):
+    """HBM bytes per gate/up launch from the committed PMC measurement (profiles/decode_gateup_traffic.json: FETCH_SIZE
+    and WRITE_SIZE per launch, each scaled by what the counter reads for a device copy of known size), rescaled to
+    this run's mean number of distinct experts (the kernel's traffic is proportional to it); None without the file."""
+    path = os.path.join(ROOT, "profiles", "decode_gateup_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return round(t["hbm_bytes_per_launch"] * distinct / t["distinct_experts_per_launch"])
+
+
+def copy_probe(torch, dev, mib: int):
+    """Three device-to-device copies of `mib` MiB: a plain copy of known size, the reference that PMC byte counters
+    (FETCH_SIZE / WRITE_SIZE) are scaled by."""
+    a = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -330,6 +352,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=8)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the workload, copy a tensor of this many MiB three times (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
@@ -353,6 +377,8 @@ def main():
     if args.workload in ("all", "fp8"):
         log("[bench] fp8 ...")
         res.update(run_fp8(args, torch, dev))
+    if args.copy_probe_mib > 0:
+        copy_probe(torch, dev, args.copy_probe_mib)
     print(json.dumps(res), flush=True)
 
 
