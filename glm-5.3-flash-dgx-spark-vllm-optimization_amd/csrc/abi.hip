@@ -71,7 +71,7 @@ DecodePlan plan_decode(int64_t P, int64_t rows_bound, int64_t n, int64_t K, int6
     for (int64_t c : {1, 2, 4, 8}) {
         if (N % c || (N / c) % 128 || decode_lds_down(d.rmax, (int)N, (int)c) > DECODE_LDS_MAX) continue;
         nr = N / c;
-        if (s_est * (K / 256) * c >= target) break;
+        if (s_est * ((K + 511) / 512) * c >= target) break;   // 512-column down workgroups
     }
     d.sk_dn = (int)(N / nr);
     return d;

@@ -111,23 +111,46 @@ __device__ __forceinline__ int xa_pos(int k) {
 struct RotIn {
     uint32_t x2, s2;
 };
+// global-address-space 4-byte load (a plain pointer from a pointer table would otherwise become a flat load, which
+// also counts against the scalar-load counter and serialises the prologue)
+typedef __attribute__((address_space(1))) const uint32_t gu32;
+__device__ __forceinline__ uint32_t ld_g32(const void* p) {
+    return *reinterpret_cast<gu32*>(reinterpret_cast<uintptr_t>(p));
+}
 __device__ __forceinline__ RotIn rot_load(const void* x, size_t xoff, const _Float16* suh, int lane) {
-    return RotIn{*reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + xoff + 2 * lane),
-                 *reinterpret_cast<const uint32_t*>(suh + 2 * lane)};
+    return RotIn{ld_g32(reinterpret_cast<const uint16_t*>(x) + xoff + 2 * lane), ld_g32(suh + 2 * lane)};
+}
+// x * suh rounded to fp16 (bf16 inputs are first rounded to fp16, as x.half() does), as two floats; branch-free in
+// the input type so the first use of a load batch needs no control-flow join
+__device__ __forceinline__ void rot_scale(const RotIn& v, int xdt, float& p0, float& p1) {
+    const bool bf = xdt == DT_BF16;
+    const _Float16 h0 = bf ? (_Float16)__builtin_bit_cast(float, v.x2 << 16) : u16_as_h(v.x2 & 0xFFFFu);
+    const _Float16 h1 = bf ? (_Float16)__builtin_bit_cast(float, v.x2 & 0xFFFF0000u) : u16_as_h(v.x2 >> 16);
+    const h2 s = __builtin_bit_cast(h2, v.s2);
+    p0 = (float)(_Float16)(h0 * s.x);
+    p1 = (float)(_Float16)(h1 * s.y);
 }
 __device__ __forceinline__ void rot_store(const RotIn& v, int xdt, uint16_t* dst, int k0, int lane) {
-    _Float16 h0, h1;
-    if (xdt == DT_BF16) {
-        h0 = (_Float16)__builtin_bit_cast(float, v.x2 << 16);
-        h1 = (_Float16)__builtin_bit_cast(float, v.x2 & 0xFFFF0000u);
-    } else {
-        h0 = u16_as_h(v.x2 & 0xFFFFu);
-        h1 = u16_as_h(v.x2 >> 16);
-    }
-    const h2 s = __builtin_bit_cast(h2, v.s2);
-    float p0 = (float)(_Float16)(h0 * s.x), p1 = (float)(_Float16)(h1 * s.y);
+    float p0, p1;
+    rot_scale(v, xdt, p0, p1);
     fwht128_w64(p0, p1, lane);
     *reinterpret_cast<h2*>(dst + xa_pos(k0 + 2 * lane)) = h2{(_Float16)(p0 * HAD_R), (_Float16)(p1 * HAD_R)};
+}
+
+// Segments of up to DUP_ROWS rows stage each input duplicated into a dword (x, x) at dword xa_pos(k) of the row,
+// so the matrix-core A operand of a word is one 16-byte LDS read (no per-step permutes).
+constexpr int DUP_ROWS = 4;
+__device__ __forceinline__ uint32_t dup16(_Float16 h) {
+    const uint32_t u = h_as_u16(h);
+    return u | (u << 16);
+}
+// rot_store into a duplicated staged row (dst = the row's first dword)
+__device__ __forceinline__ void rot_store_dup(const RotIn& v, int xdt, uint32_t* dst, int k0, int lane) {
+    float p0, p1;
+    rot_scale(v, xdt, p0, p1);
+    fwht128_w64(p0, p1, lane);
+    *reinterpret_cast<uint2*>(dst + xa_pos(k0 + 2 * lane)) =
+        make_uint2(dup16((_Float16)(p0 * HAD_R)), dup16((_Float16)(p1 * HAD_R)));
 }
 
 // The raw codebook word of a state: its two fp16 halves sum to the weight.
@@ -191,6 +214,21 @@ __device__ __forceinline__ void step_mfma2(const u32x4& wg, uint32_t pwg, const 
     }
 }
 
+// step_mfma2 with the A operands read ready-made from a duplicated staged row (xa[i] = word i's).
+__device__ __forceinline__ void step_mfma2_dup(const u32x4& wg, uint32_t pwg, const u32x4& wu, uint32_t pwu,
+                                               const u32x4 (&xa)[4], f32x4 (&ag)[2], f32x4 (&au)[2]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u32x4 b0, b1;
+        decode_word_b(i ? wg[i - 1] : pwg, wg[i], b0, b1);
+        ag[0] = mfma16(xa[i], b0, ag[0]);
+        ag[1] = mfma16(xa[i], b1, ag[1]);
+        decode_word_b(i ? wu[i - 1] : pwu, wu[i], b0, b1);
+        au[0] = mfma16(xa[i], b0, au[0]);
+        au[1] = mfma16(xa[i], b1, au[1]);
+    }
+}
+
 // Streamed weight load: a global-address-space 16-byte load marked non-temporal (read once per call).
 typedef __attribute__((address_space(1))) const u32x4 gu32x4;
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
@@ -223,9 +261,32 @@ __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
     const int K = a.K, N = a.N, NT = N >> 4;
     const int KR = K / a.sk_gu, KH = KR >> 1, kbase = ks * KR, RSH = KR + XPAD;
     constexpr int NMAT = SHARED ? 1 : 2;
-    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);              // [NMAT][rn][RSH]
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);              // [NMAT][rn][RSH] halves, or
+    uint32_t* xw = reinterpret_cast<uint32_t*>(smem);              // [rn][RSD] duplicated (SHARED, rn <= DUP_ROWS)
+    const int RSD = KR + 4;
+    const bool dup = SHARED && rn <= DUP_ROWS;
 
-    // first weight loads are issued before the prologue so their latency overlaps it
+    // prologue: the segment's rotated inputs for this K range, eight (row, matrix, 128-block) tasks per wave per
+    // batch. The first batch's input loads are issued unconditionally (task index clamped) before the weight
+    // prefetch: loads return in issue order, so inputs queued behind the prefetch would wait for all of it.
+    // The segment's token ids are read once, one per lane, and handed to tasks with readlane (per-task scalar
+    // loads would each wait for the previous one).
+    constexpr int TB = 8;
+    const int nb = KR >> 7, ntask = rn * NMAT * nb;
+    const int tokl = a.tok[row0 + min(lane, rn - 1)];
+    const _Float16* suhg = reinterpret_cast<const _Float16*>(a.wt.g_suh[e]) + kbase;
+    const _Float16* suhu = reinterpret_cast<const _Float16*>(a.wt.u_suh[e]) + kbase;
+    auto task_load = [&](int task) {
+        task = min(task, ntask - 1);
+        const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
+        const int tk = __builtin_amdgcn_readlane(tokl, r);
+        return rot_load(a.x, (size_t)tk * a.x_stride + kbase + b * 128, (mat ? suhu : suhg) + b * 128, lane);
+    };
+    RotIn v[TB];
+#pragma unroll
+    for (int c = 0; c < TB; ++c) v[c] = task_load(wv + c * GU_WAVES);
+    __builtin_amdgcn_sched_barrier(0);
+
     const int t = lane >> 3, q = lane & 7;
     const int ct = cb * 8 + cg * 2 + (t & 1);
     const u32x4* G = reinterpret_cast<const u32x4*>(a.wt.g_tr[e]);
@@ -241,69 +302,94 @@ __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
         gb[j] = ld_stream(G + idx0 + j * sstr);
         ub[j] = ld_stream(U + idx0 + j * sstr);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // prologue: the segment's rotated inputs for this K range, four blocks per wave per round (loads first)
-    const int nb = KR >> 7, ntask = rn * NMAT * nb;
-    for (int t0 = wv; t0 < ntask; t0 += 4 * GU_WAVES) {
-        RotIn v[4];
+    // the first batch in straight-line code (so its wait leaves the prefetch in flight), then any further batches
+    auto task_store = [&](int task, const RotIn& vv) {
+        const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
+        if (dup) rot_store_dup(vv, a.xdt, xw + (size_t)r * RSD, b * 128, lane);
+        else rot_store(vv, a.xdt, xs + (size_t)(mat * rn + r) * RSH, b * 128, lane);
+    };
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int task = t0 + c * GU_WAVES;
-            if (task < ntask) {
-                const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
-                const _Float16* suh =
-                    reinterpret_cast<const _Float16*>((mat ? a.wt.u_suh : a.wt.g_suh)[e]) + kbase + b * 128;
-                v[c] = rot_load(a.x, (size_t)a.tok[row0 + r] * a.x_stride + kbase + b * 128, suh, lane);
-            }
-        }
+    for (int c = 0; c < TB; ++c)
+        if (wv + c * GU_WAVES < ntask) task_store(wv + c * GU_WAVES, v[c]);
+    for (int t0 = wv + TB * GU_WAVES; t0 < ntask; t0 += TB * GU_WAVES) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int task = t0 + c * GU_WAVES;
-            if (task < ntask) {
-                const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
-                rot_store(v[c], a.xdt, xs + (size_t)(mat * rn + r) * RSH, b * 128, lane);
-            }
-        }
+        for (int c = 0; c < TB; ++c) v[c] = task_load(t0 + c * GU_WAVES);
+#pragma unroll
+        for (int c = 0; c < TB; ++c)
+            if (t0 + c * GU_WAVES < ntask) task_store(t0 + c * GU_WAVES, v[c]);
     }
     __syncthreads();
 
     const int arow = min(lane & 15, rn - 1);                         // rows >= rn repeat the last row (dropped)
-    const uint16_t* xg = xs + (size_t)arow * RSH + kh * KH + (t >> 1) * 16;
-    const uint16_t* xu = xs + (size_t)((NMAT - 1) * rn + arow) * RSH + kh * KH + (t >> 1) * 16;
     f32x4 ag[2], au[2];
     ag[0] = ag[1] = au[0] = au[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // staged inputs are read one step ahead (xc = this step's, xn = the next step's)
-    u32x4 xc[2][2], xn[2][2];
-    xc[0][0] = reinterpret_cast<const u32x4*>(xg)[0];
-    xc[0][1] = reinterpret_cast<const u32x4*>(xg)[1];
-    if (!SHARED) {
-        xc[1][0] = reinterpret_cast<const u32x4*>(xu)[0];
-        xc[1][1] = reinterpret_cast<const u32x4*>(xu)[1];
-    }
-    for (int st = 0; st < steps; st += DEPTH) {
+    // staged inputs are read one step ahead (this step's, the next step's), and so are the predecessor words (pg,
+    // pu), so no step waits on its own LDS reads
+    uint32_t pg = prev_word(gb[0][3], lane), pu = prev_word(ub[0][3], lane);
+    if (dup) {
+        const uint32_t* xr = xw + (size_t)arow * RSD + kh * KH + (t >> 1) * 16;
+        u32x4 xa[4], xn[4];
 #pragma unroll
-        for (int j = 0; j < DEPTH; ++j) {
-            const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
-            const int sn = min(st + j + 1, steps - 1);
-            xn[0][0] = reinterpret_cast<const u32x4*>(xg + sn * 64)[0];
-            xn[0][1] = reinterpret_cast<const u32x4*>(xg + sn * 64)[1];
-            if (SHARED) {
-                step_mfma2(gb[j], prev_word(gb[j][3], lane), ub[j], prev_word(ub[j][3], lane), xc[0][0], xc[0][1], ag,
-                           au);
-            } else {
-                xn[1][0] = reinterpret_cast<const u32x4*>(xu + sn * 64)[0];
-                xn[1][1] = reinterpret_cast<const u32x4*>(xu + sn * 64)[1];
-                step_mfma(gb[j], prev_word(gb[j][3], lane), xc[0][0], xc[0][1], ag);
-                step_mfma(ub[j], prev_word(ub[j][3], lane), xc[1][0], xc[1][1], au);
+        for (int i = 0; i < 4; ++i) xa[i] = reinterpret_cast<const u32x4*>(xr)[i];
+        for (int st = 0; st < steps; st += DEPTH) {
+#pragma unroll
+            for (int j = 0; j < DEPTH; ++j) {
+                const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
+                const int sn = min(st + j + 1, steps - 1);
+                const int jn = (j + 1) % DEPTH;
+                const uint32_t pgn = prev_word(gb[jn][3], lane), pun = prev_word(ub[jn][3], lane);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xn[i] = reinterpret_cast<const u32x4*>(xr + sn * 64)[i];
+                step_mfma2_dup(gb[j], pg, ub[j], pu, xa, ag, au);
+                gb[j] = ld_stream(G + nx);
+                ub[j] = ld_stream(U + nx);
+                __builtin_amdgcn_sched_barrier(0);                  // keep the refill here, not sunk to the end
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xa[i] = xn[i];
+                pg = pgn;
+                pu = pun;
             }
-            gb[j] = ld_stream(G + nx);
-            ub[j] = ld_stream(U + nx);
-            __builtin_amdgcn_sched_barrier(0);                      // keep the refill here, not sunk to the end
-            xc[0][0] = xn[0][0];
-            xc[0][1] = xn[0][1];
-            if (!SHARED) {
-                xc[1][0] = xn[1][0];
-                xc[1][1] = xn[1][1];
+        }
+    } else {
+        const uint16_t* xg = xs + (size_t)arow * RSH + kh * KH + (t >> 1) * 16;
+        const uint16_t* xu = xs + (size_t)((NMAT - 1) * rn + arow) * RSH + kh * KH + (t >> 1) * 16;
+        u32x4 xc[2][2], xn[2][2];
+        xc[0][0] = reinterpret_cast<const u32x4*>(xg)[0];
+        xc[0][1] = reinterpret_cast<const u32x4*>(xg)[1];
+        if (!SHARED) {
+            xc[1][0] = reinterpret_cast<const u32x4*>(xu)[0];
+            xc[1][1] = reinterpret_cast<const u32x4*>(xu)[1];
+        }
+        for (int st = 0; st < steps; st += DEPTH) {
+#pragma unroll
+            for (int j = 0; j < DEPTH; ++j) {
+                const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
+                const int sn = min(st + j + 1, steps - 1);
+                const int jn = (j + 1) % DEPTH;
+                const uint32_t pgn = prev_word(gb[jn][3], lane), pun = prev_word(ub[jn][3], lane);
+                xn[0][0] = reinterpret_cast<const u32x4*>(xg + sn * 64)[0];
+                xn[0][1] = reinterpret_cast<const u32x4*>(xg + sn * 64)[1];
+                if (SHARED) {
+                    step_mfma2(gb[j], pg, ub[j], pu, xc[0][0], xc[0][1], ag, au);
+                } else {
+                    xn[1][0] = reinterpret_cast<const u32x4*>(xu + sn * 64)[0];
+                    xn[1][1] = reinterpret_cast<const u32x4*>(xu + sn * 64)[1];
+                    step_mfma(gb[j], pg, xc[0][0], xc[0][1], ag);
+                    step_mfma(ub[j], pu, xc[1][0], xc[1][1], au);
+                }
+                gb[j] = ld_stream(G + nx);
+                ub[j] = ld_stream(U + nx);
+                __builtin_amdgcn_sched_barrier(0);                  // keep the refill here, not sunk to the end
+                xc[0][0] = xn[0][0];
+                xc[0][1] = xn[0][1];
+                if (!SHARED) {
+                    xc[1][0] = xn[1][0];
+                    xc[1][1] = xn[1][1];
+                }
+                pg = pgn;
+                pu = pun;
             }
         }
     }
@@ -384,8 +470,10 @@ __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
     if (a.sk_gu > 1 && tid == 0) *cnt = 0u;
 }
 
-// grid (K/256, N splits, segments), 512 threads: workgroup = 256 output columns of one segment over one N range;
-// wave w = columns 32w..32w+31 over the whole range.
+// grid (K/512, N splits, segments), 512 threads: workgroup = 512 output columns of one segment over one N range;
+// wave w = columns 64w..64w+63 (column tiles 4w..4w+3: the first pair as "g", the second as "u" of the two-matrix
+// step, sharing the staged input) over the whole range.
+constexpr int DN_COLS = 512;
 template <int DEPTH>
 __global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_down_kernel(
     DecodeArgs a) {
@@ -398,83 +486,135 @@ __global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, N = a.N, KT = K >> 4;
     const int NR = N / a.sk_dn, nbase = ks * NR, RSH = NR + XPAD;
-    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);              // [rn][RSH]
+    uint32_t* xw = reinterpret_cast<uint32_t*>(smem);              // [rn][RSD] inputs duplicated per n: (x, x)
+    const int RSD = NR + 4;
+
+    // prologue: the segment's down inputs (already rotated) for this N range, 8 halves per load; the first batch is
+    // loaded unconditionally (chunk index clamped) before the weight prefetch (loads return in issue order)
+    const int cpr = NR >> 3, nchunk = rn * cpr;                      // 16-byte chunks per row, in all
+    constexpr int PB = 2;                                            // chunks per thread per batch
+    u32x4 xv[PB];
+    auto chunk_src = [&](int i) {
+        i = min(i, nchunk - 1);
+        const int r = i / cpr, k = 8 * (i - r * cpr);
+        return *reinterpret_cast<const u32x4*>(a.xd + (size_t)(row0 + r) * N + nbase + k);
+    };
+    auto chunk_store = [&](int i, const u32x4& v) {
+        // halves k..k+7 (k = 16 g + 8 h) go duplicated to staged dwords 4 m + 2 h, 4 m + 2 h + 1 of group g
+        const int r = i / cpr, k = 8 * (i - r * cpr);
+        uint32_t* d = xw + (size_t)r * RSD + (k & ~15) + 2 * ((k >> 3) & 1);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t lo = v[m] & 0xFFFFu, hi = v[m] >> 16;
+            *reinterpret_cast<uint2*>(d + 4 * m) = make_uint2(lo | (lo << 16), hi | (hi << 16));
+        }
+    };
+#pragma unroll
+    for (int c = 0; c < PB; ++c) xv[c] = chunk_src(tid + c * DN_WAVES * 64);
+    __builtin_amdgcn_sched_barrier(0);
 
     const int t = lane >> 3, q = lane & 7;
-    const int ct = cb * 16 + wv * 2 + (t & 1);
+    const int ct = cb * (DN_COLS / 16) + wv * 4 + (t & 1);
     const u32x4* D = reinterpret_cast<const u32x4*>(a.wt.d_tr[e]);
     const size_t sstr = (size_t)KT * 8 * 4;
     const size_t idx0 = ((size_t)((nbase >> 4) + (t >> 1)) * KT + ct) * 8 + q;
     const int steps = NR >> 6;                                       // a multiple of DEPTH
-    u32x4 db[DEPTH];
+    // K % 256 == 0: in the last workgroup the upper waves may have no columns (wave-uniform; they only stage)
+    // (their prefetch re-reads column tiles 0..3 so that every wave issues the same loads)
+    const bool live = cb * DN_COLS + wv * 64 < K;
+    const size_t pf0 = live ? idx0 : ((size_t)((nbase >> 4) + (t >> 1)) * KT + (t & 1)) * 8 + q;
+    u32x4 gb[DEPTH], ub[DEPTH];                                      // column tiles ct and ct + 2
 #pragma unroll
-    for (int j = 0; j < DEPTH; ++j) db[j] = ld_stream(D + idx0 + j * sstr);
+    for (int j = 0; j < DEPTH; ++j) {
+        gb[j] = ld_stream(D + pf0 + j * sstr);
+        ub[j] = ld_stream(D + pf0 + 16 + j * sstr);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
-    // prologue: the segment's down inputs (already rotated) for this N range, into the staged layout
-    for (int i = tid; i < rn * (NR >> 1); i += DN_WAVES * 64) {
-        const int r = i / (NR >> 1), k = 2 * (i - r * (NR >> 1));
-        *reinterpret_cast<uint32_t*>(xs + (size_t)r * RSH + xa_pos(k)) =
-            *reinterpret_cast<const uint32_t*>(a.xd + (size_t)(row0 + r) * N + nbase + k);
+#pragma unroll
+    for (int c = 0; c < PB; ++c)
+        if (tid + c * DN_WAVES * 64 < nchunk) chunk_store(tid + c * DN_WAVES * 64, xv[c]);
+    for (int i0 = tid + PB * DN_WAVES * 64; i0 < nchunk; i0 += PB * DN_WAVES * 64) {
+#pragma unroll
+        for (int c = 0; c < PB; ++c) xv[c] = chunk_src(i0 + c * DN_WAVES * 64);
+#pragma unroll
+        for (int c = 0; c < PB; ++c)
+            if (i0 + c * DN_WAVES * 64 < nchunk) chunk_store(i0 + c * DN_WAVES * 64, xv[c]);
     }
     __syncthreads();
 
     const int arow = min(lane & 15, rn - 1);
-    const uint16_t* xr = xs + (size_t)arow * RSH + (t >> 1) * 16;
-    f32x4 ad[2];
-    ad[0] = ad[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    u32x4 xc0 = reinterpret_cast<const u32x4*>(xr)[0], xc1 = reinterpret_cast<const u32x4*>(xr)[1];
-    for (int st = 0; st < steps; st += DEPTH) {
+    const uint32_t* xr = xw + (size_t)arow * RSD + (t >> 1) * 16;
+    f32x4 ag[2], au[2];
+    ag[0] = ag[1] = au[0] = au[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 xa[4], xn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xa[i] = reinterpret_cast<const u32x4*>(xr)[i];
+    uint32_t pg = prev_word(gb[0][3], lane), pu = prev_word(ub[0][3], lane);
+    for (int st = 0; live && st < steps; st += DEPTH) {
 #pragma unroll
         for (int j = 0; j < DEPTH; ++j) {
             const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
             const int sn = min(st + j + 1, steps - 1);
-            const u32x4 xn0 = reinterpret_cast<const u32x4*>(xr + sn * 64)[0];
-            const u32x4 xn1 = reinterpret_cast<const u32x4*>(xr + sn * 64)[1];
-            step_mfma(db[j], prev_word(db[j][3], lane), xc0, xc1, ad);
-            db[j] = ld_stream(D + nx);
+            const int jn = (j + 1) % DEPTH;
+            const uint32_t pgn = prev_word(gb[jn][3], lane), pun = prev_word(ub[jn][3], lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xn[i] = reinterpret_cast<const u32x4*>(xr + sn * 64)[i];
+            step_mfma2_dup(gb[j], pg, ub[j], pu, xa, ag, au);
+            gb[j] = ld_stream(D + nx);
+            ub[j] = ld_stream(D + nx + 16);
             __builtin_amdgcn_sched_barrier(0);
-            xc0 = xn0;
-            xc1 = xn1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xa[i] = xn[i];
+            pg = pgn;
+            pu = pun;
         }
     }
     __syncthreads();                                                 // the staged inputs are no longer read
-    float* zs = reinterpret_cast<float*>(smem);                     // [ZS_ROWS][256]
+    float* zs = reinterpret_cast<float*>(smem);                     // [ZS_ROWS][DN_COLS]
     {
-        const int col = wv * 32 + acc_col(lane), rb = 4 * (lane >> 4);
+        const int col = wv * 64 + acc_col(lane), rb = 4 * (lane >> 4);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            if (rb + r < rn) {
-                zs[(rb + r) * 256 + col] = ad[0][r];
-                zs[(rb + r) * 256 + col + 8] = ad[1][r];
+            if (live && rb + r < rn) {
+                zs[(rb + r) * DN_COLS + col] = ag[0][r];
+                zs[(rb + r) * DN_COLS + col + 8] = ag[1][r];
+                zs[(rb + r) * DN_COLS + col + 32] = au[0][r];
+                zs[(rb + r) * DN_COLS + col + 40] = au[1][r];
             }
     }
     __syncthreads();
 
     const size_t P = a.P;
-    unsigned* cnt = a.cnt_dn + (size_t)s * (K >> 8) + cb;
+    const int ncol = min(DN_COLS, K - cb * DN_COLS);                // 256 or 512
+    unsigned* cnt = a.cnt_dn + (size_t)s * ((K + DN_COLS - 1) / DN_COLS) + cb;
     if (a.sk_dn > 1) {
-        for (int i = tid; i < rn * 256; i += DN_WAVES * 64) {
-            const int r = i >> 8, c = i & 255;
-            st_coherent(a.zd + ((size_t)ks * P + row0 + r) * K + cb * 256 + c, zs[r * 256 + c]);
+        for (int i = tid; i < rn * DN_COLS; i += DN_WAVES * 64) {
+            const int r = i / DN_COLS, c = i % DN_COLS;
+            if (c < ncol)
+                st_coherent(a.zd + ((size_t)ks * P + row0 + r) * K + cb * DN_COLS + c, zs[r * DN_COLS + c]);
         }
         if (!arrive_last(cnt, (unsigned)a.sk_dn, &last_flag)) return;
-        for (int i = tid; i < rn * 256; i += DN_WAVES * 64) {
-            const int r = i >> 8, c = i & 255;
+        for (int i = tid; i < rn * DN_COLS; i += DN_WAVES * 64) {
+            const int r = i / DN_COLS, c = i % DN_COLS;
+            if (c >= ncol) continue;
             float v = 0.f;
-            for (int k = 0; k < a.sk_dn; ++k) v += ld_coherent(a.zd + ((size_t)k * P + row0 + r) * K + cb * 256 + c);
-            zs[r * 256 + c] = v;
+            for (int k = 0; k < a.sk_dn; ++k)
+                v += ld_coherent(a.zd + ((size_t)k * P + row0 + r) * K + cb * DN_COLS + c);
+            zs[r * DN_COLS + c] = v;
         }
         __syncthreads();
     }
 
-    // epilogue: (row, 128-column half) tasks; output Hadamard, scale, then atomics or the per-pair contribution
-    for (int task = wv; task < rn * 2; task += DN_WAVES) {
-        const int r = task >> 1, hb = task & 1;
+    // epilogue: (row, 128-column block) tasks; output Hadamard, scale, then atomics or the per-pair contribution
+    const int NBLK = ncol / 128;
+    for (int task = wv; task < rn * NBLK; task += DN_WAVES) {
+        const int r = task / NBLK, hb = task % NBLK;
         const size_t row = row0 + r;
         if (a.pe[row] < 0) continue;                                 // a row whose token id was out of range
-        const int col = cb * 256 + hb * 128 + 2 * lane;
+        const int col = cb * DN_COLS + hb * 128 + 2 * lane;
         const h2 svd = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + col);
-        float v[2] = {zs[r * 256 + hb * 128 + 2 * lane], zs[r * 256 + hb * 128 + 2 * lane + 1]};
+        float v[2] = {zs[r * DN_COLS + hb * 128 + 2 * lane], zs[r * DN_COLS + hb * 128 + 2 * lane + 1]};
         fwht128_w64(v[0], v[1], lane);
         const float rs = HAD_R * (float)u16_as_h(a.w16[row]);
         v[0] = v[0] * rs * (float)svd.x;
@@ -528,12 +668,13 @@ int launch_rot_in(const void* x, int xdt, int64_t x_stride, const int* tok, cons
 }
 
 size_t decode_lds_gateup(int rmax, int K, int sk_gu, int shared_suh) {
-    const size_t staged = (size_t)(shared_suh ? 1 : 2) * rmax * (K / sk_gu + XPAD) * 2;
+    size_t staged = (size_t)(shared_suh ? 1 : 2) * rmax * (K / sk_gu + XPAD) * 2;
+    if (shared_suh) staged = std::max(staged, (size_t)std::min(rmax, DUP_ROWS) * (K / sk_gu + 4) * 4);
     const size_t reduce = (size_t)(4 * 64 * 16 + 2 * ZS_ROWS * 128) * 4;
     return std::max(staged, reduce);
 }
 size_t decode_lds_down(int rmax, int N, int sk_dn) {
-    return std::max((size_t)rmax * (N / sk_dn + XPAD) * 2, (size_t)ZS_ROWS * 256 * 4);
+    return std::max((size_t)rmax * (N / sk_dn + 4) * 4, (size_t)ZS_ROWS * DN_COLS * 4);
 }
 
 template <typename F>
@@ -572,7 +713,7 @@ int launch_decode(const DecodeArgs& a0, int rmax, hipStream_t st, int kernels) {
         }
     }
     if (kernels & 2) {
-        const dim3 grid(a.K / 256, a.sk_dn, a.S_cap);
+        const dim3 grid((a.K + DN_COLS - 1) / DN_COLS, a.sk_dn, a.S_cap);
         const size_t lds = decode_lds_down(rmax, a.N, a.sk_dn);
         if (((a.N / a.sk_dn) >> 6) % 4 == 0)
             hipLaunchKernelGGL(dec_down_kernel<4>, grid, dim3(DN_WAVES * 64), lds, st, a);
