@@ -52,10 +52,11 @@ def build_problem(torch, synthetic, ops, dev, T, n_layers, n_inputs):
 
 
 def step_fn(ops, layer, router, x, bufs):
+    """One decode layer call from hidden states: the whole-layer entry (router GEMV, top-k, permutation, expert
+    GEMVs, combine)."""
     w, b = router
-    logits = ops.router_logits(x, w)
-    ids, wts = ops.router_topk(logits, TOPK, b, routed_scale=SCALE)
-    ops.moe_forward_ids(layer, x, ids, wts, limit=LIMIT, out=bufs["out"])
+    _, ids, wts = ops.moe_layer(layer, x, router_w=w, topk=TOPK, bias=b, routed_scale=SCALE, limit=LIMIT,
+                                out=bufs["out"], picks_out=(bufs["ids"], bufs["wts"]))
     return ids, wts
 
 
@@ -92,7 +93,9 @@ def run_decode(args, torch, mi355moe, dev):
         " GB) ...")
     layers, routers, xs = build_problem(torch, synthetic, ops, dev, T, n_layers, n_inputs)
     combos = [(l, i) for i in range(n_inputs) for l in range(n_layers)]
-    bufs = {c: {"out": torch.empty(T, K, dtype=torch.bfloat16, device=dev)} for c in combos}
+    bufs = {c: {"out": torch.empty(T, K, dtype=torch.bfloat16, device=dev),
+                "ids": torch.empty(T, TOPK, dtype=torch.int32, device=dev),
+                "wts": torch.empty(T, TOPK, dtype=torch.float32, device=dev)} for c in combos}
     # eager pass: routing of every combo (distinct experts per call) and workspace sizing before capture
     info = {}
     for c in combos:

@@ -379,6 +379,54 @@ int mi355moe_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* x, in
                                        workspace_bytes, MI355MOE_PATH_AUTO, MI355MOE_STAGE_ALL, stream);
 }
 
+// The decode path's plan, workspace carve and argument blocks for T tokens x topk pairs (route tables: the caller
+// sets the id and weight sources).
+static int prep_decode(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride, int64_t T,
+                       int64_t topk, float limit, void* out, int out_dtype, int64_t out_stride, void* workspace,
+                       size_t workspace_bytes, DecodePlan& p, DecodeWs& w) {
+    const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n, P = T * topk;
+    p = plan_decode(P, T, n, K, N, shared_flag(layer));
+    if (p.S_cap > 65535) return MI355MOE_ELIMIT;
+    carve_decode(workspace, P, n, K, N, p, true, w);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    RouteArgs& r = w.ra;
+    r.P = (int)P;
+    r.topk = (int)topk;
+    r.n = (int)n;
+    r.R = 1 << 30;
+    r.seg = p.seg;
+    r.S_cap = p.S_cap;
+    DecodeArgs& d = w.da;
+    d.wt = tables(layer);
+    d.n = (int)n;
+    d.K = (int)K;
+    d.N = (int)N;
+    d.P = (int)P;
+    d.T = (int)T;
+    d.x = x;
+    d.xdt = dt_act(x_dtype);
+    d.x_stride = x_stride;
+    d.tok = r.tok;
+    d.w16 = r.w16;
+    d.pe = r.pe;
+    d.inv = r.inv;
+    d.seg_expert = r.seg_expert;
+    d.seg_row0 = r.seg_row0;
+    d.seg_rows = r.seg_rows;
+    d.nseg = r.nseg;
+    d.S_cap = p.S_cap;
+    d.sk_gu = p.sk_gu;
+    d.sk_dn = p.sk_dn;
+    d.shared_suh = shared_flag(layer);
+    d.limit = limit;
+    d.out = out;
+    d.odt = dt_w(out_dtype);
+    d.out_stride = out_stride;
+    d.accumulate = 0;
+    d.topk = (int)topk;
+    return 0;
+}
+
 int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
                                 int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
                                 int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
@@ -400,8 +448,8 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
     const int use = choose_path(layer, P, path);
     if (use == MI355MOE_PATH_PREFILL && !(layer->flags & MI355MOE_LAYER_SHARED_W13_SUH))
         return MI355MOE_EUNSUPPORTED;                   // the grouped tier gathers once with the gate's suh
-    RouteArgs r;
     if (use == MI355MOE_PATH_PREFILL) {
+        RouteArgs r;
         PrefillWs w;
         int S_cap;
         carve_prefill(workspace, P, T, n, K, N, w, S_cap);
@@ -452,55 +500,82 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
         if (stages & MI355MOE_STAGE_COMBINE) kernels |= 8;
         return rc_launch(launch_prefill(d, stream, kernels));
     }
-    const DecodePlan p = plan_decode(P, T, n, K, N, shared_flag(layer));
-    if (p.S_cap > 65535) return MI355MOE_ELIMIT;
+    DecodePlan p;
     DecodeWs w;
-    carve_decode(workspace, P, n, K, N, p, true, w);
-    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
-    r = w.ra;
+    if (int rc = prep_decode(layer, x, x_dtype, x_stride, T, topk, limit, out, out_dtype, out_stride, workspace,
+                             workspace_bytes, p, w))
+        return rc;
+    RouteArgs& r = w.ra;
     r.ids = ids;
     r.ids64 = ids_dtype == MI355MOE_I64;
     r.w = weights;
     r.wdt = dt_w(weights_dtype);
     r.emap = expert_map;
     r.n_global = expert_map ? n_global : 0;
-    r.P = (int)P;
-    r.topk = (int)topk;
-    r.n = (int)n;
-    r.R = 1 << 30;
-    r.seg = p.seg;
-    r.S_cap = p.S_cap;
-    DecodeArgs& d = w.da;
-    d.wt = tables(layer);
-    d.n = (int)n;
-    d.K = (int)K;
-    d.N = (int)N;
-    d.P = (int)P;
-    d.T = (int)T;
-    d.x = x;
-    d.xdt = dt_act(x_dtype);
-    d.x_stride = x_stride;
-    d.tok = r.tok;
-    d.w16 = r.w16;
-    d.pe = r.pe;
-    d.inv = r.inv;
-    d.seg_expert = r.seg_expert;
-    d.seg_row0 = r.seg_row0;
-    d.seg_rows = r.seg_rows;
-    d.nseg = r.nseg;
-    d.S_cap = p.S_cap;
-    d.sk_gu = p.sk_gu;
-    d.sk_dn = p.sk_dn;
-    d.shared_suh = shared_flag(layer);
-    d.limit = limit;
-    d.out = out;
-    d.odt = dt_w(out_dtype);
-    d.out_stride = out_stride;
-    d.accumulate = 0;
-    d.topk = (int)topk;
     if (stages & MI355MOE_STAGE_ROUTE)
         if (int rc = launch_route(r, stream)) return rc_launch(rc);
-    return rc_launch(launch_decode(d, p.rmax, stream, stages >> 1));
+    return rc_launch(launch_decode(w.da, p.rmax, stream, stages >> 1));
+}
+
+// ---------------------------------------------------------------------------------------------- whole layer
+
+// the router scratch after the expert path's workspace: logits [T][E], picks [T][topk] (ids, weights)
+static size_t router_scratch(void* base, int64_t T, int64_t topk, int64_t E, float** logits, int32_t** ids,
+                             float** wts) {
+    Carve c(base);
+    float* l = c.take<float>((size_t)std::max<int64_t>(1, T * E));
+    int32_t* i = c.take<int32_t>((size_t)std::max<int64_t>(1, T * topk));
+    float* wv = c.take<float>((size_t)std::max<int64_t>(1, T * topk));
+    if (logits) *logits = l;
+    if (ids) *ids = i;
+    if (wts) *wts = wv;
+    return c.off;
+}
+
+int64_t mi355moe_moe_layer_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk, int64_t E) {
+    const int64_t base = mi355moe_moe_workspace_bytes_path(layer, T, topk, MI355MOE_PATH_AUTO);
+    if (base < 0 || E < 1 || E > 1024) return -1;
+    return (int64_t)(align_up((size_t)base) + router_scratch(nullptr, T, topk, E, nullptr, nullptr, nullptr));
+}
+
+int mi355moe_moe_layer(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride, int64_t T,
+                       const void* router_w, const float* logits, int64_t E, const float* bias, int64_t topk,
+                       float routed_scale, int renormalize, float limit, void* out, int out_dtype, int64_t out_stride,
+                       int32_t* ids_out, float* weights_out, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+    if (int r = layer_shape_ok(layer)) return r;
+    if (!x || !out || !workspace || (!router_w) == (!logits)) return MI355MOE_EINVAL;
+    if (dt_act(x_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;
+    if (router_w && x_dtype != MI355MOE_BF16) return MI355MOE_EDTYPE;        // the router GEMV reads bf16
+    const int64_t K = layer->hidden;
+    if (E < 1 || E > 1024 || topk < 1 || topk > MAX_TOPK || topk > E || T < 0) return MI355MOE_ELIMIT;
+    if (router_w && (K % 512 || K > 8192 || x_stride % 8)) return MI355MOE_ESHAPE;
+    if (x_stride < K || x_stride % 2 || out_stride < K || out_stride % 2) return MI355MOE_ESHAPE;
+    if (T * topk > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (T == 0) return 0;
+    const int64_t base = mi355moe_moe_workspace_bytes_path(layer, T, topk, MI355MOE_PATH_AUTO);
+    const int64_t need = mi355moe_moe_layer_workspace_bytes(layer, T, topk, E);
+    if (base < 0 || need < 0 || (int64_t)workspace_bytes < need) return MI355MOE_EWORKSPACE;
+    float* lg;
+    int32_t* ids;
+    float* wts;
+    router_scratch(static_cast<char*>(workspace) + align_up((size_t)base), T, topk, E, &lg, &ids, &wts);
+    if (ids_out) ids = ids_out;
+    if (weights_out) wts = weights_out;
+    // router GEMV, top-k, then the routed experts from the picks
+    const float* lsrc = logits;
+    if (router_w) {
+        if (int rc = launch_router_logits(static_cast<const uint16_t*>(x), x_stride,
+                                          static_cast<const uint16_t*>(router_w), (int)T, (int)K, (int)E, lg, stream))
+            return rc_launch(rc);
+        lsrc = lg;
+    }
+    if (int rc = launch_router_topk(lsrc, (int)T, (int)E, bias, (int)topk, routed_scale, renormalize ? 1 : 0, ids, wts,
+                                    stream))
+        return rc_launch(rc);
+    return mi355moe_moe_forward_ids_ex(layer, x, x_dtype, x_stride, T, ids, MI355MOE_I32, wts, MI355MOE_F32, topk,
+                                       nullptr, 0, limit, out, out_dtype, out_stride, workspace, (size_t)base,
+                                       MI355MOE_PATH_AUTO, MI355MOE_STAGE_ALL, stream);
 }
 
 int64_t mi355moe_exl3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t P) {

@@ -65,6 +65,58 @@ __device__ __forceinline__ uint32_t prev_word(uint32_t w3, int lane) {
     return (uint32_t)__shfl((int)w3, (lane & ~7) | ((lane + 7) & 7), 64);
 }
 
+// The lane index from an opaque instruction sequence: values derived from it are recomputed where used instead of
+// being kept live (or spilled) across a long loop.
+__device__ __forceinline__ int opaque_lane() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
+// One stage of fwht128_x16 across lanes: partner = the value of lane l ^ m (m = 1, 2, 8 via DPP control CTRL);
+// the lower lane of the pair keeps own + partner, the upper partner - own (fma with +-1: exact, one rounding).
+template <int CTRL>
+__device__ __forceinline__ void fwht_xstage(float (&v)[8], bool upper) {
+    const float sg = upper ? -1.0f : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float p = __builtin_bit_cast(
+            float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), CTRL, 0xF, 0xF, false));
+        v[i] = __builtin_fmaf(v[i], sg, p);
+    }
+}
+
+// 128-point Walsh-Hadamard of four blocks per wave held 8 consecutive elements per lane (block = lane / 16, elements
+// 8 (lane % 16) .. + 7): the butterfly order of fwht128_w64 (element strides 1, 2, 4 in registers, then 8, 16, 32,
+// 64 across lanes xor 1, 2, 4, 8 inside each 16-lane row, by DPP), the lower element of every pair keeping a + b
+// and the upper a - b, so the results are bit-identical.
+__device__ __forceinline__ void fwht128_x16(float (&v)[8], int lane) {
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & h)) {
+                const float a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+    }
+    fwht_xstage<0xB1>(v, lane & 1);                                  // quad_perm [1,0,3,2]: lane ^ 1
+    fwht_xstage<0x4E>(v, lane & 2);                                  // quad_perm [2,3,0,1]: lane ^ 2
+    {
+        // lane ^ 4: row_ror:12 reads lane + 4 (lanes 0-3, 8-11 of a row), row_ror:4 lane - 4 (banks 1 and 3)
+        const float sg = (lane & 4) ? -1.0f : 1.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int x = __builtin_bit_cast(int, v[i]);
+            const int lo = __builtin_amdgcn_update_dpp(0, x, 0x12C, 0xF, 0xF, false);
+            const float p = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(lo, x, 0x124, 0xF, 0xA, false));
+            v[i] = __builtin_fmaf(v[i], sg, p);
+        }
+    }
+    fwht_xstage<0x128>(v, lane & 8);                                 // row_ror:8: lane ^ 8
+}
+
 // 128-point Walsh-Hadamard of one row held as two values per lane (lane l: elements 2l, 2l+1) of a wave:
 // butterfly strides 1 (in registers), then 2, 4, ..., 64 across lanes xor 1, 2, ..., 32; the lower element of
 // every pair keeps a + b, the upper a - b (the fixed fp32 order of exl3.cu:273-284).
@@ -115,6 +167,12 @@ __device__ __forceinline__ void st_coherent(float* p, float v) {
 }
 __device__ __forceinline__ float ld_coherent(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_coherent(const int* p) {
+    return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Returns true in the workgroup that completes counter `c` (the `total`-th arrival); it then resets the counter.

@@ -105,53 +105,67 @@ __device__ __forceinline__ int xa_pos(int k) {
     return 16 * (k >> 4) + 4 * ((kk & 7) >> 1) + (kk & 1) + 2 * (kk >> 3);
 }
 
-// rot_in_block in two phases so a wave can have several blocks' loads in flight: rot_load fetches this lane's two
-// inputs and two suh values, rot_store rotates them and writes them into a staged row (dst = the row, k0 = local k
-// of the block, a multiple of 128).
-struct RotIn {
-    uint32_t x2, s2;
+// Staged-input preparation, four 128-blocks per wave (one per 16-lane row, 8 consecutive inputs per lane):
+// rot8_load fetches a lane's 8 inputs and 8 suh values, rot8_scale forms fp16(x * suh) as floats (bf16 inputs are
+// first rounded to fp16, as x.half() does), fwht128_x16 rotates, and the stores write fp16(v * r) into the staged
+// row in the matrix-core order (xa_pos), plain or duplicated.
+struct RotIn8 {
+    uint32_t x[4];
+    u32x4 s;
 };
-// global-address-space 4-byte load (a plain pointer from a pointer table would otherwise become a flat load, which
-// also counts against the scalar-load counter and serialises the prologue)
+// global-address-space loads (a plain pointer from a pointer table would otherwise become a flat load, which also
+// counts against the scalar-load counter and serialises the prologue)
 typedef __attribute__((address_space(1))) const uint32_t gu32;
+typedef __attribute__((address_space(1))) const u32x4 gu32x4;
 __device__ __forceinline__ uint32_t ld_g32(const void* p) {
     return *reinterpret_cast<gu32*>(reinterpret_cast<uintptr_t>(p));
 }
-__device__ __forceinline__ RotIn rot_load(const void* x, size_t xoff, const _Float16* suh, int lane) {
-    return RotIn{ld_g32(reinterpret_cast<const uint16_t*>(x) + xoff + 2 * lane), ld_g32(suh + 2 * lane)};
+__device__ __forceinline__ u32x4 ld_g128(const void* p) {
+    return *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(p));
 }
-// x * suh rounded to fp16 (bf16 inputs are first rounded to fp16, as x.half() does), as two floats; branch-free in
-// the input type so the first use of a load batch needs no control-flow join
-__device__ __forceinline__ void rot_scale(const RotIn& v, int xdt, float& p0, float& p1) {
+// x: 4-byte aligned (even row stride), read as dwords; suh: whole 16-byte chunks
+__device__ __forceinline__ RotIn8 rot8_load(const void* x, size_t xoff, const _Float16* suh) {
+    const uint16_t* xp = reinterpret_cast<const uint16_t*>(x) + xoff;
+    return RotIn8{{ld_g32(xp), ld_g32(xp + 2), ld_g32(xp + 4), ld_g32(xp + 6)}, ld_g128(suh)};
+}
+// branch-free in the input type, so the first use of a load batch needs no control-flow join
+__device__ __forceinline__ void rot8_scale(const RotIn8& v, int xdt, float (&p)[8]) {
     const bool bf = xdt == DT_BF16;
-    const _Float16 h0 = bf ? (_Float16)__builtin_bit_cast(float, v.x2 << 16) : u16_as_h(v.x2 & 0xFFFFu);
-    const _Float16 h1 = bf ? (_Float16)__builtin_bit_cast(float, v.x2 & 0xFFFF0000u) : u16_as_h(v.x2 >> 16);
-    const h2 s = __builtin_bit_cast(h2, v.s2);
-    p0 = (float)(_Float16)(h0 * s.x);
-    p1 = (float)(_Float16)(h1 * s.y);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = v.x[i];
+        const _Float16 h0 = bf ? (_Float16)__builtin_bit_cast(float, w << 16) : u16_as_h(w & 0xFFFFu);
+        const _Float16 h1 = bf ? (_Float16)__builtin_bit_cast(float, w & 0xFFFF0000u) : u16_as_h(w >> 16);
+        // (the suh word goes through a scalar first: hipcc miscompiles bit_cast of an ext_vector element indexed in
+        // an unrolled loop, reading element 0 every time)
+        const uint32_t sw = v.s[i];
+        p[2 * i] = (float)(_Float16)(h0 * u16_as_h(sw & 0xFFFFu));
+        p[2 * i + 1] = (float)(_Float16)(h1 * u16_as_h(sw >> 16));
+    }
 }
-__device__ __forceinline__ void rot_store(const RotIn& v, int xdt, uint16_t* dst, int k0, int lane) {
-    float p0, p1;
-    rot_scale(v, xdt, p0, p1);
-    fwht128_w64(p0, p1, lane);
-    *reinterpret_cast<h2*>(dst + xa_pos(k0 + 2 * lane)) = h2{(_Float16)(p0 * HAD_R), (_Float16)(p1 * HAD_R)};
+__device__ __forceinline__ uint32_t dup16(_Float16 h) {
+    const uint32_t u = h_as_u16(h);
+    return u | (u << 16);
+}
+// 8 consecutive values at local k0 (a multiple of 8) of a staged row: value j goes to position xa_pos(k0 + j) =
+// 16 (k0 / 16) + 4 (j / 2) + j % 2 + 2 ((k0 / 8) % 2), as halves (plain) or duplicated dwords
+__device__ __forceinline__ void stage8_store(const float (&p)[8], uint16_t* row, int k0) {
+    uint16_t* d = row + (k0 & ~15) + 2 * ((k0 >> 3) & 1);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<h2*>(d + 4 * m) = h2{(_Float16)(p[2 * m] * HAD_R), (_Float16)(p[2 * m + 1] * HAD_R)};
+}
+__device__ __forceinline__ void stage8_store_dup(const float (&p)[8], uint32_t* row, int k0) {
+    uint32_t* d = row + (k0 & ~15) + 2 * ((k0 >> 3) & 1);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<uint2*>(d + 4 * m) =
+            make_uint2(dup16((_Float16)(p[2 * m] * HAD_R)), dup16((_Float16)(p[2 * m + 1] * HAD_R)));
 }
 
 // Segments of up to DUP_ROWS rows stage each input duplicated into a dword (x, x) at dword xa_pos(k) of the row,
 // so the matrix-core A operand of a word is one 16-byte LDS read (no per-step permutes).
 constexpr int DUP_ROWS = 4;
-__device__ __forceinline__ uint32_t dup16(_Float16 h) {
-    const uint32_t u = h_as_u16(h);
-    return u | (u << 16);
-}
-// rot_store into a duplicated staged row (dst = the row's first dword)
-__device__ __forceinline__ void rot_store_dup(const RotIn& v, int xdt, uint32_t* dst, int k0, int lane) {
-    float p0, p1;
-    rot_scale(v, xdt, p0, p1);
-    fwht128_w64(p0, p1, lane);
-    *reinterpret_cast<uint2*>(dst + xa_pos(k0 + 2 * lane)) =
-        make_uint2(dup16((_Float16)(p0 * HAD_R)), dup16((_Float16)(p1 * HAD_R)));
-}
 
 // The raw codebook word of a state: its two fp16 halves sum to the weight.
 __device__ __forceinline__ uint32_t mcg_word(uint32_t s) { return ((s * MCG_MUL) & MCG_MASK) ^ MCG_FLIP; }
@@ -230,7 +244,6 @@ __device__ __forceinline__ void step_mfma2_dup(const u32x4& wg, uint32_t pwg, co
 }
 
 // Streamed weight load: a global-address-space 16-byte load marked non-temporal (read once per call).
-typedef __attribute__((address_space(1))) const u32x4 gu32x4;
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
     return __builtin_nontemporal_load(reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(p)));
 }
@@ -266,25 +279,38 @@ __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
     const int RSD = KR + 4;
     const bool dup = SHARED && rn <= DUP_ROWS;
 
-    // prologue: the segment's rotated inputs for this K range, eight (row, matrix, 128-block) tasks per wave per
-    // batch. The first batch's input loads are issued unconditionally (task index clamped) before the weight
-    // prefetch: loads return in issue order, so inputs queued behind the prefetch would wait for all of it.
-    // The segment's token ids are read once, one per lane, and handed to tasks with readlane (per-task scalar
-    // loads would each wait for the previous one).
-    constexpr int TB = 8;
+    // prologue: the segment's rotated inputs for this K range as (row, matrix, 128-block) tasks, four per wave at
+    // a time (one per 16-lane row), one quad per wave per batch. The first batch's loads are issued unconditionally
+    // (task index clamped) before the weight prefetch: loads return in issue order, so inputs queued behind the
+    // prefetch would wait for all of it. The segment's token ids are read once, one per lane.
+    const int g4 = lane >> 4, l16 = lane & 15;
     const int nb = KR >> 7, ntask = rn * NMAT * nb;
     const int tokl = a.tok[row0 + min(lane, rn - 1)];
     const _Float16* suhg = reinterpret_cast<const _Float16*>(a.wt.g_suh[e]) + kbase;
     const _Float16* suhu = reinterpret_cast<const _Float16*>(a.wt.u_suh[e]) + kbase;
+    auto task_of = [&](int c, int t0) { return t0 + 4 * (c * GU_WAVES + wv) + g4; };   // t0: batch base
     auto task_load = [&](int task) {
         task = min(task, ntask - 1);
         const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
-        const int tk = __builtin_amdgcn_readlane(tokl, r);
-        return rot_load(a.x, (size_t)tk * a.x_stride + kbase + b * 128, (mat ? suhu : suhg) + b * 128, lane);
+        const int tk = __shfl(tokl, r, 64);
+        return rot8_load(a.x, (size_t)tk * a.x_stride + kbase + b * 128 + 8 * l16,
+                         (mat ? suhu : suhg) + b * 128 + 8 * l16);
     };
-    RotIn v[TB];
+    auto task_store = [&](int task, const RotIn8& vv) {
+        float p[8];
+        rot8_scale(vv, a.xdt, p);
+        fwht128_x16(p, lane);
+        const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
+        if (task < ntask) {
+            if (dup) stage8_store_dup(p, xw + (size_t)r * RSD, b * 128 + 8 * l16);
+            else stage8_store(p, xs + (size_t)(mat * rn + r) * RSH, b * 128 + 8 * l16);
+        }
+    };
+    constexpr int QB = 1;                                            // quads per wave per batch
+    constexpr int BT = 4 * QB * GU_WAVES;                            // tasks per batch
+    RotIn8 v[QB];
 #pragma unroll
-    for (int c = 0; c < TB; ++c) v[c] = task_load(wv + c * GU_WAVES);
+    for (int c = 0; c < QB; ++c) v[c] = task_load(task_of(c, 0));
     __builtin_amdgcn_sched_barrier(0);
 
     const int t = lane >> 3, q = lane & 7;
@@ -305,20 +331,13 @@ __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
     __builtin_amdgcn_sched_barrier(0);
 
     // the first batch in straight-line code (so its wait leaves the prefetch in flight), then any further batches
-    auto task_store = [&](int task, const RotIn& vv) {
-        const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
-        if (dup) rot_store_dup(vv, a.xdt, xw + (size_t)r * RSD, b * 128, lane);
-        else rot_store(vv, a.xdt, xs + (size_t)(mat * rn + r) * RSH, b * 128, lane);
-    };
 #pragma unroll
-    for (int c = 0; c < TB; ++c)
-        if (wv + c * GU_WAVES < ntask) task_store(wv + c * GU_WAVES, v[c]);
-    for (int t0 = wv + TB * GU_WAVES; t0 < ntask; t0 += TB * GU_WAVES) {
+    for (int c = 0; c < QB; ++c) task_store(task_of(c, 0), v[c]);
+    for (int t0 = BT; t0 < ntask; t0 += BT) {
 #pragma unroll
-        for (int c = 0; c < TB; ++c) v[c] = task_load(t0 + c * GU_WAVES);
+        for (int c = 0; c < QB; ++c) v[c] = task_load(task_of(c, t0));
 #pragma unroll
-        for (int c = 0; c < TB; ++c)
-            if (t0 + c * GU_WAVES < ntask) task_store(t0 + c * GU_WAVES, v[c]);
+        for (int c = 0; c < QB; ++c) task_store(task_of(c, t0), v[c]);
     }
     __syncthreads();
 
@@ -439,33 +458,45 @@ __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
         __syncthreads();
     }
 
-    // epilogue: output Hadamard, SwiGLU, down-input rotation; wave w takes rows w, w + 8
-    const int col = cb * 128 + 2 * lane;
-    const h2 svg = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + col);
-    const h2 svu = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + col);
-    const h2 sud = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + col);
-    const float L = a.limit;
-    for (int r = wv; r < rn; r += GU_WAVES) {
-        const size_t row = row0 + r;
-        float g[2] = {zs[r * 128 + 2 * lane], zs[r * 128 + 2 * lane + 1]};
-        float u[2] = {zs[(ZS_ROWS + r) * 128 + 2 * lane], zs[(ZS_ROWS + r) * 128 + 2 * lane + 1]};
-        fwht128_w64(g[0], g[1], lane);
-        fwht128_w64(u[0], u[1], lane);
-        float b[2];
+    // epilogue: output Hadamard, SwiGLU, down-input rotation; wave w takes rows 4w .. 4w + 3 (one per 16-lane row),
+    // lane columns 8 (lane % 16) .. + 7 of the block; rows past rn repeat the last row and are not stored
+    if (wv * 4 < rn) {
+        // the lane's coordinates are re-derived here so nothing of the epilogue stays live across the main loop
+        const int ln = opaque_lane(), eg4 = ln >> 4, el16 = ln & 15;
+        const int rr = wv * 4 + eg4, r = min(rr, rn - 1);
+        const int colb = cb * 128 + 8 * el16;
+        const u32x4 svg = ld_g128(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + colb);
+        const u32x4 svu = ld_g128(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + colb);
+        const u32x4 sud = ld_g128(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + colb);
+        auto half = [](const u32x4& v, int i) { return u16_as_h(v[i >> 1] >> (16 * (i & 1))); };
+        const float L = a.limit;
+        float g[8], u[8], bv[8];
+        *reinterpret_cast<float4*>(g) = *reinterpret_cast<const float4*>(zs + r * 128 + 8 * el16);
+        *reinterpret_cast<float4*>(g + 4) = *reinterpret_cast<const float4*>(zs + r * 128 + 8 * el16 + 4);
+        *reinterpret_cast<float4*>(u) = *reinterpret_cast<const float4*>(zs + (ZS_ROWS + r) * 128 + 8 * el16);
+        *reinterpret_cast<float4*>(u + 4) = *reinterpret_cast<const float4*>(zs + (ZS_ROWS + r) * 128 + 8 * el16 + 4);
+        fwht128_x16(g, ln);
+        fwht128_x16(u, ln);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float gv = g[i] * HAD_R * (float)(i ? svg.y : svg.x);
-            float uv = u[i] * HAD_R * (float)(i ? svu.y : svu.x);
+        for (int i = 0; i < 8; ++i) {
+            const float gv = g[i] * HAD_R * (float)half(svg, i);
+            float uv = u[i] * HAD_R * (float)half(svu, i);
             float sv = gv * sigmoid_dexp(gv);
             if (L != 0.0f) {
                 sv = fminf(sv, L);
                 uv = fminf(fmaxf(uv, -L), L);
             }
             const _Float16 a16 = (_Float16)(sv * uv);
-            b[i] = (float)(_Float16)(a16 * (i ? sud.y : sud.x));
+            bv[i] = (float)(_Float16)(a16 * half(sud, i));
         }
-        fwht128_w64(b[0], b[1], lane);
-        *reinterpret_cast<h2*>(a.xd + row * N + col) = h2{(_Float16)(b[0] * HAD_R), (_Float16)(b[1] * HAD_R)};
+        fwht128_x16(bv, ln);
+        if (rr < rn) {
+            u32x4 o;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                o[m] = h_as_u16((_Float16)(bv[2 * m] * HAD_R)) | (h_as_u16((_Float16)(bv[2 * m + 1] * HAD_R)) << 16);
+            *reinterpret_cast<u32x4*>(a.xd + (size_t)(row0 + rr) * N + colb) = o;
+        }
     }
     if (a.sk_gu > 1 && tid == 0) *cnt = 0u;
 }
@@ -606,25 +637,33 @@ __global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
         __syncthreads();
     }
 
-    // epilogue: (row, 128-column block) tasks; output Hadamard, scale, then atomics or the per-pair contribution
-    const int NBLK = ncol / 128;
-    for (int task = wv; task < rn * NBLK; task += DN_WAVES) {
-        const int r = task / NBLK, hb = task % NBLK;
+    // epilogue: (row, 128-column block) tasks, four per wave at a time (one per 16-lane row, 8 columns per lane);
+    // output Hadamard, scale, then atomics or the per-pair contribution
+    const int NBLK = ncol / 128, ntk = rn * NBLK;
+    const int ln = opaque_lane(), g4 = ln >> 4, l16 = ln & 15;
+    for (int t0 = 4 * wv; t0 < ntk; t0 += 4 * DN_WAVES) {
+        const int task = t0 + g4, tc = min(task, ntk - 1);
+        const int r = tc / NBLK, hb = tc - r * NBLK;
         const size_t row = row0 + r;
-        if (a.pe[row] < 0) continue;                                 // a row whose token id was out of range
-        const int col = cb * DN_COLS + hb * 128 + 2 * lane;
-        const h2 svd = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + col);
-        float v[2] = {zs[r * DN_COLS + hb * 128 + 2 * lane], zs[r * DN_COLS + hb * 128 + 2 * lane + 1]};
-        fwht128_w64(v[0], v[1], lane);
+        const int col = cb * DN_COLS + hb * 128 + 8 * l16;
+        const u32x4 svd = ld_g128(reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + col);
+        float v[8];
+        *reinterpret_cast<float4*>(v) = *reinterpret_cast<const float4*>(zs + r * DN_COLS + hb * 128 + 8 * l16);
+        *reinterpret_cast<float4*>(v + 4) = *reinterpret_cast<const float4*>(zs + r * DN_COLS + hb * 128 + 8 * l16 + 4);
+        fwht128_x16(v, ln);
         const float rs = HAD_R * (float)u16_as_h(a.w16[row]);
-        v[0] = v[0] * rs * (float)svd.x;
-        v[1] = v[1] * rs * (float)svd.y;
-        if (a.accumulate) {
-            float* o = reinterpret_cast<float*>(a.out) + (size_t)a.tok[row] * a.out_stride + col;
-            atomicAdd(o, v[0]);
-            atomicAdd(o + 1, v[1]);
-        } else {
-            *reinterpret_cast<float2*>(a.contrib + row * K + col) = make_float2(v[0], v[1]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = v[i] * rs * (float)u16_as_h(svd[i >> 1] >> (16 * (i & 1)));
+        if (task < ntk && a.pe[row] >= 0) {                          // pe < 0: a row whose token id was out of range
+            if (a.accumulate) {
+                float* o = reinterpret_cast<float*>(a.out) + (size_t)a.tok[row] * a.out_stride + col;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) atomicAdd(o + i, v[i]);
+            } else {
+                float4* o = reinterpret_cast<float4*>(a.contrib + row * K + col);
+                o[0] = make_float4(v[0], v[1], v[2], v[3]);
+                o[1] = make_float4(v[4], v[5], v[6], v[7]);
+            }
         }
     }
     if (a.sk_dn > 1 && tid == 0) *cnt = 0u;

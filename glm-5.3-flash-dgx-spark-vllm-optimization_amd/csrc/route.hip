@@ -23,15 +23,14 @@ constexpr int RL_MAXC = 16;    // K chunks of 512 (K <= 8192)
 // One workgroup per expert, one wave per 512-wide chunk c of K. Lane l of chunk c accumulates k = 512c + 8l + i,
 // i = 0..7, sequentially in fp32 (bf16 x bf16 products are exact in fp32, so the fused multiply-add rounds like
 // an add); the 64 lane partials are combined by the xor butterfly m = 32, 16, ..., 1; the chunk sums are then added
-// in chunk order c = 0, 1, ... (wave 0 adds them from LDS).
-__global__ __launch_bounds__(1024) void router_logits_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
-                                                             const uint16_t* __restrict__ w, int T, int K, int E,
-                                                             float* __restrict__ logits) {
+// in chunk order c = 0, 1, ... (wave 0 adds them from LDS). Waves past K/512 only join the barriers.
+__device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int64_t x_stride,
+                                            const uint16_t* __restrict__ w, int T, int K, int E, int e,
+                                            float* __restrict__ logits) {
     __shared__ float part[RL_MAXC][RL_TCHUNK];
     const int lane = threadIdx.x & 63;
     const int c = threadIdx.x >> 6;                 // chunk of this wave
     const int chunks = K / 512;
-    const int e = blockIdx.x;
     const int k0 = c * 512 + lane * 8;
     u32x4 wv = {0u, 0u, 0u, 0u};
     if (c < chunks) wv = *reinterpret_cast<const u32x4*>(w + (size_t)e * K + k0);
@@ -61,12 +60,18 @@ __global__ __launch_bounds__(1024) void router_logits_kernel(const uint16_t* __r
         }
         __syncthreads();
         if (threadIdx.x < RL_TCHUNK && t0 + (int)threadIdx.x < T) {
-            float s = part[0][threadIdx.x];
-            for (int cc = 1; cc < chunks; ++cc) s = s + part[cc][threadIdx.x];
-            logits[(size_t)(t0 + threadIdx.x) * E + e] = s;
+            float sum = part[0][threadIdx.x];
+            for (int cc = 1; cc < chunks; ++cc) sum = sum + part[cc][threadIdx.x];
+            logits[(size_t)(t0 + threadIdx.x) * E + e] = sum;
         }
         __syncthreads();
     }
+}
+
+__global__ __launch_bounds__(1024) void router_logits_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                             const uint16_t* __restrict__ w, int T, int K, int E,
+                                                             float* __restrict__ logits) {
+    logits_body(x, x_stride, w, T, K, E, blockIdx.x, logits);
 }
 
 // ------------------------------------------------------------------------------------------------ router top-k
@@ -74,26 +79,26 @@ __global__ __launch_bounds__(1024) void router_logits_kernel(const uint16_t* __r
 constexpr int TOPK_MAX_E = 1024;   // experts per token row
 constexpr int TOPK_MAX_K = 32;
 
-// grid T, 1024 threads per token: scores s = sigmoid(logit) (through double exp) and choice keys s + bias go to
+// 1024 threads per token: scores s = sigmoid(logit) (through double exp) and choice keys s + bias go to
 // LDS; every candidate's rank = the number of candidates with a larger key, or an equal key and a lower id (ranks
 // are distinct and follow the reference's order: largest first, lower id on ties). Q = 1024 / E16 threads share a
 // candidate, each counting over a slice of the keys; the topk lowest ranks write themselves to their slot and the
-// renormalising total is summed sequentially in pick order.
-__global__ __launch_bounds__(1024) void router_topk_kernel(const float* __restrict__ logits, int T, int E,
-                                                           const float* __restrict__ bias, int topk, float scale,
-                                                           int renorm, int32_t* __restrict__ ids,
-                                                           float* __restrict__ wts) {
+// renormalising total is summed sequentially in pick order. blockDim.x = 512 or 1024 >= E16.
+__device__ __forceinline__ void topk_body(const float* __restrict__ lrow, int E, const float* __restrict__ bias,
+                                          int topk, float scale, int renorm, int32_t* __restrict__ ids_row,
+                                          float* __restrict__ wts_row) {
     __shared__ __align__(16) float key[TOPK_MAX_E];
     __shared__ float sco[TOPK_MAX_E];
     __shared__ int part[1024];
     __shared__ int pick_e[TOPK_MAX_K];
     __shared__ float pick_s[TOPK_MAX_K];
-    const int t = blockIdx.x, tid = threadIdx.x;
+    const int tid = threadIdx.x;
     const int E16 = (E + 15) & ~15;                                  // keys padded with -inf (never ahead of a key)
-    for (int e = tid; e < E16; e += 1024) {
+    const int BD = blockDim.x;                                       // 512 or 1024; E16 <= BD
+    for (int e = tid; e < E16; e += BD) {
         float sv = 0.f, kv = -__builtin_inff();
         if (e < E) {
-            const float lg = logits[(size_t)t * E + e];
+            const float lg = lrow[e];
             sv = (float)(1.0 / (1.0 + exp(-(double)lg)));
             kv = sv + (bias ? bias[e] : 0.f);
         }
@@ -101,7 +106,7 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(const float* __restri
         key[e] = kv;
     }
     __syncthreads();
-    const int Q = E16 <= 256 ? 4 : (E16 <= 512 ? 2 : 1);
+    const int Q = E16 <= BD / 4 ? 4 : (E16 <= BD / 2 ? 2 : 1);
     const int c = tid / Q, p = tid - c * Q;
     const int slice = E16 / Q;                                       // a multiple of 4 (E16 % 16 == 0)
     int greater = 0, tie = 0;
@@ -138,9 +143,18 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(const float* __restri
         float wv = pick_s[tid];
         if (renorm) wv = __fdiv_rn(wv, total + 1e-20f);
         wv = wv * scale;
-        ids[(size_t)t * topk + tid] = pick_e[tid];
-        wts[(size_t)t * topk + tid] = wv;
+        ids_row[tid] = pick_e[tid];
+        wts_row[tid] = wv;
     }
+}
+
+// grid T, 1024 threads: one token's top-k per workgroup
+__global__ __launch_bounds__(1024) void router_topk_kernel(const float* __restrict__ logits, int T, int E,
+                                                           const float* __restrict__ bias, int topk, float scale,
+                                                           int renorm, int32_t* __restrict__ ids,
+                                                           float* __restrict__ wts) {
+    const int t = blockIdx.x;
+    topk_body(logits + (size_t)t * E, E, bias, topk, scale, renorm, ids + (size_t)t * topk, wts + (size_t)t * topk);
 }
 
 // ------------------------------------------------------------------------------------------------ permutation
@@ -231,16 +245,16 @@ __device__ __forceinline__ void zero_counters(const RouteArgs& a) {
         a.zero[i] = 0u;
 }
 
-// One block does the whole permutation (P <= ROUTE_SMALL_MAX_P). Shared memory: local[P], cnt[n+1], start[n+1].
+// One block does the whole permutation (P <= ROUTE_SMALL_MAX_P). Shared memory sh: local[P], cnt[n+1], start[n+1].
 template <typename IT>
-__global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
-    extern __shared__ int sh[];
+__device__ void route_small_body(const RouteArgs& a, int* sh) {
     __shared__ int tot[16];
     int* loc = sh;
     int* cnt = sh + a.P;
     int* start = cnt + (a.n + 1);
     const IT* ids = reinterpret_cast<const IT*>(a.ids);
-    zero_counters(a);
+    if (a.zero)
+        for (int64_t i = threadIdx.x; i < a.zero_words; i += blockDim.x) a.zero[i] = 0u;
     for (int e = threadIdx.x; e <= a.n; e += blockDim.x) cnt[e] = 0;
     __syncthreads();
     for (int j = threadIdx.x; j < a.P; j += blockDim.x) {
@@ -273,6 +287,12 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
         a.pe[pos] = (l < a.n && cnt[l] <= a.R) ? l : -1;
         a.inv[j] = pos;
     }
+}
+
+template <typename IT>
+__global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
+    extern __shared__ int sh[];
+    route_small_body<IT>(a, sh);
 }
 
 // Tables from pre-sorted pairs (the exl3_moe contract): counts [n+1] int64 give each expert's span of the sorted

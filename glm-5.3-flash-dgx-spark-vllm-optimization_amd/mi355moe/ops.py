@@ -188,3 +188,58 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
         float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), int(path),
         int(stages), _stream(dev)))
     return out
+
+
+def moe_layer(experts: Exl3Experts, x: torch.Tensor, router_w: torch.Tensor | None = None,
+              logits: torch.Tensor | None = None, topk: int = 8, bias: torch.Tensor | None = None,
+              routed_scale: float = 1.0, renormalize: bool = True, limit: float = 10.0,
+              out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+              return_picks: bool = False, picks_out: tuple | None = None):
+    """Routed-expert output [T, K] of one MoE layer from its hidden states: router logits (from router_w bf16
+    [E, K], or the given fp32 logits [T, E]), sigmoid + bias top-k, permutation, expert GEMMs and combine in one
+    call (small calls run router, top-k and permutation as one launch). With return_picks, also (ids int32, weights
+    fp32), both [T, topk], written into picks_out when given."""
+    if (router_w is None) == (logits is None):
+        raise ValueError("give exactly one of router_w and logits")
+    dev = _need_cuda(x, router_w, logits, bias)
+    if dev != experts.device:
+        raise ValueError(f"activations on {dev}, experts on {experts.device}")
+    if x.dim() != 2 or x.shape[1] != experts.K or x.stride(1) != 1:
+        raise ValueError(f"x must be [T, {experts.K}] with unit column stride")
+    T = x.shape[0]
+    if router_w is not None:
+        if x.dtype != torch.bfloat16 or router_w.dtype != torch.bfloat16:
+            raise ValueError("the router GEMV takes bf16 x and bf16 router_w")
+        rw = router_w.contiguous()
+        E = rw.shape[0]
+        lg = None
+    else:
+        lg = logits.float().contiguous()
+        E = lg.shape[1]
+        rw = None
+    b = None if bias is None else bias.float().contiguous()
+    if b is not None and b.numel() != E:
+        raise ValueError("bias must have one entry per expert")
+    if out is None:
+        out = torch.empty(T, experts.K, dtype=out_dtype or x.dtype, device=dev)
+    if out.shape != (T, experts.K) or out.stride(1) != 1:
+        raise ValueError("out must be [T, K] with unit column stride")
+    ids = wts = None
+    if picks_out is not None:
+        ids, wts = picks_out
+        if (ids.shape != (T, topk) or ids.dtype != torch.int32 or not ids.is_contiguous() or wts.shape != (T, topk)
+                or wts.dtype != torch.float32 or not wts.is_contiguous()):
+            raise ValueError("picks_out must be contiguous (int32 [T, topk], fp32 [T, topk])")
+    elif return_picks:
+        ids = torch.empty(T, topk, dtype=torch.int32, device=dev)
+        wts = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    nb = L.mi355moe_moe_layer_workspace_bytes(ctypes.byref(experts.desc), T, topk, E)
+    if nb < 0:
+        raise ValueError("mi355moe_moe_layer_workspace_bytes rejected the shape")
+    ws = workspace(dev, nb)
+    _lib.check("mi355moe_moe_layer", L.mi355moe_moe_layer(
+        ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(rw), _p(lg), E, _p(b), topk,
+        float(routed_scale), int(bool(renormalize)), float(limit), _p(out), weight_dtype_code(out.dtype),
+        out.stride(0), _p(ids), _p(wts), _p(ws), ws.numel(), _stream(dev)))
+    return (out, ids, wts) if (return_picks or picks_out is not None) else out

@@ -147,6 +147,22 @@ int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int6
                       int gate_mul1, int up_mcg, int up_mul1, int down_mcg, int down_mul1, float act_limit,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* The routed-expert output of one MoE layer from its hidden states, in one call: router logits x . W^T in fp32
+ * (mi355moe_router_logits' order) or given logits, sigmoid + bias top-k with renormalisation and routed scale
+ * (mi355moe_router_topk), the token -> expert permutation, the expert GEMMs and the slot-order combine. Replaces the
+ * routed part of the model's MoE block: the gate linear (code/fork/docs/BF16_GEMV.md:27,38), vLLM grouped_topk with
+ * one group (code/fork/tests/router_topk_agreement.py:58-61) and FusedMoE.apply (code/fork/docs/
+ * prod_exl3_reference.py:1788-1823). Exactly one of router_w (bf16 [E][hidden]; x must then be BF16 with
+ * x_stride % 8 == 0 and hidden % 512 == 0, hidden <= 8192) and logits (fp32 [T][E]) is given; bias may be NULL.
+ * The results equal those of the separate entry points chained, bit for bit. ids_out / weights_out (optional,
+ * int32 / fp32 [T][topk]) receive the picks. E <= 1024, topk <= 32. */
+int64_t mi355moe_moe_layer_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk, int64_t E);
+int mi355moe_moe_layer(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride, int64_t T,
+                       const void* router_w, const float* logits, int64_t E, const float* bias, int64_t topk,
+                       float routed_scale, int renormalize, float limit, void* out, int out_dtype, int64_t out_stride,
+                       int32_t* ids_out, float* weights_out, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
 /* ---------------------------------------------------------------- e4m3 expert variant */
 
 /* One layer of block-scaled e4m3 routed experts in vLLM's fp8 w8a8 block-quantised MoE layout (128x128 blocks):
