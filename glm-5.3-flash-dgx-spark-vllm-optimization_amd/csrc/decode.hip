@@ -260,12 +260,10 @@ constexpr int ZS_ROWS = 16;
 // (all of K unless small segment counts call for splits); wave (cg, kh) = columns 32cg..32cg+31 over half kh of the
 // range, DEPTH steps of loads in flight. The halves are added in LDS; with one split the epilogue follows directly,
 // with several each split stores its partial and the workgroup that arrives last adds them in split order.
+// The gate/up tile (column block cb, K split ks, segment s) of a 512-thread workgroup; smem: the dynamic LDS.
 template <int DEPTH, bool SHARED>
-__global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_gateup_kernel(
-    DecodeArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int ks, int s, unsigned char* smem) {
     __shared__ int last_flag;
-    const int cb = blockIdx.x, ks = blockIdx.y, s = blockIdx.z;
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -501,16 +499,21 @@ __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
     if (a.sk_gu > 1 && tid == 0) *cnt = 0u;
 }
 
+template <int DEPTH, bool SHARED>
+__global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_gateup_kernel(
+    DecodeArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    gateup_tile<DEPTH, SHARED>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+}
+
 // grid (K/512, N splits, segments), 512 threads: workgroup = 512 output columns of one segment over one N range;
 // wave w = columns 64w..64w+63 (column tiles 4w..4w+3: the first pair as "g", the second as "u" of the two-matrix
 // step, sharing the staged input) over the whole range.
 constexpr int DN_COLS = 512;
+// The down tile (column block cb, N split ks, segment s) of a 512-thread workgroup; smem: the dynamic LDS.
 template <int DEPTH>
-__global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_down_kernel(
-    DecodeArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int ks, int s, unsigned char* smem) {
     __shared__ int last_flag;
-    const int cb = blockIdx.x, ks = blockIdx.y, s = blockIdx.z;
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -561,7 +564,6 @@ __global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
         ub[j] = ld_stream(D + pf0 + 16 + j * sstr);
     }
     __builtin_amdgcn_sched_barrier(0);
-
 #pragma unroll
     for (int c = 0; c < PB; ++c)
         if (tid + c * DN_WAVES * 64 < nchunk) chunk_store(tid + c * DN_WAVES * 64, xv[c]);
@@ -667,6 +669,13 @@ __global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
         }
     }
     if (a.sk_dn > 1 && tid == 0) *cnt = 0u;
+}
+
+template <int DEPTH>
+__global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_down_kernel(
+    DecodeArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    down_tile<DEPTH>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }
 
 // grid (T, K/256), 128 threads x 2 columns: out[t] = sum over slots k (in order) of the valid pairs' contributions
