@@ -186,4 +186,26 @@ __device__ __forceinline__ bool arrive_last(unsigned* c, unsigned total, int* fl
     return *flag != 0;
 }
 
+// ---------------------------------------------------------------------------------------------- LDS staging
+
+// Wave instruction: 64 lanes x 16 bytes, lane l -> LDS bytes lds_wave + 16 l (global_load_lds_dwordx4). Written as
+// inline assembly so the compiler adds no wait of its own for these loads: the kernels wait for them explicitly
+// (WAIT_VM) before the barrier that publishes a stage, and issue no other global loads while any are in flight.
+__device__ __forceinline__ void dma16(const void* src_lane, unsigned char* lds_wave) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src_lane)
+                 : "memory", "m0");
+}
+// The same with 4 bytes per lane: lane l -> LDS bytes lds_wave + 4 l (global_load_lds_dword).
+__device__ __forceinline__ void dma4(const void* src_lane, unsigned char* lds_wave) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(m0), "v"(src_lane)
+                 : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (n <= 15): this wave's staged loads up to the one n before the last have landed in
+// LDS, and its LDS reads of the buffer about to be refilled have returned
+#define WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0070 | (n))
+#define LDS_BARRIER() asm volatile("s_barrier" ::: "memory")
+
 }  // namespace mi355moe

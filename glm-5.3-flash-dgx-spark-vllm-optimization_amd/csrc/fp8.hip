@@ -86,16 +86,6 @@ __device__ __forceinline__ f32x16 mfma_fp8(const u32x4& a0, const u32x4& a1, con
 // lines, and the fragment reads below (32 consecutive rows, one chunk each) are free of bank conflicts.
 __device__ __forceinline__ int swz(int R) { return (R >> 1) & 7; }
 
-// Wave instruction: 64 lanes x 16 bytes, lane l -> LDS bytes lds_wave + 16 l (rows of 128 bytes: row l / 8, slot
-// l % 8). Written as inline assembly so the compiler adds no wait of its own for these loads: the kernels wait for
-// them explicitly (WAIT_VM) before the barrier that publishes a stage, and issue no other global loads while any
-// are in flight.
-__device__ __forceinline__ void dma16(const uint8_t* src_lane, unsigned char* lds_wave) {
-    const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src_lane)
-                 : "memory", "m0");
-}
-
 // The 64 bytes of row R at k half h (chunks 4h..4h+3) as four 16-byte LDS reads.
 __device__ __forceinline__ void frag64(const unsigned char* st, int R, int h, u32x4 (&v)[4]) {
     const unsigned char* row = st + R * 128;
@@ -117,10 +107,6 @@ __device__ __forceinline__ void block_acc(const u32x4 (&xa)[4], const u32x4 (&wb
 // Accumulator layout of a 32x32 tile: lane l holds column l % 32, register r row 8 (r / 4) + 4 (l / 32) + r % 4.
 __device__ __forceinline__ int tile_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
-// s_waitcnt vmcnt(n) lgkmcnt(0) (n <= 15): this wave's staged loads up to the one n before the last have landed in
-// LDS, and its LDS reads of the buffer about to be refilled have returned
-#define WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0070 | (n))
-#define LDS_BARRIER() asm volatile("s_barrier" ::: "memory")
 
 constexpr int FP8_MAX_KB = 128;           // 128-k blocks per row (hidden and intermediate <= 16384)
 constexpr int GU_ROWS = 320;              // 128 gate + 128 up weight rows + 64 activation rows per stage

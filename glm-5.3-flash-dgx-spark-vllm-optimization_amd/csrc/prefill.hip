@@ -25,10 +25,12 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int PF_TM = PREFILL_TM;   // rows per tile (segment height)
 constexpr int PF_THREADS = 512;     // 8 waves
-constexpr int PF_LD = 40;           // halves per LDS row of a 32-k step (32 + 8 padding)
-constexpr int PF_AS = PF_TM * PF_LD;            // one A stage (halves)
-constexpr int PF_BS = 2 * 128 * PF_LD;          // one B stage: 2 x 128 columns (halves)
-constexpr size_t PF_LDS = (size_t)(2 * PF_AS + 2 * PF_BS) * 2;   // 81,920 bytes
+constexpr int PF_LD = 40;           // halves per LDS row of a decoded B step (32 k + 8 padding)
+constexpr int PF_NS = 4;            // staged steps in flight (A rows and raw trellis words)
+constexpr int PF_ASB = PF_TM * 64;              // one A stage: 256 rows x 32 k fp16, bytes
+constexpr int PF_WSB = 4096;                    // one raw-word stage: 2 halves x 2 k tiles x 8 column tiles x 128 B
+constexpr int PF_BS = 2 * 128 * PF_LD;          // one decoded B stage: 2 x 128 columns (halves)
+constexpr size_t PF_LDS = (size_t)PF_NS * (PF_ASB + PF_WSB) + (size_t)2 * PF_BS * 2;   // 122,880 bytes
 
 // ------------------------------------------------------------------------------------------------ gather
 
@@ -65,14 +67,14 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
 
 // ------------------------------------------------------------------------------------------------ GEMM core
 
-// Decode this thread's two trellis words (words 2wp, 2wp+1 of one tile; the tile's 16 threads are 16 consecutive
-// lanes) into the B stage: column-major [col][k] with the k of the 32-step contiguous.
-__device__ __forceinline__ void pf_store_b(uint2 bw, int lane, int wp, _Float16* B, int col_base, int krow) {
-    const uint32_t prev = (uint32_t)__shfl((int)bw.y, (lane & ~15) | ((lane + 15) & 15), 64);
+// Decode this thread's two trellis words (words 2wp, 2wp+1 of one tile, pw = word 2wp - 1 mod 32) into the B
+// stage: column-major [col][k] with the k of the 32-step contiguous.
+__device__ __forceinline__ void pf_store_b(uint32_t pw0, uint32_t w0, uint32_t w1, int wp, _Float16* B, int col_base,
+                                           int krow) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const uint32_t w = i ? bw.y : bw.x;
-        const uint32_t pw = i ? bw.x : prev;
+        const uint32_t w = i ? w1 : w0;
+        const uint32_t pw = i ? w0 : pw0;
         const int l = 2 * wp + i;
         h2 d[4];
         decode_word(pw, w, d);
@@ -95,68 +97,112 @@ struct PfTile {
     int bcol0[2];                 // first column tile of half 0 / 1
 };
 
+// A stage row R: 64 bytes = four 16-byte chunks (k 0-7, 8-15, 16-23, 24-31), chunk g at slot g ^ pf_swz(R): the
+// fragment reads (16 consecutive rows per LDS pass, one chunk each) then touch every bank once.
+__device__ __forceinline__ int pf_swz(int R) { return (R >> 2) & 3; }
+
+// Staging, PF_NS steps deep, entirely by LDS DMA (global_load_lds): per 32-k step every wave copies 32 A rows (two
+// 1 KB instructions: 16 rows x 4 chunks, swizzled through the source addresses) and a quarter of the step's raw
+// trellis words (two 256-byte instructions). Step it + PF_NS - 1 is issued while step it is multiplied, so each
+// load has PF_NS - 1 steps of MFMA work to arrive; loads past the last step re-read it. The decoded B stage of step
+// it + 1 is built from its raw words during step it (double-buffered), so the decode arithmetic runs beside the
+// MFMAs. One wait + barrier per step publishes A(it) and the raw words of step it + 1.
 __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[2][4]) {
-    _Float16* As = reinterpret_cast<_Float16*>(smem);
-    _Float16* Bs = As + 2 * PF_AS;
+    unsigned char* Ast = smem;                                        // [PF_NS][256 rows][64 B]
+    unsigned char* Wst = smem + PF_NS * PF_ASB;                       // [PF_NS][4 KB]
+    _Float16* Bs = reinterpret_cast<_Float16*>(Wst + PF_NS * PF_WSB); // [2][2 halves][128 cols][PF_LD]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rg = wv >> 1, half = wv & 1;
-    // A loader: rows ar and ar + 128, 16-byte chunk ac of the 64-byte step slice
-    const int ar = tid >> 2, ac = tid & 3;
-    const int ra0 = min(ar, t.rn - 1), ra1 = min(ar + 128, t.rn - 1);
-    const u32x4* A0 = reinterpret_cast<const u32x4*>(t.a_rows + (size_t)ra0 * t.kdim) + ac;
-    const u32x4* A1 = reinterpret_cast<const u32x4*>(t.a_rows + (size_t)ra1 * t.kdim) + ac;
-    // B loader: half bm, tile bt (k tile bkt, column tile bct), word pair wp
-    const int bm = tid >> 8, bt = (tid >> 4) & 15, bkt = bt >> 3, bct = bt & 7, wp = tid & 15;
-    const uint32_t* Bg = t.btr[bm] + ((size_t)bkt * t.btiles_n + t.bcol0[bm] + bct) * 32 + 2 * wp;
-    const size_t bstep = (size_t)2 * t.btiles_n * 32;      // two k tiles
     const int steps = t.kdim / 32;
+    // A DMA sources: instruction i of this wave = rows 32 wv + 16 i + lane / 4, slot lane % 4
+    const uint16_t* asrc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int R = 32 * wv + 16 * i + (lane >> 2);
+        const int chunk = (lane & 3) ^ pf_swz(R);
+        asrc[i] = t.a_rows + (size_t)min(R, t.rn - 1) * t.kdim + 8 * chunk;
+    }
+    // raw-word DMA sources: instruction i of this wave = 256-byte part p of block (half hb, k tile kb)
+    const uint32_t* wsrc[2];
+    int wdst[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ins = 2 * wv + i, blk = ins >> 2, part = ins & 3, hb = blk >> 1, kb = blk & 1;
+        wsrc[i] = t.btr[hb] + ((size_t)kb * t.btiles_n + t.bcol0[hb]) * 32 + part * 64 + lane;
+        wdst[i] = blk * 1024 + part * 256;
+    }
+    const size_t wstep = (size_t)2 * t.btiles_n * 32;                 // words per step (two k tiles)
+    auto issue = [&](int sa, int sw) {                                // A of step sa, raw words of step sw (clamped)
+        sa = min(sa, steps - 1);
+        sw = min(sw, steps - 1);
+        unsigned char* ad = Ast + (sa % PF_NS) * PF_ASB + wv * 2048;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dma16(asrc[i] + (size_t)sa * 32, ad + i * 1024);
+        unsigned char* wd = Wst + (sw % PF_NS) * PF_WSB;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dma4(wsrc[i] + (size_t)sw * wstep, wd + wdst[i]);
+    };
+    // decoder role of this thread: half bm, tile bt (k tile bkt, column tile bct), word pair wp
+    const int bm = tid >> 8, bt = (tid >> 4) & 15, bkt = bt >> 3, bct = bt & 7, wp = tid & 15;
+    const int wofs = ((bm * 2 + bkt) * 8 + bct) * 128;               // the tile's 128 bytes in a raw-word stage
+    auto decode = [&](int sw, int bb) {                               // raw words of step sw -> decoded stage bb
+        const unsigned char* ws = Wst + (sw % PF_NS) * PF_WSB + wofs;
+        const uint2 w = *reinterpret_cast<const uint2*>(ws + 8 * wp);
+        const uint32_t pw = *reinterpret_cast<const uint32_t*>(ws + 4 * ((2 * wp + 31) & 31));
+        pf_store_b(pw, w.x, w.y, wp, Bs + bb * PF_BS + bm * 128 * PF_LD, bct * 16, bkt * 16);
+    };
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[rb][c][r] = 0.f;
-
-    u32x4 a0 = A0[0], a1 = A1[0];
-    uint2 bw = *reinterpret_cast<const uint2*>(Bg);
-    *reinterpret_cast<u32x4*>(As + ar * PF_LD + ac * 8) = a0;
-    *reinterpret_cast<u32x4*>(As + (ar + 128) * PF_LD + ac * 8) = a1;
-    pf_store_b(bw, lane, wp, Bs + bm * 128 * PF_LD, bct * 16, bkt * 16);
-    __syncthreads();
-    for (int it = 0; it < steps; ++it) {
-        const int st = it & 1;
-        const bool more = it + 1 < steps;
-        if (more) {
-            a0 = A0[(it + 1) * 4];
-            a1 = A1[(it + 1) * 4];
-            bw = *reinterpret_cast<const uint2*>(Bg + (size_t)(it + 1) * bstep);
-        }
-        const _Float16* as = As + st * PF_AS;
-        const _Float16* bs = Bs + st * PF_BS + half * 128 * PF_LD;
+    // prologue: raw words of step 0 first, then the batches that step it = 0, 1, 2 of the loop would have issued
+    // (A(0..PF_NS-2), words(1..PF_NS-1)); decode step 0
+    {
+        unsigned char* wd = Wst;
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-            const int k = 16 * kh + 8 * (lane >> 5);
-            h8 af[2], bf[4];
+        for (int i = 0; i < 2; ++i) dma4(wsrc[i], wd + wdst[i]);
+    }
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-                af[rb] = *reinterpret_cast<const h8*>(as + (64 * rg + 32 * rb + (lane & 31)) * PF_LD + k);
+    for (int j = 0; j < PF_NS - 1; ++j) issue(j, j + 1);
+    WAIT_VM(4 * (PF_NS - 1));                                         // the step-0 words
+    LDS_BARRIER();
+    decode(0, 0);
+    for (int it0 = 0; it0 < steps; it0 += PF_NS) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) bf[c] = *reinterpret_cast<const h8*>(bs + (32 * c + (lane & 31)) * PF_LD + k);
+        for (int j = 0; j < PF_NS; ++j) {
+            const int it = it0 + j;
+            WAIT_VM(4 * (PF_NS - 2));                                 // A(it) and words(it + 1): the oldest batch
+            LDS_BARRIER();
+            issue(it + PF_NS - 1, it + PF_NS);
+            const unsigned char* as = Ast + j * PF_ASB;               // it % PF_NS == j
+            const _Float16* bs = Bs + (j & 1) * PF_BS + half * 128 * PF_LD;
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
+            for (int kh = 0; kh < 2; ++kh) {
+                h8 af[2], bf[4];
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb) {
+                    const int R = 64 * rg + 32 * rb + (lane & 31);
+                    const int slot = (2 * kh + (lane >> 5)) ^ pf_swz(R);
+                    af[rb] = *reinterpret_cast<const h8*>(as + R * 64 + 16 * slot);
+                }
+                const int k = 16 * kh + 8 * (lane >> 5);
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    acc[rb][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], bf[c], acc[rb][c], 0, 0, 0);
+                    bf[c] = *reinterpret_cast<const h8*>(bs + (32 * c + (lane & 31)) * PF_LD + k);
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        acc[rb][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], bf[c], acc[rb][c], 0, 0, 0);
+            }
+            decode(it + 1, (j + 1) & 1);                              // step it + 1 (past the end: never used)
         }
-        if (more) {
-            _Float16* an = As + (st ^ 1) * PF_AS;
-            *reinterpret_cast<u32x4*>(an + ar * PF_LD + ac * 8) = a0;
-            *reinterpret_cast<u32x4*>(an + (ar + 128) * PF_LD + ac * 8) = a1;
-            pf_store_b(bw, lane, wp, Bs + (st ^ 1) * PF_BS + bm * 128 * PF_LD, bct * 16, bkt * 16);
-        }
-        __syncthreads();
     }
+    WAIT_VM(0);                                                       // nothing in flight when LDS is reused
+    LDS_BARRIER();
 }
 
 // Stage the accumulators of row block (rg2, rb) (32 rows x 256 columns) into Cs [32][256] fp32.
@@ -174,11 +220,24 @@ __device__ __forceinline__ void pf_stage_rows(const f16v (&acc)[2][4], float* Cs
         }
 }
 
+// ------------------------------------------------------------------------------------------------ tile order
+
+// Tile (segment s, column block cb) of 1D workgroup b: consecutive workgroups are dealt round-robin to the 8 XCDs
+// (b % 8), so XCD x runs segments x, x + 8, x + 16, ... with all ncb column blocks of a segment in a row. The
+// column blocks of one segment therefore share the XCD's L2 for their common A rows (read from HBM once per
+// segment instead of once per column block). Grid: 8 * ncb * ceil(S_cap / 8).
+__device__ __forceinline__ void pf_tile_of(int b, int ncb, int& s, int& cb) {
+    const int x = b & 7, q = b >> 3;
+    cb = q % ncb;
+    s = 8 * (q / ncb) + x;
+}
+
 // ------------------------------------------------------------------------------------------------ gate/up
 
 __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int cb = blockIdx.x, s = blockIdx.y;
+    int s, cb;
+    pf_tile_of(blockIdx.x, a.N >> 7, s, cb);
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int K = a.K, N = a.N;
@@ -239,7 +298,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
 
 __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    const int cb = blockIdx.x, s = blockIdx.y;
+    int s, cb;
+    pf_tile_of(blockIdx.x, a.K >> 8, s, cb);
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int K = a.K, N = a.N;
@@ -332,9 +392,11 @@ int prefill_setup() {
 int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
     if (prefill_setup()) return -1;
     if (kernels & 1) hipLaunchKernelGGL(pf_gather_kernel, dim3(4096), dim3(256), 0, st, a);
+    const int sg = (a.S_cap + 7) / 8;                               // segment groups of 8 (one per XCD)
     if (kernels & 2)
-        hipLaunchKernelGGL(pf_gateup_kernel, dim3(a.N / 128, a.S_cap), dim3(PF_THREADS), PF_LDS, st, a);
-    if (kernels & 4) hipLaunchKernelGGL(pf_down_kernel, dim3(a.K / 256, a.S_cap), dim3(PF_THREADS), PF_LDS, st, a);
+        hipLaunchKernelGGL(pf_gateup_kernel, dim3(8 * (a.N / 128) * sg), dim3(PF_THREADS), PF_LDS, st, a);
+    if (kernels & 4)
+        hipLaunchKernelGGL(pf_down_kernel, dim3(8 * (a.K / 256) * sg), dim3(PF_THREADS), PF_LDS, st, a);
     if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3(a.T, a.K / 256), dim3(128), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
