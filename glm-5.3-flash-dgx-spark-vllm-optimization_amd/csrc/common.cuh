@@ -203,9 +203,9 @@ __device__ __forceinline__ void dma4(const void* src_lane, unsigned char* lds_wa
                  : "memory", "m0");
 }
 
-// s_waitcnt vmcnt(n) lgkmcnt(0) (n <= 15): this wave's staged loads up to the one n before the last have landed in
-// LDS, and its LDS reads of the buffer about to be refilled have returned
-#define WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0070 | (n))
+// s_waitcnt vmcnt(n) lgkmcnt(0) (n <= 63; vmcnt bits 3:0 and 15:14): this wave's staged loads up to the one n before
+// the last have landed in LDS, and its LDS reads of the buffer about to be refilled have returned
+#define WAIT_VM(n) __builtin_amdgcn_s_waitcnt(0x0070 | ((n) & 15) | (((n) >> 4) << 14))
 #define LDS_BARRIER() asm volatile("s_barrier" ::: "memory")
 
 }  // namespace mi355moe

@@ -1,12 +1,12 @@
 // Prefill-path kernels (many rows per expert, the E3 grouped tier): gather + input rotation, the gate/up grouped
 // GEMM and the down grouped GEMM on fp16 MFMA (v_mfma_f32_32x32x16_f16) with the EXL3 trellis decoded into LDS.
 //
-// Tiles: a workgroup of 8 waves owns a 256-row segment of one expert (rows sorted by expert) and one column block:
-//   gate/up: 128 columns of gate and the same 128 of up (waves 2g and 2g+1: rows 64g..64g+63 of gate / of up);
-//   down:    256 output columns (two 128-column halves).
-// Per K step of 32: every thread loads 8 bytes of trellis (two words of one 16x16 tile) and 32 bytes of the A rows
-// for the next step while the MFMAs of the current step run; the decoded B step (32 k x 256 columns fp16) and the A
-// step (256 rows x 32 k fp16) are double-buffered in LDS. Each weight value is decoded once per 256-row tile.
+// Tiles: a workgroup of 4 waves (one per SIMD) owns a 256-row segment of one expert (rows sorted by expert) and one
+// column block; each wave multiplies all 256 rows by its own 64 columns:
+//   gate/up: 128 columns of gate (waves 0, 1) and the same 128 of up (waves 2, 3);
+//   down:    256 output columns.
+// The A rows are staged in LDS (shared by the 4 waves); each wave decodes its own trellis words straight into MFMA
+// operands, so every weight value is decoded once per 256-row tile and never goes through LDS.
 // Numerics (oracle/csrc/oracle.c mode 1 = the E3 kernels, code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu):
 //   gather   h13 = fp16(H(fp16(x * suh_g)) * r)                                         (exl3_fat_moe.cu:95-126)
 //   gate/up  g = (H(acc_g) * r) * svh_g, u likewise; iff L != 0: g = min(g, L), u = clamp(u, -L, L);
@@ -24,199 +24,238 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int PF_TM = PREFILL_TM;   // rows per tile (segment height)
-constexpr int PF_THREADS = 512;     // 8 waves
-constexpr int PF_LD = 40;           // halves per LDS row of a decoded B step (32 k + 8 padding)
-constexpr int PF_NS = 4;            // staged steps in flight (A rows and raw trellis words)
+constexpr int PF_THREADS = 256;     // 4 waves, one per SIMD: each owns 64 columns of the tile for all 256 rows
+constexpr int PF_NS = 8;            // staged steps in flight (A rows and raw trellis words)
 constexpr int PF_ASB = PF_TM * 64;              // one A stage: 256 rows x 32 k fp16, bytes
-constexpr int PF_WSB = 4096;                    // one raw-word stage: 2 halves x 2 k tiles x 8 column tiles x 128 B
-constexpr int PF_BS = 2 * 128 * PF_LD;          // one decoded B stage: 2 x 128 columns (halves)
-constexpr size_t PF_LDS = (size_t)PF_NS * (PF_ASB + PF_WSB) + (size_t)2 * PF_BS * 2;   // 122,880 bytes
+constexpr int PF_WSB = 4096;                    // one raw-word stage: 4 waves x 2 k tiles x 4 column tiles x 128 B
+constexpr size_t PF_LDS = (size_t)PF_NS * (PF_ASB + PF_WSB);   // 163,840 bytes (the whole LDS)
+constexpr int PF_CLD = 260;                     // epilogue staging row stride (floats): [32][PF_CLD] fp32
+
+// Rotated activations (h13, h2) are stored with k permuted inside every group of 16: storage pair p (halves 2p,
+// 2p+1) holds k pair j with p = 2 (j % 4) + j / 4, i.e. storage order k = 0,1,8,9, 2,3,10,11, 4,5,12,13, 6,7,14,15.
+// That is the k order in which one lane decodes two consecutive trellis words of a column, so the decoded weights
+// go straight into MFMA operands (8 consecutive k slots per lane) and the activations match them slot for slot.
+__device__ __forceinline__ int pf_kperm_pair(int j) { return 2 * (j & 3) + (j >> 2); }
 
 // ------------------------------------------------------------------------------------------------ gather
 
-// h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0; one wave per
-// (row, 128-block) task, grid-stride.
+// h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0. A wave rotates four
+// (row, 128-block) tasks at once: 16 lanes per task, lane c holding elements 8c .. 8c + 7 (DPP Hadamard); grid-stride.
 __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
+    const int c = lane & 15;
     const int nb = a.K >> 7;
     const int64_t tasks = (int64_t)a.P * nb;
-    for (int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); task < tasks; task += (int64_t)gridDim.x * 4) {
+    const int sto = 16 * (c >> 1) + 2 * (c & 1);                      // storage of pair m: sto + 4 m
+    const int64_t stride = (int64_t)gridDim.x * 16;
+    for (int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4; t0 < tasks; t0 += stride) {
+        const int64_t task = min(t0 + (lane >> 4), tasks - 1);
         const int pos = (int)(task / nb), blk = (int)(task - (int64_t)pos * nb);
         const int e = a.pe[pos];
-        if (e < 0) continue;
-        const _Float16* suh = reinterpret_cast<const _Float16*>(a.wt.g_suh[e]) + blk * 128;
-        const size_t xoff = (size_t)a.tok[pos] * a.x_stride + blk * 128;
-        _Float16 h0, h1;
-        if (a.xdt == DT_BF16) {
-            const uint32_t v = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(a.x) + xoff +
-                                                                   2 * lane);
-            h0 = (_Float16)__builtin_bit_cast(float, v << 16);
-            h1 = (_Float16)__builtin_bit_cast(float, v & 0xFFFF0000u);
-        } else {
-            const h2 v = *reinterpret_cast<const h2*>(reinterpret_cast<const uint16_t*>(a.x) + xoff + 2 * lane);
-            h0 = v.x;
-            h1 = v.y;
+        const bool store = e >= 0 && t0 + (lane >> 4) < tasks;
+        const int ee = max(e, 0);
+        const int tk = e >= 0 ? a.tok[pos] : 0;
+        const _Float16* suh = reinterpret_cast<const _Float16*>(a.wt.g_suh[ee]) + blk * 128 + 8 * c;
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)tk * a.x_stride + blk * 128 + 8 * c;
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            _Float16 h0, h1;
+            if (a.xdt == DT_BF16) {
+                const uint32_t v = *reinterpret_cast<const uint32_t*>(xr + i);
+                h0 = (_Float16)__builtin_bit_cast(float, v << 16);
+                h1 = (_Float16)__builtin_bit_cast(float, v & 0xFFFF0000u);
+            } else {
+                const h2 v = *reinterpret_cast<const h2*>(xr + i);
+                h0 = v.x;
+                h1 = v.y;
+            }
+            const h2 sv = *reinterpret_cast<const h2*>(suh + i);
+            p[i] = (float)(_Float16)(h0 * sv.x);
+            p[i + 1] = (float)(_Float16)(h1 * sv.y);
         }
-        const h2 s = *reinterpret_cast<const h2*>(suh + 2 * lane);
-        float p0 = (float)(_Float16)(h0 * s.x), p1 = (float)(_Float16)(h1 * s.y);
-        fwht128_w64(p0, p1, lane);
-        *reinterpret_cast<h2*>(reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + blk * 128 + 2 * lane) =
-            h2{(_Float16)(p0 * HAD_R), (_Float16)(p1 * HAD_R)};
+        fwht128_x16(p, lane);
+        if (store) {
+            _Float16* dst = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + blk * 128 + sto;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                *reinterpret_cast<h2*>(dst + 4 * m) = h2{(_Float16)(p[2 * m] * HAD_R), (_Float16)(p[2 * m + 1] * HAD_R)};
+        }
     }
 }
 
 // ------------------------------------------------------------------------------------------------ GEMM core
 
-// Decode this thread's two trellis words (words 2wp, 2wp+1 of one tile, pw = word 2wp - 1 mod 32) into the B
-// stage: column-major [col][k] with the k of the 32-step contiguous.
-__device__ __forceinline__ void pf_store_b(uint32_t pw0, uint32_t w0, uint32_t w1, int wp, _Float16* B, int col_base,
-                                           int krow) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t w = i ? w1 : w0;
-        const uint32_t pw = i ? w0 : pw0;
-        const int l = 2 * wp + i;
-        h2 d[4];
-        decode_word(pw, w, d);
-        const int c0 = col_base + (l >> 2), r0 = krow + 2 * (l & 3);
-        *reinterpret_cast<h2*>(B + c0 * PF_LD + r0) = d[0];
-        *reinterpret_cast<h2*>(B + c0 * PF_LD + r0 + 8) = d[1];
-        *reinterpret_cast<h2*>(B + (c0 + 8) * PF_LD + r0) = d[2];
-        *reinterpret_cast<h2*>(B + (c0 + 8) * PF_LD + r0 + 8) = d[3];
-    }
-}
-
-// The tile GEMM: acc[rb][c4] (32x32 blocks) of rows 64*rg + 32*rb, columns 32*c4 of B half `half` (128 columns),
-// over kdim. A rows come from `a_rows` (row stride kdim), clamped to rn - 1. B tiles: (k tile, column tile) ->
-// trellis words of matrix `bmat[half]` at ((kt * btiles_n) + bcol0[half] + ct) * 32.
+// The tile GEMM of one wave: acc[rb][s] (32x32 blocks, rows 32 rb of the segment) over kdim, for the wave's 64
+// columns = four trellis column tiles. MFMA column n of block s is column 16 (n / 8) + n % 8 + 8 s of the wave.
+// A rows come from `a_rows` (row stride kdim, k permuted as stored), clamped to rn - 1.
 struct PfTile {
     const uint16_t* a_rows;       // first row of the segment
     int rn, kdim;
-    const uint32_t* btr[2];       // trellis of half 0 / 1
+    const uint32_t* btr;          // this wave's trellis matrix
     int btiles_n;                 // tiles per trellis row (the matrix's column tiles)
-    int bcol0[2];                 // first column tile of half 0 / 1
+    int bcol0;                    // this wave's first column tile
 };
 
-// A stage row R: 64 bytes = four 16-byte chunks (k 0-7, 8-15, 16-23, 24-31), chunk g at slot g ^ pf_swz(R): the
-// fragment reads (16 consecutive rows per LDS pass, one chunk each) then touch every bank once.
+// A stage row R: 64 bytes = four 16-byte chunks (storage k 0-7, 8-15, 16-23, 24-31), chunk g at slot g ^ pf_swz(R):
+// the fragment reads (16 consecutive rows per LDS pass, one chunk each) then touch every bank once.
 __device__ __forceinline__ int pf_swz(int R) { return (R >> 2) & 3; }
 
-// Staging, PF_NS steps deep, entirely by LDS DMA (global_load_lds): per 32-k step every wave copies 32 A rows (two
-// 1 KB instructions: 16 rows x 4 chunks, swizzled through the source addresses) and a quarter of the step's raw
-// trellis words (two 256-byte instructions). Step it + PF_NS - 1 is issued while step it is multiplied, so each
-// load has PF_NS - 1 steps of MFMA work to arrive; loads past the last step re-read it. The decoded B stage of step
-// it + 1 is built from its raw words during step it (double-buffered), so the decode arithmetic runs beside the
-// MFMAs. One wait + barrier per step publishes A(it) and the raw words of step it + 1.
-__device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[2][4]) {
+// Decoded B operands, one fp16 pair at a time. Lane (n = lane % 32, h = lane / 32) of a k tile reads words
+// wp = 4c + 2h and wp + 1 of column tile t (c = n % 8, t = n / 8) and the predecessor word wp - 1 (mod 32):
+// w[0] = word wp - 1, w[1] = word wp, w[2] = word wp + 1. Pair p (0..7) of the lane: word wp (p < 4) or wp + 1,
+// states 2 (p % 4) and 2 (p % 4) + 1 of that word (decode_word's order); the operand of column 16t + c is pairs
+// 0, 1, 4, 5 (k slots 8h .. 8h + 7) and that of column 16t + c + 8 is pairs 2, 3, 6, 7.
+__device__ __forceinline__ void pf_load_words(const unsigned char* wk, int lane, uint32_t (&w)[3]) {
+    const int n = lane & 31, wp = 4 * (n & 7) + 2 * (lane >> 5);
+    const unsigned char* tile = wk + (n >> 3) * 128;
+    const uint2 v = *reinterpret_cast<const uint2*>(tile + 4 * wp);
+    w[0] = *reinterpret_cast<const uint32_t*>(tile + 4 * ((wp + 31) & 31));
+    w[1] = v.x;
+    w[2] = v.y;
+}
+__device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p) {
+    const uint32_t pw = w[p >> 2], x = w[(p >> 2) + 1];
+    uint32_t s0, s1;
+    switch (p & 3) {
+        case 0: {
+            const uint32_t D = __builtin_amdgcn_alignbit(pw, x, 20);
+            s0 = __builtin_amdgcn_ubfe(D, 8, 16);
+            s1 = __builtin_amdgcn_ubfe(D, 4, 16);
+            break;
+        }
+        case 1:
+            s0 = __builtin_amdgcn_alignbit(pw, x, 20) & 0xFFFFu;
+            s1 = x >> 16;
+            break;
+        case 2:
+            s0 = __builtin_amdgcn_ubfe(x, 12, 16);
+            s1 = __builtin_amdgcn_ubfe(x, 8, 16);
+            break;
+        default:
+            s0 = __builtin_amdgcn_ubfe(x, 4, 16);
+            s1 = x & 0xFFFFu;
+            break;
+    }
+    return __builtin_bit_cast(uint32_t, h2{mcg_value(s0), mcg_value(s1)});
+}
+
+// Staging, PF_NS steps deep, entirely by LDS DMA (global_load_lds_dwordx4): per 32-k step every wave copies 64 A
+// rows (four 1 KB instructions: 16 rows x 4 chunks, swizzled through the source addresses) and its own raw trellis
+// words (one 1 KB instruction: 2 k tiles x 4 column tiles). Step it + PF_NS - 1 is issued while step it is
+// multiplied, so each load has PF_NS - 1 steps of MFMA work to arrive; loads past the last step re-read it. The B
+// operands of step it + 1 are decoded in registers during step it (no LDS round trip: each wave decodes only its own
+// columns). One wait + barrier per step publishes A(it) (all waves) and the raw words of step it + 1 (this wave).
+__device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[8][2]) {
     unsigned char* Ast = smem;                                        // [PF_NS][256 rows][64 B]
-    unsigned char* Wst = smem + PF_NS * PF_ASB;                       // [PF_NS][4 KB]
-    _Float16* Bs = reinterpret_cast<_Float16*>(Wst + PF_NS * PF_WSB); // [2][2 halves][128 cols][PF_LD]
+    unsigned char* Wst = smem + PF_NS * PF_ASB;                       // [PF_NS][4 waves][2 k tiles][4 tiles][128 B]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rg = wv >> 1, half = wv & 1;
     const int steps = t.kdim / 32;
-    // A DMA sources: instruction i of this wave = rows 32 wv + 16 i + lane / 4, slot lane % 4
-    const uint16_t* asrc[2];
+    // A DMA sources: instruction i of this wave = rows 64 wv + 16 i + lane / 4, slot lane % 4
+    const uint16_t* asrc[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int R = 32 * wv + 16 * i + (lane >> 2);
+    for (int i = 0; i < 4; ++i) {
+        const int R = 64 * wv + 16 * i + (lane >> 2);
         const int chunk = (lane & 3) ^ pf_swz(R);
         asrc[i] = t.a_rows + (size_t)min(R, t.rn - 1) * t.kdim + 8 * chunk;
     }
-    // raw-word DMA sources: instruction i of this wave = 256-byte part p of block (half hb, k tile kb)
-    const uint32_t* wsrc[2];
-    int wdst[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int ins = 2 * wv + i, blk = ins >> 2, part = ins & 3, hb = blk >> 1, kb = blk & 1;
-        wsrc[i] = t.btr[hb] + ((size_t)kb * t.btiles_n + t.bcol0[hb]) * 32 + part * 64 + lane;
-        wdst[i] = blk * 1024 + part * 256;
-    }
+    // raw-word DMA source: lane -> k tile lane / 32, column tile (lane / 8) % 4, 16-byte piece lane % 8
+    const uint32_t* wsrc = t.btr + ((size_t)(lane >> 5) * t.btiles_n + t.bcol0 + ((lane >> 3) & 3)) * 32 + 4 * (lane & 7);
     const size_t wstep = (size_t)2 * t.btiles_n * 32;                 // words per step (two k tiles)
     auto issue = [&](int sa, int sw) {                                // A of step sa, raw words of step sw (clamped)
         sa = min(sa, steps - 1);
         sw = min(sw, steps - 1);
-        unsigned char* ad = Ast + (sa % PF_NS) * PF_ASB + wv * 2048;
+        unsigned char* ad = Ast + (sa % PF_NS) * PF_ASB + wv * 4096;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) dma16(asrc[i] + (size_t)sa * 32, ad + i * 1024);
-        unsigned char* wd = Wst + (sw % PF_NS) * PF_WSB;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) dma4(wsrc[i] + (size_t)sw * wstep, wd + wdst[i]);
+        for (int i = 0; i < 4; ++i) dma16(asrc[i] + (size_t)sa * 32, ad + i * 1024);
+        dma16(wsrc + (size_t)sw * wstep, Wst + (sw % PF_NS) * PF_WSB + wv * 1024);
     };
-    // decoder role of this thread: half bm, tile bt (k tile bkt, column tile bct), word pair wp
-    const int bm = tid >> 8, bt = (tid >> 4) & 15, bkt = bt >> 3, bct = bt & 7, wp = tid & 15;
-    const int wofs = ((bm * 2 + bkt) * 8 + bct) * 128;               // the tile's 128 bytes in a raw-word stage
-    auto decode = [&](int sw, int bb) {                               // raw words of step sw -> decoded stage bb
-        const unsigned char* ws = Wst + (sw % PF_NS) * PF_WSB + wofs;
-        const uint2 w = *reinterpret_cast<const uint2*>(ws + 8 * wp);
-        const uint32_t pw = *reinterpret_cast<const uint32_t*>(ws + 4 * ((2 * wp + 31) & 31));
-        pf_store_b(pw, w.x, w.y, wp, Bs + bb * PF_BS + bm * 128 * PF_LD, bct * 16, bkt * 16);
+    auto words = [&](int sw, uint32_t (&w)[2][3]) {                  // this lane's raw words of step sw
+        const unsigned char* wr = Wst + (sw % PF_NS) * PF_WSB + wv * 1024;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) pf_load_words(wr + kh * 512, lane, w[kh]);
+    };
+    auto operands = [&](const uint32_t (&q)[2][8], h8 (&b)[2][2]) {   // decoded pairs -> B operands
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            b[kh][0] = __builtin_bit_cast(h8, u32x4{q[kh][0], q[kh][1], q[kh][4], q[kh][5]});
+            b[kh][1] = __builtin_bit_cast(h8, u32x4{q[kh][2], q[kh][3], q[kh][6], q[kh][7]});
+        }
+    };
+    auto afrag = [&](const unsigned char* as, int i) {                // A fragment i = (k tile i / 8, rows 32 (i % 8))
+        const int R = 32 * (i & 7) + (lane & 31);
+        const int slot = (2 * (i >> 3) + (lane >> 5)) ^ pf_swz(R);
+        return *reinterpret_cast<const h8*>(as + R * 64 + 16 * slot);
+    };
+    // One step, in a fixed instruction order (one wave per SIMD issues everything itself): the 32 MFMAs of step it,
+    // each followed by half of one fp16 pair's decode for step it + 1 (VALU work issued while the MFMA runs), the A
+    // fragments read four MFMA pairs ahead.
+    auto step = [&](int it, const h8 (&bc)[2][2], h8 (&bn)[2][2]) {
+        WAIT_VM(5 * (PF_NS - 2));                                     // A(it) and words(it + 1): the oldest batch
+        LDS_BARRIER();
+        issue(it + PF_NS - 1, it + PF_NS);
+        __builtin_amdgcn_sched_barrier(0);
+        const unsigned char* as = Ast + (it % PF_NS) * PF_ASB;
+        uint32_t w[2][3];
+        words(it + 1, w);                                             // step it + 1 (past the end: never used)
+        h8 af[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[i] = afrag(as, i);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t q[2][8];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (i + 4 < 16) af[i + 4] = afrag(as, i + 4);
+            const int kh = i >> 3, rb = i & 7;
+            acc[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kh][0], acc[rb][0], 0, 0, 0);
+            q[i >> 3][i & 7] = pf_decode_pair(w[i >> 3], i & 7);
+            acc[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kh][1], acc[rb][1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        operands(q, bn);
     };
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int s = 0; s < 2; ++s)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[rb][c][r] = 0.f;
-    // prologue: raw words of step 0 first, then the batches that step it = 0, 1, 2 of the loop would have issued
-    // (A(0..PF_NS-2), words(1..PF_NS-1)); decode step 0
-    {
-        unsigned char* wd = Wst;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) dma4(wsrc[i], wd + wdst[i]);
-    }
+            for (int r = 0; r < 16; ++r) acc[rb][s][r] = 0.f;
+    // prologue: raw words of step 0 first, then the batches that steps 0 .. PF_NS - 2 of the loop would have issued
+    // (A(0 .. PF_NS - 2), words(1 .. PF_NS - 1)); decode step 0
+    dma16(wsrc, Wst + wv * 1024);
 #pragma unroll
     for (int j = 0; j < PF_NS - 1; ++j) issue(j, j + 1);
-    WAIT_VM(4 * (PF_NS - 1));                                         // the step-0 words
-    LDS_BARRIER();
-    decode(0, 0);
-    for (int it0 = 0; it0 < steps; it0 += PF_NS) {
+    WAIT_VM(5 * (PF_NS - 1));                                         // the step-0 words (this wave's own)
+    h8 bA[2][2], bB[2][2];
+    {
+        uint32_t w[2][3], q[2][8];
+        words(0, w);
 #pragma unroll
-        for (int j = 0; j < PF_NS; ++j) {
-            const int it = it0 + j;
-            WAIT_VM(4 * (PF_NS - 2));                                 // A(it) and words(it + 1): the oldest batch
-            LDS_BARRIER();
-            issue(it + PF_NS - 1, it + PF_NS);
-            const unsigned char* as = Ast + j * PF_ASB;               // it % PF_NS == j
-            const _Float16* bs = Bs + (j & 1) * PF_BS + half * 128 * PF_LD;
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-                h8 af[2], bf[4];
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb) {
-                    const int R = 64 * rg + 32 * rb + (lane & 31);
-                    const int slot = (2 * kh + (lane >> 5)) ^ pf_swz(R);
-                    af[rb] = *reinterpret_cast<const h8*>(as + R * 64 + 16 * slot);
-                }
-                const int k = 16 * kh + 8 * (lane >> 5);
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    bf[c] = *reinterpret_cast<const h8*>(bs + (32 * c + (lane & 31)) * PF_LD + k);
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        acc[rb][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], bf[c], acc[rb][c], 0, 0, 0);
-            }
-            decode(it + 1, (j + 1) & 1);                              // step it + 1 (past the end: never used)
-        }
+        for (int i = 0; i < 16; ++i) q[i >> 3][i & 7] = pf_decode_pair(w[i >> 3], i & 7);
+        operands(q, bA);
+    }
+    static_assert(5 * (PF_NS - 1) <= 63, "stages within the vmcnt range");
+    for (int it = 0; it < steps; it += 2) {                           // steps is even (kdim % 64 == 0)
+        step(it, bA, bB);
+        step(it + 1, bB, bA);
     }
     WAIT_VM(0);                                                       // nothing in flight when LDS is reused
     LDS_BARRIER();
 }
 
-// Stage the accumulators of row block (rg2, rb) (32 rows x 256 columns) into Cs [32][256] fp32.
-__device__ __forceinline__ void pf_stage_rows(const f16v (&acc)[2][4], float* Cs, int rg2, int rb) {
+// Stage the accumulators of row block rb (32 rows x 256 columns of the tile) into Cs [32][PF_CLD] fp32.
+__device__ __forceinline__ void pf_stage_rows(const f16v (&acc)[8][2], float* Cs, int rb) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if ((wv >> 1) != rg2) return;
-    const int half = wv & 1;
+    const int n = lane & 31;
+    const int col = 64 * wv + 16 * (n >> 3) + (n & 7);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            Cs[row * 256 + half * 128 + 32 * c + (lane & 31)] = acc[rb][c][r];
+            Cs[row * PF_CLD + col + 8 * s] = acc[rb][s][r];
         }
 }
 
@@ -241,57 +280,78 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int K = a.K, N = a.N;
-    PfTile t;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    PfTile t;                                                        // waves 0, 1: gate columns; 2, 3: up columns
     t.a_rows = a.h13 + (size_t)row0 * K;
     t.rn = rn;
     t.kdim = K;
-    t.btr[0] = reinterpret_cast<const uint32_t*>(a.wt.g_tr[e]);
-    t.btr[1] = reinterpret_cast<const uint32_t*>(a.wt.u_tr[e]);
+    t.btr = reinterpret_cast<const uint32_t*>(wv < 2 ? a.wt.g_tr[e] : a.wt.u_tr[e]);
     t.btiles_n = N >> 4;
-    t.bcol0[0] = t.bcol0[1] = cb * 8;
-    f16v acc[2][4];
+    t.bcol0 = cb * 8 + 4 * (wv & 1);
+    f16v acc[8][2];
     pf_gemm(t, smem, acc);
 
+    // epilogue, 32 rows at a time through LDS; a wave finishes 4 rows at once: 16 lanes per row, lane c holding
+    // columns 8c .. 8c + 7 (the 128-point Hadamards run across the 16 lanes by DPP)
     float* Cs = reinterpret_cast<float*>(smem);
     const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int col = cb * 128 + 2 * lane;
-    const h2 svg = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + col);
-    const h2 svu = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + col);
-    const h2 sud = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + col);
-    const float L = a.limit;
-    for (int rg2 = 0; rg2 < 4; ++rg2)
-        for (int rb = 0; rb < 2; ++rb) {
-            if (64 * rg2 + 32 * rb >= rn) continue;                 // uniform over the workgroup
-            pf_stage_rows(acc, Cs, rg2, rb);
-            __syncthreads();
-            for (int rr = 0; rr < 4; ++rr) {
-                const int rl = wv * 4 + rr;
-                const int trow = 64 * rg2 + 32 * rb + rl;
-                if (trow < rn) {
-                    float g[2] = {Cs[rl * 256 + 2 * lane], Cs[rl * 256 + 2 * lane + 1]};
-                    float u[2] = {Cs[rl * 256 + 128 + 2 * lane], Cs[rl * 256 + 128 + 2 * lane + 1]};
-                    fwht128_w64(g[0], g[1], lane);
-                    fwht128_w64(u[0], u[1], lane);
-                    float b[2];
+    const int c = lane & 15, rsub = lane >> 4;
+    const int col = cb * 128 + 8 * c;
+    float svg[8], svu[8];
+    _Float16 sud[8];
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        float gv = g[i] * HAD_R * (float)(i ? svg.y : svg.x);
-                        float uv = u[i] * HAD_R * (float)(i ? svu.y : svu.x);
-                        if (L != 0.0f) {
-                            gv = fminf(gv, L);
-                            uv = fminf(fmaxf(uv, -L), L);
-                        }
-                        const float act = sigmoid_dexp(gv) * gv * uv;
-                        b[i] = (float)(_Float16)((_Float16)act * (i ? sud.y : sud.x));
-                    }
-                    fwht128_w64(b[0], b[1], lane);
-                    *reinterpret_cast<h2*>(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow) * N + col) =
-                        h2{(_Float16)(b[0] * HAD_R), (_Float16)(b[1] * HAD_R)};
-                }
+    for (int i = 0; i < 8; i += 2) {
+        const h2 g2 = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + col + i);
+        const h2 u2 = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + col + i);
+        const h2 d2 = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + col + i);
+        svg[i] = (float)g2.x, svg[i + 1] = (float)g2.y;
+        svu[i] = (float)u2.x, svu[i + 1] = (float)u2.y;
+        sud[i] = d2.x, sud[i + 1] = d2.y;
+    }
+    // storage of the lane's pairs m = 0..3 (columns 8c + 2m, + 1): k pair j = 4 (c % 2) + m of group c / 2
+    const int sto = cb * 128 + 16 * (c >> 1) + 2 * (c & 1);
+    const float L = a.limit;
+#pragma unroll
+    for (int rb = 0; rb < 8; ++rb) {
+        if (32 * rb >= rn) break;                                    // uniform over the workgroup
+        pf_stage_rows(acc, Cs, rb);
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            const int rl = wv * 8 + pass * 4 + rsub;
+            const int trow = 32 * rb + rl;
+            const float* cr = Cs + rl * PF_CLD + 8 * c;
+            float g[8], u[8], b[8];
+#pragma unroll
+            for (int i = 0; i < 8; i += 4) {
+                const float4 g4 = *reinterpret_cast<const float4*>(cr + i);
+                const float4 u4 = *reinterpret_cast<const float4*>(cr + 128 + i);
+                g[i] = g4.x, g[i + 1] = g4.y, g[i + 2] = g4.z, g[i + 3] = g4.w;
+                u[i] = u4.x, u[i + 1] = u4.y, u[i + 2] = u4.z, u[i + 3] = u4.w;
             }
-            __syncthreads();
+            fwht128_x16(g, lane);
+            fwht128_x16(u, lane);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float gv = g[i] * HAD_R * svg[i];
+                float uv = u[i] * HAD_R * svu[i];
+                if (L != 0.0f) {
+                    gv = fminf(gv, L);
+                    uv = fminf(fmaxf(uv, -L), L);
+                }
+                const float act = sigmoid_dexp(gv) * gv * uv;
+                b[i] = (float)(_Float16)((_Float16)act * sud[i]);
+            }
+            fwht128_x16(b, lane);
+            if (trow < rn) {
+                _Float16* dst = reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow) * N + sto;
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    *reinterpret_cast<h2*>(dst + 4 * m) = h2{(_Float16)(b[2 * m] * HAD_R), (_Float16)(b[2 * m + 1] * HAD_R)};
+            }
         }
+        __syncthreads();
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ down
@@ -303,48 +363,63 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int K = a.K, N = a.N;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     PfTile t;
     t.a_rows = a.h2 + (size_t)row0 * N;
     t.rn = rn;
     t.kdim = N;
-    t.btr[0] = t.btr[1] = reinterpret_cast<const uint32_t*>(a.wt.d_tr[e]);
+    t.btr = reinterpret_cast<const uint32_t*>(a.wt.d_tr[e]);
     t.btiles_n = K >> 4;
-    t.bcol0[0] = cb * 16;
-    t.bcol0[1] = cb * 16 + 8;
-    f16v acc[2][4];
+    t.bcol0 = cb * 16 + 4 * wv;
+    f16v acc[8][2];
     pf_gemm(t, smem, acc);
 
+    // epilogue as in the gate/up kernel: 4 rows per wave at once, lane c of a row holding columns 8c .. 8c + 7 of
+    // each 128-column half
     float* Cs = reinterpret_cast<float*>(smem);
     const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const _Float16* svd = reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + cb * 256;
-    const h2 sv0 = *reinterpret_cast<const h2*>(svd + 2 * lane);
-    const h2 sv1 = *reinterpret_cast<const h2*>(svd + 128 + 2 * lane);
-    for (int rg2 = 0; rg2 < 4; ++rg2)
-        for (int rb = 0; rb < 2; ++rb) {
-            if (64 * rg2 + 32 * rb >= rn) continue;
-            pf_stage_rows(acc, Cs, rg2, rb);
-            __syncthreads();
-            for (int rr = 0; rr < 4; ++rr) {
-                const int rl = wv * 4 + rr;
-                const int trow = 64 * rg2 + 32 * rb + rl;
-                if (trow < rn) {
-                    const int row = row0 + trow;
-                    const float w = (float)u16_as_h(a.w16[row]);
-                    float* o = a.contrib + (size_t)row * K + cb * 256 + 2 * lane;
+    const int c = lane & 15, rsub = lane >> 4;
+    const _Float16* svd = reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + cb * 256 + 8 * c;
+    float sv[2][8];
 #pragma unroll
-                    for (int hf = 0; hf < 2; ++hf) {
-                        float v0 = Cs[rl * 256 + hf * 128 + 2 * lane], v1 = Cs[rl * 256 + hf * 128 + 2 * lane + 1];
-                        fwht128_w64(v0, v1, lane);
-                        const h2 sv = hf ? sv1 : sv0;
-                        v0 = v0 * HAD_R * (float)sv.x * w;
-                        v1 = v1 * HAD_R * (float)sv.y * w;
-                        *reinterpret_cast<float2*>(o + hf * 128) = make_float2(v0, v1);
-                    }
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const h2 v2 = *reinterpret_cast<const h2*>(svd + hf * 128 + i);
+            sv[hf][i] = (float)v2.x, sv[hf][i + 1] = (float)v2.y;
+        }
+#pragma unroll
+    for (int rb = 0; rb < 8; ++rb) {
+        if (32 * rb >= rn) break;
+        pf_stage_rows(acc, Cs, rb);
+        __syncthreads();
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            const int rl = wv * 8 + pass * 4 + rsub;
+            const int trow = 32 * rb + rl;
+            const int row = row0 + min(trow, rn - 1);
+            const float w = (float)u16_as_h(a.w16[row]);
+            float* o = a.contrib + (size_t)row * K + cb * 256 + 8 * c;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const float* cr = Cs + rl * PF_CLD + hf * 128 + 8 * c;
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 8; i += 4) {
+                    const float4 v4 = *reinterpret_cast<const float4*>(cr + i);
+                    v[i] = v4.x, v[i + 1] = v4.y, v[i + 2] = v4.z, v[i + 3] = v4.w;
+                }
+                fwht128_x16(v, lane);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = v[i] * HAD_R * sv[hf][i] * w;
+                if (trow < rn) {
+                    *reinterpret_cast<float4*>(o + hf * 128) = make_float4(v[0], v[1], v[2], v[3]);
+                    *reinterpret_cast<float4*>(o + hf * 128 + 4) = make_float4(v[4], v[5], v[6], v[7]);
                 }
             }
-            __syncthreads();
         }
+        __syncthreads();
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ combine
