@@ -39,47 +39,66 @@ __device__ __forceinline__ int pf_kperm_pair(int j) { return 2 * (j & 3) + (j >>
 
 // ------------------------------------------------------------------------------------------------ gather
 
-// h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0. A wave rotates four
-// (row, 128-block) tasks at once: 16 lanes per task, lane c holding elements 8c .. 8c + 7 (DPP Hadamard); grid-stride.
+// h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0. One wave per row
+// (grid-stride): a pass rotates four 128-blocks at once (16 lanes per block, lane c holding elements 8c .. 8c + 7,
+// DPP Hadamard); the loads of all passes of the row are issued before the first rotation.
+constexpr int PF_GATHER_PASSES = 8;                 // passes of 4 blocks in flight (K up to 4096 in one round)
 __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
-    const int c = lane & 15;
+    const int c = lane & 15, q = lane >> 4;
     const int nb = a.K >> 7;
-    const int64_t tasks = (int64_t)a.P * nb;
     const int sto = 16 * (c >> 1) + 2 * (c & 1);                      // storage of pair m: sto + 4 m
-    const int64_t stride = (int64_t)gridDim.x * 16;
-    for (int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4; t0 < tasks; t0 += stride) {
-        const int64_t task = min(t0 + (lane >> 4), tasks - 1);
-        const int pos = (int)(task / nb), blk = (int)(task - (int64_t)pos * nb);
+    const bool vec = ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.x_stride * 2)) & 15) == 0;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+    for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
         const int e = a.pe[pos];
-        const bool store = e >= 0 && t0 + (lane >> 4) < tasks;
-        const int ee = max(e, 0);
-        const int tk = e >= 0 ? a.tok[pos] : 0;
-        const _Float16* suh = reinterpret_cast<const _Float16*>(a.wt.g_suh[ee]) + blk * 128 + 8 * c;
-        const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)tk * a.x_stride + blk * 128 + 8 * c;
-        float p[8];
+        if (e < 0) continue;                                          // uniform: one row per wave
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)a.tok[pos] * a.x_stride + 8 * c;
+        const uint16_t* sr = reinterpret_cast<const uint16_t*>(a.wt.g_suh[e]) + 8 * c;
+        _Float16* dst = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + sto;
+        for (int b0 = 0; b0 < nb; b0 += 4 * PF_GATHER_PASSES) {
+            u32x4 xv[PF_GATHER_PASSES], sv[PF_GATHER_PASSES];
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            _Float16 h0, h1;
-            if (a.xdt == DT_BF16) {
-                const uint32_t v = *reinterpret_cast<const uint32_t*>(xr + i);
-                h0 = (_Float16)__builtin_bit_cast(float, v << 16);
-                h1 = (_Float16)__builtin_bit_cast(float, v & 0xFFFF0000u);
-            } else {
-                const h2 v = *reinterpret_cast<const h2*>(xr + i);
-                h0 = v.x;
-                h1 = v.y;
+            for (int j = 0; j < PF_GATHER_PASSES; ++j) {
+                const int blk = min(b0 + 4 * j + q, nb - 1);
+                const uint16_t* xp = xr + blk * 128;
+                if (vec) {
+                    xv[j] = *reinterpret_cast<const u32x4*>(xp);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) xv[j][i] = *reinterpret_cast<const uint32_t*>(xp + 2 * i);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sv[j][i] = *reinterpret_cast<const uint32_t*>(sr + blk * 128 + 2 * i);
             }
-            const h2 sv = *reinterpret_cast<const h2*>(suh + i);
-            p[i] = (float)(_Float16)(h0 * sv.x);
-            p[i + 1] = (float)(_Float16)(h1 * sv.y);
-        }
-        fwht128_x16(p, lane);
-        if (store) {
-            _Float16* dst = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + blk * 128 + sto;
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
-                *reinterpret_cast<h2*>(dst + 4 * m) = h2{(_Float16)(p[2 * m] * HAD_R), (_Float16)(p[2 * m + 1] * HAD_R)};
+            for (int j = 0; j < PF_GATHER_PASSES; ++j) {
+                const int blk = b0 + 4 * j + q;
+                if (b0 + 4 * j >= nb) break;                          // uniform
+                float p[8];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t v = xv[j][i];
+                    _Float16 h0, h1;
+                    if (a.xdt == DT_BF16) {
+                        h0 = (_Float16)__builtin_bit_cast(float, v << 16);
+                        h1 = (_Float16)__builtin_bit_cast(float, v & 0xFFFF0000u);
+                    } else {
+                        h0 = u16_as_h(v & 0xFFFFu);
+                        h1 = u16_as_h(v >> 16);
+                    }
+                    const uint32_t sw = sv[j][i];
+                    p[2 * i] = (float)(_Float16)(h0 * u16_as_h(sw & 0xFFFFu));
+                    p[2 * i + 1] = (float)(_Float16)(h1 * u16_as_h(sw >> 16));
+                }
+                fwht128_x16(p, lane);
+                if (blk < nb) {
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        *reinterpret_cast<h2*>(dst + blk * 128 + 4 * m) =
+                            h2{(_Float16)(p[2 * m] * HAD_R), (_Float16)(p[2 * m + 1] * HAD_R)};
+                }
+            }
         }
     }
 }
@@ -424,27 +443,44 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
 
 // ------------------------------------------------------------------------------------------------ combine
 
-// grid (T, K/256), 128 threads x 2 columns: out[t] = sum over the token's slots k (in order) of the valid pairs'
-// contributions, in the output dtype (deterministic: no atomics).
-__global__ __launch_bounds__(128) void pf_combine_kernel(PrefillArgs a) {
-    const int t = blockIdx.x;
-    const int col = blockIdx.y * 256 + 2 * threadIdx.x;
-    float s0 = 0.f, s1 = 0.f;
-    for (int k = 0; k < a.topk; ++k) {
-        const int pos = a.inv[t * a.topk + k];
-        if (a.pe[pos] < 0) continue;
-        const float2 c = *reinterpret_cast<const float2*>(a.contrib + (size_t)pos * a.K + col);
-        s0 += c.x;
-        s1 += c.y;
+// One wave per (token t, 256 columns), 4 columns per lane: out[t] = sum over the token's slots k (in order) of the
+// valid pairs' contributions, in the output dtype (deterministic: no atomics). The slots' loads are all issued first.
+__global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
+    const int t = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+    if (t >= a.T) return;
+    const int col = blockIdx.y * 256 + 4 * (threadIdx.x & 63);
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < a.topk; k0 += 8) {                          // slots in order, 8 loads in flight
+        f32x4 cv[8];
+        bool ok[8];
+        // lanes 0..7 fetch the positions and validity of slots k0 .. k0 + 7 (one vector load each), broadcast by readlane;
+        // the eight row loads are then unconditional (no control-flow joins between them)
+        const int lk = k0 + (threadIdx.x & 7);
+        const int pl = a.inv[t * a.topk + min(lk, a.topk - 1)];
+        const int okl = (int)(lk < a.topk) & (int)(a.pe[pl] >= 0);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int pos = __builtin_amdgcn_readlane(pl, k);
+            ok[k] = __builtin_amdgcn_readlane(okl, k) != 0;
+            cv[k] = *reinterpret_cast<const f32x4*>(a.contrib + (size_t)pos * a.K + col);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (ok[k]) sum += cv[k];
     }
     const size_t o = (size_t)t * a.out_stride + col;
     if (a.odt == DT_F32) {
-        *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.out) + o) = make_float2(s0, s1);
+        float* op = reinterpret_cast<float*>(a.out) + o;
+        *reinterpret_cast<float2*>(op) = make_float2(sum[0], sum[1]);
+        *reinterpret_cast<float2*>(op + 2) = make_float2(sum[2], sum[3]);
     } else if (a.odt == DT_BF16) {
-        const uint32_t v = (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);
-        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + o) = v;
+        uint32_t* op = reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + o);
+        op[0] = (uint32_t)f32_to_bf16(sum[0]) | ((uint32_t)f32_to_bf16(sum[1]) << 16);
+        op[1] = (uint32_t)f32_to_bf16(sum[2]) | ((uint32_t)f32_to_bf16(sum[3]) << 16);
     } else {
-        *reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o) = h2{(_Float16)s0, (_Float16)s1};
+        h2* op = reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o);
+        op[0] = h2{(_Float16)sum[0], (_Float16)sum[1]};
+        op[1] = h2{(_Float16)sum[2], (_Float16)sum[3]};
     }
 }
 
@@ -472,7 +508,7 @@ int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
         hipLaunchKernelGGL(pf_gateup_kernel, dim3(8 * (a.N / 128) * sg), dim3(PF_THREADS), PF_LDS, st, a);
     if (kernels & 4)
         hipLaunchKernelGGL(pf_down_kernel, dim3(8 * (a.K / 256) * sg), dim3(PF_THREADS), PF_LDS, st, a);
-    if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3(a.T, a.K / 256), dim3(128), 0, st, a);
+    if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3((a.T + 3) / 4, a.K / 256), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
