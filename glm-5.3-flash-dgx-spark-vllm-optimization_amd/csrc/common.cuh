@@ -80,8 +80,8 @@ __device__ __forceinline__ void fwht_xstage(float (&v)[8], bool upper) {
     const float sg = upper ? -1.0f : 1.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float p = __builtin_bit_cast(
-            float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), CTRL, 0xF, 0xF, false));
+        const float p = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v[i]), CTRL, 0xF,
+                                                                           0xF, true));
         v[i] = __builtin_fmaf(v[i], sg, p);
     }
 }
@@ -109,7 +109,7 @@ __device__ __forceinline__ void fwht128_x16(float (&v)[8], int lane) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int x = __builtin_bit_cast(int, v[i]);
-            const int lo = __builtin_amdgcn_update_dpp(0, x, 0x12C, 0xF, 0xF, false);
+            const int lo = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0xF, true);
             const float p = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(lo, x, 0x124, 0xF, 0xA, false));
             v[i] = __builtin_fmaf(v[i], sg, p);
         }
@@ -156,6 +156,16 @@ __device__ __forceinline__ void fwht128_h32(float (&v)[4], int lane) {
 __device__ __forceinline__ float sigmoid_dexp(float g) {
     const float e = (float)exp(-(double)g);
     return __fdiv_rn(1.0f, 1.0f + e);
+}
+
+// sigmoid in fp32 for the wide prefill epilogues (within a few ulp of sigmoid_dexp): e^-g = 2^y (1 + e ln 2) with
+// y = fp32(-g log2 e) and e its rounding residual, then one reciprocal (v_exp_f32 and v_rcp_f32 are ~1 ulp each)
+__device__ __forceinline__ float sigmoid_fast(float g) {
+    constexpr float L2E = 1.44269502162933349609375f, L2E_LO = 1.925963033500011079e-8f, LN2 = 0.693147180559945f;
+    const float y = -g * L2E;
+    const float e = __builtin_fmaf(-g, L2E, -y) - g * L2E_LO;
+    const float t = __builtin_amdgcn_exp2f(y);
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_fmaf(t, e * LN2, t));
 }
 
 // Split-K partials cross workgroups (and XCDs, each with its own L2) through device-coherent accesses instead of

@@ -10,7 +10,8 @@
 // Numerics (oracle/csrc/oracle.c mode 1 = the E3 kernels, code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu):
 //   gather   h13 = fp16(H(fp16(x * suh_g)) * r)                                         (exl3_fat_moe.cu:95-126)
 //   gate/up  g = (H(acc_g) * r) * svh_g, u likewise; iff L != 0: g = min(g, L), u = clamp(u, -L, L);
-//            a = (1 / (1 + (float)exp(-(double)g))) * g * u; h2 = fp16(H(fp16(fp16(a) * suh_d)) * r)  (:340-378)
+//            a = sigmoid(g) * g * u; h2 = fp16(H(fp16(fp16(a) * suh_d)) * r)  (:340-378; the reference's sigmoid is
+//            1 / (1 + (float)exp(-(double)g)), here an fp32 one within a few ulp of it)
 //   down     contribution ((H(acc_d) * r) * svh_d) * w16 per pair                       (:443-457); out[token] =
 //            the token's contributions summed in slot order (fp32), then the output dtype
 #include <algorithm>
@@ -358,7 +359,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
                     gv = fminf(gv, L);
                     uv = fminf(fmaxf(uv, -L), L);
                 }
-                const float act = sigmoid_dexp(gv) * gv * uv;
+                const float act = sigmoid_fast(gv) * gv * uv;
                 b[i] = (float)(_Float16)((_Float16)act * sud[i]);
             }
             fwht128_x16(b, lane);
