@@ -106,7 +106,7 @@ struct PrefillArgs {
     float limit;
     uint16_t* h13;          // [P][K] rotated gate/up inputs
     uint16_t* h2;           // [P][N] rotated down inputs
-    float* contrib;         // [P][K] per-pair weighted contribution (sorted position order)
+    float* contrib;         // [P][K] per-pair raw down accumulators (sorted position order)
     const int* inv;         // [P] pair j -> sorted position
     int topk;
     void* out;

@@ -13,7 +13,8 @@
 //            a = sigmoid(g) * g * u; h2 = fp16(H(fp16(fp16(a) * suh_d)) * r)  (:340-378; the reference's sigmoid is
 //            1 / (1 + (float)exp(-(double)g)), here an fp32 one within a few ulp of it)
 //   down     contribution ((H(acc_d) * r) * svh_d) * w16 per pair                       (:443-457); out[token] =
-//            the token's contributions summed in slot order (fp32), then the output dtype
+//            the token's contributions summed in slot order (fp32), then the output dtype. The down kernel stores the
+//            raw accumulators acc_d; the combine applies H, r, svh_d and w16 before summing.
 #include <algorithm>
 
 #include "common.cuh"
@@ -394,94 +395,95 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     f16v acc[8][2];
     pf_gemm(t, smem, acc);
 
-    // epilogue as in the gate/up kernel: 4 rows per wave at once, lane c of a row holding columns 8c .. 8c + 7 of
-    // each 128-column half
-    float* Cs = reinterpret_cast<float*>(smem);
+    // epilogue: the raw accumulators (rows < rn) straight from registers into contrib; the output rotation, svh and
+    // router weight are applied by the combine (the VALU work runs there, beside its memory traffic, instead of after
+    // this kernel's MFMAs). Lane n of block s holds column 16 (n / 8) + n % 8 + 8 s of the wave.
     const int lane = threadIdx.x & 63;
-    const int c = lane & 15, rsub = lane >> 4;
-    const _Float16* svd = reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + cb * 256 + 8 * c;
-    float sv[2][8];
+    const int n = lane & 31;
+    float* o = a.contrib + (size_t)row0 * K + cb * 256 + 64 * wv + 16 * (n >> 3) + (n & 7);
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
+    for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-        for (int i = 0; i < 8; i += 2) {
-            const h2 v2 = *reinterpret_cast<const h2*>(svd + hf * 128 + i);
-            sv[hf][i] = (float)v2.x, sv[hf][i + 1] = (float)v2.y;
-        }
-#pragma unroll
-    for (int rb = 0; rb < 8; ++rb) {
-        if (32 * rb >= rn) break;
-        pf_stage_rows(acc, Cs, rb);
-        __syncthreads();
-#pragma unroll
-        for (int pass = 0; pass < 2; ++pass) {
-            const int rl = wv * 8 + pass * 4 + rsub;
-            const int trow = 32 * rb + rl;
-            const int row = row0 + min(trow, rn - 1);
-            const float w = (float)u16_as_h(a.w16[row]);
-            float* o = a.contrib + (size_t)row * K + cb * 256 + 8 * c;
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const float* cr = Cs + rl * PF_CLD + hf * 128 + 8 * c;
-                float v[8];
-#pragma unroll
-                for (int i = 0; i < 8; i += 4) {
-                    const float4 v4 = *reinterpret_cast<const float4*>(cr + i);
-                    v[i] = v4.x, v[i + 1] = v4.y, v[i + 2] = v4.z, v[i + 3] = v4.w;
-                }
-                fwht128_x16(v, lane);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = v[i] * HAD_R * sv[hf][i] * w;
-                if (trow < rn) {
-                    *reinterpret_cast<float4*>(o + hf * 128) = make_float4(v[0], v[1], v[2], v[3]);
-                    *reinterpret_cast<float4*>(o + hf * 128 + 4) = make_float4(v[4], v[5], v[6], v[7]);
-                }
+        for (int r = 0; r < 16; ++r) {
+            const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (trow < rn) {
+                o[(size_t)trow * K] = acc[rb][0][r];
+                o[(size_t)trow * K + 8] = acc[rb][1][r];
             }
         }
-        __syncthreads();
-    }
 }
 
 // ------------------------------------------------------------------------------------------------ combine
 
-// One wave per (token t, 256 columns), 4 columns per lane: out[t] = sum over the token's slots k (in order) of the
-// valid pairs' contributions, in the output dtype (deterministic: no atomics). The slots' loads are all issued first.
+// One wave per (token t, 512 columns): out[t] = sum over the token's slots k (in order) of the valid pairs'
+// contributions ((H(acc) * r) * svh_d) * w16, in the output dtype (deterministic: no atomics). A 16-lane group
+// rotates one 128-column block (lane c holding columns 8c .. 8c + 7, DPP Hadamard); the loads of eight slots (their
+// raw rows and their experts' svh) are issued before the first rotation.
 __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     const int t = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
     if (t >= a.T) return;
-    const int col = blockIdx.y * 256 + 4 * (threadIdx.x & 63);
-    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < a.topk; k0 += 8) {                          // slots in order, 8 loads in flight
-        f32x4 cv[8];
-        bool ok[8];
-        // lanes 0..7 fetch the positions and validity of slots k0 .. k0 + 7 (one vector load each), broadcast by readlane;
-        // the eight row loads are then unconditional (no control-flow joins between them)
-        const int lk = k0 + (threadIdx.x & 7);
+    const int lane = threadIdx.x & 63;
+    const int col = blockIdx.y * 512 + 128 * (lane >> 4) + 8 * (lane & 15);
+    const bool live = blockIdx.y * 512 + 128 * (lane >> 4) < a.K;    // whole 16-lane groups
+    const int colc = live ? col : 0;
+    float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < a.topk; k0 += 8) {
+        // lanes 0..7 fetch slot k0 + lane's position, expert and weight (one vector load each), broadcast by readlane
+        const int lk = k0 + (lane & 7);
         const int pl = a.inv[t * a.topk + min(lk, a.topk - 1)];
-        const int okl = (int)(lk < a.topk) & (int)(a.pe[pl] >= 0);
+        const int el = a.pe[pl];
+        const int okl = (int)(lk < a.topk) & (int)(el >= 0);
+        const float wl = (float)u16_as_h(a.w16[pl]);
+        const int64_t svl = a.wt.d_svh[max(el, 0)];
+        f32x4 raw[8][2];
+        u32x4 sv[8];
+        bool ok[8];
+        float w[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < 8; ++k) {                                 // unconditional loads (no joins between them)
             const int pos = __builtin_amdgcn_readlane(pl, k);
             ok[k] = __builtin_amdgcn_readlane(okl, k) != 0;
-            cv[k] = *reinterpret_cast<const f32x4*>(a.contrib + (size_t)pos * a.K + col);
+            w[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k));
+            const uint64_t sp = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)svl, k)) |
+                                ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(svl >> 32), k) << 32);
+            const float* rp = a.contrib + (size_t)pos * a.K + colc;
+            raw[k][0] = *reinterpret_cast<const f32x4*>(rp);
+            raw[k][1] = *reinterpret_cast<const f32x4*>(rp + 4);
+            const uint16_t* svp = reinterpret_cast<const uint16_t*>(sp) + colc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[k][i] = *reinterpret_cast<const uint32_t*>(svp + 2 * i);
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (ok[k]) sum += cv[k];
+        for (int k = 0; k < 8; ++k) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = raw[k][0][i];
+                v[4 + i] = raw[k][1][i];
+            }
+            fwht128_x16(v, lane);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t s2 = sv[k][i >> 1];
+                const float svf = (float)u16_as_h((i & 1) ? s2 >> 16 : s2 & 0xFFFFu);
+                if (ok[k]) sum[i] += v[i] * HAD_R * svf * w[k];
+            }
+        }
     }
+    if (!live) return;
     const size_t o = (size_t)t * a.out_stride + col;
     if (a.odt == DT_F32) {
         float* op = reinterpret_cast<float*>(a.out) + o;
-        *reinterpret_cast<float2*>(op) = make_float2(sum[0], sum[1]);
-        *reinterpret_cast<float2*>(op + 2) = make_float2(sum[2], sum[3]);
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) *reinterpret_cast<float2*>(op + i) = make_float2(sum[i], sum[i + 1]);
     } else if (a.odt == DT_BF16) {
         uint32_t* op = reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + o);
-        op[0] = (uint32_t)f32_to_bf16(sum[0]) | ((uint32_t)f32_to_bf16(sum[1]) << 16);
-        op[1] = (uint32_t)f32_to_bf16(sum[2]) | ((uint32_t)f32_to_bf16(sum[3]) << 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) op[i] = (uint32_t)f32_to_bf16(sum[2 * i]) | ((uint32_t)f32_to_bf16(sum[2 * i + 1]) << 16);
     } else {
         h2* op = reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o);
-        op[0] = h2{(_Float16)sum[0], (_Float16)sum[1]};
-        op[1] = h2{(_Float16)sum[2], (_Float16)sum[3]};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) op[i] = h2{(_Float16)sum[2 * i], (_Float16)sum[2 * i + 1]};
     }
 }
 
@@ -509,7 +511,7 @@ int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
         hipLaunchKernelGGL(pf_gateup_kernel, dim3(8 * (a.N / 128) * sg), dim3(PF_THREADS), PF_LDS, st, a);
     if (kernels & 4)
         hipLaunchKernelGGL(pf_down_kernel, dim3(8 * (a.K / 256) * sg), dim3(PF_THREADS), PF_LDS, st, a);
-    if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3((a.T + 3) / 4, a.K / 256), dim3(256), 0, st, a);
+    if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3((a.T + 3) / 4, (a.K + 511) / 512), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
