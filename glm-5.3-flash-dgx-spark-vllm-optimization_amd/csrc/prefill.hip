@@ -158,7 +158,15 @@ __device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p
             s1 = x & 0xFFFFu;
             break;
     }
-    return __builtin_bit_cast(uint32_t, h2{mcg_value(s0), mcg_value(s1)});
+    // x = (s * MCG_MUL & MCG_MASK) ^ MCG_FLIP; value = fp16(x.lo) + fp16(x.hi), the pair's two values written to
+    // the low and high halves of one register by two SDWA adds (the second preserves the first)
+    const uint32_t x0 = ((s0 * MCG_MUL) & MCG_MASK) ^ MCG_FLIP, x1 = ((s1 * MCG_MUL) & MCG_MASK) ^ MCG_FLIP;
+    uint32_t d;
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=v"(d) : "v"(x0));
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+        : "+v"(d) : "v"(x1));
+    return d;
 }
 
 // Staging, PF_NS steps deep, entirely by LDS DMA (global_load_lds_dwordx4): per 32-k step every wave copies 64 A
