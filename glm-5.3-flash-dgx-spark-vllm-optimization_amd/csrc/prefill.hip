@@ -27,9 +27,13 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int PF_TM = PREFILL_TM;   // rows per tile (segment height)
 constexpr int PF_THREADS = 256;     // 4 waves, one per SIMD: each owns 64 columns of the tile for all 256 rows
-constexpr int PF_NS = 8;            // staged steps in flight (A rows and raw trellis words)
-constexpr int PF_ASB = PF_TM * 64;              // one A stage: 256 rows x 32 k fp16, bytes
-constexpr int PF_WSB = 4096;                    // one raw-word stage: 4 waves x 2 k tiles x 4 column tiles x 128 B
+constexpr int PF_KT = 4;            // 16-k trellis tiles per step (one wait + barrier per step)
+constexpr int PF_NS = 4;            // staged steps in flight (A rows and raw trellis words)
+constexpr int PF_RB = 32 * PF_KT;               // bytes of one A row in a stage (fp16, k permuted as stored)
+constexpr int PF_ASB = PF_TM * PF_RB;           // one A stage: 256 rows x 16 PF_KT k
+constexpr int PF_WWB = 512 * PF_KT;             // one wave's raw words of a step: PF_KT k tiles x 4 column tiles x 128 B
+constexpr int PF_WSB = 4 * PF_WWB;              // one raw-word stage (4 waves)
+constexpr int PF_DMA = PF_RB / 16 + PF_KT / 2;  // DMA instructions per wave per step
 constexpr size_t PF_LDS = (size_t)PF_NS * (PF_ASB + PF_WSB);   // 163,840 bytes (the whole LDS)
 constexpr int PF_CLD = 260;                     // epilogue staging row stride (floats): [32][PF_CLD] fp32
 
@@ -118,9 +122,9 @@ struct PfTile {
     int bcol0;                    // this wave's first column tile
 };
 
-// A stage row R: 64 bytes = four 16-byte chunks (storage k 0-7, 8-15, 16-23, 24-31), chunk g at slot g ^ pf_swz(R):
-// the fragment reads (16 consecutive rows per LDS pass, one chunk each) then touch every bank once.
-__device__ __forceinline__ int pf_swz(int R) { return (R >> 2) & 3; }
+// A stage row R: PF_RB bytes = 2 PF_KT 16-byte chunks (storage k 8g .. 8g + 7), chunk g at slot g ^ pf_swz(R): the
+// fragment reads (16 consecutive rows per LDS pass, one chunk each) then touch every bank once.
+__device__ __forceinline__ int pf_swz(int R) { return PF_RB == 64 ? (R >> 2) & 3 : (R >> 1) & 7; }
 
 // Decoded B operands, one fp16 pair at a time. Lane (n = lane % 32, h = lane / 32) of a k tile reads words
 // wp = 4c + 2h and wp + 1 of column tile t (c = n % 8, t = n / 8) and the predecessor word wp - 1 (mod 32):
@@ -169,77 +173,85 @@ __device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p
     return d;
 }
 
-// Staging, PF_NS steps deep, entirely by LDS DMA (global_load_lds_dwordx4): per 32-k step every wave copies 64 A
-// rows (four 1 KB instructions: 16 rows x 4 chunks, swizzled through the source addresses) and its own raw trellis
-// words (one 1 KB instruction: 2 k tiles x 4 column tiles). Step it + PF_NS - 1 is issued while step it is
-// multiplied, so each load has PF_NS - 1 steps of MFMA work to arrive; loads past the last step re-read it. The B
-// operands of step it + 1 are decoded in registers during step it (no LDS round trip: each wave decodes only its own
-// columns). One wait + barrier per step publishes A(it) (all waves) and the raw words of step it + 1 (this wave).
+// Staging, PF_NS steps of 16 PF_KT k deep, entirely by LDS DMA (global_load_lds_dwordx4): per step every wave copies
+// 64 A rows (1 KB instructions, swizzled through the source addresses) and its own raw trellis words (PF_KT k tiles x
+// 4 column tiles). Step it + PF_NS - 1 is issued while step it is multiplied, so each load has PF_NS - 1 steps of MFMA
+// work to arrive; loads past the last step re-read it. The B operands of step it + 1 are decoded in registers during
+// step it (no LDS round trip: each wave decodes only its own columns). One wait + barrier per step publishes A(it)
+// (all waves) and the raw words of step it + 1 (this wave).
 __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[8][2]) {
-    unsigned char* Ast = smem;                                        // [PF_NS][256 rows][64 B]
-    unsigned char* Wst = smem + PF_NS * PF_ASB;                       // [PF_NS][4 waves][2 k tiles][4 tiles][128 B]
+    unsigned char* Ast = smem;                                        // [PF_NS][256 rows][PF_RB]
+    unsigned char* Wst = smem + PF_NS * PF_ASB;                       // [PF_NS][4 waves][PF_KT k tiles][4 tiles][128 B]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int steps = t.kdim / 32;
-    // A DMA sources: instruction i of this wave = rows 64 wv + 16 i + lane / 4, slot lane % 4
-    const uint16_t* asrc[4];
+    constexpr int CPR = PF_RB / 16;                                   // 16-byte chunks per A row
+    const int steps = t.kdim / (16 * PF_KT);
+    // A DMA sources: instruction i of this wave = rows 64 wv + (64 / CPR) i + lane / CPR, slot lane % CPR
+    const uint16_t* asrc[CPR];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int R = 64 * wv + 16 * i + (lane >> 2);
-        const int chunk = (lane & 3) ^ pf_swz(R);
+    for (int i = 0; i < CPR; ++i) {
+        const int R = 64 * wv + (64 / CPR) * i + lane / CPR;
+        const int chunk = (lane % CPR) ^ pf_swz(R);
         asrc[i] = t.a_rows + (size_t)min(R, t.rn - 1) * t.kdim + 8 * chunk;
     }
-    // raw-word DMA source: lane -> k tile lane / 32, column tile (lane / 8) % 4, 16-byte piece lane % 8
+    // raw-word DMA sources: instruction i, lane -> k tile 2i + lane / 32, column tile (lane / 8) % 4, piece lane % 8
     const uint32_t* wsrc = t.btr + ((size_t)(lane >> 5) * t.btiles_n + t.bcol0 + ((lane >> 3) & 3)) * 32 + 4 * (lane & 7);
-    const size_t wstep = (size_t)2 * t.btiles_n * 32;                 // words per step (two k tiles)
+    const size_t wstep = (size_t)PF_KT * t.btiles_n * 32;             // words per step (PF_KT k tiles)
+    const size_t wins = (size_t)2 * t.btiles_n * 32;                  // words between a wave's W instructions
+    auto issue_w = [&](int sw) {
+        unsigned char* wd = Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB;
+#pragma unroll
+        for (int i = 0; i < PF_KT / 2; ++i) dma16(wsrc + (size_t)sw * wstep + i * wins, wd + i * 1024);
+    };
     auto issue = [&](int sa, int sw) {                                // A of step sa, raw words of step sw (clamped)
         sa = min(sa, steps - 1);
         sw = min(sw, steps - 1);
-        unsigned char* ad = Ast + (sa % PF_NS) * PF_ASB + wv * 4096;
+        unsigned char* ad = Ast + (sa % PF_NS) * PF_ASB + wv * 64 * PF_RB;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dma16(asrc[i] + (size_t)sa * 32, ad + i * 1024);
-        dma16(wsrc + (size_t)sw * wstep, Wst + (sw % PF_NS) * PF_WSB + wv * 1024);
+        for (int i = 0; i < CPR; ++i) dma16(asrc[i] + (size_t)sa * 16 * PF_KT, ad + i * 1024);
+        issue_w(sw);
     };
-    auto words = [&](int sw, uint32_t (&w)[2][3]) {                  // this lane's raw words of step sw
-        const unsigned char* wr = Wst + (sw % PF_NS) * PF_WSB + wv * 1024;
+    auto words = [&](int sw, uint32_t (&w)[PF_KT][3]) {              // this lane's raw words of step sw
+        const unsigned char* wr = Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB;
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) pf_load_words(wr + kh * 512, lane, w[kh]);
+        for (int kt = 0; kt < PF_KT; ++kt) pf_load_words(wr + kt * 512, lane, w[kt]);
     };
-    auto operands = [&](const uint32_t (&q)[2][8], h8 (&b)[2][2]) {   // decoded pairs -> B operands
+    auto operands = [&](const uint32_t (&q)[PF_KT][8], h8 (&b)[PF_KT][2]) {   // decoded pairs -> B operands
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-            b[kh][0] = __builtin_bit_cast(h8, u32x4{q[kh][0], q[kh][1], q[kh][4], q[kh][5]});
-            b[kh][1] = __builtin_bit_cast(h8, u32x4{q[kh][2], q[kh][3], q[kh][6], q[kh][7]});
+        for (int kt = 0; kt < PF_KT; ++kt) {
+            b[kt][0] = __builtin_bit_cast(h8, u32x4{q[kt][0], q[kt][1], q[kt][4], q[kt][5]});
+            b[kt][1] = __builtin_bit_cast(h8, u32x4{q[kt][2], q[kt][3], q[kt][6], q[kt][7]});
         }
     };
     auto afrag = [&](const unsigned char* as, int i) {                // A fragment i = (k tile i / 8, rows 32 (i % 8))
         const int R = 32 * (i & 7) + (lane & 31);
         const int slot = (2 * (i >> 3) + (lane >> 5)) ^ pf_swz(R);
-        return *reinterpret_cast<const h8*>(as + R * 64 + 16 * slot);
+        return *reinterpret_cast<const h8*>(as + R * PF_RB + 16 * slot);
     };
-    // One step, in a fixed instruction order (one wave per SIMD issues everything itself): the 32 MFMAs of step it,
-    // each followed by half of one fp16 pair's decode for step it + 1 (VALU work issued while the MFMA runs), the A
-    // fragments read four MFMA pairs ahead.
-    auto step = [&](int it, const h8 (&bc)[2][2], h8 (&bn)[2][2]) {
-        WAIT_VM(5 * (PF_NS - 2));                                     // A(it) and words(it + 1): the oldest batch
+    // One step, in a fixed instruction order (one wave per SIMD issues everything itself): the 16 PF_KT MFMAs of
+    // step it, each pair with one fp16 pair's decode for step it + 1 between them (VALU work issued while the MFMAs
+    // run), the A fragments read four MFMA pairs ahead.
+    constexpr int NF = 8 * PF_KT;                                     // A fragments (and decoded pairs) per step
+    auto step = [&](int it, const h8 (&bc)[PF_KT][2], h8 (&bn)[PF_KT][2]) {
+        WAIT_VM(PF_DMA * (PF_NS - 2));                                // A(it) and words(it + 1): the oldest batch
         LDS_BARRIER();
         issue(it + PF_NS - 1, it + PF_NS);
         __builtin_amdgcn_sched_barrier(0);
         const unsigned char* as = Ast + (it % PF_NS) * PF_ASB;
-        uint32_t w[2][3];
+        uint32_t w[PF_KT][3];
         words(it + 1, w);                                             // step it + 1 (past the end: never used)
-        h8 af[16];
+        h8 af[NF];
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[i] = afrag(as, i);
         __builtin_amdgcn_sched_barrier(0);
-        uint32_t q[2][8];
+        uint32_t q[PF_KT][8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            if (i + 4 < 16) af[i + 4] = afrag(as, i + 4);
-            const int kh = i >> 3, rb = i & 7;
-            acc[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kh][0], acc[rb][0], 0, 0, 0);
-            q[i >> 3][i & 7] = pf_decode_pair(w[i >> 3], i & 7);
-            acc[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kh][1], acc[rb][1], 0, 0, 0);
+        for (int i = 0; i < NF; ++i) {
+            if (i + 4 < NF) af[i + 4] = afrag(as, i + 4);
+            const int kt = i >> 3, rb = i & 7;
+            acc[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][0], acc[rb][0], 0, 0, 0);
+            q[kt][i & 7] = pf_decode_pair(w[kt], i & 7);
+            acc[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][1], acc[rb][1], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
         operands(q, bn);
@@ -252,20 +264,20 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
             for (int r = 0; r < 16; ++r) acc[rb][s][r] = 0.f;
     // prologue: raw words of step 0 first, then the batches that steps 0 .. PF_NS - 2 of the loop would have issued
     // (A(0 .. PF_NS - 2), words(1 .. PF_NS - 1)); decode step 0
-    dma16(wsrc, Wst + wv * 1024);
+    issue_w(0);
 #pragma unroll
     for (int j = 0; j < PF_NS - 1; ++j) issue(j, j + 1);
-    WAIT_VM(5 * (PF_NS - 1));                                         // the step-0 words (this wave's own)
-    h8 bA[2][2], bB[2][2];
+    WAIT_VM(PF_DMA * (PF_NS - 1));                                    // the step-0 words (this wave's own)
+    h8 bA[PF_KT][2], bB[PF_KT][2];
     {
-        uint32_t w[2][3], q[2][8];
+        uint32_t w[PF_KT][3], q[PF_KT][8];
         words(0, w);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) q[i >> 3][i & 7] = pf_decode_pair(w[i >> 3], i & 7);
+        for (int i = 0; i < NF; ++i) q[i >> 3][i & 7] = pf_decode_pair(w[i >> 3], i & 7);
         operands(q, bA);
     }
-    static_assert(5 * (PF_NS - 1) <= 63, "stages within the vmcnt range");
-    for (int it = 0; it < steps; it += 2) {                           // steps is even (kdim % 64 == 0)
+    static_assert(PF_DMA * (PF_NS - 1) <= 63 && PF_KT % 2 == 0, "stages within the vmcnt range");
+    for (int it = 0; it < steps; it += 2) {                           // steps is even (kdim % (32 PF_KT) == 0)
         step(it, bA, bB);
         step(it + 1, bB, bA);
     }
