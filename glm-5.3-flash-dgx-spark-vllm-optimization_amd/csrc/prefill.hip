@@ -203,13 +203,17 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
 #pragma unroll
         for (int i = 0; i < PF_KT / 2; ++i) dma16(wsrc + (size_t)sw * wstep + i * wins, wd + i * 1024);
     };
-    auto issue = [&](int sa, int sw) {                                // A of step sa, raw words of step sw (clamped)
+    auto issue_one = [&](int k, int sa, int sw) {                     // DMA instruction k of the batch (A(sa), W(sw))
         sa = min(sa, steps - 1);
         sw = min(sw, steps - 1);
-        unsigned char* ad = Ast + (sa % PF_NS) * PF_ASB + wv * 64 * PF_RB;
+        if (k < CPR)
+            dma16(asrc[k] + (size_t)sa * 16 * PF_KT, Ast + (sa % PF_NS) * PF_ASB + wv * 64 * PF_RB + k * 1024);
+        else
+            dma16(wsrc + (size_t)sw * wstep + (k - CPR) * wins, Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB + (k - CPR) * 1024);
+    };
+    auto issue = [&](int sa, int sw) {                                // the whole batch
 #pragma unroll
-        for (int i = 0; i < CPR; ++i) dma16(asrc[i] + (size_t)sa * 16 * PF_KT, ad + i * 1024);
-        issue_w(sw);
+        for (int k = 0; k < PF_DMA; ++k) issue_one(k, sa, sw);
     };
     auto words = [&](int sw, uint32_t (&w)[PF_KT][3]) {              // this lane's raw words of step sw
         const unsigned char* wr = Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB;
@@ -232,10 +236,10 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     // step it, each pair with one fp16 pair's decode for step it + 1 between them (VALU work issued while the MFMAs
     // run), the A fragments read four MFMA pairs ahead.
     constexpr int NF = 8 * PF_KT;                                     // A fragments (and decoded pairs) per step
+    constexpr int DMA_EVERY = NF / PF_DMA;                            // MFMA pairs between DMA instructions
     auto step = [&](int it, const h8 (&bc)[PF_KT][2], h8 (&bn)[PF_KT][2]) {
         WAIT_VM(PF_DMA * (PF_NS - 2));                                // A(it) and words(it + 1): the oldest batch
         LDS_BARRIER();
-        issue(it + PF_NS - 1, it + PF_NS);
         __builtin_amdgcn_sched_barrier(0);
         const unsigned char* as = Ast + (it % PF_NS) * PF_ASB;
         uint32_t w[PF_KT][3];
@@ -247,6 +251,9 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         uint32_t q[PF_KT][8];
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
+            // the next batch's DMA instructions spread over the step (the CU's address path takes them one at a
+            // time; issued together after the barrier they would stall every wave behind each other)
+            if (i % DMA_EVERY == 0 && i / DMA_EVERY < PF_DMA) issue_one(i / DMA_EVERY, it + PF_NS - 1, it + PF_NS);
             if (i + 4 < NF) af[i + 4] = afrag(as, i + 4);
             const int kt = i >> 3, rb = i & 7;
             acc[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][0], acc[rb][0], 0, 0, 0);
