@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the routed-MoE layer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|prefill|fp8]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|prefill|fp8|stack]
 
 Default workload (one "step" = one MoE layer call): the decode MoE layer, T=8 tokens, hidden 4096, 288 experts,
 sigmoid router + bias, top-8, routed scale 2.5, intermediate 1024 (one tensor-parallel rank's shard), EXL3 4-bit
@@ -322,6 +322,78 @@ def run_fp8(args, torch, dev):
                           f"{steps} timed steps"}
 
 
+def run_stack(args, torch, dev):
+    """42-layer stacked decode, T=8, captured as one HIP graph and replayed: each layer has its own 288 EXL3 experts
+    (42 x 1.82 GB = 76.4 GB, far beyond every cache) and its own router; the layer's output is added to the residual
+    stream that feeds the next layer's router. Expert popularity is Zipf(1.2)-skewed in the router logits: one
+    hidden channel is held at a constant c and the router column that reads it is -1.2 ln(rank + 1) / c over a
+    per-layer random ranking of the experts, so logit_e = x.W_e - 1.2 ln(rank_e + 1). Bytes per replay = sum over
+    layers of D_l x (6,291,456 + 30,720) + router weight and bias + activations, D_l counted per layer."""
+    from mi355moe import ops, synthetic
+    T, nl, c0 = args.tokens, args.stack_layers, 8.0
+    log(f"[bench] building {nl} layers x {E} experts ({nl * E * (EXPERT_TRELLIS + EXPERT_SCALES) / 1e9:.1f} GB) ...")
+    layers, routers = [], []
+    for l in range(nl):
+        layers.append(synthetic.exl3_layer(E, K, N, seed=700 + l, device=dev))
+        w, b = synthetic.router(E, K, seed=800 + l, device=dev)
+        g = torch.Generator(device="cpu")
+        g.manual_seed(900 + l)
+        rank = torch.empty(E, dtype=torch.float32)
+        rank[torch.randperm(E, generator=g)] = torch.arange(E, dtype=torch.float32)
+        w[:, 0] = (-1.2 * torch.log(rank + 1.0) / c0).to(dev, torch.bfloat16)
+        routers.append((w, b))
+    xs = [synthetic.activations(T, K, seed=950, device=dev)] + [torch.empty(T, K, dtype=torch.bfloat16, device=dev)
+                                                              for _ in range(nl)]
+    xs[0][:, 0] = c0
+    outs = [torch.empty(T, K, dtype=torch.bfloat16, device=dev) for _ in range(nl)]
+    ids = [torch.empty(T, TOPK, dtype=torch.int32, device=dev) for _ in range(nl)]
+    wts = [torch.empty(T, TOPK, dtype=torch.float32, device=dev) for _ in range(nl)]
+
+    def forward():
+        for l in range(nl):
+            w, b = routers[l]
+            ops.moe_layer(layers[l], xs[l], router_w=w, topk=TOPK, bias=b, routed_scale=SCALE, limit=LIMIT,
+                          out=outs[l], picks_out=(ids[l], wts[l]))
+            torch.add(xs[l], outs[l], out=xs[l + 1])
+
+    forward()                                                 # eager: sizes the workspace, fixes the routing
+    torch.cuda.synchronize()
+    ref = xs[nl].clone()
+    distinct = [int(torch.unique(i).numel()) for i in ids]
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        forward()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        forward()
+    graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(ref, xs[nl]):
+        raise RuntimeError("stacked-layer graph replay differs from the eager pass")
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    reps = max(4, args.steps // 4)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    nbytes = sum(d * (EXPERT_TRELLIS + EXPERT_SCALES) for d in distinct) + nl * (E * K * 2 + E * 4 + 3 * T * K * 2)
+    gbs = nbytes / (ms / 1000.0) / 1e9
+    return {"stack_us_per_layer": round(ms * 1000.0 / nl, 2), "stack_ms_per_replay": round(ms, 4),
+            "stack_gbs": round(gbs, 1), "stack_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "stack_distinct_mean": round(sum(distinct) / nl, 2),
+            "stack_config": f"{nl}-layer stacked decode, T={T}, {E} EXL3 experts per layer "
+                            f"({nl * E * (EXPERT_TRELLIS + EXPERT_SCALES) / 1e9:.1f} GB), Zipf(1.2) expert popularity "
+                            f"in the router logits, residual stream between layers, one HIP graph, {reps} replays"}
+
+
 def _traffic(distinct: float):
     """HBM bytes per gate/up launch from the committed PMC measurement (profiles/decode_gateup_traffic.json: FETCH_SIZE
     and WRITE_SIZE per launch, each scaled by what the counter reads for a device copy of known size), rescaled to
@@ -349,7 +421,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill", "fp8"])
+    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill", "fp8", "stack"])
+    ap.add_argument("--stack-layers", type=int, default=42)
     ap.add_argument("--prefill-tokens", type=int, default=8192)
     ap.add_argument("--fp8-tokens", type=int, default=2048)
     ap.add_argument("--tokens", type=int, default=8)
@@ -369,7 +442,7 @@ def main():
     import mi355moe
     mi355moe._lib.lib()
     dev = torch.device("cuda", 0)
-    if args.workload in ("prefill", "fp8"):
+    if args.workload in ("prefill", "fp8", "stack"):
         args.no_cpu_baseline = True
         res = run_decode(argparse.Namespace(**{**vars(args), "steps": 8, "warmup": 2}), torch, mi355moe, dev)
     else:
@@ -380,6 +453,9 @@ def main():
     if args.workload in ("all", "fp8"):
         log("[bench] fp8 ...")
         res.update(run_fp8(args, torch, dev))
+    if args.workload in ("all", "stack"):
+        log("[bench] stacked decode ...")
+        res.update(run_stack(args, torch, dev))
     if args.copy_probe_mib > 0:
         copy_probe(torch, dev, args.copy_probe_mib)
     print(json.dumps(res), flush=True)
