@@ -188,6 +188,7 @@ def run_decode(args, torch, mi355moe, dev):
         threads = min(16, os.cpu_count() or 1)
         c = combos[0]
         sec, reps, d = cpu_baseline(torch, layers[c[0]], xs[c[1]], info[c][1], info[c][2], threads)
+        res["cpu_block_a"] = cpu_block_a(torch, threads)
         res["cpu_baseline"] = {"value": round(step_bytes(c) / sec / 1e9, 4), "unit": "GB/s", "cores": threads,
                                "kind": "port", "seconds_per_call": round(sec, 4),
                                "sample": f"{reps} repetitions of one full T={T} layer call ({d} distinct experts) "
@@ -392,6 +393,47 @@ def run_stack(args, torch, dev):
             "stack_config": f"{nl}-layer stacked decode, T={T}, {E} EXL3 experts per layer "
                             f"({nl * E * (EXPERT_TRELLIS + EXPERT_SCALES) / 1e9:.1f} GB), Zipf(1.2) expert popularity "
                             f"in the router logits, residual stream between layers, one HIP graph, {reps} replays"}
+
+
+def cpu_block_a(torch, threads: int):
+    """Configuration A, the CPU-runnable case: a dense MoE block (T=64, hidden 1024, 32 experts, softmax top-4
+    renormalised, intermediate 512, SwiGLU, bf16 weights ~N(0, 0.02), activations ~N(0, 1)) in torch on the host,
+    fp32 accumulation on the bf16 weights; seeded draws in the order router, w13, w2, x. A reported baseline only
+    (median of 9 calls after 3 warm-ups)."""
+    import statistics
+    T_, d, n, k, inter = 64, 1024, 32, 4, 512
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(20261201)
+    wr = (torch.randn(n, d, generator=g) * 0.02).to(torch.bfloat16)
+    w13 = (torch.randn(n, 2 * inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(n, d, inter, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(T_, d, generator=g).to(torch.bfloat16)
+
+    def block():
+        p = torch.softmax(x.float() @ wr.float().t(), dim=-1)
+        w, ids = torch.topk(p, k, dim=-1)
+        w = w / w.sum(-1, keepdim=True)
+        out = torch.zeros(T_, d)
+        for e in ids.unique().tolist():
+            rows, slot = (ids == e).nonzero(as_tuple=True)
+            h = x[rows].float() @ w13[e].float().t()
+            a = torch.nn.functional.silu(h[:, :inter]) * h[:, inter:]
+            out.index_add_(0, rows, (a @ w2[e].float().t()) * w[rows, slot, None])
+        return out.to(torch.bfloat16)
+
+    for _ in range(3):
+        block()
+    ts = []
+    for _ in range(9):
+        t0 = time.perf_counter()
+        block()
+        ts.append(time.perf_counter() - t0)
+    ms = statistics.median(ts) * 1000.0
+    flop = 2.0 * T_ * k * 3 * d * inter
+    return {"value": round(ms, 3), "unit": "ms per block call", "cores": threads, "kind": "torch",
+            "gflops": round(flop / (ms / 1000.0) / 1e9, 2),
+            "sample": f"T={T_}, hidden {d}, {n} experts, softmax top-{k}, intermediate {inter}, bf16 weights, "
+                      "fp32 accumulation, median of 9 calls"}
 
 
 def _traffic(distinct: float):
