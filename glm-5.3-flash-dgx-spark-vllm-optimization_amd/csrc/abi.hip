@@ -570,6 +570,26 @@ int mi355moe_moe_layer(const mi355moe_exl3_layer* layer, const void* x, int x_dt
             return rc_launch(rc);
         lsrc = lg;
     }
+    const int64_t P = T * topk;
+    if (choose_path(layer, P, MI355MOE_PATH_AUTO) == MI355MOE_PATH_DECODE && P <= ROUTE_SMALL_MAX_P) {
+        // decode sizes: the top-k and the permutation in one workgroup, then the expert GEMVs and the combine
+        DecodePlan p;
+        DecodeWs w;
+        if (int rc = prep_decode(layer, x, x_dtype, x_stride, T, topk, limit, out, out_dtype, out_stride, workspace,
+                                 (size_t)base, p, w))
+            return rc;
+        RouteArgs& r = w.ra;
+        r.ids = ids;
+        r.ids64 = 0;
+        r.w = wts;
+        r.wdt = dt_w(MI355MOE_F32);
+        r.emap = nullptr;
+        r.n_global = 0;
+        if (int rc = launch_topk_route(lsrc, (int)T, (int)E, bias, (int)topk, routed_scale, renormalize ? 1 : 0, ids,
+                                       wts, r, stream))
+            return rc_launch(rc);
+        return rc_launch(launch_decode(w.da, p.rmax, stream, MI355MOE_STAGE_ALL >> 1));
+    }
     if (int rc = launch_router_topk(lsrc, (int)T, (int)E, bias, (int)topk, routed_scale, renormalize ? 1 : 0, ids, wts,
                                     stream))
         return rc_launch(rc);

@@ -295,6 +295,114 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
     route_small_body<IT>(a, sh);
 }
 
+// ------------------------------------------------------------------------------------------------ top-k + permutation
+
+// Order key of a candidate: the choice key (score + bias; -0 made +0) mapped to an unsigned integer with the same
+// order, above the complement of its id, so the largest 64-bit key is the largest choice key with the lowest id among
+// equal ones (the reference's order).
+__device__ __forceinline__ uint64_t topk_order(float key, int e) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, key + 0.0f);
+    const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+// One wave's top-k of one token (E <= 1024 candidates, lane l holding candidates l + 64 j): topk rounds of "largest
+// order key" (the lane-local best, then a butterfly max over the wave); the owner of the winner drops it. Scores s
+// (sigmoid through double exp, as topk_body) go to sco [E] for the weights; weights are renormalised over the picks
+// summed in pick order and scaled, as topk_body.
+// Maximum of a 64-bit value over the wave, returned in every lane: rotations by 1, 2, 4, 8 inside each 16-lane row
+// (DPP, no LDS), then the four row maxima by readlane.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    uint64_t o = dpp_u64<0x121>(v);                                   // row_ror:1
+    v = o > v ? o : v;
+    o = dpp_u64<0x122>(v);                                            // row_ror:2
+    v = o > v ? o : v;
+    o = dpp_u64<0x124>(v);                                            // row_ror:4
+    v = o > v ? o : v;
+    o = dpp_u64<0x128>(v);                                            // row_ror:8
+    v = o > v ? o : v;
+    uint64_t m = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint64_t rv = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 16 * r) << 32) |
+                            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
+        m = rv > m ? rv : m;
+    }
+    return m;
+}
+
+template <int J>                                                      // J >= ceil(E / 64)
+__device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E, const float* __restrict__ bias,
+                                          int topk, float scale, int renorm, float* sco, int32_t* __restrict__ ids_row,
+                                          float* __restrict__ wts_row) {
+    const int lane = threadIdx.x & 63;
+    uint64_t ok[J];
+    const int nj = (E + 63) >> 6;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        ok[j] = 0;
+        const int e = lane + 64 * j;
+        if (j < nj && e < E) {
+            const float lg = lrow[e];
+            const float sv = (float)(1.0 / (1.0 + exp(-(double)lg)));
+            sco[e] = sv;
+            ok[j] = topk_order(sv + (bias ? bias[e] : 0.f), e);
+        }
+    }
+    float total = 0.f, mine = 0.f;
+    int mine_e = 0;
+    for (int k = 0; k < topk; ++k) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) best = ok[j] > best ? ok[j] : best;
+        best = wave_max_u64(best);
+        const int e = (int)(0xFFFFFFFFu - (uint32_t)best);
+        if ((e & 63) == lane) {
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (j == (e >> 6)) ok[j] = 0;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const float sv = sco[e];                                      // the owner wrote it before the first round
+        total = total + sv;
+        if (lane == k) {
+            mine = sv;
+            mine_e = e;
+        }
+    }
+    if (lane < topk) {
+        float wv = mine;
+        if (renorm) wv = __fdiv_rn(wv, total + 1e-20f);
+        ids_row[lane] = mine_e;
+        wts_row[lane] = wv * scale;
+    }
+}
+
+// The decode-size front end in one workgroup (1024 threads, P = T topk <= ROUTE_SMALL_MAX_P): every wave takes the
+// top-k of tokens w, w + 16, ...; then the whole permutation of route_small_body over the picks (int32 ids, fp32
+// weights). The picks reach the permutation through global memory inside the workgroup (written, then a barrier).
+// Shared memory: the permutation's P + 2 (n + 1) ints, then 16 x E scores.
+template <int J>
+__global__ __launch_bounds__(1024) void topk_route_kernel(const float* __restrict__ logits, int T, int E,
+                                                          const float* __restrict__ bias, int topk, float scale,
+                                                          int renorm, int32_t* __restrict__ ids,
+                                                          float* __restrict__ wts, RouteArgs a) {
+    extern __shared__ int sh[];
+    const int wv = threadIdx.x >> 6;
+    float* sco = reinterpret_cast<float*>(sh + a.P + 2 * (a.n + 1)) + wv * E;
+    for (int t = wv; t < T; t += 16)
+        topk_wave<J>(logits + (size_t)t * E, E, bias, topk, scale, renorm, sco, ids + (size_t)t * topk,
+                     wts + (size_t)t * topk);
+    __syncthreads();
+    route_small_body<int32_t>(a, sh);
+}
+
 // Tables from pre-sorted pairs (the exl3_moe contract): counts [n+1] int64 give each expert's span of the sorted
 // arrays; experts with 0 < count <= R get segments and pe = e on their span, every other row pe = -1; token ids
 // outside [0, B) are skipped (pe = -1). code/fork/kernels/exl3.cu:529-566 (route_prep).
@@ -430,6 +538,26 @@ int launch_router_topk(const float* logits, int T, int E, const float* bias, int
     if (T > 0)
         hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(1024), 0, st, logits, T, E, bias, topk, scale, renorm,
                            ids, wts);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_topk_route(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
+                      int32_t* ids, float* wts, const RouteArgs& a, hipStream_t st) {
+    if (a.P > ROUTE_SMALL_MAX_P || a.ids64 || a.ids != ids || E > TOPK_MAX_E) return -1;
+    const size_t shm = (size_t)(a.P + 2 * (a.n + 1)) * sizeof(int) + (size_t)16 * E * sizeof(float);
+    static bool attr = false;                                         // up to 37 KB + 64 KB for E = 1024
+    if (!attr) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(topk_route_kernel<16>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024) != hipSuccess)
+            return -1;
+        attr = true;
+    }
+    if (E <= 320)
+        hipLaunchKernelGGL(topk_route_kernel<5>, dim3(1), dim3(1024), shm, st, logits, T, E, bias, topk, scale, renorm,
+                           ids, wts, a);
+    else
+        hipLaunchKernelGGL(topk_route_kernel<16>, dim3(1), dim3(1024), shm, st, logits, T, E, bias, topk, scale,
+                           renorm, ids, wts, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
