@@ -184,22 +184,25 @@ __device__ __forceinline__ float weight_f32(const void* w, int wdt, int j) {
 }
 
 // block-wide inclusive scan of one int per thread (blockDim.x a multiple of 64, <= 1024)
+// Inclusive scan over the 64 lanes of a wave by DPP (no LDS): shifts by 1, 2, 4, 8 inside each 16-lane row (lanes
+// without a source add 0), then lane 15 of rows 0 and 2 into rows 1 and 3 and lane 31 into rows 2 and 3.
+__device__ __forceinline__ int wave_scan_incl(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return v;
+}
+
 __device__ __forceinline__ int block_scan_incl(int v, int* tot, int& total) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(v, o, 64);
-        if (lane >= o) v += y;
-    }
+    v = wave_scan_incl(v);
     if (lane == 63) tot[wv] = v;
     __syncthreads();
     if (wv == 0) {
-        int s = lane < nw ? tot[lane] : 0;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(s, o, 64);
-            if (lane >= o) s += y;
-        }
+        int s = wave_scan_incl(lane < nw ? tot[lane] : 0);
         if (lane < nw) tot[lane] = s;
     }
     __syncthreads();
@@ -278,8 +281,14 @@ __device__ void route_small_body(const RouteArgs& a, int* sh) {
     build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot);
     for (int j = threadIdx.x; j < a.P; j += blockDim.x) {
         const int l = loc[j];
-        int rank = 0;
-        for (int i = 0; i < j; ++i) rank += loc[i] == l;
+        int rank = 0;                                                // earlier pairs with the same local id
+        const int4* l4 = reinterpret_cast<const int4*>(loc);
+#pragma unroll 8
+        for (int i4 = 0; i4 < (j >> 2); ++i4) {
+            const int4 v = l4[i4];
+            rank += (v.x == l) + (v.y == l) + (v.z == l) + (v.w == l);
+        }
+        for (int i = j & ~3; i < j; ++i) rank += loc[i] == l;
         const int pos = start[l] + rank;
         a.tok[pos] = j / a.topk;
         a.w16[pos] = weight_f16(a.w, a.wdt, j);
@@ -355,27 +364,23 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E,
             ok[j] = topk_order(sv + (bias ? bias[e] : 0.f), e);
         }
     }
-    float total = 0.f, mine = 0.f;
-    int mine_e = 0;
+    int mine_e = 0;                                                   // lane k: the k-th pick
     for (int k = 0; k < topk; ++k) {
         uint64_t best = 0;
 #pragma unroll
         for (int j = 0; j < J; ++j) best = ok[j] > best ? ok[j] : best;
         best = wave_max_u64(best);
         const int e = (int)(0xFFFFFFFFu - (uint32_t)best);
-        if ((e & 63) == lane) {
 #pragma unroll
-            for (int j = 0; j < J; ++j)
-                if (j == (e >> 6)) ok[j] = 0;
-        }
-        __builtin_amdgcn_wave_barrier();
-        const float sv = sco[e];                                      // the owner wrote it before the first round
-        total = total + sv;
-        if (lane == k) {
-            mine = sv;
-            mine_e = e;
-        }
+        for (int j = 0; j < J; ++j)
+            if (j == (e >> 6) && lane == (e & 63)) ok[j] = 0;
+        if (lane == k) mine_e = e;
     }
+    // scores of the picks (written by their owners before the rounds), summed in pick order
+    const float mine = lane < topk ? sco[mine_e] : 0.f;
+    float total = 0.f;
+    for (int k = 0; k < topk; ++k)
+        total = total + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), k));
     if (lane < topk) {
         float wv = mine;
         if (renorm) wv = __fdiv_rn(wv, total + 1e-20f);
