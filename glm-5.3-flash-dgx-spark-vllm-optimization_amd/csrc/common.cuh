@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace mi355moe {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -117,6 +119,26 @@ __device__ __forceinline__ void fwht128_x16(float (&v)[8], int lane) {
     fwht_xstage<0x128>(v, lane & 8);                                 // row_ror:8: lane ^ 8
 }
 
+// The value of lane l ^ M (M = 1, 2, 4, 8, 16, 32) without LDS: quad permutes (1, 2), two row rotations with bank
+// masks (4), a row rotation (8), v_permlane16_swap (16) and v_permlane32_swap (32).
+template <int M>
+__device__ __forceinline__ float xor_lane(float v, int lane) {
+    const int x = __builtin_bit_cast(int, v);
+    if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true));
+    if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true));
+    if constexpr (M == 4) {
+        const int lo = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0xF, true);          // row_ror:12: lane + 4
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(lo, x, 0x124, 0xF, 0xA, false));  // lane - 4
+    }
+    if constexpr (M == 8) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true));
+    if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+        return __builtin_bit_cast(float, (lane & 16) ? r[0] : r[1]);
+    }
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    return __builtin_bit_cast(float, (lane & 32) ? r[0] : r[1]);
+}
+
 // 128-point Walsh-Hadamard of one row held as two values per lane (lane l: elements 2l, 2l+1) of a wave:
 // butterfly strides 1 (in registers), then 2, 4, ..., 64 across lanes xor 1, 2, ..., 32; the lower element of
 // every pair keeps a + b, the upper a - b (the fixed fp32 order of exl3.cu:273-284).
@@ -124,13 +146,19 @@ __device__ __forceinline__ void fwht128_w64(float& a, float& b, int lane) {
     const float s = a + b, d = a - b;
     a = s;
     b = d;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const float pa = __shfl_xor(a, m, 64), pb = __shfl_xor(b, m, 64);
+    auto stage = [&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        const float pa = xor_lane<m>(a, lane), pb = xor_lane<m>(b, lane);
         const bool up = (lane & m) != 0;
         a = up ? pa - a : a + pa;
         b = up ? pb - b : b + pb;
-    }
+    };
+    stage(std::integral_constant<int, 1>());
+    stage(std::integral_constant<int, 2>());
+    stage(std::integral_constant<int, 4>());
+    stage(std::integral_constant<int, 8>());
+    stage(std::integral_constant<int, 16>());
+    stage(std::integral_constant<int, 32>());
 }
 
 // 128-point Walsh-Hadamard of a row held as four values per lane by 32 lanes (lane l of the half-wave:

@@ -53,8 +53,13 @@ __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int6
                         acc = __builtin_fmaf(__builtin_bit_cast(float, xv[i] & 0xFFFF0000u), wf[2 * i + 1], acc);
                     }
                 }
-#pragma unroll
-                for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m, 64);
+                // butterfly m = 32, 16, ..., 1 (the fixed order), partners by permlane / DPP
+                acc = acc + xor_lane<32>(acc, lane);
+                acc = acc + xor_lane<16>(acc, lane);
+                acc = acc + xor_lane<8>(acc, lane);
+                acc = acc + xor_lane<4>(acc, lane);
+                acc = acc + xor_lane<2>(acc, lane);
+                acc = acc + xor_lane<1>(acc, lane);
                 if (lane == 0) part[c][tt] = acc;
             }
         }
