@@ -139,6 +139,46 @@ __device__ __forceinline__ void pf_load_words(const unsigned char* wk, int lane,
     w[1] = v.x;
     w[2] = v.y;
 }
+// The pair's decode in two halves (software-pipelined across MFMA pairs by the GEMM loop): pf_pair_products =
+// the two states times MCG_MUL, pf_pair_values = mask, flip and the fp16 sums.
+struct PfPair {
+    uint32_t x0, x1;
+};
+__device__ __forceinline__ PfPair pf_pair_products(const uint32_t (&w)[3], int p) {
+    const uint32_t pw = w[p >> 2], x = w[(p >> 2) + 1];
+    uint32_t s0, s1;
+    switch (p & 3) {
+        case 0: {
+            const uint32_t D = __builtin_amdgcn_alignbit(pw, x, 20);
+            s0 = __builtin_amdgcn_ubfe(D, 8, 16);
+            s1 = __builtin_amdgcn_ubfe(D, 4, 16);
+            break;
+        }
+        case 1:
+            s0 = __builtin_amdgcn_alignbit(pw, x, 20) & 0xFFFFu;
+            s1 = x >> 16;
+            break;
+        case 2:
+            s0 = __builtin_amdgcn_ubfe(x, 12, 16);
+            s1 = __builtin_amdgcn_ubfe(x, 8, 16);
+            break;
+        default:
+            s0 = __builtin_amdgcn_ubfe(x, 4, 16);
+            s1 = x & 0xFFFFu;
+            break;
+    }
+    return PfPair{s0 * MCG_MUL, s1 * MCG_MUL};
+}
+__device__ __forceinline__ uint32_t pf_pair_values(PfPair m) {
+    const uint32_t x0 = (m.x0 & MCG_MASK) ^ MCG_FLIP, x1 = (m.x1 & MCG_MASK) ^ MCG_FLIP;
+    uint32_t d;
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=v"(d) : "v"(x0));
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+        : "+v"(d) : "v"(x1));
+    return d;
+}
+
 __device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p) {
     const uint32_t pw = w[p >> 2], x = w[(p >> 2) + 1];
     uint32_t s0, s1;
@@ -249,6 +289,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         for (int i = 0; i < 4; ++i) af[i] = afrag(as, i);
         __builtin_amdgcn_sched_barrier(0);
         uint32_t q[PF_KT][8];
+        PfPair prev{0u, 0u};
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             // the next batch's DMA instructions spread over the step (the CU's address path takes them one at a
@@ -256,11 +297,16 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
             if (i % DMA_EVERY == 0 && i / DMA_EVERY < PF_DMA) issue_one(i / DMA_EVERY, it + PF_NS - 1, it + PF_NS);
             if (i + 4 < NF) af[i + 4] = afrag(as, i + 4);
             const int kt = i >> 3, rb = i & 7;
+            // pair i's products after the first MFMA, pair i - 1's values after the second: no VALU instruction
+            // waits on the one before it while the MFMAs run
             acc[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][0], acc[rb][0], 0, 0, 0);
-            q[kt][i & 7] = pf_decode_pair(w[kt], i & 7);
+            const PfPair cur = pf_pair_products(w[kt], i & 7);
             acc[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][1], acc[rb][1], 0, 0, 0);
+            if (i > 0) q[(i - 1) >> 3][(i - 1) & 7] = pf_pair_values(prev);
+            prev = cur;
             __builtin_amdgcn_sched_barrier(0);
         }
+        q[PF_KT - 1][7] = pf_pair_values(prev);
         operands(q, bn);
     };
 #pragma unroll
