@@ -53,6 +53,27 @@ def test_layer_equals_chained_entries(cuda, model, T, given_logits):
         assert torch.equal(got, ref_o), out_dtype
 
 
+@pytest.mark.parametrize("E2,topk,T", [(1024, 32, 5), (32, 4, 3), (320, 8, 16), (321, 8, 16)])
+def test_layer_router_widths(cuda, E2, topk, T):
+    """Router widths on both sides of the one-wave top-k's 320-candidate unroll, and top-32 of 1024: the layer's
+    picks against the oracle router and its output against the chained entry points."""
+    from mi355moe import ops, synthetic
+    K2, N2 = 512, 256
+    _say(f"moe_layer E={E2} topk={topk} T={T}")
+    ex = synthetic.exl3_layer(E2, K2, N2, seed=E2 + topk, device=cuda, svh_scale=0.05)
+    w, b = synthetic.router(E2, K2, seed=E2 + 1, device=cuda)
+    x = synthetic.activations(T, K2, seed=E2 + 2, device=cuda)
+    got, ids, wts = ops.moe_layer(ex, x, router_w=w, topk=topk, bias=b, routed_scale=2.5, return_picks=True)
+    ref, rid, rw = _chained(ex, x, w, b, topk, 2.5)
+    torch.cuda.synchronize()
+    lg = routing.router_logits(x.float().cpu().numpy(), w.float().cpu().numpy())
+    oid, ow = routing.topk_sigmoid_bias(lg, b.float().cpu().numpy(), topk, 2.5)
+    assert np.array_equal(ids.cpu().numpy(), oid)
+    assert np.array_equal(wts.cpu().numpy(), ow)
+    assert torch.equal(ids, rid) and torch.equal(wts, rw)
+    assert torch.equal(got, ref)
+
+
 def test_layer_routing_vs_oracle(cuda, model):
     from mi355moe import ops, synthetic
     ex, w, b = model
