@@ -25,10 +25,15 @@ int rc_launch(int r) {
     return e == hipSuccess ? -1 : -(int)e;
 }
 
-// Bump allocator over the caller's workspace (or a dry run that only measures).
+// Every workspace layout starts with a control block of words that keep their value between calls (zero), at the
+// same offset whatever the shapes of the calls sharing the workspace: data of one call never lands on them.
+// Word 0: the arrival counter of the one-launch decode front end.
+constexpr size_t WS_CONTROL_BYTES = 256;
+
+// Bump allocator over the caller's workspace (or a dry run that only measures), past the control block.
 struct Carve {
     char* base;
-    size_t off = 0;
+    size_t off = WS_CONTROL_BYTES;
     explicit Carve(void* b) : base(static_cast<char*>(b)) {}
     template <typename T>
     T* take(size_t count) {
@@ -239,7 +244,7 @@ int mi355moe_router_topk(const float* logits, int64_t T, int64_t E, const float*
 
 int64_t mi355moe_route_workspace_bytes(int64_t P, int64_t n) {
     if (P < 0 || n < 0) return -1;
-    return (int64_t)(align_up((size_t)P * 4) + align_up(((size_t)(P + 1023) / 1024) * (n + 1) * 4) +
+    return (int64_t)(WS_CONTROL_BYTES + align_up((size_t)P * 4) + align_up(((size_t)(P + 1023) / 1024) * (n + 1) * 4) +
                      align_up((size_t)(n + 1) * 4));
 }
 
@@ -523,6 +528,7 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
 static size_t router_scratch(void* base, int64_t T, int64_t topk, int64_t E, float** logits, int32_t** ids,
                              float** wts) {
     Carve c(base);
+    c.off = 0;
     float* l = c.take<float>((size_t)std::max<int64_t>(1, T * E));
     int32_t* i = c.take<int32_t>((size_t)std::max<int64_t>(1, T * topk));
     float* wv = c.take<float>((size_t)std::max<int64_t>(1, T * topk));
@@ -559,20 +565,23 @@ int mi355moe_moe_layer(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     float* lg;
     int32_t* ids;
     float* wts;
+    unsigned* arrivals = static_cast<unsigned*>(workspace);         // control word 0
     router_scratch(static_cast<char*>(workspace) + align_up((size_t)base), T, topk, E, &lg, &ids, &wts);
     if (ids_out) ids = ids_out;
     if (weights_out) wts = weights_out;
     // router GEMV, top-k, then the routed experts from the picks
+    const int64_t P = T * topk;
+    const bool small = choose_path(layer, P, MI355MOE_PATH_AUTO) == MI355MOE_PATH_DECODE && P <= ROUTE_SMALL_MAX_P;
     const float* lsrc = logits;
-    if (router_w) {
+    if (router_w && !small) {
         if (int rc = launch_router_logits(static_cast<const uint16_t*>(x), x_stride,
                                           static_cast<const uint16_t*>(router_w), (int)T, (int)K, (int)E, lg, stream))
             return rc_launch(rc);
         lsrc = lg;
     }
-    const int64_t P = T * topk;
-    if (choose_path(layer, P, MI355MOE_PATH_AUTO) == MI355MOE_PATH_DECODE && P <= ROUTE_SMALL_MAX_P) {
-        // decode sizes: the top-k and the permutation in one workgroup, then the expert GEMVs and the combine
+    if (small) {
+        // decode sizes: the router GEMV (when given the weight), the top-k and the permutation in one launch (the
+        // last router workgroup ranks), then the expert GEMVs and the combine
         DecodePlan p;
         DecodeWs w;
         if (int rc = prep_decode(layer, x, x_dtype, x_stride, T, topk, limit, out, out_dtype, out_stride, workspace,
@@ -585,9 +594,13 @@ int mi355moe_moe_layer(const mi355moe_exl3_layer* layer, const void* x, int x_dt
         r.wdt = dt_w(MI355MOE_F32);
         r.emap = nullptr;
         r.n_global = 0;
-        if (int rc = launch_topk_route(lsrc, (int)T, (int)E, bias, (int)topk, routed_scale, renormalize ? 1 : 0, ids,
-                                       wts, r, stream))
-            return rc_launch(rc);
+        const int rc = router_w ? launch_router_route(static_cast<const uint16_t*>(x), x_stride,
+                                                      static_cast<const uint16_t*>(router_w), (int)K, lg, (int)T,
+                                                      (int)E, bias, (int)topk, routed_scale, renormalize ? 1 : 0, ids,
+                                                      wts, r, arrivals, stream)
+                                : launch_topk_route(lsrc, (int)T, (int)E, bias, (int)topk, routed_scale,
+                                                    renormalize ? 1 : 0, ids, wts, r, stream);
+        if (rc) return rc_launch(rc);
         return rc_launch(launch_decode(w.da, p.rmax, stream, MI355MOE_STAGE_ALL >> 1));
     }
     if (int rc = launch_router_topk(lsrc, (int)T, (int)E, bias, (int)topk, routed_scale, renormalize ? 1 : 0, ids, wts,

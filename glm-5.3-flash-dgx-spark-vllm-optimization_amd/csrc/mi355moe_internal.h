@@ -163,6 +163,10 @@ int launch_route(const RouteArgs& a, hipStream_t st);
 // top-k of T tokens' logits and the permutation of the picks in one workgroup (P <= ROUTE_SMALL_MAX_P, a.ids = ids)
 int launch_topk_route(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
                       int32_t* ids, float* wts, const RouteArgs& a, hipStream_t st);
+// router GEMV + top-k + permutation in one launch (bf16 x and router weight, K % 512 == 0)
+int launch_router_route(const uint16_t* x, int64_t x_stride, const uint16_t* w, int K, float* logits, int T, int E,
+                        const float* bias, int topk, float scale, int renorm, int32_t* ids, float* wts,
+                        const RouteArgs& a, unsigned* arrivals, hipStream_t st);
 int launch_route_counts(const int64_t* counts64, const int64_t* token_sorted, const uint16_t* weight_sorted, int B,
                         const RouteArgs& a, hipStream_t st);
 // kernels: bit 0 gate/up, bit 1 down, bit 2 combine

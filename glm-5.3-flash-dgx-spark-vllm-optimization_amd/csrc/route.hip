@@ -24,6 +24,8 @@ constexpr int RL_MAXC = 16;    // K chunks of 512 (K <= 8192)
 // i = 0..7, sequentially in fp32 (bf16 x bf16 products are exact in fp32, so the fused multiply-add rounds like
 // an add); the 64 lane partials are combined by the xor butterfly m = 32, 16, ..., 1; the chunk sums are then added
 // in chunk order c = 0, 1, ... (wave 0 adds them from LDS). Waves past K/512 only join the barriers.
+// COH: the logits are stored as device-coherent words (read back by another workgroup of the same grid).
+template <bool COH = false>
 __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int64_t x_stride,
                                             const uint16_t* __restrict__ w, int T, int K, int E, int e,
                                             float* __restrict__ logits) {
@@ -67,7 +69,8 @@ __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int6
         if (threadIdx.x < RL_TCHUNK && t0 + (int)threadIdx.x < T) {
             float sum = part[0][threadIdx.x];
             for (int cc = 1; cc < chunks; ++cc) sum = sum + part[cc][threadIdx.x];
-            logits[(size_t)(t0 + threadIdx.x) * E + e] = sum;
+            if (COH) st_coherent(logits + (size_t)(t0 + threadIdx.x) * E + e, sum);
+            else logits[(size_t)(t0 + threadIdx.x) * E + e] = sum;
         }
         __syncthreads();
     }
@@ -351,10 +354,10 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return m;
 }
 
-template <int J>                                                      // J >= ceil(E / 64)
+template <int J, bool COH = false>                                   // J >= ceil(E / 64); COH: coherent logit loads
 __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E, const float* __restrict__ bias,
                                           int topk, float scale, int renorm, float* sco, int32_t* __restrict__ ids_row,
-                                          float* __restrict__ wts_row) {
+                                          float* __restrict__ wts_row, int* ids_sh, float* wts_sh) {
     const int lane = threadIdx.x & 63;
     uint64_t ok[J];
     const int nj = (E + 63) >> 6;
@@ -363,7 +366,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E,
         ok[j] = 0;
         const int e = lane + 64 * j;
         if (j < nj && e < E) {
-            const float lg = lrow[e];
+            const float lg = COH ? ld_coherent(lrow + e) : lrow[e];
             const float sv = (float)(1.0 / (1.0 + exp(-(double)lg)));
             sco[e] = sv;
             ok[j] = topk_order(sv + (bias ? bias[e] : 0.f), e);
@@ -391,26 +394,69 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E,
         if (renorm) wv = __fdiv_rn(wv, total + 1e-20f);
         ids_row[lane] = mine_e;
         wts_row[lane] = wv * scale;
+        ids_sh[lane] = mine_e;
+        wts_sh[lane] = wv * scale;
     }
 }
 
-// The decode-size front end in one workgroup (1024 threads, P = T topk <= ROUTE_SMALL_MAX_P): every wave takes the
-// top-k of tokens w, w + 16, ...; then the whole permutation of route_small_body over the picks (int32 ids, fp32
-// weights). The picks reach the permutation through global memory inside the workgroup (written, then a barrier).
-// Shared memory: the permutation's P + 2 (n + 1) ints, then 16 x E scores.
+// The decode-size front end in one workgroup (P = T topk <= ROUTE_SMALL_MAX_P): wave w of the workgroup's nw takes
+// the top-k of tokens w, w + nw, ...; then the whole permutation of route_small_body over the picks (int32 ids, fp32
+// weights). The picks are written to global memory (the caller's copy) and to shared memory, from which the
+// permutation reads them. Shared memory: the permutation's P + 2 (n + 1) ints, nw x E scores, then the picks' P ids
+// and P weights.
+template <int J, bool COH>
+__device__ __forceinline__ void topk_route_body(const float* __restrict__ logits, int T, int E,
+                                                const float* __restrict__ bias, int topk, float scale, int renorm,
+                                                int32_t* __restrict__ ids, float* __restrict__ wts, const RouteArgs& a,
+                                                int* sh) {
+    const int wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    float* sco = reinterpret_cast<float*>(sh + a.P + 2 * (a.n + 1)) + wv * E;
+    int* ids_sh = sh + a.P + 2 * (a.n + 1) + nw * E;
+    float* wts_sh = reinterpret_cast<float*>(ids_sh + a.P);
+    for (int t = wv; t < T; t += nw)
+        topk_wave<J, COH>(logits + (size_t)t * E, E, bias, topk, scale, renorm, sco, ids + (size_t)t * topk,
+                          wts + (size_t)t * topk, ids_sh + t * topk, wts_sh + t * topk);
+    __syncthreads();
+    RouteArgs b = a;
+    b.ids = ids_sh;
+    b.w = wts_sh;
+    b.wdt = DT_F32;
+    route_small_body<int32_t>(b, sh);
+}
+
 template <int J>
 __global__ __launch_bounds__(1024) void topk_route_kernel(const float* __restrict__ logits, int T, int E,
                                                           const float* __restrict__ bias, int topk, float scale,
                                                           int renorm, int32_t* __restrict__ ids,
                                                           float* __restrict__ wts, RouteArgs a) {
     extern __shared__ int sh[];
-    const int wv = threadIdx.x >> 6;
-    float* sco = reinterpret_cast<float*>(sh + a.P + 2 * (a.n + 1)) + wv * E;
-    for (int t = wv; t < T; t += 16)
-        topk_wave<J>(logits + (size_t)t * E, E, bias, topk, scale, renorm, sco, ids + (size_t)t * topk,
-                     wts + (size_t)t * topk);
+    topk_route_body<J, false>(logits, T, E, bias, topk, scale, renorm, ids, wts, a, sh);
+}
+
+// The whole decode-size front end in one launch: the router GEMV (one workgroup per expert, logits_body), then the
+// workgroup that finishes last (an arrival counter at a fixed workspace offset, returned to zero by that
+// workgroup) runs topk_route_body over all logits. Logits cross workgroups, and XCDs with their own L2, as device-coherent stores and loads; a workgroup
+// arrives only after its stores have completed.
+template <int J>
+__global__ __launch_bounds__(1024) void router_route_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                            const uint16_t* __restrict__ w, int T, int K, int E,
+                                                            float* __restrict__ logits, const float* __restrict__ bias,
+                                                            int topk, float scale, int renorm,
+                                                            int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                            RouteArgs a, unsigned* arrivals) {
+    extern __shared__ int sh[];
+    __shared__ int last;
+    logits_body<true>(x, x_stride, w, T, K, E, blockIdx.x, logits);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    route_small_body<int32_t>(a, sh);
+    // the E-th arrival ranks; counted modulo E so that a counter left non-zero (a workspace not zero-filled before
+    // its first use) still elects one workgroup per call and the tables are always rebuilt
+    if (threadIdx.x == 0)
+        last = (__hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) % (unsigned)E == 0u;
+    __syncthreads();
+    if (!last) return;
+    if (threadIdx.x == 0) *arrivals = 0u;
+    topk_route_body<J, true>(logits, T, E, bias, topk, scale, renorm, ids, wts, a, sh);
 }
 
 // Tables from pre-sorted pairs (the exl3_moe contract): counts [n+1] int64 give each expert's span of the sorted
@@ -554,8 +600,8 @@ int launch_router_topk(const float* logits, int T, int E, const float* bias, int
 int launch_topk_route(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
                       int32_t* ids, float* wts, const RouteArgs& a, hipStream_t st) {
     if (a.P > ROUTE_SMALL_MAX_P || a.ids64 || a.ids != ids || E > TOPK_MAX_E) return -1;
-    const size_t shm = (size_t)(a.P + 2 * (a.n + 1)) * sizeof(int) + (size_t)16 * E * sizeof(float);
-    static bool attr = false;                                         // up to 37 KB + 64 KB for E = 1024
+    const size_t shm = (size_t)(3 * a.P + 2 * (a.n + 1)) * sizeof(int) + (size_t)16 * E * sizeof(float);
+    static bool attr = false;                                         // up to 45 KB + 64 KB for E = 1024
     if (!attr) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(topk_route_kernel<16>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024) != hipSuccess)
@@ -568,6 +614,28 @@ int launch_topk_route(const float* logits, int T, int E, const float* bias, int 
     else
         hipLaunchKernelGGL(topk_route_kernel<16>, dim3(1), dim3(1024), shm, st, logits, T, E, bias, topk, scale,
                            renorm, ids, wts, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_router_route(const uint16_t* x, int64_t x_stride, const uint16_t* w, int K, float* logits, int T, int E,
+                        const float* bias, int topk, float scale, int renorm, int32_t* ids, float* wts,
+                        const RouteArgs& a, unsigned* arrivals, hipStream_t st) {
+    if (a.P > ROUTE_SMALL_MAX_P || a.ids64 || a.ids != ids || E > TOPK_MAX_E || K % 512 || K / 512 > RL_MAXC) return -1;
+    const int nw = K / 512;
+    const size_t shm = (size_t)(3 * a.P + 2 * (a.n + 1)) * sizeof(int) + (size_t)nw * E * sizeof(float);
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(router_route_kernel<16>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024) != hipSuccess)
+            return -1;
+        attr = true;
+    }
+    if (E <= 320)
+        hipLaunchKernelGGL(router_route_kernel<5>, dim3(E), dim3(64 * nw), shm, st, x, x_stride, w, T, K, E, logits,
+                           bias, topk, scale, renorm, ids, wts, a, arrivals);
+    else
+        hipLaunchKernelGGL(router_route_kernel<16>, dim3(E), dim3(64 * nw), shm, st, x, x_stride, w, T, K, E, logits,
+                           bias, topk, scale, renorm, ids, wts, a, arrivals);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
