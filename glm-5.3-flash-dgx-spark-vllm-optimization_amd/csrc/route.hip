@@ -34,25 +34,26 @@ __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int6
     const int c = threadIdx.x >> 6;                 // chunk of this wave
     const int chunks = K / 512;
     const int k0 = c * 512 + lane * 8;
-    u32x4 wv = {0u, 0u, 0u, 0u};
-    if (c < chunks) wv = *reinterpret_cast<const u32x4*>(w + (size_t)e * K + k0);
-    float wf[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        wf[2 * i] = __builtin_bit_cast(float, wv[i] << 16);
-        wf[2 * i + 1] = __builtin_bit_cast(float, wv[i] & 0xFFFF0000u);
-    }
     for (int t0 = 0; t0 < T; t0 += RL_TCHUNK) {
         if (c < chunks) {
+            // the pass's token rows and the weight chunk are all loaded before any is used (one memory latency
+            // per pass; later passes find the weight in L2)
+            u32x4 xv[RL_TCHUNK];
+#pragma unroll
+            for (int tt = 0; tt < RL_TCHUNK; ++tt)
+                xv[tt] = t0 + tt < T ? *reinterpret_cast<const u32x4*>(x + (size_t)(t0 + tt) * x_stride + k0)
+                                     : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 wv = *reinterpret_cast<const u32x4*>(w + (size_t)e * K + k0);
 #pragma unroll
             for (int tt = 0; tt < RL_TCHUNK; ++tt) {
                 float acc = 0.f;
                 if (t0 + tt < T) {
-                    const u32x4 xv = *reinterpret_cast<const u32x4*>(x + (size_t)(t0 + tt) * x_stride + k0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        acc = __builtin_fmaf(__builtin_bit_cast(float, xv[i] << 16), wf[2 * i], acc);
-                        acc = __builtin_fmaf(__builtin_bit_cast(float, xv[i] & 0xFFFF0000u), wf[2 * i + 1], acc);
+                        acc = __builtin_fmaf(__builtin_bit_cast(float, xv[tt][i] << 16),
+                                             __builtin_bit_cast(float, wv[i] << 16), acc);
+                        acc = __builtin_fmaf(__builtin_bit_cast(float, xv[tt][i] & 0xFFFF0000u),
+                                             __builtin_bit_cast(float, wv[i] & 0xFFFF0000u), acc);
                     }
                 }
                 // butterfly m = 32, 16, ..., 1 (the fixed order), partners by permlane / DPP
@@ -306,6 +307,87 @@ __device__ void route_small_body(const RouteArgs& a, int* sh) {
     }
 }
 
+// One compare-exchange stage of an ascending bitonic sort across the wave: partner = lane ^ S; k = the size of the
+// sequences being merged.
+template <int S>
+__device__ __forceinline__ uint32_t bitonic_stage(uint32_t key, int lane, int k) {
+    const uint32_t o = __builtin_bit_cast(uint32_t, xor_lane<S>(__builtin_bit_cast(float, key), lane));
+    const bool up = (lane & k) == 0, low = (lane & S) == 0;
+    return (low == up) ? (o < key ? o : key) : (o > key ? o : key);
+}
+
+// route_small_body for the picks of a top-k (P <= 64 pairs, every token's picks distinct experts, seg >= T rows):
+// the workgroup zeroes the call's counters and the counts, then wave 0 alone sorts the pairs' keys (local id << 6 |
+// pair index) with a bitonic network across its lanes, which is the stable sorted order of route_small_body; an
+// expert then has c <= T <= seg pairs, so each eligible expert (c <= R, not the sentinel) is one segment, found as a
+// run of equal ids. The tables equal route_small_body's.
+template <typename IT>
+__device__ void route_wave64(const RouteArgs& a) {
+    if (a.zero)
+        for (int64_t i = threadIdx.x; i < a.zero_words; i += blockDim.x) a.zero[i] = 0u;
+    if (a.counts)
+        for (int e = threadIdx.x; e <= a.n; e += blockDim.x) a.counts[e] = 0;
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    const IT* ids = reinterpret_cast<const IT*>(a.ids);
+    uint32_t key = 0xFFFFFFFFu;
+    if (lane < a.P) key = ((uint32_t)local_id<IT>(ids[lane], a.emap, a.n_global, a.n) << 6) | (uint32_t)lane;
+    key = bitonic_stage<1>(key, lane, 2);
+    key = bitonic_stage<2>(key, lane, 4);
+    key = bitonic_stage<1>(key, lane, 4);
+    key = bitonic_stage<4>(key, lane, 8);
+    key = bitonic_stage<2>(key, lane, 8);
+    key = bitonic_stage<1>(key, lane, 8);
+    key = bitonic_stage<8>(key, lane, 16);
+    key = bitonic_stage<4>(key, lane, 16);
+    key = bitonic_stage<2>(key, lane, 16);
+    key = bitonic_stage<1>(key, lane, 16);
+    key = bitonic_stage<16>(key, lane, 32);
+    key = bitonic_stage<8>(key, lane, 32);
+    key = bitonic_stage<4>(key, lane, 32);
+    key = bitonic_stage<2>(key, lane, 32);
+    key = bitonic_stage<1>(key, lane, 32);
+    key = bitonic_stage<32>(key, lane, 64);
+    key = bitonic_stage<16>(key, lane, 64);
+    key = bitonic_stage<8>(key, lane, 64);
+    key = bitonic_stage<4>(key, lane, 64);
+    key = bitonic_stage<2>(key, lane, 64);
+    key = bitonic_stage<1>(key, lane, 64);
+    const bool valid = lane < a.P;                                   // sorted position lane holds a pair
+    const int l = (int)(key >> 6), j = (int)(key & 63u);
+    const int lprev = __shfl(l, lane > 0 ? lane - 1 : 0, 64);
+    const bool start = valid && (lane == 0 || lprev != l);
+    const uint64_t smask = __ballot(start);
+    const uint64_t above = lane == 63 ? 0ull : smask >> (lane + 1);
+    const int c = (above ? lane + 1 + __builtin_ctzll(above) : a.P) - lane;   // run length, at run starts
+    const bool elig = start && l < a.n && c <= a.R;
+    const uint64_t emask = __ballot(elig);
+    const uint64_t upto = smask & (lane == 63 ? ~0ull : ((1ull << (lane + 1)) - 1));
+    const int rs = upto ? 63 - __builtin_clzll(upto) : 0;           // this lane's run start
+    const bool run_elig = __shfl(elig ? 1 : 0, rs, 64) != 0;
+    if (valid) {
+        a.tok[lane] = j / a.topk;
+        a.w16[lane] = weight_f16(a.w, a.wdt, j);
+        if (a.w32) a.w32[lane] = weight_f32(a.w, a.wdt, j);
+        a.pe[lane] = run_elig ? l : -1;
+        a.inv[j] = lane;
+    }
+    if (elig) {
+        const int sg = __builtin_popcountll(emask & ((1ull << lane) - 1));
+        if (sg < a.S_cap) {
+            a.seg_expert[sg] = l;
+            a.seg_row0[sg] = lane;
+            a.seg_rows[sg] = c;
+        }
+    }
+    if (start && a.counts) a.counts[l] = c;
+    if (lane == 0) {
+        const int ns = __builtin_popcountll(emask);
+        a.nseg[0] = ns < a.S_cap ? ns : a.S_cap;
+    }
+}
+
 template <typename IT>
 __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
     extern __shared__ int sh[];
@@ -421,7 +503,8 @@ __device__ __forceinline__ void topk_route_body(const float* __restrict__ logits
     b.ids = ids_sh;
     b.w = wts_sh;
     b.wdt = DT_F32;
-    route_small_body<int32_t>(b, sh);
+    if (a.P <= 64 && a.seg >= T) route_wave64<int32_t>(b);
+    else route_small_body<int32_t>(b, sh);
 }
 
 template <int J>
