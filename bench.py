@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the routed-MoE layer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|prefill|fp8|stack]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|prefill|fp8|e4m3t|stack]
 
 Default workload (one "step" = one MoE layer call): the decode MoE layer, T=8 tokens, hidden 4096, 288 experts,
 sigmoid router + bias, top-8, routed scale 2.5, intermediate 1024 (one tensor-parallel rank's shard), EXL3 4-bit
@@ -332,6 +332,43 @@ def run_fp8(args, torch, dev):
                           f"{steps} timed steps"}
 
 
+def run_e4m3_trellis(args, torch, dev):
+    """Trellis-sourced e4m3 variant, T=2048 (hidden 4096, 288 EXL3 4-bit experts, top-8, intermediate 1024):
+    activations quantised per row to e4m3 after the input rotation, weights rounded to e4m3, the down input
+    requantised per row; sigmoid top-8 x2.5 of uniform-random router logits inside the step."""
+    from mi355moe import ops, synthetic
+    T = args.fp8_tokens
+    n_layers = 2
+    layers = [synthetic.exl3_layer(E, K, N, seed=640 + l, device=dev) for l in range(n_layers)]
+    x = synthetic.activations(T, K, seed=660, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(661)
+    logits = [torch.rand(T, E, generator=g, device=dev) * 4 - 2 for _ in range(n_layers)]
+    outs = [torch.empty(T, K, dtype=torch.bfloat16, device=dev) for _ in range(n_layers)]
+
+    def step(l):
+        ids, wts = ops.router_topk(logits[l], TOPK, None, routed_scale=SCALE)
+        ops.moe_forward_ids_e4m3(layers[l], x, ids, wts, limit=LIMIT, out=outs[l])
+
+    for w in range(max(2, args.warmup // 4)):
+        step(w % n_layers)
+    torch.cuda.synchronize()
+    steps = max(4, args.steps // 4)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for k in range(steps):
+        step(k % n_layers)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    P = T * TOPK
+    return {"e4m3t_tokens_per_s": round(T / (ms / 1000.0), 1), "e4m3t_ms_per_layer": round(ms, 4),
+            "e4m3t_tflops": round(2.0 * P * 3 * K * N / (ms / 1000.0) / 1e12, 2),
+            "e4m3t_config": f"T={T}, {E} EXL3 4-bit experts, trellis-sourced e4m3 numerics (per-row e4m3 activations, "
+                            f"weights rounded to e4m3, fp32 sums), sigmoid top-{TOPK} x{SCALE} of uniform-random "
+                            f"logits, {n_layers} layers alternated, {steps} timed steps"}
+
+
 def run_stack(args, torch, dev):
     """42-layer stacked decode, T=8, captured as one HIP graph and replayed: each layer has its own 288 EXL3 experts
     (42 x 1.82 GB = 76.4 GB, far beyond every cache) and its own router; the layer's output is added to the residual
@@ -472,7 +509,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill", "fp8", "stack"])
+    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill", "fp8", "e4m3t", "stack"])
     ap.add_argument("--stack-layers", type=int, default=42)
     ap.add_argument("--prefill-tokens", type=int, default=8192)
     ap.add_argument("--fp8-tokens", type=int, default=2048)
@@ -493,7 +530,7 @@ def main():
     import mi355moe
     mi355moe._lib.lib()
     dev = torch.device("cuda", 0)
-    if args.workload in ("prefill", "fp8", "stack"):
+    if args.workload in ("prefill", "fp8", "e4m3t", "stack"):
         args.no_cpu_baseline = True
         res = run_decode(argparse.Namespace(**{**vars(args), "steps": 8, "warmup": 2}), torch, mi355moe, dev)
     else:
@@ -504,6 +541,9 @@ def main():
     if args.workload in ("all", "fp8"):
         log("[bench] fp8 ...")
         res.update(run_fp8(args, torch, dev))
+    if args.workload in ("all", "e4m3t"):
+        log("[bench] e4m3 trellis ...")
+        res.update(run_e4m3_trellis(args, torch, dev))
     if args.workload in ("all", "stack"):
         log("[bench] stacked decode ...")
         res.update(run_stack(args, torch, dev))

@@ -319,7 +319,8 @@ struct PrefillWs {
     size_t bytes;
 };
 
-void carve_prefill(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t N, PrefillWs& w, int& S_cap) {
+void carve_prefill(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t N, PrefillWs& w, int& S_cap,
+                   bool e4m3 = false) {
     Carve c(ws);
     RouteArgs& r = w.ra;
     PrefillArgs& d = w.pa;
@@ -341,6 +342,14 @@ void carve_prefill(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t
     d.h13 = c.take<uint16_t>((size_t)P * K);
     d.h2 = c.take<uint16_t>((size_t)P * N);
     d.contrib = c.take<float>((size_t)P * K);
+    if (e4m3) {
+        r.w32 = c.take<float>(P);
+        d.w32 = r.w32;
+        d.asc = c.take<float>(P);
+        d.dsc = c.take<float>(P);
+        d.amaxd = c.take<unsigned>(P);
+        d.vd = c.take<float>((size_t)P * N);
+    }
     w.bytes = c.off;
 }
 
@@ -432,6 +441,67 @@ static int prep_decode(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     return 0;
 }
 
+// The grouped (prefill) tier over 256-row expert tiles for validated arguments: E3's fp16 numerics, or with e4m3 the
+// trellis-sourced e4m3 variant (activations quantized per row, weights rounded to e4m3).
+static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride, int64_t T,
+                       const void* ids, int ids_dtype, const void* weights, int weights_dtype, int64_t topk,
+                       const int64_t* expert_map, int64_t n_global, float limit, void* out, int out_dtype,
+                       int64_t out_stride, void* workspace, size_t workspace_bytes, int stages, bool e4m3,
+                       hipStream_t stream) {
+    const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n, P = T * topk;
+    RouteArgs r;
+    PrefillWs w;
+    int S_cap;
+    carve_prefill(workspace, P, T, n, K, N, w, S_cap, e4m3);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    r = w.ra;
+    r.seg = PREFILL_TM;
+    r.S_cap = S_cap;
+    PrefillArgs& d = w.pa;
+    d.wt = tables(layer);
+    d.n = (int)n;
+    d.K = (int)K;
+    d.N = (int)N;
+    d.P = (int)P;
+    d.T = (int)T;
+    d.x = x;
+    d.xdt = dt_act(x_dtype);
+    d.x_stride = x_stride;
+    d.tok = r.tok;
+    d.w16 = r.w16;
+    d.pe = r.pe;
+    d.inv = r.inv;
+    d.topk = (int)topk;
+    d.seg_expert = r.seg_expert;
+    d.seg_row0 = r.seg_row0;
+    d.seg_rows = r.seg_rows;
+    d.nseg = r.nseg;
+    d.S_cap = S_cap;
+    d.limit = limit;
+    d.out = out;
+    d.odt = dt_w(out_dtype);
+    d.out_stride = out_stride;
+    d.e4m3 = e4m3 ? 1 : 0;
+    if (prefill_setup()) return rc_launch(-1);
+    r.ids = ids;
+    r.ids64 = ids_dtype == MI355MOE_I64;
+    r.w = weights;
+    r.wdt = dt_w(weights_dtype);
+    r.emap = expert_map;
+    r.n_global = expert_map ? n_global : 0;
+    r.P = (int)P;
+    r.topk = (int)topk;
+    r.n = (int)n;
+    r.R = 1 << 30;
+    if (stages & MI355MOE_STAGE_ROUTE)
+        if (int rc = launch_route(r, stream)) return rc_launch(rc);
+    int kernels = 0;
+    if (stages & MI355MOE_STAGE_GATEUP) kernels |= 1 | 2;
+    if (stages & MI355MOE_STAGE_DOWN) kernels |= 4;
+    if (stages & MI355MOE_STAGE_COMBINE) kernels |= 8;
+    return rc_launch(launch_prefill(d, stream, kernels));
+}
+
 int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
                                 int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
                                 int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
@@ -453,58 +523,10 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
     const int use = choose_path(layer, P, path);
     if (use == MI355MOE_PATH_PREFILL && !(layer->flags & MI355MOE_LAYER_SHARED_W13_SUH))
         return MI355MOE_EUNSUPPORTED;                   // the grouped tier gathers once with the gate's suh
-    if (use == MI355MOE_PATH_PREFILL) {
-        RouteArgs r;
-        PrefillWs w;
-        int S_cap;
-        carve_prefill(workspace, P, T, n, K, N, w, S_cap);
-        if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
-        r = w.ra;
-        r.seg = PREFILL_TM;
-        r.S_cap = S_cap;
-        PrefillArgs& d = w.pa;
-        d.wt = tables(layer);
-        d.n = (int)n;
-        d.K = (int)K;
-        d.N = (int)N;
-        d.P = (int)P;
-        d.T = (int)T;
-        d.x = x;
-        d.xdt = dt_act(x_dtype);
-        d.x_stride = x_stride;
-        d.tok = r.tok;
-        d.w16 = r.w16;
-        d.pe = r.pe;
-        d.inv = r.inv;
-        d.topk = (int)topk;
-        d.seg_expert = r.seg_expert;
-        d.seg_row0 = r.seg_row0;
-        d.seg_rows = r.seg_rows;
-        d.nseg = r.nseg;
-        d.S_cap = S_cap;
-        d.limit = limit;
-        d.out = out;
-        d.odt = dt_w(out_dtype);
-        d.out_stride = out_stride;
-        if (prefill_setup()) return rc_launch(-1);
-        r.ids = ids;
-        r.ids64 = ids_dtype == MI355MOE_I64;
-        r.w = weights;
-        r.wdt = dt_w(weights_dtype);
-        r.emap = expert_map;
-        r.n_global = expert_map ? n_global : 0;
-        r.P = (int)P;
-        r.topk = (int)topk;
-        r.n = (int)n;
-        r.R = 1 << 30;
-        if (stages & MI355MOE_STAGE_ROUTE)
-            if (int rc = launch_route(r, stream)) return rc_launch(rc);
-        int kernels = 0;
-        if (stages & MI355MOE_STAGE_GATEUP) kernels |= 1 | 2;
-        if (stages & MI355MOE_STAGE_DOWN) kernels |= 4;
-        if (stages & MI355MOE_STAGE_COMBINE) kernels |= 8;
-        return rc_launch(launch_prefill(d, stream, kernels));
-    }
+    if (use == MI355MOE_PATH_PREFILL)
+        return run_grouped(layer, x, x_dtype, x_stride, T, ids, ids_dtype, weights, weights_dtype, topk, expert_map,
+                           n_global, limit, out, out_dtype, out_stride, workspace, workspace_bytes, stages, false,
+                           stream);
     DecodePlan p;
     DecodeWs w;
     if (int rc = prep_decode(layer, x, x_dtype, x_stride, T, topk, limit, out, out_dtype, out_stride, workspace,
@@ -520,6 +542,39 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
     if (stages & MI355MOE_STAGE_ROUTE)
         if (int rc = launch_route(r, stream)) return rc_launch(rc);
     return rc_launch(launch_decode(w.da, p.rmax, stream, stages >> 1));
+}
+
+// ---------------------------------------------------------------------------------------------- e4m3 variant
+
+int64_t mi355moe_e4m3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk) {
+    if (layer_shape_ok(layer) || T < 0 || topk < 1 || topk > MAX_TOPK) return -1;
+    const int64_t P = std::max<int64_t>(1, T * topk);
+    PrefillWs w;
+    int sc;
+    carve_prefill(nullptr, P, std::max<int64_t>(1, T), layer->n, layer->hidden, layer->intermediate, w, sc, true);
+    return (int64_t)w.bytes;
+}
+
+int mi355moe_e4m3_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                  int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                  int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                  int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                  int stages, hipStream_t stream) {
+    if (int r = layer_shape_ok(layer)) return r;
+    if (!x || !ids || !weights || !out || !workspace) return MI355MOE_EINVAL;
+    if (stages <= 0 || stages > MI355MOE_STAGE_ALL) return MI355MOE_EINVAL;
+    if (dt_act(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;
+    if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
+    const int64_t K = layer->hidden;
+    if (T < 0 || topk < 1 || topk > MAX_TOPK) return MI355MOE_ELIMIT;
+    if (x_stride < K || x_stride % 2 || out_stride < K || out_stride % 2) return MI355MOE_ESHAPE;
+    if (expert_map && n_global < 0) return MI355MOE_EINVAL;
+    if (!(layer->flags & MI355MOE_LAYER_SHARED_W13_SUH) || K > 4096) return MI355MOE_EUNSUPPORTED;
+    const int64_t P = T * topk;
+    if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (P == 0) return 0;
+    return run_grouped(layer, x, x_dtype, x_stride, T, ids, ids_dtype, weights, weights_dtype, topk, expert_map,
+                       n_global, limit, out, out_dtype, out_stride, workspace, workspace_bytes, stages, true, stream);
 }
 
 // ---------------------------------------------------------------------------------------------- whole layer

@@ -112,6 +112,13 @@ struct PrefillArgs {
     void* out;
     int odt;
     int64_t out_stride;
+    // the trellis-sourced e4m3 variant (e4m3 = 1; 0: the E3 fp16 numerics, these pointers unused)
+    int e4m3;
+    float* asc;             // [P] row scales of the gate/up inputs
+    float* dsc;             // [P] row scales of the down inputs (nullptr: no scaling in the combine)
+    float* vd;              // [P][N] fp32 down inputs before their quantization
+    unsigned* amaxd;        // [P] row maxima of |vd| (float bits)
+    const float* w32;       // [P] fp32 router weights for the combine (nullptr: the fp16 w16)
 };
 constexpr int PREFILL_TM = 256;
 

@@ -109,6 +109,138 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------ e4m3 helpers
+
+// Two fp16 values (|v| <= 448) rounded to their nearest e4m3 values (ties to even, e4m3 subnormals included), returned
+// as the fp16 pair of those values (every e4m3 value is an fp16): gfx950's scaled conversions with scale 1.
+__device__ __forceinline__ uint32_t e4m3_round_h2(uint32_t d) {
+    const float one = 1.0f;
+    uint32_t f8, r;
+    asm("v_cvt_scalef32_pk_fp8_f16 %0, %1, %2" : "=v"(f8) : "v"(d), "v"(one));
+    asm("v_cvt_scalef32_pk_f16_fp8 %0, %1, %2" : "=v"(r) : "v"(f8), "v"(one));
+    return r;
+}
+// Two fp32 values already divided by their row scale -> the fp16 pair of e4m3(clamp(v, -448, 448)) (round to nearest
+// even, the reference's quantiser).
+__device__ __forceinline__ uint32_t e4m3_quant_h2(float a, float b) {
+    a = __builtin_amdgcn_fmed3f(a, -448.0f, 448.0f);
+    b = __builtin_amdgcn_fmed3f(b, -448.0f, 448.0f);
+    const uint32_t f8 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    const float one = 1.0f;
+    uint32_t r;
+    asm("v_cvt_scalef32_pk_f16_fp8 %0, %1, %2" : "=v"(r) : "v"(f8), "v"(one));
+    return r;
+}
+// Row scale of the e4m3 activations: amax / 448 (IEEE division), 1 for an all-zero row.
+__device__ __forceinline__ float e4m3_row_scale(float amax) {
+    const float sc = __fdiv_rn(amax, 448.0f);
+    return sc > 0.0f ? sc : 1.0f;
+}
+
+// The e4m3 variant's gather (code/fork/kernels/moe_e4m3.cu:245-310, gather2): per row, v = H(x16 * suh) * r in fp32
+// (x rounded to fp16 first, the product and the butterflies in fp32, r applied after the transform), s = amax|v| /
+// 448, q = e4m3(clamp(v / s)) stored as the fp16 of each e4m3 value in h13's permuted order, asc[pos] = s; the row's
+// down-input maximum amaxd[pos] is zeroed for the gate/up epilogue. One wave per row; the whole row (K <= 4096) stays
+// in registers between the amax and the quantization.
+__global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15, q = lane >> 4;
+    const int nb = a.K >> 7;
+    const int sto = 16 * (c >> 1) + 2 * (c & 1);
+    const bool vec = ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.x_stride * 2)) & 15) == 0;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+    for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
+        const int e = a.pe[pos];
+        if (e < 0) continue;                                          // uniform: one row per wave
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)a.tok[pos] * a.x_stride + 8 * c;
+        const uint16_t* sr = reinterpret_cast<const uint16_t*>(a.wt.g_suh[e]) + 8 * c;
+        u32x4 xv[PF_GATHER_PASSES], sv[PF_GATHER_PASSES];
+#pragma unroll
+        for (int j = 0; j < PF_GATHER_PASSES; ++j) {
+            const int blk = min(4 * j + q, nb - 1);
+            const uint16_t* xp = xr + blk * 128;
+            if (vec) {
+                xv[j] = *reinterpret_cast<const u32x4*>(xp);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xv[j][i] = *reinterpret_cast<const uint32_t*>(xp + 2 * i);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[j][i] = *reinterpret_cast<const uint32_t*>(sr + blk * 128 + 2 * i);
+        }
+        float v[PF_GATHER_PASSES][8];
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PF_GATHER_PASSES; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t xw = xv[j][i], sw = sv[j][i];
+                _Float16 h0, h1;
+                if (a.xdt == DT_BF16) {
+                    h0 = (_Float16)__builtin_bit_cast(float, xw << 16);
+                    h1 = (_Float16)__builtin_bit_cast(float, xw & 0xFFFF0000u);
+                } else {
+                    h0 = u16_as_h(xw & 0xFFFFu);
+                    h1 = u16_as_h(xw >> 16);
+                }
+                v[j][2 * i] = (float)h0 * (float)u16_as_h(sw & 0xFFFFu);
+                v[j][2 * i + 1] = (float)h1 * (float)u16_as_h(sw >> 16);
+            }
+            fwht128_x16(v[j], lane);
+            const bool live = 4 * j + q < nb;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v[j][i] = v[j][i] * HAD_R;
+                if (live) m = fmaxf(m, fabsf(v[j][i]));
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float sc = e4m3_row_scale(m);
+        _Float16* dst = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + sto;
+#pragma unroll
+        for (int j = 0; j < PF_GATHER_PASSES; ++j) {
+            const int blk = 4 * j + q;
+            if (blk < nb) {
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm)
+                    *reinterpret_cast<uint32_t*>(dst + blk * 128 + 4 * mm) =
+                        e4m3_quant_h2(__fdiv_rn(v[j][2 * mm], sc), __fdiv_rn(v[j][2 * mm + 1], sc));
+            }
+        }
+        if (lane == 0) {
+            a.asc[pos] = sc;
+            a.amaxd[pos] = 0u;
+        }
+    }
+}
+
+// The e4m3 variant's down-input quantization: per row, s = amaxd / 448 (the maximum over the whole row, gathered by
+// the gate/up epilogues), h2 = the fp16 of e4m3(clamp(vd / s)) in the permuted order, dsc[pos] = s. One wave per row,
+// four 128-blocks per pass.
+__global__ __launch_bounds__(256) void pf_quantd_kernel(PrefillArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15, q = lane >> 4;
+    const int sto = 16 * (c >> 1) + 2 * (c & 1);
+    const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+    for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
+        if (a.pe[pos] < 0) continue;
+        const float sc = e4m3_row_scale(__builtin_bit_cast(float, a.amaxd[pos]));
+        const float* src = a.vd + (size_t)pos * a.N + 8 * c;
+        _Float16* dst = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos * a.N + sto;
+        for (int blk = q; blk < (a.N >> 7); blk += 4) {
+            const float4 lo = *reinterpret_cast<const float4*>(src + blk * 128);
+            const float4 hi = *reinterpret_cast<const float4*>(src + blk * 128 + 4);
+            const float w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm)
+                *reinterpret_cast<uint32_t*>(dst + blk * 128 + 4 * mm) =
+                    e4m3_quant_h2(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
+        }
+        if (lane == 0) a.dsc[pos] = sc;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ GEMM core
 
 // The tile GEMM of one wave: acc[rb][s] (32x32 blocks, rows 32 rb of the segment) over kdim, for the wave's 64
@@ -219,6 +351,9 @@ __device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p
 // work to arrive; loads past the last step re-read it. The B operands of step it + 1 are decoded in registers during
 // step it (no LDS round trip: each wave decodes only its own columns). One wait + barrier per step publishes A(it)
 // (all waves) and the raw words of step it + 1 (this wave).
+// E4M3: every decoded weight is rounded to the nearest e4m3 value (kept as the fp16 of that value), the trellis-
+// sourced e4m3 variant's operand; the products with e4m3 activations are then exact and summed in fp32.
+template <bool E4M3 = false>
 __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[8][2]) {
     unsigned char* Ast = smem;                                        // [PF_NS][256 rows][PF_RB]
     unsigned char* Wst = smem + PF_NS * PF_ASB;                       // [PF_NS][4 waves][PF_KT k tiles][4 tiles][128 B]
@@ -260,9 +395,13 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
 #pragma unroll
         for (int kt = 0; kt < PF_KT; ++kt) pf_load_words(wr + kt * 512, lane, w[kt]);
     };
-    auto operands = [&](const uint32_t (&q)[PF_KT][8], h8 (&b)[PF_KT][2]) {   // decoded pairs -> B operands
+    auto operands = [&](uint32_t (&q)[PF_KT][8], h8 (&b)[PF_KT][2]) {   // decoded pairs -> B operands
 #pragma unroll
         for (int kt = 0; kt < PF_KT; ++kt) {
+            if (E4M3) {
+#pragma unroll
+                for (int p = 0; p < 8; ++p) q[kt][p] = e4m3_round_h2(q[kt][p]);
+            }
             b[kt][0] = __builtin_bit_cast(h8, u32x4{q[kt][0], q[kt][1], q[kt][4], q[kt][5]});
             b[kt][1] = __builtin_bit_cast(h8, u32x4{q[kt][2], q[kt][3], q[kt][6], q[kt][7]});
         }
@@ -367,6 +506,10 @@ __device__ __forceinline__ void pf_tile_of(int b, int ncb, int& s, int& cb) {
 
 // ------------------------------------------------------------------------------------------------ gate/up
 
+// E4M3: the trellis-sourced e4m3 variant (weights rounded to e4m3 in the GEMM; accumulators times the row's
+// activation scale before the output Hadamard; the down input H(a16 * suh_d) * r kept in fp32 in vd, its row maxima
+// gathered in amaxd for pf_quantd_kernel). code/fork/overlay/glm53_moe_e4m3.py:654-674 (spec_proj, spec_ffn).
+template <bool E4M3>
 __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     int s, cb;
@@ -383,7 +526,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     t.btiles_n = N >> 4;
     t.bcol0 = cb * 8 + 4 * (wv & 1);
     f16v acc[8][2];
-    pf_gemm(t, smem, acc);
+    pf_gemm<E4M3>(t, smem, acc);
 
     // epilogue, 32 rows at a time through LDS; a wave finishes 4 rows at once: 16 lanes per row, lane c holding
     // columns 8c .. 8c + 7 (the 128-point Hadamards run across the 16 lanes by DPP)
@@ -423,6 +566,14 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
                 g[i] = g4.x, g[i + 1] = g4.y, g[i + 2] = g4.z, g[i + 3] = g4.w;
                 u[i] = u4.x, u[i + 1] = u4.y, u[i + 2] = u4.z, u[i + 3] = u4.w;
             }
+            if (E4M3) {                                              // dequantise: times the row's activation scale
+                const float rs = a.asc[row0 + min(trow, rn - 1)];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    g[i] *= rs;
+                    u[i] *= rs;
+                }
+            }
             fwht128_x16(g, lane);
             fwht128_x16(u, lane);
 #pragma unroll
@@ -434,10 +585,27 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
                     uv = fminf(fmaxf(uv, -L), L);
                 }
                 const float act = sigmoid_fast(gv) * gv * uv;
-                b[i] = (float)(_Float16)((_Float16)act * sud[i]);
+                b[i] = E4M3 ? (float)(_Float16)act * (float)sud[i] : (float)(_Float16)((_Float16)act * sud[i]);
             }
             fwht128_x16(b, lane);
-            if (trow < rn) {
+            if (E4M3) {                                              // fp32 down input and its row maximum
+                float m = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    b[i] = b[i] * HAD_R;
+                    m = fmaxf(m, fabsf(b[i]));
+                }
+                m = fmaxf(m, xor_lane<1>(m, lane));
+                m = fmaxf(m, xor_lane<2>(m, lane));
+                m = fmaxf(m, xor_lane<4>(m, lane));
+                m = fmaxf(m, xor_lane<8>(m, lane));
+                if (trow < rn) {
+                    float* vo = a.vd + (size_t)(row0 + trow) * N + col;
+                    *reinterpret_cast<float4*>(vo) = make_float4(b[0], b[1], b[2], b[3]);
+                    *reinterpret_cast<float4*>(vo + 4) = make_float4(b[4], b[5], b[6], b[7]);
+                    if (c == 0) atomicMax(a.amaxd + row0 + trow, __builtin_bit_cast(unsigned, m));
+                }
+            } else if (trow < rn) {
                 _Float16* dst = reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow) * N + sto;
 #pragma unroll
                 for (int m = 0; m < 4; ++m)
@@ -450,6 +618,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
 
 // ------------------------------------------------------------------------------------------------ down
 
+template <bool E4M3>
 __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     int s, cb;
@@ -466,7 +635,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     t.btiles_n = K >> 4;
     t.bcol0 = cb * 16 + 4 * wv;
     f16v acc[8][2];
-    pf_gemm(t, smem, acc);
+    pf_gemm<E4M3>(t, smem, acc);
 
     // epilogue: the raw accumulators (rows < rn) straight from registers into contrib; the output rotation, svh and
     // router weight are applied by the combine (the VALU work runs there, beside its memory traffic, instead of after
@@ -506,17 +675,19 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
         const int pl = a.inv[t * a.topk + min(lk, a.topk - 1)];
         const int el = a.pe[pl];
         const int okl = (int)(lk < a.topk) & (int)(el >= 0);
-        const float wl = (float)u16_as_h(a.w16[pl]);
+        const float wl = a.w32 ? a.w32[pl] : (float)u16_as_h(a.w16[pl]);
+        const float dl = a.dsc ? a.dsc[pl] : 1.0f;                   // e4m3 variant: the down input's row scale
         const int64_t svl = a.wt.d_svh[max(el, 0)];
         f32x4 raw[8][2];
         u32x4 sv[8];
         bool ok[8];
-        float w[8];
+        float w[8], ds[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {                                 // unconditional loads (no joins between them)
             const int pos = __builtin_amdgcn_readlane(pl, k);
             ok[k] = __builtin_amdgcn_readlane(okl, k) != 0;
             w[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k));
+            ds[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dl), k));
             const uint64_t sp = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)svl, k)) |
                                 ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(svl >> 32), k) << 32);
             const float* rp = a.contrib + (size_t)pos * a.K + colc;
@@ -533,6 +704,10 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
             for (int i = 0; i < 4; ++i) {
                 v[i] = raw[k][0][i];
                 v[4 + i] = raw[k][1][i];
+            }
+            if (a.dsc) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] *= ds[k];
             }
             fwht128_x16(v, lane);
 #pragma unroll
@@ -566,24 +741,38 @@ static bool g_pf_attr = false;
 
 int prefill_setup() {
     if (g_pf_attr) return 0;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(pf_gateup_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS) != hipSuccess)
-        return -1;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(pf_down_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)PF_LDS) != hipSuccess)
-        return -1;
+    const void* ks[4] = {reinterpret_cast<const void*>(pf_gateup_kernel<false>),
+                         reinterpret_cast<const void*>(pf_gateup_kernel<true>),
+                         reinterpret_cast<const void*>(pf_down_kernel<false>),
+                         reinterpret_cast<const void*>(pf_down_kernel<true>)};
+    for (const void* k : ks)
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS) != hipSuccess) return -1;
     g_pf_attr = true;
     return 0;
 }
 
 int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
     if (prefill_setup()) return -1;
-    if (kernels & 1) hipLaunchKernelGGL(pf_gather_kernel, dim3(4096), dim3(256), 0, st, a);
+    const bool f8 = a.e4m3 != 0;
+    if (f8 && (a.K > 4 * 128 * PF_GATHER_PASSES || !a.asc || !a.dsc || !a.vd || !a.amaxd)) return -1;
+    if (kernels & 1) {
+        if (f8) hipLaunchKernelGGL(pf_gather8_kernel, dim3(4096), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL(pf_gather_kernel, dim3(4096), dim3(256), 0, st, a);
+    }
     const int sg = (a.S_cap + 7) / 8;                               // segment groups of 8 (one per XCD)
-    if (kernels & 2)
-        hipLaunchKernelGGL(pf_gateup_kernel, dim3(8 * (a.N / 128) * sg), dim3(PF_THREADS), PF_LDS, st, a);
-    if (kernels & 4)
-        hipLaunchKernelGGL(pf_down_kernel, dim3(8 * (a.K / 256) * sg), dim3(PF_THREADS), PF_LDS, st, a);
+    const dim3 gu(8 * (a.N / 128) * sg), dn(8 * (a.K / 256) * sg);
+    if (kernels & 2) {
+        if (f8) hipLaunchKernelGGL(pf_gateup_kernel<true>, gu, dim3(PF_THREADS), PF_LDS, st, a);
+        else hipLaunchKernelGGL(pf_gateup_kernel<false>, gu, dim3(PF_THREADS), PF_LDS, st, a);
+    }
+    if (kernels & 4) {
+        if (f8) {
+            hipLaunchKernelGGL(pf_quantd_kernel, dim3(4096), dim3(256), 0, st, a);
+            hipLaunchKernelGGL(pf_down_kernel<true>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+        } else {
+            hipLaunchKernelGGL(pf_down_kernel<false>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+        }
+    }
     if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3((a.T + 3) / 4, (a.K + 511) / 512), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -67,6 +67,10 @@ _SIGS = {
     "mi355moe_moe_forward_ids_ex": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int,
                                            _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int, _int,
                                            _c_p]),
+    "mi355moe_e4m3_moe_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64, _i64]),
+    "mi355moe_e4m3_moe_forward_ids": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int,
+                                             _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int,
+                                             _c_p]),
     "mi355moe_exl3_moe_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64]),
     "mi355moe_moe_layer_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64, _i64, _i64]),
     "mi355moe_moe_layer": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _c_p, _i64, _c_p, _i64,

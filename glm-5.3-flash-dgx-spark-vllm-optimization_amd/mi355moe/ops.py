@@ -190,6 +190,42 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
     return out
 
 
+def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                         limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                         out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL) -> torch.Tensor:
+    """The trellis-sourced e4m3 variant of the routed experts (code/fork/overlay/glm53_moe_e4m3.py:484-592 run(),
+    numerics of spec_ffn :666-674 with DOWN16 off): activations quantized per row to e4m3 after the input rotation,
+    EXL3 weights rounded to e4m3, fp32 sums; output [T, K] written like moe_forward_ids. The layer needs gate and up
+    sharing one suh and hidden <= 4096."""
+    dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
+    if dev != experts.device:
+        raise ValueError(f"activations on {dev}, experts on {experts.device}")
+    if x.dim() != 2 or x.shape[1] != experts.K or x.stride(1) != 1:
+        raise ValueError(f"x must be [T, {experts.K}] with unit column stride")
+    T = x.shape[0]
+    ids = topk_ids.reshape(T, -1).contiguous()
+    w = topk_weights.reshape(T, -1).contiguous()
+    topk = ids.shape[1]
+    if w.shape != ids.shape:
+        raise ValueError("topk_weights must be shaped like topk_ids")
+    if out is None:
+        out = torch.empty(T, experts.K, dtype=out_dtype or x.dtype, device=dev)
+    if out.shape != (T, experts.K) or out.stride(1) != 1:
+        raise ValueError("out must be [T, K] with unit column stride")
+    L = _lib.lib()
+    nb = L.mi355moe_e4m3_moe_workspace_bytes(ctypes.byref(experts.desc), T, topk)
+    if nb < 0:
+        raise ValueError("mi355moe_e4m3_moe_workspace_bytes rejected the shape")
+    ws = workspace(dev, nb)
+    em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
+    _lib.check("mi355moe_e4m3_moe_forward_ids", L.mi355moe_e4m3_moe_forward_ids(
+        ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
+        ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em), 0 if em is None else em.numel(),
+        float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), int(stages),
+        _stream(dev)))
+    return out
+
+
 def moe_layer(experts: Exl3Experts, x: torch.Tensor, router_w: torch.Tensor | None = None,
               logits: torch.Tensor | None = None, topk: int = 8, bias: torch.Tensor | None = None,
               routed_scale: float = 1.0, renormalize: bool = True, limit: float = 10.0,

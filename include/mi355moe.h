@@ -197,6 +197,23 @@ int mi355moe_fp8_moe_forward_ids(const mi355moe_fp8_layer* layer, const void* x,
                                  int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
                                  int stages, hipStream_t stream);
 
+/* The trellis-sourced e4m3 variant of the EXL3 experts (code/fork/overlay/glm53_moe_e4m3.py:484-592 run() over a
+ * layer's EXL3 pointer tables; numerics spec_proj / spec_ffn, :654-674, DOWN16 off; kernels
+ * code/fork/kernels/moe_e4m3.cu gather2 :245-310 and the fused GEMMs :576-1856): per pair row v = H(fp16(x) * suh)
+ * * r in fp32, s = amax|v| / 448 (1 if 0), q = e4m3(clamp(v / s)); the gate and up GEMMs multiply q by the decoded
+ * weights rounded to e4m3 (W_q of the 4-bit trellis) with fp32 sums, g = H(acc * s) * r * svh (same for u),
+ * a16 = fp16(silu(min(g, L)) * clamp(u, -L, L)) (iff L != 0), the down input H(a16 * suh_d) * r quantized per row
+ * the same way, the down GEMM likewise, y = H(acc * s_d) * r * svh_d, out[t] = sum over the token's slots of w * y
+ * in slot order (fp32, deterministic), WRITTEN in out_dtype. Arguments and stages as mi355moe_moe_forward_ids_ex
+ * (grouped 256-row tiles whatever T); the layer needs MI355MOE_LAYER_SHARED_W13_SUH (one quantized copy of the
+ * input rows) and hidden <= 4096. */
+int64_t mi355moe_e4m3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk);
+int mi355moe_e4m3_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                  int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                  int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                  int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                  int stages, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
