@@ -24,54 +24,64 @@ constexpr int RL_MAXC = 16;    // K chunks of 512 (K <= 8192)
 // i = 0..7, sequentially in fp32 (bf16 x bf16 products are exact in fp32, so the fused multiply-add rounds like
 // an add); the 64 lane partials are combined by the xor butterfly m = 32, 16, ..., 1; the chunk sums are then added
 // in chunk order c = 0, 1, ... (wave 0 adds them from LDS). Waves past K/512 only join the barriers.
-// COH: the logits are stored as device-coherent words (read back by another workgroup of the same grid).
-template <bool COH = false>
+// The logits of experts e0 .. e0 + NE - 1 (those below E) for every token. COH: stored as device-coherent words (read
+// back by another workgroup of the same grid). SCORE: the stored value is the score sigmoid(logit), computed as the
+// top-k does ((float)(1 / (1 + exp(-(double)logit)))), instead of the logit.
+template <bool COH = false, int NE = 1, bool SCORE = false>
 __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int64_t x_stride,
-                                            const uint16_t* __restrict__ w, int T, int K, int E, int e,
+                                            const uint16_t* __restrict__ w, int T, int K, int E, int e0,
                                             float* __restrict__ logits) {
-    __shared__ float part[RL_MAXC][RL_TCHUNK];
+    __shared__ float part[RL_MAXC][NE * RL_TCHUNK];
     const int lane = threadIdx.x & 63;
     const int c = threadIdx.x >> 6;                 // chunk of this wave
     const int chunks = K / 512;
     const int k0 = c * 512 + lane * 8;
     for (int t0 = 0; t0 < T; t0 += RL_TCHUNK) {
         if (c < chunks) {
-            // the pass's token rows and the weight chunk are all loaded before any is used (one memory latency
-            // per pass; later passes find the weight in L2)
+            // the pass's token rows and the weight chunks are all loaded before any is used (one memory latency
+            // per pass; later passes find the weights in L2)
             u32x4 xv[RL_TCHUNK];
 #pragma unroll
             for (int tt = 0; tt < RL_TCHUNK; ++tt)
                 xv[tt] = t0 + tt < T ? *reinterpret_cast<const u32x4*>(x + (size_t)(t0 + tt) * x_stride + k0)
                                      : u32x4{0u, 0u, 0u, 0u};
-            const u32x4 wv = *reinterpret_cast<const u32x4*>(w + (size_t)e * K + k0);
+            u32x4 wv[NE];
 #pragma unroll
-            for (int tt = 0; tt < RL_TCHUNK; ++tt) {
-                float acc = 0.f;
-                if (t0 + tt < T) {
+            for (int q = 0; q < NE; ++q)
+                wv[q] = *reinterpret_cast<const u32x4*>(w + (size_t)min(e0 + q, E - 1) * K + k0);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        acc = __builtin_fmaf(__builtin_bit_cast(float, xv[tt][i] << 16),
-                                             __builtin_bit_cast(float, wv[i] << 16), acc);
-                        acc = __builtin_fmaf(__builtin_bit_cast(float, xv[tt][i] & 0xFFFF0000u),
-                                             __builtin_bit_cast(float, wv[i] & 0xFFFF0000u), acc);
+            for (int q = 0; q < NE; ++q)
+#pragma unroll
+                for (int tt = 0; tt < RL_TCHUNK; ++tt) {
+                    float acc = 0.f;
+                    if (t0 + tt < T) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            acc = __builtin_fmaf(__builtin_bit_cast(float, xv[tt][i] << 16),
+                                                 __builtin_bit_cast(float, wv[q][i] << 16), acc);
+                            acc = __builtin_fmaf(__builtin_bit_cast(float, xv[tt][i] & 0xFFFF0000u),
+                                                 __builtin_bit_cast(float, wv[q][i] & 0xFFFF0000u), acc);
+                        }
                     }
+                    // butterfly m = 32, 16, ..., 1 (the fixed order), partners by permlane / DPP
+                    acc = acc + xor_lane<32>(acc, lane);
+                    acc = acc + xor_lane<16>(acc, lane);
+                    acc = acc + xor_lane<8>(acc, lane);
+                    acc = acc + xor_lane<4>(acc, lane);
+                    acc = acc + xor_lane<2>(acc, lane);
+                    acc = acc + xor_lane<1>(acc, lane);
+                    if (lane == 0) part[c][q * RL_TCHUNK + tt] = acc;
                 }
-                // butterfly m = 32, 16, ..., 1 (the fixed order), partners by permlane / DPP
-                acc = acc + xor_lane<32>(acc, lane);
-                acc = acc + xor_lane<16>(acc, lane);
-                acc = acc + xor_lane<8>(acc, lane);
-                acc = acc + xor_lane<4>(acc, lane);
-                acc = acc + xor_lane<2>(acc, lane);
-                acc = acc + xor_lane<1>(acc, lane);
-                if (lane == 0) part[c][tt] = acc;
-            }
         }
         __syncthreads();
-        if (threadIdx.x < RL_TCHUNK && t0 + (int)threadIdx.x < T) {
+        const int q = (int)threadIdx.x / RL_TCHUNK, tt = (int)threadIdx.x % RL_TCHUNK;
+        if (q < NE && e0 + q < E && t0 + tt < T) {
             float sum = part[0][threadIdx.x];
             for (int cc = 1; cc < chunks; ++cc) sum = sum + part[cc][threadIdx.x];
-            if (COH) st_coherent(logits + (size_t)(t0 + threadIdx.x) * E + e, sum);
-            else logits[(size_t)(t0 + threadIdx.x) * E + e] = sum;
+            if (SCORE) sum = (float)(1.0 / (1.0 + exp(-(double)sum)));
+            float* dst = logits + (size_t)(t0 + tt) * E + e0 + q;
+            if (COH) st_coherent(dst, sum);
+            else *dst = sum;
         }
         __syncthreads();
     }
@@ -436,7 +446,8 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return m;
 }
 
-template <int J, bool COH = false>                                   // J >= ceil(E / 64); COH: coherent logit loads
+// J >= ceil(E / 64); COH: coherent loads of the row; SCORE: the row holds the scores sigmoid(logit) already
+template <int J, bool COH = false, bool SCORE = false>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E, const float* __restrict__ bias,
                                           int topk, float scale, int renorm, float* sco, int32_t* __restrict__ ids_row,
                                           float* __restrict__ wts_row, int* ids_sh, float* wts_sh) {
@@ -449,7 +460,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E,
         const int e = lane + 64 * j;
         if (j < nj && e < E) {
             const float lg = COH ? ld_coherent(lrow + e) : lrow[e];
-            const float sv = (float)(1.0 / (1.0 + exp(-(double)lg)));
+            const float sv = SCORE ? lg : (float)(1.0 / (1.0 + exp(-(double)lg)));
             sco[e] = sv;
             ok[j] = topk_order(sv + (bias ? bias[e] : 0.f), e);
         }
@@ -486,7 +497,7 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E,
 // weights). The picks are written to global memory (the caller's copy) and to shared memory, from which the
 // permutation reads them. Shared memory: the permutation's P + 2 (n + 1) ints, nw x E scores, then the picks' P ids
 // and P weights.
-template <int J, bool COH>
+template <int J, bool COH, bool SCORE = false>
 __device__ __forceinline__ void topk_route_body(const float* __restrict__ logits, int T, int E,
                                                 const float* __restrict__ bias, int topk, float scale, int renorm,
                                                 int32_t* __restrict__ ids, float* __restrict__ wts, const RouteArgs& a,
@@ -496,7 +507,7 @@ __device__ __forceinline__ void topk_route_body(const float* __restrict__ logits
     int* ids_sh = sh + a.P + 2 * (a.n + 1) + nw * E;
     float* wts_sh = reinterpret_cast<float*>(ids_sh + a.P);
     for (int t = wv; t < T; t += nw)
-        topk_wave<J, COH>(logits + (size_t)t * E, E, bias, topk, scale, renorm, sco, ids + (size_t)t * topk,
+        topk_wave<J, COH, SCORE>(logits + (size_t)t * E, E, bias, topk, scale, renorm, sco, ids + (size_t)t * topk,
                           wts + (size_t)t * topk, ids_sh + t * topk, wts_sh + t * topk);
     __syncthreads();
     RouteArgs b = a;
@@ -516,7 +527,9 @@ __global__ __launch_bounds__(1024) void topk_route_kernel(const float* __restric
     topk_route_body<J, false>(logits, T, E, bias, topk, scale, renorm, ids, wts, a, sh);
 }
 
-// The whole decode-size front end in one launch: the router GEMV (one workgroup per expert, logits_body), then the
+constexpr int RR_EXPERTS = 2;   // router experts per workgroup of the one-launch front end (all in one round of CUs)
+// The whole decode-size front end in one launch: the router GEMV (RR_EXPERTS experts per workgroup, logits_body, which
+// also applies the sigmoid so the ranking workgroup only loads scores), then the
 // workgroup that finishes last (an arrival counter at a fixed workspace offset, returned to zero by that
 // workgroup) runs topk_route_body over all logits. Logits cross workgroups, and XCDs with their own L2, as device-coherent stores and loads; a workgroup
 // arrives only after its stores have completed.
@@ -529,17 +542,17 @@ __global__ __launch_bounds__(1024) void router_route_kernel(const uint16_t* __re
                                                             RouteArgs a, unsigned* arrivals) {
     extern __shared__ int sh[];
     __shared__ int last;
-    logits_body<true>(x, x_stride, w, T, K, E, blockIdx.x, logits);
+    logits_body<true, RR_EXPERTS, true>(x, x_stride, w, T, K, E, RR_EXPERTS * blockIdx.x, logits);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    // the E-th arrival ranks; counted modulo E so that a counter left non-zero (a workspace not zero-filled before
-    // its first use) still elects one workgroup per call and the tables are always rebuilt
+    // the last of the grid's arrivals ranks; counted modulo the grid so that a counter left non-zero (a workspace not
+    // zero-filled before its first use) still elects one workgroup per call and the tables are always rebuilt
     if (threadIdx.x == 0)
-        last = (__hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) % (unsigned)E == 0u;
+        last = (__hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) % gridDim.x == 0u;
     __syncthreads();
     if (!last) return;
     if (threadIdx.x == 0) *arrivals = 0u;
-    topk_route_body<J, true>(logits, T, E, bias, topk, scale, renorm, ids, wts, a, sh);
+    topk_route_body<J, true, true>(logits, T, E, bias, topk, scale, renorm, ids, wts, a, sh);
 }
 
 // Tables from pre-sorted pairs (the exl3_moe contract): counts [n+1] int64 give each expert's span of the sorted
@@ -713,11 +726,12 @@ int launch_router_route(const uint16_t* x, int64_t x_stride, const uint16_t* w, 
             return -1;
         attr = true;
     }
+    const dim3 grid((E + RR_EXPERTS - 1) / RR_EXPERTS);
     if (E <= 320)
-        hipLaunchKernelGGL(router_route_kernel<5>, dim3(E), dim3(64 * nw), shm, st, x, x_stride, w, T, K, E, logits,
+        hipLaunchKernelGGL(router_route_kernel<5>, grid, dim3(64 * nw), shm, st, x, x_stride, w, T, K, E, logits,
                            bias, topk, scale, renorm, ids, wts, a, arrivals);
     else
-        hipLaunchKernelGGL(router_route_kernel<16>, dim3(E), dim3(64 * nw), shm, st, x, x_stride, w, T, K, E, logits,
+        hipLaunchKernelGGL(router_route_kernel<16>, grid, dim3(64 * nw), shm, st, x, x_stride, w, T, K, E, logits,
                            bias, topk, scale, renorm, ids, wts, a, arrivals);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
