@@ -683,12 +683,25 @@ __global__ __launch_bounds__(128) void combine_kernel(DecodeArgs a) {
     const int t = blockIdx.x;
     const int col = blockIdx.y * 256 + 2 * threadIdx.x;
     float s0 = 0.f, s1 = 0.f;
-    for (int k = 0; k < a.topk; ++k) {
-        const int pos = a.inv[t * a.topk + k];
-        if (a.pe[pos] < 0) continue;
-        const float2 c = *reinterpret_cast<const float2*>(a.contrib + (size_t)pos * a.K + col);
-        s0 += c.x;
-        s1 += c.y;
+    // eight slots at a time, each level of loads issued together: positions, then validity and contributions (a
+    // slot's contribution row is loaded whether or not it is valid; only valid ones are added, in slot order)
+    for (int k0 = 0; k0 < a.topk; k0 += 8) {
+        int pos[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pos[k] = a.inv[t * a.topk + min(k0 + k, a.topk - 1)];
+        int pv[8];
+        float2 c[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            pv[k] = a.pe[pos[k]];
+            c[k] = *reinterpret_cast<const float2*>(a.contrib + (size_t)pos[k] * a.K + col);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k0 + k < a.topk && pv[k] >= 0) {
+                s0 += c[k].x;
+                s1 += c[k].y;
+            }
     }
     const size_t o = (size_t)t * a.out_stride + col;
     if (a.odt == DT_F32) {
