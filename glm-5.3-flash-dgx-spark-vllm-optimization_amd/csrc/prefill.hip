@@ -353,7 +353,9 @@ __device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p
 // (all waves) and the raw words of step it + 1 (this wave).
 // E4M3: every decoded weight is rounded to the nearest e4m3 value (kept as the fp16 of that value), the trellis-
 // sourced e4m3 variant's operand; the products with e4m3 activations are then exact and summed in fp32.
-template <bool E4M3 = false>
+// NRB: the 32-row blocks of the tile that are multiplied (a compile-time count: tiles of up to 32 NRB rows skip the
+// MFMAs and A reads of the other blocks, whose accumulators stay zero and are never stored; the decode is the same).
+template <bool E4M3 = false, int NRB = 8>
 __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[8][2]) {
     unsigned char* Ast = smem;                                        // [PF_NS][256 rows][PF_RB]
     unsigned char* Wst = smem + PF_NS * PF_ASB;                       // [PF_NS][4 waves][PF_KT k tiles][4 tiles][128 B]
@@ -425,7 +427,8 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         words(it + 1, w);                                             // step it + 1 (past the end: never used)
         h8 af[NF];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = afrag(as, i);
+        for (int i = 0; i < 4; ++i)
+            if (i < NRB) af[i] = afrag(as, i);
         __builtin_amdgcn_sched_barrier(0);
         uint32_t q[PF_KT][8];
         PfPair prev{0u, 0u};
@@ -434,13 +437,13 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
             // the next batch's DMA instructions spread over the step (the CU's address path takes them one at a
             // time; issued together after the barrier they would stall every wave behind each other)
             if (i % DMA_EVERY == 0 && i / DMA_EVERY < PF_DMA) issue_one(i / DMA_EVERY, it + PF_NS - 1, it + PF_NS);
-            if (i + 4 < NF) af[i + 4] = afrag(as, i + 4);
+            if (i + 4 < NF && ((i + 4) & 7) < NRB) af[i + 4] = afrag(as, i + 4);
             const int kt = i >> 3, rb = i & 7;
             // pair i's products after the first MFMA, pair i - 1's values after the second: no VALU instruction
             // waits on the one before it while the MFMAs run
-            acc[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][0], acc[rb][0], 0, 0, 0);
+            if (rb < NRB) acc[rb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][0], acc[rb][0], 0, 0, 0);
             const PfPair cur = pf_pair_products(w[kt], i & 7);
-            acc[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][1], acc[rb][1], 0, 0, 0);
+            if (rb < NRB) acc[rb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bc[kt][1], acc[rb][1], 0, 0, 0);
             if (i > 0) q[(i - 1) >> 3][(i - 1) & 7] = pf_pair_values(prev);
             prev = cur;
             __builtin_amdgcn_sched_barrier(0);
@@ -526,7 +529,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     t.btiles_n = N >> 4;
     t.bcol0 = cb * 8 + 4 * (wv & 1);
     f16v acc[8][2];
-    pf_gemm<E4M3>(t, smem, acc);
+    if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);                   // uniform: small tiles multiply two row blocks
+    else pf_gemm<E4M3, 8>(t, smem, acc);
 
     // epilogue, 32 rows at a time through LDS; a wave finishes 4 rows at once: 16 lanes per row, lane c holding
     // columns 8c .. 8c + 7 (the 128-point Hadamards run across the 16 lanes by DPP)
@@ -635,7 +639,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     t.btiles_n = K >> 4;
     t.bcol0 = cb * 16 + 4 * wv;
     f16v acc[8][2];
-    pf_gemm<E4M3>(t, smem, acc);
+    if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);
+    else pf_gemm<E4M3, 8>(t, smem, acc);
 
     // epilogue: the raw accumulators (rows < rn) straight from registers into contrib; the output rotation, svh and
     // router weight are applied by the combine (the VALU work runs there, beside its memory traffic, instead of after
