@@ -6,7 +6,8 @@
 Default workload (one "step" = one MoE layer call): the decode MoE layer, T=8 tokens, hidden 4096, 288 experts,
 sigmoid router + bias, top-8, routed scale 2.5, intermediate 1024 (one tensor-parallel rank's shard), EXL3 4-bit
 synthetic experts. A step runs the router GEMM, the sigmoid/bias top-k, the permutation, the grouped gate/up and
-down trellis GEMVs and the combine, replayed from HIP graphs captured per (layer, input) pair. Steps cycle over
+down trellis GEMVs and the combine, replayed from one HIP graph holding a layer call for every (layer, input) pair (as a
+served model's forward graph holds its layers). Steps cycle over
 several distinct layers so every step streams cold expert weights (the set exceeds the 256 MiB last-level cache).
 
 Printed (one JSON line): value = achieved HBM GB/s over the timed steps, counting per step the bytes a layer call
@@ -122,6 +123,12 @@ def run_decode(args, torch, mi355moe, dev):
         with torch.cuda.graph(g):
             step_fn(ops, layers[c[0]], routers[c[0]], xs[c[1]], bufs[c])
         graphs[c] = g
+    # every combo's layer call in one graph, as a served model's forward graph holds its layers: the timed steps
+    # replay it whole (one graph launch per len(combos) layer calls), the remainder through the per-combo graphs
+    chain = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(chain):
+        for c in combos:
+            step_fn(ops, layers[c[0]], routers[c[0]], xs[c[1]], bufs[c])
     torch.cuda.synchronize()
     # correctness guard: a replay equals the eager result
     ref = bufs[combos[0]]["out"].clone()
@@ -129,6 +136,15 @@ def run_decode(args, torch, mi355moe, dev):
     torch.cuda.synchronize()
     if not torch.equal(ref, bufs[combos[0]]["out"]):
         raise RuntimeError("graph replay differs from the eager step")
+    refs = []
+    for c in combos:
+        graphs[c].replay()
+        torch.cuda.synchronize()
+        refs.append(bufs[c]["out"].clone())
+    chain.replay()
+    torch.cuda.synchronize()
+    if not all(torch.equal(r, bufs[c]["out"]) for r, c in zip(refs, combos)):
+        raise RuntimeError("the chained graph differs from the per-call graphs")
 
     def step_bytes(c):
         d = info[c][0]
@@ -136,14 +152,21 @@ def run_decode(args, torch, mi355moe, dev):
 
     for w in range(args.warmup):
         graphs[combos[w % len(combos)]].replay()
+    chain.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
     total_bytes = 0
     dsum = 0
-    for k in range(args.steps):
-        c = combos[k % len(combos)]
+    k = 0
+    while k + len(combos) <= args.steps:
+        chain.replay()
+        for c in combos:
+            total_bytes += step_bytes(c)
+            dsum += info[c][0]
+        k += len(combos)
+    for c in combos[:args.steps - k]:
         graphs[c].replay()
         total_bytes += step_bytes(c)
         dsum += info[c][0]
@@ -182,7 +205,7 @@ def run_decode(args, torch, mi355moe, dev):
         "config": {"workload": f"decode MoE layer T={T}: hidden {K}, {E} experts, sigmoid+bias top-{TOPK} x{SCALE}, "
                                f"intermediate {N}, EXL3 4-bit synthetic experts, {n_layers} layers cycled (cold)",
                    "tokens": T, "hidden": K, "experts": E, "topk": TOPK, "intermediate": N,
-                   "graph": "one HIP graph per (layer, input)"},
+                   "graph": f"{len(combos)} layer calls per HIP graph"},
         "decode_us_per_layer": round(us_per_step, 2),
         "distinct_experts_mean": round(dsum / args.steps, 2),
         "hbm_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
