@@ -31,9 +31,10 @@ def _experts_of(layer: torch.nn.Module) -> Exl3Experts:
 
 
 def apply_exl3_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
-                       layer: torch.nn.Module, *, limit: float = SWIGLU_LIMIT_DEFAULT) -> torch.Tensor:
+                       layer: torch.nn.Module, *, limit: float = SWIGLU_LIMIT_DEFAULT, e4m3: bool = False) -> torch.Tensor:
     """Routed-expert output [.., T, K] in x's dtype (prod_exl3_reference.py:1788-1823). topk_ids are global ids;
-    layer.expert_map (optional, global -> local or -1) selects this rank's experts."""
+    layer.expert_map (optional, global -> local or -1) selects this rank's experts. e4m3: the trellis-sourced e4m3
+    numerics (code/fork/overlay/glm53_moe_e4m3.py:484-592 run() in place of the fp16 paths)."""
     experts = _experts_of(layer)
     tokens, hidden = x.shape[-2], x.shape[-1]
     x2d = x.reshape(tokens, hidden)
@@ -42,7 +43,8 @@ def apply_exl3_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: to
     ids = topk_ids.reshape(tokens, -1)
     w = topk_weights.reshape(tokens, -1)
     emap = getattr(layer, "expert_map", None)
-    out = ops.moe_forward_ids(experts, x2d, ids, w, limit=limit, expert_map=emap, out_dtype=x.dtype)
+    fwd = ops.moe_forward_ids_e4m3 if e4m3 else ops.moe_forward_ids
+    out = fwd(experts, x2d, ids, w, limit=limit, expert_map=emap, out_dtype=x.dtype)
     return out.reshape(x.shape)
 
 
@@ -69,11 +71,12 @@ _FUSED_CACHE: dict = {}
 class Exl3MoEMethod:
     """FusedMoE quant method for EXL3 4-bit trellis routed experts (prod_exl3_reference.py:2030-2343)."""
 
-    def __init__(self, bits: int = 4, swiglu_limit: float | None = None):
+    def __init__(self, bits: int = 4, swiglu_limit: float | None = None, e4m3: bool = False):
         if bits != 4:
             raise ValueError("this build decodes 4-bit EXL3 trellis tiles only")
         self.bits = bits
         self.swiglu_limit = swiglu_limit
+        self.e4m3 = e4m3                  # the overlay's e4m3 expert numerics instead of the fp16 paths
 
     def create_weights(self, layer: torch.nn.Module, num_experts: int, hidden_size: int,
                        intermediate_size_per_partition: int, params_dtype=None, device=None, **_) -> None:
@@ -108,7 +111,7 @@ class Exl3MoEMethod:
               shared_experts=None, shared_experts_input=None) -> torch.Tensor:
         del shared_experts, shared_experts_input
         limit = self.swiglu_limit or SWIGLU_LIMIT_DEFAULT
-        return apply_exl3_experts(x, topk_ids, topk_weights, layer, limit=float(limit))
+        return apply_exl3_experts(x, topk_ids, topk_weights, layer, limit=float(limit), e4m3=self.e4m3)
 
 
 def exl3_moe(hidden, out, expert_count, token_sorted, weight_sorted, temp_state_g, temp_state_u,

@@ -187,3 +187,7 @@ def test_apply_contracts(cuda, layer32):
     assert got.dtype == x.dtype and torch.equal(got, ref)
     got2 = fused_experts(x, ex.w13_trellis, ex.w2_trellis, w, ids, (ex.w13_suh, ex.w13_svh, ex.w2_suh, ex.w2_svh))
     assert torch.equal(got2, ref)
+    # the e4m3 numerics switch routes apply() to the e4m3 variant's entry point
+    m.e4m3 = True
+    got3 = m.apply(layer, x, w, ids, None, None)
+    assert got3.dtype == x.dtype and torch.equal(got3, ops.moe_forward_ids_e4m3(ex, x, ids, w))
