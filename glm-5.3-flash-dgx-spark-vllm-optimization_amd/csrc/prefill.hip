@@ -43,6 +43,19 @@ constexpr int PF_CLD = 260;                     // epilogue staging row stride (
 // go straight into MFMA operands (8 consecutive k slots per lane) and the activations match them slot for slot.
 __device__ __forceinline__ int pf_kperm_pair(int j) { return 2 * (j & 3) + (j >> 2); }
 
+// Store a lane's four packed pairs (k pairs 4h .. 4h + 3 of 16-group g, lane c = 2g + h) at their permuted positions
+// with one 16-byte store: the lanes c, c ^ 1 of a group own its 32 bytes interleaved (storage pair 2m + h = the lane's
+// pair m), so they swap two pairs (DPP lane ^ 1) and lane h then writes storage pairs 4h .. 4h + 3 contiguously.
+// grp: the 16-group's first element.
+__device__ __forceinline__ void pf_store_group(_Float16* grp, const uint32_t (&wm)[4], int c) {
+    const bool hi = c & 1;
+    const uint32_t s0 = hi ? wm[0] : wm[2], s1 = hi ? wm[1] : wm[3];
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s0, 0xB1, 0xF, 0xF, true);   // lane ^ 1
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s1, 0xB1, 0xF, 0xF, true);
+    const u32x4 v = hi ? u32x4{r0, wm[2], r1, wm[3]} : u32x4{wm[0], r0, wm[1], r1};
+    *reinterpret_cast<u32x4*>(grp + 8 * (c & 1)) = v;
+}
+
 // ------------------------------------------------------------------------------------------------ gather
 
 // h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0. One wave per row
@@ -53,7 +66,6 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
     const int nb = a.K >> 7;
-    const int sto = 16 * (c >> 1) + 2 * (c & 1);                      // storage of pair m: sto + 4 m
     const bool vec = ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.x_stride * 2)) & 15) == 0;
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
     for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
@@ -61,7 +73,7 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
         if (e < 0) continue;                                          // uniform: one row per wave
         const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)a.tok[pos] * a.x_stride + 8 * c;
         const uint16_t* sr = reinterpret_cast<const uint16_t*>(a.wt.g_suh[e]) + 8 * c;
-        _Float16* dst = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + sto;
+        _Float16* dst0 = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + 16 * (c >> 1);
         for (int b0 = 0; b0 < nb; b0 += 4 * PF_GATHER_PASSES) {
             u32x4 xv[PF_GATHER_PASSES], sv[PF_GATHER_PASSES];
 #pragma unroll
@@ -98,12 +110,11 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
                     p[2 * i + 1] = (float)(_Float16)(h1 * u16_as_h(sw >> 16));
                 }
                 fwht128_x16(p, lane);
-                if (blk < nb) {
+                uint32_t wm[4];
 #pragma unroll
-                    for (int m = 0; m < 4; ++m)
-                        *reinterpret_cast<h2*>(dst + blk * 128 + 4 * m) =
-                            h2{(_Float16)(p[2 * m] * HAD_R), (_Float16)(p[2 * m + 1] * HAD_R)};
-                }
+                for (int m = 0; m < 4; ++m)
+                    wm[m] = __builtin_bit_cast(uint32_t, h2{(_Float16)(p[2 * m] * HAD_R), (_Float16)(p[2 * m + 1] * HAD_R)});
+                if (blk < nb) pf_store_group(dst0 + blk * 128, wm, c);
             }
         }
     }
@@ -146,7 +157,6 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
     const int nb = a.K >> 7;
-    const int sto = 16 * (c >> 1) + 2 * (c & 1);
     const bool vec = ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.x_stride * 2)) & 15) == 0;
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
     for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
@@ -197,15 +207,16 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         const float sc = e4m3_row_scale(m);
-        _Float16* dst = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + sto;
+        _Float16* dst0 = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + 16 * (c >> 1);
 #pragma unroll
         for (int j = 0; j < PF_GATHER_PASSES; ++j) {
             const int blk = 4 * j + q;
             if (blk < nb) {
+                uint32_t wm[4];
 #pragma unroll
                 for (int mm = 0; mm < 4; ++mm)
-                    *reinterpret_cast<uint32_t*>(dst + blk * 128 + 4 * mm) =
-                        e4m3_quant_h2(__fdiv_rn(v[j][2 * mm], sc), __fdiv_rn(v[j][2 * mm + 1], sc));
+                    wm[mm] = e4m3_quant_h2(__fdiv_rn(v[j][2 * mm], sc), __fdiv_rn(v[j][2 * mm + 1], sc));
+                pf_store_group(dst0 + blk * 128, wm, c);
             }
         }
         if (lane == 0) {
@@ -221,21 +232,20 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
 __global__ __launch_bounds__(256) void pf_quantd_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
-    const int sto = 16 * (c >> 1) + 2 * (c & 1);
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
     for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
         if (a.pe[pos] < 0) continue;
         const float sc = e4m3_row_scale(__builtin_bit_cast(float, a.amaxd[pos]));
         const float* src = a.vd + (size_t)pos * a.N + 8 * c;
-        _Float16* dst = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos * a.N + sto;
+        _Float16* dst0 = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos * a.N + 16 * (c >> 1);
         for (int blk = q; blk < (a.N >> 7); blk += 4) {
             const float4 lo = *reinterpret_cast<const float4*>(src + blk * 128);
             const float4 hi = *reinterpret_cast<const float4*>(src + blk * 128 + 4);
             const float w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            uint32_t wm[4];
 #pragma unroll
-            for (int mm = 0; mm < 4; ++mm)
-                *reinterpret_cast<uint32_t*>(dst + blk * 128 + 4 * mm) =
-                    e4m3_quant_h2(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
+            for (int mm = 0; mm < 4; ++mm) wm[mm] = e4m3_quant_h2(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
+            pf_store_group(dst0 + blk * 128, wm, c);
         }
         if (lane == 0) a.dsc[pos] = sc;
     }
@@ -550,7 +560,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
         sud[i] = d2.x, sud[i + 1] = d2.y;
     }
     // storage of the lane's pairs m = 0..3 (columns 8c + 2m, + 1): k pair j = 4 (c % 2) + m of group c / 2
-    const int sto = cb * 128 + 16 * (c >> 1) + 2 * (c & 1);
+    const int grp0 = cb * 128 + 16 * (c >> 1);                      // the lane's 16-group of the block
     const float L = a.limit;
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb) {
@@ -610,10 +620,11 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
                     if (c == 0) atomicMax(a.amaxd + row0 + trow, __builtin_bit_cast(unsigned, m));
                 }
             } else if (trow < rn) {
-                _Float16* dst = reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow) * N + sto;
+                uint32_t wm[4];
 #pragma unroll
                 for (int m = 0; m < 4; ++m)
-                    *reinterpret_cast<h2*>(dst + 4 * m) = h2{(_Float16)(b[2 * m] * HAD_R), (_Float16)(b[2 * m + 1] * HAD_R)};
+                    wm[m] = __builtin_bit_cast(uint32_t, h2{(_Float16)(b[2 * m] * HAD_R), (_Float16)(b[2 * m + 1] * HAD_R)});
+                pf_store_group(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow) * N + grp0, wm, c);
             }
         }
         __syncthreads();
