@@ -35,6 +35,9 @@ def _table(t: torch.Tensor, per_expert: tuple[int, ...]) -> torch.Tensor:
         off += i * t.stride(d)
     base = t.data_ptr() + off * t.element_size()
     step = t.stride(0) * t.element_size()
+    if base % 16 or step % 16:
+        raise ValueError("EXL3 expert tensors: every expert's trellis, suh and svh must start on a 16-byte boundary "
+                         "(the kernels read them with 16-byte loads)")
     return (torch.arange(n, dtype=torch.int64) * step + base).to(t.device)
 
 

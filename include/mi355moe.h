@@ -46,7 +46,7 @@ typedef struct mi355moe_exl3_layer {
     int64_t n;              /* local experts */
     int64_t hidden;         /* K, multiple of 256 */
     int64_t intermediate;   /* N, multiple of 128 */
-    const int64_t* gate_trellis;   /* device int64 [n] each */
+    const int64_t* gate_trellis;   /* device int64 [n] each: expert i's tensor address, 16-byte aligned */
     const int64_t* gate_suh;
     const int64_t* gate_svh;
     const int64_t* up_trellis;

@@ -89,3 +89,14 @@ def test_python_layer_rejects_cpu_tensors_and_bad_shapes():
     from mi355moe.layer import Exl3Experts
     with pytest.raises(ValueError):
         Exl3Experts(torch.zeros(2, 2, 4, 4, 48, dtype=torch.int16), *[torch.zeros(1)] * 5)
+
+
+def test_expert_pointer_tables_require_16_byte_alignment():
+    from mi355moe.layer import _table
+    t = torch.zeros(3, 2, 256, dtype=torch.float16)
+    tab = _table(t, (1,))
+    assert tab.tolist() == [t.data_ptr() + 512 + 1024 * e for e in range(3)]
+    with pytest.raises(ValueError):
+        _table(torch.zeros(3 * 256 + 1, dtype=torch.float16)[1:].view(3, 256), ())   # base 2 bytes off
+    with pytest.raises(ValueError):
+        _table(torch.zeros(3, 260, dtype=torch.float16), ())                          # 520-byte expert stride
