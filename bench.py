@@ -405,16 +405,9 @@ def run_stack(args, torch, dev):
     layers, routers = [], []
     for l in range(nl):
         layers.append(synthetic.exl3_layer(E, K, N, seed=700 + l, device=dev))
-        w, b = synthetic.router(E, K, seed=800 + l, device=dev)
-        g = torch.Generator(device="cpu")
-        g.manual_seed(900 + l)
-        rank = torch.empty(E, dtype=torch.float32)
-        rank[torch.randperm(E, generator=g)] = torch.arange(E, dtype=torch.float32)
-        w[:, 0] = (-1.2 * torch.log(rank + 1.0) / c0).to(dev, torch.bfloat16)
-        routers.append((w, b))
-    xs = [synthetic.activations(T, K, seed=950, device=dev)] + [torch.empty(T, K, dtype=torch.bfloat16, device=dev)
-                                                              for _ in range(nl)]
-    xs[0][:, 0] = c0
+        routers.append(synthetic.zipf_router(E, K, seed=800 + l, rank_seed=900 + l, device=dev, c0=c0))
+    xs = [synthetic.zipf_activations(T, K, seed=950, device=dev, c0=c0)] + [
+        torch.empty(T, K, dtype=torch.bfloat16, device=dev) for _ in range(nl)]
     outs = [torch.empty(T, K, dtype=torch.bfloat16, device=dev) for _ in range(nl)]
     ids = [torch.empty(T, TOPK, dtype=torch.int32, device=dev) for _ in range(nl)]
     wts = [torch.empty(T, TOPK, dtype=torch.float32, device=dev) for _ in range(nl)]

@@ -1,7 +1,7 @@
 // Router and token->expert permutation kernels.
 //
-// router_logits  logits[t][e] = x[t] . W[e] (bf16 operands, fp32) in a fixed order (reproducible bit for bit):
-//                per 512-wide chunk, lane sums of 8 products, a lane butterfly, then the chunks in order.
+// router_logits  logits[t][e] = bf16(x[t] . W[e]) widened to fp32: the bf16 products summed in float64 (exact for
+//                router-sized operands, so independent of the order) and rounded to bf16 through fp32.
 //                Replaces F.linear(x, W).to(float32) (code/fork/docs/BF16_GEMV.md:27,38).
 // router_topk    vLLM grouped_topk with n_group = topk_group = 1 as restated by code/fork/docs/ref/tf_glue.py:371-401:
 //                score = sigmoid(logit), pick the topk largest score + bias (lower id first among equals),
@@ -20,18 +20,35 @@ namespace mi355moe {
 constexpr int RL_TCHUNK = 8;   // tokens per pass
 constexpr int RL_MAXC = 16;    // K chunks of 512 (K <= 8192)
 
-// One workgroup per expert, one wave per 512-wide chunk c of K. Lane l of chunk c accumulates k = 512c + 8l + i,
-// i = 0..7, sequentially in fp32 (bf16 x bf16 products are exact in fp32, so the fused multiply-add rounds like
-// an add); the 64 lane partials are combined by the xor butterfly m = 32, 16, ..., 1; the chunk sums are then added
-// in chunk order c = 0, 1, ... (wave 0 adds them from LDS). Waves past K/512 only join the barriers.
-// The logits of experts e0 .. e0 + NE - 1 (those below E) for every token. COH: stored as device-coherent words (read
-// back by another workgroup of the same grid). SCORE: the stored value is the score sigmoid(logit), computed as the
-// top-k does ((float)(1 / (1 + exp(-(double)logit)))), instead of the logit.
+// The value of lane l ^ M for a double (its two words moved by xor_lane).
+template <int M>
+__device__ __forceinline__ double xor_lane_f64(double v, int lane) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_bit_cast(uint32_t, xor_lane<M>(__builtin_bit_cast(float, (uint32_t)u), lane));
+    const uint32_t hi = __builtin_bit_cast(uint32_t, xor_lane<M>(__builtin_bit_cast(float, (uint32_t)(u >> 32)), lane));
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// The router logit as production returns it: F.linear in bf16 rounds the dot product to bf16, .to(float32) widens
+// it back (code/fork/docs/BF16_GEMV.md:27,38; the reference's router oracle is (X.double() @ W.t()).to(bfloat16),
+// code/fork/tests/router_topk_agreement.py:82, and torch narrows a double to bf16 through fp32). `dot` is the
+// float64 sum of the bf16 products; (float) rounds it to nearest even, f32_to_bf16 likewise.
+__device__ __forceinline__ float router_round(double dot) { return bf16_to_f32(f32_to_bf16((float)dot)); }
+
+// One workgroup per expert, one wave per 512-wide chunk c of K. Every bf16 x bf16 product is exact in fp32 and its
+// significand has at most 16 bits, so float64 adds them without rounding whenever the terms span fewer than ~37
+// binades (x ~ N(0, 1) and router weights ~ N(0, 0.02) span far fewer): the float64 sum is then the exact dot
+// product whatever the order, and the bf16 logit is that of the exact value. Lane l of chunk c accumulates
+// k = 512c + 8l + i, i = 0..7; the 64 lane partials are combined by the xor butterfly m = 32, 16, ..., 1; the chunk
+// sums are then added in chunk order c = 0, 1, ... (wave 0 adds them from LDS). Waves past K/512 only join the
+// barriers. The logits of experts e0 .. e0 + NE - 1 (those below E) for every token. COH: stored as device-coherent
+// words (read back by another workgroup of the same grid). SCORE: the stored value is the score sigmoid(logit),
+// computed as the top-k does ((float)(1 / (1 + exp(-(double)logit)))), instead of the logit.
 template <bool COH = false, int NE = 1, bool SCORE = false>
 __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int64_t x_stride,
                                             const uint16_t* __restrict__ w, int T, int K, int E, int e0,
                                             float* __restrict__ logits) {
-    __shared__ float part[RL_MAXC][NE * RL_TCHUNK];
+    __shared__ double part[RL_MAXC][NE * RL_TCHUNK];
     const int lane = threadIdx.x & 63;
     const int c = threadIdx.x >> 6;                 // chunk of this wave
     const int chunks = K / 512;
@@ -45,39 +62,46 @@ __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int6
             for (int tt = 0; tt < RL_TCHUNK; ++tt)
                 xv[tt] = t0 + tt < T ? *reinterpret_cast<const u32x4*>(x + (size_t)(t0 + tt) * x_stride + k0)
                                      : u32x4{0u, 0u, 0u, 0u};
-            u32x4 wv[NE];
+            double wd[NE][8];
 #pragma unroll
-            for (int q = 0; q < NE; ++q)
-                wv[q] = *reinterpret_cast<const u32x4*>(w + (size_t)min(e0 + q, E - 1) * K + k0);
+            for (int q = 0; q < NE; ++q) {
+                const u32x4 wv = *reinterpret_cast<const u32x4*>(w + (size_t)min(e0 + q, E - 1) * K + k0);
 #pragma unroll
-            for (int q = 0; q < NE; ++q)
+                for (int i = 0; i < 4; ++i) {
+                    wd[q][2 * i] = (double)__builtin_bit_cast(float, wv[i] << 16);
+                    wd[q][2 * i + 1] = (double)__builtin_bit_cast(float, wv[i] & 0xFFFF0000u);
+                }
+            }
 #pragma unroll
-                for (int tt = 0; tt < RL_TCHUNK; ++tt) {
-                    float acc = 0.f;
-                    if (t0 + tt < T) {
+            for (int tt = 0; tt < RL_TCHUNK; ++tt) {
+                double xd[8];
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            acc = __builtin_fmaf(__builtin_bit_cast(float, xv[tt][i] << 16),
-                                                 __builtin_bit_cast(float, wv[q][i] << 16), acc);
-                            acc = __builtin_fmaf(__builtin_bit_cast(float, xv[tt][i] & 0xFFFF0000u),
-                                                 __builtin_bit_cast(float, wv[q][i] & 0xFFFF0000u), acc);
-                        }
-                    }
-                    // butterfly m = 32, 16, ..., 1 (the fixed order), partners by permlane / DPP
-                    acc = acc + xor_lane<32>(acc, lane);
-                    acc = acc + xor_lane<16>(acc, lane);
-                    acc = acc + xor_lane<8>(acc, lane);
-                    acc = acc + xor_lane<4>(acc, lane);
-                    acc = acc + xor_lane<2>(acc, lane);
-                    acc = acc + xor_lane<1>(acc, lane);
+                for (int i = 0; i < 4; ++i) {
+                    xd[2 * i] = (double)__builtin_bit_cast(float, xv[tt][i] << 16);
+                    xd[2 * i + 1] = (double)__builtin_bit_cast(float, xv[tt][i] & 0xFFFF0000u);
+                }
+#pragma unroll
+                for (int q = 0; q < NE; ++q) {
+                    double acc = 0.0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc = __builtin_fma(xd[i], wd[q][i], acc);
+                    // butterfly m = 32, 16, ..., 1, partners by permlane / DPP
+                    acc = acc + xor_lane_f64<32>(acc, lane);
+                    acc = acc + xor_lane_f64<16>(acc, lane);
+                    acc = acc + xor_lane_f64<8>(acc, lane);
+                    acc = acc + xor_lane_f64<4>(acc, lane);
+                    acc = acc + xor_lane_f64<2>(acc, lane);
+                    acc = acc + xor_lane_f64<1>(acc, lane);
                     if (lane == 0) part[c][q * RL_TCHUNK + tt] = acc;
                 }
+            }
         }
         __syncthreads();
         const int q = (int)threadIdx.x / RL_TCHUNK, tt = (int)threadIdx.x % RL_TCHUNK;
         if (q < NE && e0 + q < E && t0 + tt < T) {
-            float sum = part[0][threadIdx.x];
-            for (int cc = 1; cc < chunks; ++cc) sum = sum + part[cc][threadIdx.x];
+            double dot = part[0][threadIdx.x];
+            for (int cc = 1; cc < chunks; ++cc) dot = dot + part[cc][threadIdx.x];
+            float sum = router_round(dot);
             if (SCORE) sum = (float)(1.0 / (1.0 + exp(-(double)sum)));
             float* dst = logits + (size_t)(t0 + tt) * E + e0 + q;
             if (COH) st_coherent(dst, sum);
@@ -551,6 +575,7 @@ __global__ __launch_bounds__(1024) void router_route_kernel(const uint16_t* __re
         last = (__hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) % gridDim.x == 0u;
     __syncthreads();
     if (!last) return;
+    acquire_agent();
     if (threadIdx.x == 0) *arrivals = 0u;
     topk_route_body<J, true, true>(logits, T, E, bias, topk, scale, renorm, ids, wts, a, sh);
 }

@@ -103,8 +103,27 @@ class Exl3Experts:
                            layer.w2_suh.data, layer.w2_svh.data)
 
 
+_CHECKED_TABLES: set = set()
+
+
+def _check_aligned(name: str, t: torch.Tensor, n: int) -> None:
+    """Every address in a caller-built pointer table must be 16-byte aligned (the kernels read trellis words and
+    scales with 16-byte loads). Checked on the host once per table (address, length, version); the check copies the
+    table to the host, so it cannot run during graph capture."""
+    key = (t.data_ptr(), n, t._version, str(t.device))
+    if key in _CHECKED_TABLES:
+        return
+    if t.is_cuda and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"{name}: pointer table not yet validated; make one eager call with these tables before "
+                           "graph capture")
+    if bool(((t[:n].cpu() % 16) != 0).any()):
+        raise ValueError(f"{name}: every expert's address must be a multiple of 16 bytes")
+    _CHECKED_TABLES.add(key)
+
+
 def tables_desc(n: int, K: int, N: int, tables: dict, shared_suh: bool = False) -> _lib.Exl3LayerDesc:
-    """Descriptor from caller-built pointer tables (the exl3_moe contract passes them directly)."""
+    """Descriptor from caller-built pointer tables (the exl3_moe contract passes them directly); every table entry is
+    checked for 16-byte alignment the first time the table is seen."""
     d = _lib.Exl3LayerDesc()
     d.n, d.hidden, d.intermediate = n, K, N
     d.flags = _lib.LAYER_SHARED_W13_SUH if shared_suh else 0
@@ -113,5 +132,6 @@ def tables_desc(n: int, K: int, N: int, tables: dict, shared_suh: bool = False) 
         t = tables[k]
         if t.dtype != torch.int64 or t.dim() != 1 or t.numel() < n or not t.is_contiguous():
             raise ValueError(f"{k}: pointer table must be a contiguous int64 [>= n] tensor")
+        _check_aligned(k, t, n)
         setattr(d, k, ctypes.c_void_p(t.data_ptr()))
     return d

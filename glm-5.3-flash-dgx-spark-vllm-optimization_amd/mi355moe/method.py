@@ -48,35 +48,57 @@ def apply_exl3_experts(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: to
     return out.reshape(x.shape)
 
 
+def _fused_key(ts) -> tuple:
+    """Identity of the weight tensors for the descriptor cache: storage address, shape, strides, dtype, device and
+    torch's version counter (bumped by every in-place write, so a reload through copy_ builds a new descriptor)."""
+    return tuple((t.data_ptr(), tuple(t.shape), t.stride(), t.dtype, str(t.device), t._version) for t in ts)
+
+
 def fused_experts(hidden: torch.Tensor, w13: torch.Tensor, w2: torch.Tensor, topk_weights: torch.Tensor,
                   topk_ids: torch.Tensor, scales: tuple, *, limit: float = SWIGLU_LIMIT_DEFAULT,
                   expert_map: torch.Tensor | None = None) -> torch.Tensor:
     """apply(hidden, w13, w2, topk_weights, topk_ids, scales): w13 = w13_trellis [n, 2, K/16, N/16, 64],
-    w2 = w2_trellis [n, N/16, K/16, 64], scales = (w13_suh, w13_svh, w2_suh, w2_svh). Pointer tables are cached per
-    weight tensor, so repeated calls with the same weights do no host work beyond the launch."""
-    key = (w13.data_ptr(), w2.data_ptr(), tuple(s.data_ptr() for s in scales))
-    ex = _FUSED_CACHE.get(key)
+    w2 = w2_trellis [n, N/16, K/16, 64], scales = (w13_suh, w13_svh, w2_suh, w2_svh). The experts object (pointer
+    tables, shared-suh flag) is cached per weight tensors (address, shape, strides, dtype, version), at most
+    _FUSED_CACHE_MAX layers, least recently used dropped first; weights rewritten in a way that does not move the
+    passed tensor's version counter (through .data, or outside torch) need clear_fused_cache()."""
+    w13_suh, w13_svh, w2_suh, w2_svh = scales
+    key = _fused_key((w13, w2, w13_suh, w13_svh, w2_suh, w2_svh))
+    ex = _FUSED_CACHE.pop(key, None)
     if ex is None:
-        w13_suh, w13_svh, w2_suh, w2_svh = scales
         ex = Exl3Experts(w13, w13_suh, w13_svh, w2, w2_suh, w2_svh)
-        _FUSED_CACHE[key] = ex
+    _FUSED_CACHE[key] = ex                        # most recently used last
+    while len(_FUSED_CACHE) > _FUSED_CACHE_MAX:
+        _FUSED_CACHE.pop(next(iter(_FUSED_CACHE)))
     T = hidden.shape[0]
     return ops.moe_forward_ids(ex, hidden, topk_ids.reshape(T, -1), topk_weights.reshape(T, -1), limit=limit,
                                expert_map=expert_map, out_dtype=hidden.dtype)
 
 
 _FUSED_CACHE: dict = {}
+_FUSED_CACHE_MAX = 128            # layers; a served model has one entry per MoE layer
+
+
+def clear_fused_cache() -> None:
+    """Drop every cached experts object of fused_experts (and the references it holds to weight tensors)."""
+    _FUSED_CACHE.clear()
 
 
 class Exl3MoEMethod:
     """FusedMoE quant method for EXL3 4-bit trellis routed experts (prod_exl3_reference.py:2030-2343)."""
 
-    def __init__(self, bits: int = 4, swiglu_limit: float | None = None, e4m3: bool = False):
+    def __init__(self, bits: int = 4, swiglu_limit: float | None = None, e4m3: bool = False,
+                 max_num_tokens: int | None = None, topk: int = 8):
         if bits != 4:
             raise ValueError("this build decodes 4-bit EXL3 trellis tiles only")
         self.bits = bits
         self.swiglu_limit = swiglu_limit
         self.e4m3 = e4m3                  # the overlay's e4m3 expert numerics instead of the fp16 paths
+        # with max_num_tokens the device workspace is sized once after weight load for every call up to that many
+        # tokens (top-k picks each), so later calls never reallocate it (the reference's Scratch, sized at
+        # registration, code/fork/tf_exl3_moe.py:391-418)
+        self.max_num_tokens = max_num_tokens
+        self.topk = topk
 
     def create_weights(self, layer: torch.nn.Module, num_experts: int, hidden_size: int,
                        intermediate_size_per_partition: int, params_dtype=None, device=None, **_) -> None:
@@ -106,6 +128,8 @@ class Exl3MoEMethod:
                 raise RuntimeError("EXL3 mcg marker is not the MCG int32 0xCBAC1FED / "
                                    f"{MCG_MARKER}; packed ABI mismatch")
         layer._mi355_experts = Exl3Experts.from_module(layer)
+        if self.max_num_tokens:
+            ops.reserve(layer._mi355_experts, self.max_num_tokens, self.topk)
 
     def apply(self, layer: torch.nn.Module, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
               shared_experts=None, shared_experts_input=None) -> torch.Tensor:

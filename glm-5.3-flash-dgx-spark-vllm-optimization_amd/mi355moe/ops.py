@@ -2,7 +2,8 @@
 
 Every function validates its tensors on the host, then calls one C entry point, which checks its arguments again
 before enqueuing anything. No function synchronizes with the host or allocates per call except for its outputs
-(the persistent workspace is allocated once per device and grown when a larger call needs it).
+(the persistent workspace is allocated once per device, reserved up front with `reserve`, or replaced by a larger one
+when a call outgrows it; a replaced workspace is kept alive for the graphs captured on it).
 """
 from __future__ import annotations
 
@@ -13,7 +14,8 @@ import torch
 from . import _lib
 from .layer import Exl3Experts
 
-_WS: dict = {}
+_WS: dict = {}           # device -> the workspace calls use
+_RETIRED: dict = {}      # device -> superseded workspaces, kept alive for graphs captured on them
 
 
 def _stream(dev: torch.device) -> ctypes.c_void_p:
@@ -60,15 +62,66 @@ def ids_dtype_code(dt: torch.dtype) -> int:
     raise ValueError(f"router ids must be int32 or int64, got {dt}")
 
 
+def _capturing(dev: torch.device) -> bool:
+    """True while the current stream of a GPU device is being captured into a graph."""
+    return dev.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
+
 def workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    """The persistent zero-initialised workspace of `dev`, at least `nbytes` (grown, never shrunk). Calls keep
-    its counters at zero; calls that share it must be stream-ordered."""
+    """The persistent zero-initialised workspace of `dev`, at least `nbytes`. Calls keep its counters at zero; calls
+    that share it must be stream-ordered.
+
+    When a call needs more than the current workspace, a larger one replaces it for later calls and the old one is
+    retired but never freed: a HIP graph captured earlier keeps replaying into the memory it captured, which no other
+    tensor can be given. Growing during a graph capture raises instead (the capture would record the new buffer's
+    zero fill); size the workspace beforehand with reserve_workspace / reserve, or by one eager call of the largest
+    shape."""
     key = (dev.type, dev.index)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
+        if _capturing(dev):
+            have = 0 if ws is None else ws.numel()
+            raise RuntimeError(f"mi355moe: this call needs a {int(nbytes)}-byte workspace on {dev} but {have} bytes "
+                               "are reserved, and it cannot grow during graph capture; call "
+                               "mi355moe.ops.reserve(...) or run one eager call of this shape before capturing")
+        if ws is not None:
+            _RETIRED.setdefault(key, []).append(ws)
         ws = torch.zeros(max(int(nbytes), 1 << 20), dtype=torch.uint8, device=dev)
         _WS[key] = ws
     return ws
+
+
+def reserve_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """Size the workspace of `dev` to at least `nbytes` now (at load time, before any capture)."""
+    return workspace(torch.device(dev), int(nbytes))
+
+
+def workspace_bytes(experts: Exl3Experts, tokens: int, topk: int = 8, router_experts: int | None = None) -> int:
+    """The largest workspace any entry point of this module needs for calls of up to `tokens` tokens over `experts`
+    (decode and grouped tiers, the trellis-sourced e4m3 variant, and with router_experts the whole-layer call)."""
+    L = _lib.lib()
+    d = ctypes.byref(experts.desc)
+    need = 0
+    for path in (_lib.PATH_AUTO, _lib.PATH_DECODE, _lib.PATH_PREFILL):
+        if path == _lib.PATH_PREFILL and not experts.shared_suh:
+            continue
+        need = max(need, L.mi355moe_moe_workspace_bytes_path(d, tokens, topk, path))
+    if experts.shared_suh and experts.K <= 4096:
+        need = max(need, L.mi355moe_e4m3_moe_workspace_bytes(d, tokens, topk))
+    if router_experts is not None:
+        need = max(need, L.mi355moe_moe_layer_workspace_bytes(d, tokens, topk, router_experts))
+    if need < 0:
+        raise ValueError("mi355moe: the workspace size query rejected the shape")
+    return int(need)
+
+
+def reserve(experts: Exl3Experts, max_tokens: int, topk: int = 8, router_experts: int | None = None) -> torch.Tensor:
+    """Reserve the workspace for every call of up to max_tokens tokens over `experts` once, as the reference sizes
+    its persistent scratch at registration (code/fork/tf_exl3_moe.py:391-418): later calls within that size never
+    reallocate, so graphs may be captured at any point after this."""
+    top = max(1, int(max_tokens))
+    sizes = {top} | {1 << i for i in range(top.bit_length()) if 1 << i <= top}
+    return workspace(experts.device, max(workspace_bytes(experts, t, topk, router_experts) for t in sizes))
 
 
 def dequant(trellis: torch.Tensor) -> torch.Tensor:
@@ -84,7 +137,8 @@ def dequant(trellis: torch.Tensor) -> torch.Tensor:
 
 
 def router_logits(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """fp32 [T, E] = x bf16 [T, K] @ w bf16 [E, K]^T in the library's fixed summation order."""
+    """fp32 [T, E] holding bf16(x bf16 [T, K] @ w bf16 [E, K]^T): the exact (float64) dot products rounded to bf16
+    through fp32, what F.linear(x, w).to(torch.float32) returns (code/fork/docs/BF16_GEMV.md:27,38)."""
     dev = _need_cuda(x, w)
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
         raise ValueError("router_logits: bf16 x [T, K] and bf16 W [E, K]")

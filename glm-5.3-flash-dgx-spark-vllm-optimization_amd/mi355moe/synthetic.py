@@ -47,6 +47,47 @@ def exl3_layer(n: int, K: int, N: int, seed: int, device="cuda", svh_scale: floa
     return Exl3Experts(w13_trellis, w13_suh, w13_svh, w2_trellis, w2_suh, w2_svh)
 
 
+def codebook_std() -> float:
+    """Standard deviation of the 4-bit mcg codebook over all 65,536 states (uniform random trellis words give
+    uniform states): x = s * 0xCBAC1FED mod 2^32, (x & 0x8FFF8FFF) ^ 0x3B603B60, fp16(lo) + fp16(hi)."""
+    s = torch.arange(65536, dtype=torch.int64)
+    x = ((s * 0xCBAC1FED) & 0xFFFFFFFF & 0x8FFF8FFF) ^ 0x3B603B60
+    lo = (x & 0xFFFF).to(torch.int32).to(torch.int16).view(torch.float16)
+    hi = (x >> 16).to(torch.int32).to(torch.int16).view(torch.float16)
+    return float((lo + hi).double().std())
+
+
+def _scaled_signs(shape, scale, g, device) -> torch.Tensor:
+    """fp16 of random sign x (1 + 0.25 U(-1, 1)) x scale."""
+    mag = 1.0 + 0.25 * (torch.rand(shape, generator=g, device=device) * 2 - 1)
+    return (_signs(shape, g, device) * mag * scale).to(torch.float16)
+
+
+def calibrated_layer(n: int, K: int, N: int, seed: int, device="cuda", g_std: float = 5.0, svh_d: float = 0.001,
+                     shared_suh: bool = True) -> Exl3Experts:
+    """n random EXL3 4-bit experts with scales calibrated as the reference's test harness does
+    (code/fork/tests/harness.py:178-200): suh, svh and down suh are random signs x (1 +- 25 %) x a scale, the gate/up
+    svh scale chosen so that the gate and up pre-activations have standard deviation g_std for x ~ N(0, 1)
+    (std(g) = sqrt(K) * codebook std * E|suh| * E|svh|); with g_std = 5 and the SwiGLU limit 10 about 5 % of the
+    gate values are clamped. Down suh ~ 8 / sqrt(N) as there; the down svh scale (svh_d; the reference uses 1.0, which
+    gives routed outputs of RMS ~200) is 0.001 by default, for routed outputs of RMS ~0.2."""
+    device = torch.device(device)
+    g = _gen(seed, device)
+    mag_rms = math.sqrt(1 + 0.25 ** 2 / 3)
+    s_svh = g_std / (math.sqrt(K) * codebook_std() * mag_rms * mag_rms)
+    w13_trellis = torch.randint(-32768, 32768, (n, 2, K // 16, N // 16, 64), generator=g, device=device,
+                                dtype=torch.int32).to(torch.int16)
+    w13_suh = _scaled_signs((n, 2, K), 1.0, g, device)
+    if shared_suh:
+        w13_suh[:, 1].copy_(w13_suh[:, 0])
+    w13_svh = _scaled_signs((n, 2, N), s_svh, g, device)
+    w2_trellis = torch.randint(-32768, 32768, (n, N // 16, K // 16, 64), generator=g, device=device,
+                               dtype=torch.int32).to(torch.int16)
+    w2_suh = _scaled_signs((n, N), 8.0 / math.sqrt(N), g, device)
+    w2_svh = _scaled_signs((n, K), svh_d, g, device)
+    return Exl3Experts(w13_trellis, w13_suh, w13_svh, w2_trellis, w2_suh, w2_svh)
+
+
 def block_quant_e4m3(w: torch.Tensor, block: int = 128) -> tuple[torch.Tensor, torch.Tensor]:
     """e4m3 codes (uint8) and fp32 scales of float32 matrices [..., R, C] with one scale per block x block tile:
     s = amax(tile) / 448 (1 if 0), codes = e4m3(clamp(w / s, -448, 448))."""
@@ -117,6 +158,26 @@ def zipf_logits(T: int, E: int, seed: int, s: float = 1.2, noise: torch.Tensor |
     if noise is not None:
         lg = lg + noise
     return lg
+
+
+def zipf_router(E: int, K: int, seed: int, rank_seed: int, device="cuda", s: float = 1.2,
+                c0: float = 8.0) -> tuple[torch.Tensor, torch.Tensor]:
+    """A router (W, bias) whose GEMM itself produces Zipf(s)-skewed expert popularity: column 0 of W is
+    -s ln(rank_e + 1) / c0 over a random ranking of the experts, so for activations whose channel 0 holds c0
+    (zipf_activations) logit_e = x.W_e - s ln(rank_e + 1) plus the N(0, 0.02) weights' noise."""
+    w, b = router(E, K, seed, device=device)
+    g = _gen(rank_seed, torch.device("cpu"))
+    rank = torch.empty(E, dtype=torch.float32)
+    rank[torch.randperm(E, generator=g)] = torch.arange(E, dtype=torch.float32)
+    w[:, 0] = (-s * torch.log(rank + 1.0) / c0).to(w.device, torch.bfloat16)
+    return w, b
+
+
+def zipf_activations(T: int, K: int, seed: int, device="cuda", c0: float = 8.0) -> torch.Tensor:
+    """bf16 x ~ N(0, 1) [T, K] with channel 0 held at c0 (the channel zipf_router's skew column reads)."""
+    x = activations(T, K, seed, device=device)
+    x[:, 0] = c0
+    return x
 
 
 def expected_distinct(n: int, topk: int, T: int) -> float:

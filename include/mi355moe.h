@@ -46,7 +46,9 @@ typedef struct mi355moe_exl3_layer {
     int64_t n;              /* local experts */
     int64_t hidden;         /* K, multiple of 256 */
     int64_t intermediate;   /* N, multiple of 128 */
-    const int64_t* gate_trellis;   /* device int64 [n] each: expert i's tensor address, 16-byte aligned */
+    /* nine device int64 [n] tables; entry i = expert i's tensor address. EVERY entry of every table must be
+     * 16-byte aligned (trellis words and scales are read with 16-byte loads). */
+    const int64_t* gate_trellis;
     const int64_t* gate_suh;
     const int64_t* gate_svh;
     const int64_t* up_trellis;
@@ -70,9 +72,10 @@ const char* mi355moe_strerror(int code);
  * code/fork/tests/test_layout_equiv.py:1-46). n_tiles must be a multiple of 8. */
 int mi355moe_exl3_dequant(const void* trellis, int64_t k_tiles, int64_t n_tiles, void* wq, hipStream_t stream);
 
-/* Router logits fp32 [T][E] = x bf16 [T][K] (row stride x_stride) times W bf16 [E][K]^T, in a fixed summation
- * order (replaces F.linear(x, W).to(torch.float32), code/fork/docs/BF16_GEMV.md:27,38). K % 512 == 0,
- * K <= 8192. */
+/* Router logits fp32 [T][E] = x bf16 [T][K] (row stride x_stride) times W bf16 [E][K]^T, each the bf16 rounding
+ * (through fp32, nearest even) of the float64 sum of the bf16 products, as F.linear(x, W).to(torch.float32)
+ * returns it (code/fork/docs/BF16_GEMV.md:27,38; reference oracle (X.double() @ W.t()).to(bfloat16),
+ * code/fork/tests/router_topk_agreement.py:82). K % 512 == 0, K <= 8192. */
 int mi355moe_router_logits(const void* x, int64_t T, int64_t K, int64_t x_stride, const void* w, int64_t E,
                            float* logits, hipStream_t stream);
 
@@ -148,7 +151,7 @@ int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int6
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* The routed-expert output of one MoE layer from its hidden states, in one call: router logits x . W^T in fp32
- * (mi355moe_router_logits' order) or given logits, sigmoid + bias top-k with renormalisation and routed scale
+ * (mi355moe_router_logits' bf16-rounded values) or given logits, sigmoid + bias top-k with renormalisation and routed scale
  * (mi355moe_router_topk), the token -> expert permutation, the expert GEMMs and the slot-order combine. Replaces the
  * routed part of the model's MoE block: the gate linear (code/fork/docs/BF16_GEMV.md:27,38), vLLM grouped_topk with
  * one group (code/fork/tests/router_topk_agreement.py:58-61) and FusedMoE.apply (code/fork/docs/

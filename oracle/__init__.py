@@ -10,6 +10,6 @@ Contents (each function cites the reference file:line it restates):
   routing.py  router (sigmoid + bias top-k, softmax top-k), map_topk_to_local, stable permutation, segment tables
   moe.py      routed-MoE forward: float64 reference and the rounding-faithful kernel paths (C, via ctypes)
   e4m3.py     e4m3 quantisation (RN, saturating), per-token activation quant, block-scaled expert FFN
-  dense.py    the bf16 dense CPU MoE block (softmax top-4 router, SwiGLU experts)
+  e4m3_trellis.py  the trellis-sourced e4m3 variant (per-row e4m3 activations, EXL3 weights rounded to e4m3)
   csrc/       the C restatement (oracle.c) behind moe.py, built by oracle/Makefile into oracle/_build/
 """

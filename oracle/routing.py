@@ -4,8 +4,8 @@ References:
   router     sigmoid scores, top-k of (score + e_score_correction_bias) with the lower id first among equals,
              weights = score / (sum + 1e-20) * routed_scale in pick order: code/fork/docs/ref/tf_glue.py:371-401
              (TensorFold's restatement of vLLM grouped_topk with n_group = topk_group = 1,
-             code/fork/tests/router_topk_agreement.py:58-61). Logits = x @ W^T in fp32 from bf16 operands
-             (code/fork/docs/BF16_GEMV.md:27,38).
+             code/fork/tests/router_topk_agreement.py:58-61). Logits = bf16(x @ W^T) widened to fp32
+             (code/fork/docs/BF16_GEMV.md:27,38; code/fork/tests/router_topk_agreement.py:82).
   local ids  map_topk_to_local, code/fork/docs/prod_exl3_reference.py:936-958.
   order      pairs j = t*topk + k grouped by local expert, the sentinel group (id n) last, and inside a group by
              pair index -- torch.argsort(local, stable=True) (code/fork/overlay/glm53_moe_e4m3.py:462;
@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import numpy as np
 
-ROUTER_CHUNK = 512          # K elements one router wave reads per step (64 lanes x 8 bf16)
+ROUTER_CHUNK = 512          # the router kernel's K granularity (64 lanes x 8 bf16)
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
@@ -29,32 +29,17 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 
 
 def router_logits(x: np.ndarray, w: np.ndarray) -> np.ndarray:
-    """fp32 logits [T, E] of bf16 x [T, K] and bf16 W [E, K] (given as float32 arrays holding bf16 values), in the
-    summation order of this build's router kernel: for every 512-wide chunk c of K, lane l (of 64) adds
-    k = 512c + 8l + i for i = 0..7 sequentially in fp32 from 0 (each bf16 x bf16 product is exact in fp32, so a
-    fused multiply-add rounds like an add); the 64 lane sums are combined by the xor butterfly p[l] += p[l ^ m],
-    m = 32, 16, ..., 1; the chunk sums are then added in chunk order."""
-    x = np.asarray(x, np.float32)
-    w = np.asarray(w, np.float32)
-    T, K = x.shape
-    E = w.shape[0]
-    if K % ROUTER_CHUNK:
+    """Router logits [T, E] as production returns them: F.linear(x, W) in bf16, then .to(float32)
+    (code/fork/docs/BF16_GEMV.md:27,38), i.e. the dot product rounded to bf16. Following the reference's own router
+    oracle, (X.double() @ W.t()).to(bfloat16).float() (code/fork/tests/router_topk_agreement.py:82), the dot
+    product of the bf16 values (given as float32 arrays) is taken in float64 -- exact for router-sized operands,
+    since every product has at most 16 significant bits -- then narrowed to fp32 and to bf16, both to nearest even
+    (torch narrows a double to bf16 through fp32)."""
+    x = np.asarray(x, np.float32).astype(np.float64)
+    w = np.asarray(w, np.float32).astype(np.float64)
+    if x.shape[1] % ROUTER_CHUNK:
         raise ValueError("K must be a multiple of 512")
-    C = K // ROUTER_CHUNK
-    xc = x.reshape(T, C, 64, 8)
-    wc = w.reshape(E, C, 64, 8)
-    acc = np.zeros((T, E, C, 64), np.float32)
-    for i in range(8):
-        acc = acc + xc[:, None, :, :, i] * wc[None, :, :, :, i]
-    m = 32
-    lanes = np.arange(64)
-    while m:
-        acc = acc + acc[..., lanes ^ m]
-        m >>= 1
-    tot = acc[..., 0, 0].copy()
-    for c in range(1, C):
-        tot = tot + acc[..., c, 0]
-    return tot
+    return bf16_round((x @ w.T).astype(np.float32))
 
 
 def sigmoid_f32(logits: np.ndarray) -> np.ndarray:

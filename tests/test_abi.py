@@ -100,3 +100,25 @@ def test_expert_pointer_tables_require_16_byte_alignment():
         _table(torch.zeros(3 * 256 + 1, dtype=torch.float16)[1:].view(3, 256), ())   # base 2 bytes off
     with pytest.raises(ValueError):
         _table(torch.zeros(3, 260, dtype=torch.float16), ())                          # 520-byte expert stride
+
+
+def test_workspace_growth_keeps_old_buffer_and_refuses_under_capture(monkeypatch):
+    """Host logic of the persistent workspace (on the CPU device): growth retires the old buffer without freeing
+    it, and growth while a graph is being captured raises."""
+    import torch
+    from mi355moe import ops
+    dev = torch.device("cpu")
+    key = (dev.type, dev.index)
+    ops._WS.pop(key, None)
+    ops._RETIRED.pop(key, None)
+    a = ops.workspace(dev, 100)
+    assert a.numel() == 1 << 20 and ops.workspace(dev, 1 << 20) is a
+    b = ops.workspace(dev, (1 << 20) + 1)
+    assert b is not a and b.numel() == (1 << 20) + 1
+    assert ops._RETIRED[key] == [a]
+    monkeypatch.setattr(ops, "_capturing", lambda d: True)
+    assert ops.workspace(dev, 1000) is b                             # no growth needed: fine under capture
+    with pytest.raises(RuntimeError, match="cannot grow during graph capture"):
+        ops.workspace(dev, 4 << 20)
+    ops._WS.pop(key, None)
+    ops._RETIRED.pop(key, None)

@@ -118,3 +118,44 @@ def test_layer_repeat_graph_and_shared_workspace(cuda, model):
         assert torch.equal(out, a), i
         ops.moe_forward_ids(ex, xb, ids, wts)                # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_graph_survives_workspace_growth(cuda, model):
+    """A decode layer call captured in a graph, then an eager call that outgrows the workspace (T=8192 on the
+    grouped tier): the larger call gets a new workspace and the captured graph keeps replaying into the old one,
+    which stays allocated; every replay equals the eager result."""
+    from mi355moe import ops, synthetic
+    ex, w, b = model
+    T = 8
+    _say("graph capture, workspace growth, replay")
+    x = synthetic.activations(T, K, seed=95, device=cuda)
+    a = ops.moe_layer(ex, x, router_w=w, topk=8, bias=b, routed_scale=2.5)
+    out = torch.empty_like(a)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.moe_layer(ex, x, router_w=w, topk=8, bias=b, routed_scale=2.5, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.moe_layer(ex, x, router_w=w, topk=8, bias=b, routed_scale=2.5, out=out)
+    before = ops.workspace(cuda, 0)
+    xb = synthetic.activations(8192, K, seed=96, device=cuda)
+    ids = synthetic.random_ids(8192, E, 8, seed=97, device=cuda)
+    wts = synthetic.softmax_weights(8192, 8, seed=98, device=cuda)
+    need = ops.workspace_bytes(ex, 8192, 8)
+    ops.reserve_workspace(cuda, max(need, before.numel() + (64 << 20)))   # grows, whatever ran before this test
+    assert ops.workspace(cuda, 0).data_ptr() != before.data_ptr()
+    del before
+    big = ops.moe_forward_ids(ex, xb, ids, wts)
+    torch.cuda.synchronize()
+    assert torch.isfinite(big.float()).all()
+    filler = torch.full((64 << 20,), 7, dtype=torch.uint8, device=cuda)   # memory handed out after the growth
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, a), i
+        ops.moe_forward_ids(ex, xb, ids, wts)
+        torch.cuda.synchronize()
+    del filler

@@ -62,14 +62,42 @@ def test_rot_in_bit_exact(cuda, xdt):
         assert np.array_equal(got[j].numpy().view(np.uint16), ref.view(np.uint16)), j
 
 
-def test_router_logits_bit_exact(cuda):
+@pytest.mark.parametrize("T", [8, 300])
+def test_router_logits_bit_exact(cuda, T):
+    """Logits = bf16(x . W) through fp32, bit for bit; the first rows hold constructed dot products on either side of
+    a bf16 midpoint after fp32 rounding (1 + 2**-8 + 2**-30 ties to 1.0, 1 + 2**-8 + 2**-22 rounds up)."""
     from mi355moe import ops, synthetic
-    _say("router_logits T=8 E=288 K=4096")
+    _say(f"router_logits T={T} E=288 K=4096")
     w, _ = synthetic.router(288, 4096, seed=1, device="cpu")
-    x = synthetic.activations(8, 4096, seed=2, device="cpu")
+    x = synthetic.activations(T, 4096, seed=2, device="cpu")
+    x[:2] = 0
+    w[0] = 0
+    x[0, :3] = torch.tensor([1.0, 2.0 ** -8, 2.0 ** -15])
+    x[1, :3] = torch.tensor([1.0, 2.0 ** -8, 2.0 ** -7])
+    w[0, :3] = torch.tensor([1.0, 1.0, 2.0 ** -15])
     got = ops.router_logits(x.to(cuda), w.to(cuda)).cpu().numpy()
     ref = routing.router_logits(x.float().numpy(), w.float().numpy())
+    assert got[0, 0] == 1.0 and got[1, 0] == 1.0 + 2.0 ** -7
     assert np.array_equal(got, ref)
+
+
+def test_router_picks_4096_tokens(cuda):
+    """Top-8 sets of 4,096 tokens from the GPU router (logits + top-k) against the top-8 of the reference's router
+    oracle, bf16(float64 dot) (code/fork/tests/router_topk_agreement.py:82): ids in pick order bit for bit (largest
+    score + bias first, lower id among equals), and the weights of the first 64 tokens against the oracle's loop."""
+    from mi355moe import ops, synthetic
+    _say("router logits + top-8, T=4096 E=288")
+    T = 4096
+    w, b = synthetic.router(288, 4096, seed=11, device="cpu")
+    x = synthetic.activations(T, 4096, seed=12, device="cpu")
+    ids, wts = ops.router_topk(ops.router_logits(x.to(cuda), w.to(cuda)), 8, b.to(cuda), routed_scale=2.5)
+    lg = routing.router_logits(x.float().numpy(), w.float().numpy())
+    choice = (routing.sigmoid_f32(lg) + b.numpy()[None, :]).astype(np.float32)
+    want = np.argsort(-choice.astype(np.float64), axis=1, kind="stable")[:, :8]
+    assert np.array_equal(ids.cpu().numpy(), want)
+    rid, rw = routing.topk_sigmoid_bias(lg[:64], b.numpy(), 8, 2.5)
+    assert np.array_equal(ids[:64].cpu().numpy(), rid)
+    assert np.array_equal(wts[:64].cpu().numpy(), rw)
 
 
 @pytest.mark.parametrize("T,E,topk", [(64, 288, 8), (5, 32, 4), (3, 1024, 32)])

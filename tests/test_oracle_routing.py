@@ -23,39 +23,78 @@ def test_bf16_round_matches_torch():
     assert np.array_equal(routing.bf16_round(v), ref)
 
 
-def test_router_logits_order_by_explicit_loops():
+def _round_dyadic(num: int, shift: int, bits: int) -> tuple[int, int]:
+    """num / 2**shift rounded to `bits` significant bits, nearest even, as (m, e) with value m * 2**e (integers
+    only; no subnormals are involved at router magnitudes)."""
+    if num == 0:
+        return 0, 0
+    sign = -1 if num < 0 else 1
+    a = abs(num)
+    drop = a.bit_length() - bits
+    if drop <= 0:
+        return sign * a, -shift
+    q, r = divmod(a, 1 << drop)
+    half = 1 << (drop - 1)
+    if r > half or (r == half and q & 1):
+        q += 1
+    return sign * q, drop - shift
+
+
+def _exact_router_logit(xrow, wrow) -> float:
+    """bf16(fp32(exact dot)) by integer arithmetic: every bf16 value is m * 2**e with integer m, so the dot product is
+    an integer over a power of two; it is rounded to 24 then to 8 significant bits (nearest even) with integers."""
+    terms = []
+    for a, b in zip(xrow, wrow):
+        ma, ea = math.frexp(float(a))
+        mb, eb = math.frexp(float(b))
+        terms.append((int(ma * (1 << 24)) * int(mb * (1 << 24)), ea + eb - 48))
+    lo = min(e for _, e in terms)
+    num = sum(m << (e - lo) for m, e in terms)
+    m24, e24 = _round_dyadic(num, -lo, 24)
+    m8, e8 = _round_dyadic(m24, -e24, 8)
+    return math.ldexp(m8, e8)
+
+
+def test_router_logits_exact_rational():
+    """Every oracle logit equals the bf16 rounding (through fp32) of the exact dot product, computed with integers."""
     rng = np.random.default_rng(1)
-    T, E, K = 2, 3, 1024
+    T, E, K = 3, 5, 1024
     x, w = _bf16_values(rng, (T, K)), _bf16_values(rng, (E, K), 0.02)
     got = routing.router_logits(x, w)
     for t in range(T):
         for e in range(E):
-            chunk_sums = []
-            for c in range(K // 512):
-                part = []
-                for lane in range(64):
-                    acc = np.float32(0)
-                    for i in range(8):
-                        k = c * 512 + lane * 8 + i
-                        acc = np.float32(acc + np.float32(x[t, k] * w[e, k]))
-                    part.append(acc)
-                m = 32
-                while m:
-                    part = [np.float32(part[l] + part[l ^ m]) for l in range(64)]
-                    m //= 2
-                chunk_sums.append(part[0])
-            tot = chunk_sums[0]
-            for s in chunk_sums[1:]:
-                tot = np.float32(tot + s)
-            assert got[t, e] == tot
+            assert float(got[t, e]) == _exact_router_logit(x[t], w[e]), (t, e)
 
 
-def test_router_logits_close_to_f64():
+def test_router_logits_double_rounding_through_fp32():
+    """A dot product of exactly 1 + 2**-8 + 2**-30: rounded straight to bf16 it is 1 + 2**-7, but fp32 first rounds
+    it onto the bf16 midpoint 1 + 2**-8, which then ties to the even 1.0 -- what torch's double -> bf16 and an fp32
+    GEMM with a bf16 output both give."""
+    K = 512
+    x = np.zeros((2, K), np.float32)
+    w = np.zeros((1, K), np.float32)
+    x[0, :3] = [1.0, 2.0 ** -8, 2.0 ** -15]
+    w[0, :3] = [1.0, 1.0, 2.0 ** -15]
+    x[1, :3] = [1.0, 2.0 ** -8, 2.0 ** -7]          # 1 + 2**-8 + 2**-22: fp32 keeps it above the midpoint
+    got = routing.router_logits(x, w)
+    assert got[0, 0] == np.float32(1.0)
+    assert got[1, 0] == np.float32(1.0 + 2.0 ** -7)
+    ref = (torch.from_numpy(x).double() @ torch.from_numpy(w).double().t()).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got, ref)
+
+
+def test_router_logits_match_reference_oracle_expression():
+    """The reference's own router oracle, (X.double() @ W.t()).to(bfloat16).float()
+    (code/fork/tests/router_topk_agreement.py:82), evaluated by torch at the decode configuration's shapes."""
     rng = np.random.default_rng(2)
-    x, w = _bf16_values(rng, (8, 4096)), _bf16_values(rng, (288, 4096), 0.02)
-    got = routing.router_logits(x, w).astype(np.float64)
-    ref = x.astype(np.float64) @ w.astype(np.float64).T
-    assert np.max(np.abs(got - ref)) < 1e-5
+    x, w = _bf16_values(rng, (64, 4096)), _bf16_values(rng, (288, 4096), 0.02)
+    got = routing.router_logits(x, w)
+    ref = (torch.from_numpy(x).double() @ torch.from_numpy(w).double().t()).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got, ref)
+    # and the values are bf16 (low 16 bits clear) within one bf16 step of the float64 dot product
+    assert not np.any(got.view(np.uint32) & 0xFFFF)
+    f64 = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.all(np.abs(got - f64) <= np.abs(f64) * 2.0 ** -8 + 1e-30)
 
 
 def test_sigmoid_is_correctly_rounded_on_samples():
