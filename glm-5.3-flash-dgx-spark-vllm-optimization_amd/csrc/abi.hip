@@ -1,6 +1,7 @@
 // C-ABI entry points: argument checks (all before the first launch), launch planning and workspace layout.
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/mi355moe.h"
 #include "common.cuh"
@@ -212,6 +213,8 @@ const char* mi355moe_strerror(int code) {
         case MI355MOE_EWORKSPACE: return "workspace too small";
         case MI355MOE_EDTYPE: return "unsupported dtype";
         case MI355MOE_EUNSUPPORTED: return "unsupported format variant";
+        case MI355MOE_ESCRATCH:
+            return "the call needs more device scratch than the allocation-free entry point's fixed array holds";
         default: return code < 0 ? "HIP launch error" : "unknown error";
     }
 }
@@ -664,6 +667,93 @@ int mi355moe_moe_layer(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     return mi355moe_moe_forward_ids_ex(layer, x, x_dtype, x_stride, T, ids, MI355MOE_I32, wts, MI355MOE_F32, topk,
                                        nullptr, 0, limit, out, out_dtype, out_stride, workspace, (size_t)base,
                                        MI355MOE_PATH_AUTO, MI355MOE_STAGE_ALL, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------------- allocation-free layer
+
+namespace {
+
+// The device scratch of mi355moe_moe_layer_noalloc: one array per GPU, alive until the process ends, shared by every
+// call on that GPU. Host code never uses this name as an address (in host code it is only a stand-in for the symbol):
+// every kernel argument and fill goes through the per-device address hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[MI355MOE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[NOALLOC_MAX_DEVICES];          // per device: the address of its copy of `scratch`
+
+// zeroes the control block (the arrival counter words calls expect at zero) of a device's scratch
+__global__ void zero_control_kernel(unsigned* words, int n) {
+    if ((int)threadIdx.x < n) words[threadIdx.x] = 0u;
+}
+
+bool g_noalloc_zeroed[NOALLOC_MAX_DEVICES];        // per device: its control block was zeroed outside a capture
+
+// The current device's scratch address, looked up with that device current the first time the device is used. Until
+// a call has zeroed the control block on a stream that was not being captured, every call zeroes it on `stream`
+// ahead of its own kernels (a fill kernel, not a memset node; inside a captured graph it re-zeroes words that every
+// call leaves at zero anyway). nullptr with *rc set when a HIP call fails.
+void* noalloc_scratch(hipStream_t stream, int* rc) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+        *rc = e != hipSuccess ? -(int)e : MI355MOE_ELIMIT;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            *rc = e != hipSuccess ? -(int)e : -1;
+            return nullptr;
+        }
+        g_noalloc_ptr[dev] = p;
+    }
+    if (!g_noalloc_zeroed[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) {
+            *rc = -(int)e;
+            return nullptr;
+        }
+        hipLaunchKernelGGL(zero_control_kernel, dim3(1), dim3(64), 0, stream,
+                           static_cast<unsigned*>(g_noalloc_ptr[dev]), (int)(WS_CONTROL_BYTES / sizeof(unsigned)));
+        e = hipGetLastError();
+        if (e != hipSuccess) {
+            *rc = -(int)e;
+            return nullptr;
+        }
+        if (cs == hipStreamCaptureStatusNone) g_noalloc_zeroed[dev] = true;
+    }
+    return g_noalloc_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi355moe_moe_layer_noalloc(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                               int64_t T, const void* router_w, const float* logits, int64_t E, const float* bias,
+                               int64_t topk, float routed_scale, int renormalize, float limit, void* out,
+                               int out_dtype, int64_t out_stride, int32_t* ids_out, float* weights_out,
+                               hipStream_t stream) {
+    if (int r = layer_shape_ok(layer)) return r;
+    if (!x || !out || (!router_w) == (!logits)) return MI355MOE_EINVAL;
+    if (E < 1 || E > 1024 || topk < 1 || topk > MAX_TOPK || topk > E || T < 0) return MI355MOE_ELIMIT;
+    if (T * topk > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (T == 0) return 0;
+    const int64_t need = mi355moe_moe_layer_workspace_bytes(layer, T, topk, E);
+    if (need < 0) return MI355MOE_ESHAPE;
+    if (need > (int64_t)MI355MOE_NOALLOC_SCRATCH_BYTES) return MI355MOE_ESCRATCH;
+    int rc = 0;
+    void* ws = noalloc_scratch(stream, &rc);
+    if (!ws) return rc;
+    return mi355moe_moe_layer(layer, x, x_dtype, x_stride, T, router_w, logits, E, bias, topk, routed_scale,
+                              renormalize, limit, out, out_dtype, out_stride, ids_out, weights_out, ws,
+                              (size_t)MI355MOE_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int64_t mi355moe_exl3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t P) {

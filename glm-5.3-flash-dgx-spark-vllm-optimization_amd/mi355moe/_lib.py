@@ -17,6 +17,8 @@ STAGE_ROUTE, STAGE_GATEUP, STAGE_DOWN, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 8, 15
 PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
 LAYER_SHARED_W13_SUH = 1
 PREFILL_MIN_PAIRS = 4096
+NOALLOC_SCRATCH_BYTES = 32 << 20
+ESCRATCH = 7
 
 _c_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -75,6 +77,8 @@ _SIGS = {
     "mi355moe_moe_layer_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64, _i64, _i64]),
     "mi355moe_moe_layer": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _c_p, _i64, _c_p, _i64,
                                   _f, _int, _f, _c_p, _int, _i64, _c_p, _c_p, _c_p, _sz, _c_p]),
+    "mi355moe_moe_layer_noalloc": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _c_p, _i64,
+                                          _c_p, _i64, _f, _int, _f, _c_p, _int, _i64, _c_p, _c_p, _c_p]),
     "mi355moe_fp8_quant_rows": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _c_p]),
     "mi355moe_fp8_moe_workspace_bytes": (_i64, [ctypes.POINTER(Fp8LayerDesc), _i64, _i64]),
     "mi355moe_fp8_moe_forward_ids": (_int, [ctypes.POINTER(Fp8LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int, _c_p,

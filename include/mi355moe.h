@@ -36,7 +36,8 @@ enum {
     MI355MOE_ELIMIT = 3,       /* beyond a documented limit (pairs, experts, topk) */
     MI355MOE_EWORKSPACE = 4,   /* workspace too small */
     MI355MOE_EDTYPE = 5,       /* unsupported dtype code */
-    MI355MOE_EUNSUPPORTED = 6  /* a format variant this library does not implement (e.g. bits != 4) */
+    MI355MOE_EUNSUPPORTED = 6, /* a format variant this library does not implement (e.g. bits != 4) */
+    MI355MOE_ESCRATCH = 7      /* needs more than the fixed scratch of mi355moe_moe_layer_noalloc */
 };
 
 /* dtype codes */
@@ -165,6 +166,22 @@ int mi355moe_moe_layer(const mi355moe_exl3_layer* layer, const void* x, int x_dt
                        float routed_scale, int renormalize, float limit, void* out, int out_dtype, int64_t out_stride,
                        int32_t* ids_out, float* weights_out, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
+
+/* mi355moe_moe_layer without a workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation); it has no counterpart in the reference.
+ * The scratch is a fixed array of MI355MOE_NOALLOC_SCRATCH_BYTES in the library's device memory, one per GPU, held
+ * until the process ends: enough for decode-size calls (T <= 64 tokens at top-8 with hidden 4096, intermediate 1024
+ * and E <= 1024 router experts; mi355moe_moe_layer_workspace_bytes says what a shape needs). Larger calls return
+ * MI355MOE_ESCRATCH before anything is enqueued. The call allocates nothing (no hipMalloc, no library allocation);
+ * the first call on a GPU looks the array up and zeroes its control block on `stream`. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (concurrent streams, or concurrently replayed graphs) race. The
+ * results equal mi355moe_moe_layer's bit for bit. */
+#define MI355MOE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int mi355moe_moe_layer_noalloc(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                               int64_t T, const void* router_w, const float* logits, int64_t E, const float* bias,
+                               int64_t topk, float routed_scale, int renormalize, float limit, void* out,
+                               int out_dtype, int64_t out_stride, int32_t* ids_out, float* weights_out,
+                               hipStream_t stream);
 
 /* ---------------------------------------------------------------- e4m3 expert variant */
 
