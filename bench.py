@@ -92,6 +92,60 @@ def cpu_baseline(torch, layer, x, ids, wts, threads, min_seconds=10.0):
     return el / reps, reps, len(used)
 
 
+def _sample_pairs(ids, wts, n_tok):
+    """The first n_tok tokens' routing as (used experts, local ids [n_tok, topk], weights) with the experts renumbered
+    0..len(used)-1 in id order."""
+    import numpy as np
+    ids_np = ids[:n_tok].cpu().numpy()
+    used = np.unique(ids_np[ids_np >= 0])
+    remap = {int(e): i for i, e in enumerate(used)}
+    local = np.vectorize(lambda e: remap.get(int(e), len(used)))(ids_np)
+    return used, local, wts[:n_tok].cpu().numpy()
+
+
+def cpu_baseline_prefill(torch, layer, x, ids, wts, threads, n_tok=512):
+    """The oracle's C port (E3 rounding points, OpenMP) on a reduced sample of the prefill workload: its first n_tok
+    tokens with their routing. At n_tok = 512 (4,096 pairs) every one of the 288 experts is routed, so each is decoded
+    once, as in the full T=8192 call; tokens/s of the sample is therefore a lower bound on the full call's (the decode
+    is amortised over 16x fewer tokens)."""
+    from oracle import moe
+    used, local, w = _sample_pairs(ids, wts, n_tok)
+    sel = torch.as_tensor(used, dtype=torch.long, device=layer.device)
+    lay = {k: getattr(layer, k).index_select(0, sel).cpu().numpy() for k in
+           ("w13_trellis", "w13_suh", "w13_svh", "w2_trellis", "w2_suh", "w2_svh")}
+    tok, ex, w16 = moe.pairs_from_routing(local, w, len(used), local.shape[1])
+    x16 = x[:n_tok].to(torch.float16).cpu().numpy()
+    moe.lib()
+    t0 = time.perf_counter()
+    moe.forward(lay, x16, tok, ex, w16, LIMIT, "e3", threads=threads)
+    sec = time.perf_counter() - t0
+    return {"value": round(n_tok / sec, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "seconds": round(sec, 3),
+            "sample": f"first {n_tok} tokens of the T=8192 prefill call ({len(used)} distinct experts, each decoded "
+                      "once) through the oracle's C port (oracle/csrc/oracle.c, E3 rounding points, OpenMP "
+                      f"{threads} threads); a lower bound on the full call's tokens/s"}
+
+
+def cpu_baseline_fp8(torch, layer, x, ids, wts, threads, n_tok=256):
+    """The oracle's C port of the block-scaled e4m3 layer (weights dequantised per 128x128 block, fp32 sums) on the
+    first n_tok tokens of the e4m3 workload with their routing (at 256 tokens all 288 experts are routed)."""
+    from oracle import e4m3
+    used, local, w = _sample_pairs(ids, wts, n_tok)
+    sel = torch.as_tensor(used, dtype=torch.long, device=layer.w13.device)
+    lay = {"w13": layer.w13.index_select(0, sel).cpu().numpy(), "w13_scale": layer.w13_scale.index_select(0, sel).cpu().numpy(),
+           "w2": layer.w2.index_select(0, sel).cpu().numpy(), "w2_scale": layer.w2_scale.index_select(0, sel).cpu().numpy()}
+    tok, ex, pw = e4m3.pairs_fp32(local, w, len(used))
+    xs = x[:n_tok].float().cpu().numpy()
+    t0 = time.perf_counter()
+    e4m3.forward(lay, xs, tok, ex, pw, LIMIT, "kernel", threads=threads)
+    sec = time.perf_counter() - t0
+    return {"value": round(n_tok / sec, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "seconds": round(sec, 3),
+            "sample": f"first {n_tok} tokens of the T=2048 e4m3 call ({len(used)} distinct experts) through the oracle's "
+                      "C port (oracle/csrc/fp8.c: dequantise-then-fp32 GEMM per 128-block, OpenMP "
+                      f"{threads} threads)"}
+
+
 def run_decode(args, torch, mi355moe, dev):
     from mi355moe import _lib, ops, synthetic
     T = args.tokens
@@ -277,7 +331,11 @@ def run_prefill(args, torch, dev):
     P = sum(pairs) / len(pairs)
     flops = 2.0 * P * (K * 2 * N + N * K)
     gu_flops = 2.0 * P * K * 2 * N
-    return {"prefill_tokens_per_s": round(T / (ms / 1000.0), 1), "prefill_ms_per_layer": round(ms, 4),
+    extra = {}
+    if not args.no_cpu_baseline:
+        extra["cpu_baseline_prefill"] = cpu_baseline_prefill(torch, layers[0], x, info[0][0], info[0][1],
+                                                             min(16, os.cpu_count() or 1))
+    return {**extra, "prefill_tokens_per_s": round(T / (ms / 1000.0), 1), "prefill_ms_per_layer": round(ms, 4),
             "prefill_tflops": round(flops / (ms / 1000.0) / 1e12, 2),
             "roofline_prefill": {"bound": "mfma", "kernel": "pf_gateup_kernel (includes the gather launch)",
                                  "achieved": round(gu_flops / (gu_ms / 1000.0) / 1e12, 2),
@@ -342,7 +400,11 @@ def run_fp8(args, torch, dev):
     layer_bytes = D * (3 * K * N + scales) + T * K * 2 * 2
     gu_bytes = D * (2 * K * N + 4 * 2 * (K // 128) * (N // 128))
     P = T * TOPK
-    return {"fp8_tokens_per_s": round(T / (ms / 1000.0), 1), "fp8_ms_per_layer": round(ms, 4),
+    extra = {}
+    if not args.no_cpu_baseline:
+        extra["cpu_baseline_fp8"] = cpu_baseline_fp8(torch, layers[0], x, info[0][0], info[0][1],
+                                                     min(16, os.cpu_count() or 1))
+    return {**extra, "fp8_tokens_per_s": round(T / (ms / 1000.0), 1), "fp8_ms_per_layer": round(ms, 4),
             "fp8_gbs": round(layer_bytes / (ms / 1000.0) / 1e9, 1),
             "fp8_tflops": round(2.0 * P * 3 * K * N / (ms / 1000.0) / 1e12, 2),
             "fp8_distinct_experts": D,
@@ -449,7 +511,26 @@ def run_stack(args, torch, dev):
     ms = e0.elapsed_time(e1) / reps
     nbytes = sum(d * (EXPERT_TRELLIS + EXPERT_SCALES) for d in distinct) + nl * (E * K * 2 + E * 4 + 3 * T * K * 2)
     gbs = nbytes / (ms / 1000.0) / 1e9
-    return {"stack_us_per_layer": round(ms * 1000.0 / nl, 2), "stack_ms_per_replay": round(ms, 4),
+    # the dominant kernel (the grouped gate/up GEMV) alone, every layer once with its own routing: route staged
+    # untimed, the gate/up launch bracketed by HIP events on its stream
+    from mi355moe import _lib
+    gu, gu_bytes = [], 0
+    for l in range(nl):
+        ops.moe_forward_ids(layers[l], xs[l], ids[l], wts[l], limit=LIMIT, out=outs[l], stages=_lib.STAGE_ROUTE)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(HOLD_CYCLES)
+        a.record()
+        ops.moe_forward_ids(layers[l], xs[l], ids[l], wts[l], limit=LIMIT, out=outs[l], stages=_lib.STAGE_GATEUP)
+        b.record()
+        gu.append((a, b))
+        gu_bytes += distinct[l] * (2 * K * N // 2 + 2 * (2 * K + 3 * N)) + T * K * 2
+    torch.cuda.synchronize()
+    gu_us = sum(a.elapsed_time(b) for a, b in gu) * 1000.0 / nl
+    gu_gbs = gu_bytes / nl / (gu_us * 1e-6) / 1e9
+    return {"roofline_stack": {"bound": "hbm", "kernel": "dec_gateup_kernel", "achieved": round(gu_gbs, 1),
+                               "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                               "avg_launch_us": round(gu_us, 2)},
+            "stack_us_per_layer": round(ms * 1000.0 / nl, 2), "stack_ms_per_replay": round(ms, 4),
             "stack_gbs": round(gbs, 1), "stack_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
             "stack_distinct_mean": round(sum(distinct) / nl, 2),
             "stack_config": f"{nl}-layer stacked decode, T={T}, {E} EXL3 experts per layer "

@@ -669,6 +669,259 @@ int mi355moe_moe_layer(const mi355moe_exl3_layer* layer, const void* x, int x_dt
                                        MI355MOE_PATH_AUTO, MI355MOE_STAGE_ALL, stream);
 }
 
+// ---------------------------------------------------------------------------------------------- stage entries over
+// caller-built row tables: the grouped (E3) trio and the e4m3 extension's stages
+
+int64_t mi355moe_e3_tile_rows(void) { return PREFILL_TM; }
+
+int mi355moe_e3_gather(const void* x, int x_dtype, int64_t x_stride, int64_t tokens, int64_t K,
+                       const int64_t* row_token, const int32_t* row_expert, int64_t rows_cap, int64_t n,
+                       const int64_t* suh_table, void* h13, const int32_t* num_rows, hipStream_t stream) {
+    if (!x || !row_token || !row_expert || !suh_table || !h13 || !num_rows) return MI355MOE_EINVAL;
+    if (dt_act(x_dtype) < 0) return MI355MOE_EDTYPE;
+    if (K < 256 || K % 256 || K > 8192 || x_stride < K || x_stride % 2 || tokens < 0) return MI355MOE_ESHAPE;
+    if (rows_cap < 0 || rows_cap > MAX_PAIRS || n < 1 || n > MAX_EXPERTS) return MI355MOE_ELIMIT;
+    if (rows_cap == 0 || tokens == 0) return 0;
+    PrefillArgs a;
+    memset(&a, 0, sizeof(a));
+    a.wt.g_suh = suh_table;
+    a.n = (int)n;
+    a.K = (int)K;
+    a.P = (int)rows_cap;
+    a.T = (int)tokens;
+    a.x = x;
+    a.xdt = dt_act(x_dtype);
+    a.x_stride = x_stride;
+    a.pe = row_expert;
+    a.tok64 = row_token;
+    a.nrows = num_rows;
+    a.h13 = static_cast<uint16_t*>(h13);
+    return rc_launch(launch_prefill(a, stream, 1));
+}
+
+int mi355moe_e3_gateup(const void* h13, int64_t rows_cap, int64_t K, int64_t N, int64_t n,
+                       const int64_t* gate_trellis, const int64_t* up_trellis, const int64_t* gate_svh,
+                       const int64_t* up_svh, const int64_t* down_suh, void* h2, const int32_t* seg_expert,
+                       const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap, const int32_t* num_segs,
+                       float act_limit, hipStream_t stream) {
+    if (!h13 || !gate_trellis || !up_trellis || !gate_svh || !up_svh || !down_suh || !h2 || !seg_expert ||
+        !seg_row0 || !seg_rows || !num_segs)
+        return MI355MOE_EINVAL;
+    if (K < 256 || K % 256 || N < 128 || N % 128) return MI355MOE_ESHAPE;
+    if (rows_cap < 0 || rows_cap > MAX_PAIRS || n < 1 || n > MAX_EXPERTS || seg_cap < 0 || seg_cap > 65535)
+        return MI355MOE_ELIMIT;
+    if (rows_cap == 0 || seg_cap == 0) return 0;
+    PrefillArgs a;
+    memset(&a, 0, sizeof(a));
+    a.wt.g_tr = gate_trellis;
+    a.wt.u_tr = up_trellis;
+    a.wt.g_svh = gate_svh;
+    a.wt.u_svh = up_svh;
+    a.wt.d_suh = down_suh;
+    a.n = (int)n;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.P = (int)rows_cap;
+    a.seg_expert = seg_expert;
+    a.seg_row0 = seg_row0;
+    a.seg_rows = seg_rows;
+    a.nseg = num_segs;
+    a.S_cap = (int)seg_cap;
+    a.limit = act_limit;
+    a.h13 = const_cast<uint16_t*>(static_cast<const uint16_t*>(h13));
+    a.h2 = static_cast<uint16_t*>(h2);
+    return rc_launch(launch_prefill(a, stream, 2));
+}
+
+namespace {
+// Workspace of the row-table down stages: row experts [rows], raw down accumulators [rows][K], token row counts
+// [tokens] and lists [tokens][PF_ROWS_PER_TOKEN]; with e4m3 also the fp32 down inputs [rows][N], their row maxima
+// [rows], their e4m3 values [rows][N] (fp16) and row scales [rows].
+struct RowsWs {
+    int* pe;
+    float* contrib;
+    int* cnt;
+    int2* list;
+    float* vd;
+    unsigned* amaxd;
+    uint16_t* h2;
+    float* dsc;
+    size_t bytes;
+};
+RowsWs carve_rows(void* ws, int64_t rows, int64_t K, int64_t N, int64_t tokens, bool e4m3) {
+    Carve c(ws);
+    RowsWs w;
+    memset(&w, 0, sizeof(w));
+    w.pe = c.take<int>(std::max<int64_t>(1, rows));
+    w.contrib = c.take<float>((size_t)std::max<int64_t>(1, rows) * K);
+    w.cnt = c.take<int>(std::max<int64_t>(1, tokens));
+    w.list = c.take<int2>((size_t)std::max<int64_t>(1, tokens) * PF_ROWS_PER_TOKEN);
+    if (e4m3) {
+        w.vd = c.take<float>((size_t)std::max<int64_t>(1, rows) * N);
+        w.amaxd = c.take<unsigned>(std::max<int64_t>(1, rows));
+        w.h2 = c.take<uint16_t>((size_t)std::max<int64_t>(1, rows) * N);
+        w.dsc = c.take<float>(std::max<int64_t>(1, rows));
+    }
+    w.bytes = c.off;
+    return w;
+}
+}  // namespace
+
+int64_t mi355moe_e3_down_workspace_bytes(int64_t rows_cap, int64_t K, int64_t tokens) {
+    if (rows_cap < 0 || K < 0 || tokens < 0) return -1;
+    return (int64_t)carve_rows(nullptr, rows_cap, K, 0, tokens, false).bytes;
+}
+
+int mi355moe_e3_down(const void* h2, int64_t rows_cap, int64_t K, int64_t N, int64_t n, const int64_t* down_trellis,
+                     const int64_t* down_svh, float* out, int64_t tokens, int64_t out_stride,
+                     const int64_t* row_token, const void* row_weight, const int32_t* seg_expert,
+                     const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap, const int32_t* num_segs,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!h2 || !down_trellis || !down_svh || !out || !row_token || !row_weight || !seg_expert || !seg_row0 ||
+        !seg_rows || !num_segs || !workspace)
+        return MI355MOE_EINVAL;
+    if (K < 256 || K % 256 || N < 128 || N % 128 || out_stride < K) return MI355MOE_ESHAPE;
+    if (rows_cap < 0 || rows_cap > MAX_PAIRS || n < 1 || n > MAX_EXPERTS || seg_cap < 0 || seg_cap > 65535 ||
+        tokens < 0 || tokens > (1 << 24))
+        return MI355MOE_ELIMIT;
+    if (rows_cap == 0 || seg_cap == 0 || tokens == 0) return 0;
+    const RowsWs w = carve_rows(workspace, rows_cap, K, N, tokens, false);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    PrefillArgs a;
+    memset(&a, 0, sizeof(a));
+    a.wt.d_tr = down_trellis;
+    a.wt.d_svh = down_svh;
+    a.n = (int)n;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.P = (int)rows_cap;
+    a.T = (int)tokens;
+    a.seg_expert = seg_expert;
+    a.seg_row0 = seg_row0;
+    a.seg_rows = seg_rows;
+    a.nseg = num_segs;
+    a.S_cap = (int)seg_cap;
+    a.h2 = const_cast<uint16_t*>(static_cast<const uint16_t*>(h2));
+    a.pe = w.pe;
+    a.contrib = w.contrib;
+    a.w16 = static_cast<const uint16_t*>(row_weight);
+    a.out = out;
+    a.odt = DT_F32;
+    a.out_stride = out_stride;
+    return rc_launch(launch_prefill_rows_down(a, row_token, (int)tokens, w.cnt, w.list, stream));
+}
+
+int64_t mi355moe_e4m3_tile_rows(void) { return PREFILL_TM; }
+
+int mi355moe_e4m3_seg_tables(const int64_t* counts, int64_t n, int64_t tile, int64_t rows_cap, int32_t* seg_expert,
+                             int32_t* seg_row0, int32_t* seg_rows, int64_t max_segs, int32_t* num_segs,
+                             int32_t* num_rows, hipStream_t stream) {
+    if (!counts || !seg_expert || !seg_row0 || !seg_rows || !num_segs || !num_rows) return MI355MOE_EINVAL;
+    if (n < 1 || n > MAX_EXPERTS || tile < 16 || tile > 4096 || rows_cap < 0 || rows_cap > MAX_PAIRS)
+        return MI355MOE_ELIMIT;
+    if (max_segs < (rows_cap + tile - 1) / tile + n) return MI355MOE_ESHAPE;
+    return rc_launch(launch_seg_tables(counts, (int)n, (int)tile, (int)std::min<int64_t>(max_segs, 1 << 30), seg_expert,
+                                       seg_row0, seg_rows, num_segs, num_rows, stream));
+}
+
+int mi355moe_e4m3_gather2(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, const int32_t* local,
+                          const int32_t* pos, int64_t topk, int64_t n, const int64_t* gate_suh, void* a_rows,
+                          float* asc, void* out, int out_dtype, int64_t out_stride, hipStream_t stream) {
+    if (!x || !local || !pos || !gate_suh || !a_rows || !asc) return MI355MOE_EINVAL;
+    if (dt_act(x_dtype) < 0) return MI355MOE_EDTYPE;
+    if (out && out_dtype != MI355MOE_F32 && out_dtype != MI355MOE_BF16) return MI355MOE_EDTYPE;
+    if (K < 256 || K % 256 || K > 4096 || x_stride < K || x_stride % 2 || (out && out_stride < K))
+        return MI355MOE_ESHAPE;
+    if (T < 0 || topk < 1 || topk > MAX_TOPK || T * topk > MAX_PAIRS || n < 1 || n > MAX_EXPERTS)
+        return MI355MOE_ELIMIT;
+    if (T == 0) return 0;
+    PrefillArgs a;
+    memset(&a, 0, sizeof(a));
+    a.wt.g_suh = gate_suh;
+    a.n = (int)n;
+    a.K = (int)K;
+    a.P = (int)(T * topk);
+    a.T = (int)T;
+    a.topk = (int)topk;
+    a.x = x;
+    a.xdt = dt_act(x_dtype);
+    a.x_stride = x_stride;
+    a.pair_local = local;
+    a.pair_pos = pos;
+    a.h13 = static_cast<uint16_t*>(a_rows);
+    a.asc = asc;
+    a.e4m3 = 1;
+    if (out) {
+        PrefillArgs z = a;
+        z.out = out;
+        z.odt = dt_w(out_dtype);
+        z.out_stride = out_stride;
+        if (int rc = launch_zero_out(z, stream)) return rc_launch(rc);
+    }
+    return rc_launch(launch_prefill(a, stream, 1));
+}
+
+int64_t mi355moe_e4m3_fused_workspace_bytes(int64_t rows_cap, int64_t K, int64_t N, int64_t tokens) {
+    if (rows_cap < 0 || K < 0 || N < 0 || tokens < 0) return -1;
+    return (int64_t)carve_rows(nullptr, rows_cap, K, N, tokens, true).bytes;
+}
+
+int mi355moe_e4m3_fused(const void* a_rows, const float* asc, void* out, int out_dtype, int64_t tokens,
+                        int64_t out_stride, int64_t K, int64_t N, int64_t n, const int64_t* gate_trellis,
+                        const int64_t* up_trellis, const int64_t* gate_svh, const int64_t* up_svh,
+                        const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                        const int64_t* row_token, const float* row_weight, int64_t rows_cap,
+                        const int32_t* seg_expert, const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap,
+                        const int32_t* num_segs, float limit, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+    if (!a_rows || !asc || !out || !gate_trellis || !up_trellis || !gate_svh || !up_svh || !down_trellis ||
+        !down_suh || !down_svh || !row_token || !row_weight || !seg_expert || !seg_row0 || !seg_rows || !num_segs ||
+        !workspace)
+        return MI355MOE_EINVAL;
+    if (out_dtype != MI355MOE_F32 && out_dtype != MI355MOE_BF16) return MI355MOE_EDTYPE;
+    if (K < 256 || K % 256 || K > 4096 || N < 128 || N % 128 || out_stride < K) return MI355MOE_ESHAPE;
+    if (rows_cap < 0 || rows_cap > MAX_PAIRS || n < 1 || n > MAX_EXPERTS || seg_cap < 0 || seg_cap > 65535 ||
+        tokens < 0 || tokens > (1 << 24))
+        return MI355MOE_ELIMIT;
+    if (rows_cap == 0 || seg_cap == 0 || tokens == 0) return 0;
+    const RowsWs w = carve_rows(workspace, rows_cap, K, N, tokens, true);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    PrefillArgs a;
+    memset(&a, 0, sizeof(a));
+    a.wt.g_tr = gate_trellis;
+    a.wt.u_tr = up_trellis;
+    a.wt.g_svh = gate_svh;
+    a.wt.u_svh = up_svh;
+    a.wt.d_tr = down_trellis;
+    a.wt.d_suh = down_suh;
+    a.wt.d_svh = down_svh;
+    a.n = (int)n;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.P = (int)rows_cap;
+    a.T = (int)tokens;
+    a.seg_expert = seg_expert;
+    a.seg_row0 = seg_row0;
+    a.seg_rows = seg_rows;
+    a.nseg = num_segs;
+    a.S_cap = (int)seg_cap;
+    a.limit = limit;
+    a.h13 = const_cast<uint16_t*>(static_cast<const uint16_t*>(a_rows));
+    a.h2 = w.h2;
+    a.pe = w.pe;
+    a.contrib = w.contrib;
+    a.e4m3 = 1;
+    a.asc = const_cast<float*>(asc);
+    a.dsc = w.dsc;
+    a.vd = w.vd;
+    a.amaxd = w.amaxd;
+    a.w32 = row_weight;
+    a.out = out;
+    a.odt = dt_w(out_dtype);
+    a.out_stride = out_stride;
+    return rc_launch(launch_prefill_rows_down(a, row_token, (int)tokens, w.cnt, w.list, stream));
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------------------------- allocation-free layer

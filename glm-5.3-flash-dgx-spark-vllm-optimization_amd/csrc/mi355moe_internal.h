@@ -119,11 +119,27 @@ struct PrefillArgs {
     float* vd;              // [P][N] fp32 down inputs before their quantization
     unsigned* amaxd;        // [P] row maxima of |vd| (float bits)
     const float* w32;       // [P] fp32 router weights for the combine (nullptr: the fp16 w16)
+    // gathers over caller-built tables (the stage entries): work item i is row i with token tok64[i] (instead of
+    // tok) for i < nrows[0] (device count; nullptr: all P), or, with pair_pos, routed pair i = (token i / topk, slot
+    // i % topk) with local expert pair_local[i] (>= n or < 0: skipped) written to row pair_pos[i]
+    const int64_t* tok64;
+    const int* nrows;
+    const int* pair_local;
+    const int* pair_pos;
 };
 constexpr int PREFILL_TM = 256;
+constexpr int PF_ROWS_PER_TOKEN = 32;   // rows of one token the row-table combine handles (topk <= 32)
 
 // kernels: bit 0 gather, bit 1 gate/up, bit 2 down, bit 3 slot-order combine into the output dtype
 int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels);
+// The down half over caller-built row tables (rows a.P = rows_cap, segments a.seg_*/a.nseg): row experts from the
+// segments into a.pe, (e4m3: the gate/up GEMM too, then the down-input quantization,) the down GEMM, then every
+// token's rows (row_token) summed in row order and ADDED to out (fp32 or bf16 [tokens][K], row stride a.out_stride);
+// router weights a.w32 (fp32) or a.w16 (fp16) per row. cnt [tokens] and list [tokens][PF_ROWS_PER_TOKEN] are scratch.
+int launch_prefill_rows_down(const PrefillArgs& a, const int64_t* row_token, int tokens, int* cnt, int2* list,
+                             hipStream_t st);
+// out[t][0 .. K) = 0 for t < a.T (a.out, a.odt F32 or BF16, a.out_stride)
+int launch_zero_out(const PrefillArgs& a, hipStream_t st);
 int prefill_setup();
 
 // The block-scaled e4m3 expert path: per-token e4m3 activations, grouped fp8 MFMA GEMMs over 64-row segments.
@@ -167,6 +183,9 @@ int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w,
 int launch_router_topk(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
                        int32_t* ids, float* wts, hipStream_t st);
 int launch_route(const RouteArgs& a, hipStream_t st);
+// segment tables of rows grouped by expert from int64 counts [n] (n <= 4096), ceil(count / tile) segments each
+int launch_seg_tables(const int64_t* counts, int n, int tile, int max_segs, int* se, int* sr0, int* sr, int* ns,
+                      int* nr, hipStream_t st);
 // top-k of T tokens' logits and the permutation of the picks in one workgroup (P <= ROUTE_SMALL_MAX_P, a.ids = ids)
 int launch_topk_route(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
                       int32_t* ids, float* wts, const RouteArgs& a, hipStream_t st);

@@ -58,6 +58,34 @@ __device__ __forceinline__ void pf_store_group(_Float16* grp, const uint32_t (&w
 
 // ------------------------------------------------------------------------------------------------ gather
 
+// Work item i of a gather: the row it writes, the token it reads and the expert whose suh it applies; false when the
+// item is skipped (see PrefillArgs: sorted positions with pe/tok, caller row tables with tok64, or routed pairs).
+__device__ __forceinline__ bool pf_gather_item(const PrefillArgs& a, int i, int& pos, int& tok, int& e) {
+    if (a.pair_pos) {
+        e = a.pair_local[i];
+        if (e < 0 || e >= a.n) return false;
+        pos = a.pair_pos[i];
+        if (pos < 0 || pos >= a.P) return false;                      // (caller-built tables)
+        tok = i / a.topk;
+        return true;
+    }
+    e = a.pe[i];
+    if (e < 0 || e >= a.n) return false;
+    pos = i;
+    if (a.tok64) {
+        const int64_t t = a.tok64[i];
+        if (t < 0 || t >= a.T) return false;                         // (caller-built tables)
+        tok = (int)t;
+    } else {
+        tok = a.tok[i];
+    }
+    return true;
+}
+// Number of work items of a gather (a device row count caps the caller's row tables).
+__device__ __forceinline__ int pf_gather_items(const PrefillArgs& a) {
+    return a.nrows ? min(a.P, __builtin_amdgcn_readfirstlane(a.nrows[0])) : a.P;
+}
+
 // h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0. One wave per row
 // (grid-stride): a pass rotates four 128-blocks at once (16 lanes per block, lane c holding elements 8c .. 8c + 7,
 // DPP Hadamard); the loads of all passes of the row are issued before the first rotation.
@@ -68,10 +96,11 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
     const int nb = a.K >> 7;
     const bool vec = ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.x_stride * 2)) & 15) == 0;
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
-    for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
-        const int e = a.pe[pos];
-        if (e < 0) continue;                                          // uniform: one row per wave
-        const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)a.tok[pos] * a.x_stride + 8 * c;
+    const int items = pf_gather_items(a);
+    for (int it = wave; it < items; it += gridDim.x * 4) {
+        int pos, tk, e;
+        if (!pf_gather_item(a, it, pos, tk, e)) continue;             // uniform: one row per wave
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)tk * a.x_stride + 8 * c;
         const uint16_t* sr = reinterpret_cast<const uint16_t*>(a.wt.g_suh[e]) + 8 * c;
         _Float16* dst0 = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + 16 * (c >> 1);
         for (int b0 = 0; b0 < nb; b0 += 4 * PF_GATHER_PASSES) {
@@ -159,10 +188,11 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
     const int nb = a.K >> 7;
     const bool vec = ((reinterpret_cast<uintptr_t>(a.x) | ((uintptr_t)a.x_stride * 2)) & 15) == 0;
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
-    for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
-        const int e = a.pe[pos];
-        if (e < 0) continue;                                          // uniform: one row per wave
-        const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)a.tok[pos] * a.x_stride + 8 * c;
+    const int items = pf_gather_items(a);
+    for (int it = wave; it < items; it += gridDim.x * 4) {
+        int pos, tk, e;
+        if (!pf_gather_item(a, it, pos, tk, e)) continue;             // uniform: one row per wave
+        const uint16_t* xr = reinterpret_cast<const uint16_t*>(a.x) + (size_t)tk * a.x_stride + 8 * c;
         const uint16_t* sr = reinterpret_cast<const uint16_t*>(a.wt.g_suh[e]) + 8 * c;
         u32x4 xv[PF_GATHER_PASSES], sv[PF_GATHER_PASSES];
 #pragma unroll
@@ -221,7 +251,7 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
         }
         if (lane == 0) {
             a.asc[pos] = sc;
-            a.amaxd[pos] = 0u;
+            if (a.amaxd) a.amaxd[pos] = 0u;
         }
     }
 }
@@ -528,7 +558,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     int s, cb;
     pf_tile_of(blockIdx.x, a.N >> 7, s, cb);
     if (s >= a.nseg[0]) return;
-    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
+    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
+    if (rn <= 0 || row0 < 0 || row0 + rn > a.P || e < 0 || e >= a.n) return;   // (caller-built tables)
     const int K = a.K, N = a.N;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     PfTile t;                                                        // waves 0, 1: gate columns; 2, 3: up columns
@@ -639,7 +670,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     int s, cb;
     pf_tile_of(blockIdx.x, a.K >> 8, s, cb);
     if (s >= a.nseg[0]) return;
-    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
+    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
+    if (rn <= 0 || row0 < 0 || row0 + rn > a.P || e < 0 || e >= a.n) return;   // (caller-built tables)
     const int K = a.K, N = a.N;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     PfTile t;
@@ -751,6 +783,143 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------ row-table down
+
+// Rows of caller-built tables: pe[r] = -1 for every row and cnt[t] = 0 for every token, then pe[r] = the expert of the
+// segment covering row r (segments s < nseg[0]); rows no segment covers stay skipped.
+__global__ __launch_bounds__(256) void pf_rows_init_kernel(PrefillArgs a, int* pe, int* cnt, int tokens) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < max(a.P, tokens); i += gridDim.x * 256) {
+        if (i < a.P) {
+            pe[i] = -1;
+            if (a.amaxd) a.amaxd[i] = 0u;
+        }
+        if (i < tokens) cnt[i] = 0;
+    }
+}
+
+// out[t][0 .. K) = 0 for t < T (fp32 or bf16, row stride out_stride): the zero fill of an accumulated output.
+__global__ __launch_bounds__(256) void pf_zero_out_kernel(PrefillArgs a) {
+    const int per = a.K / 8;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < (int64_t)a.T * per; i += (int64_t)gridDim.x * 256) {
+        const int64_t t = i / per, c = 8 * (i % per);
+        if (a.odt == DT_F32) {
+            float* o = reinterpret_cast<float*>(a.out) + t * a.out_stride + c;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = 0.0f;
+        } else {
+            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + t * a.out_stride + c;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = 0;
+        }
+    }
+}
+__global__ __launch_bounds__(256) void pf_seg_rows_kernel(PrefillArgs a, int* pe) {
+    const int s = blockIdx.x;
+    if (s >= a.nseg[0]) return;
+    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PREFILL_TM);
+    if (e < 0 || e >= a.n) return;                                    // (the GEMM kernels skip such segments too)
+    for (int i = threadIdx.x; i < rn; i += 256)
+        if (row0 + i >= 0 && row0 + i < a.P) pe[row0 + i] = e;
+}
+
+// Every computed row r claims a slot of its token's list: list[t][k] = (r, expert) with k from an atomic counter (so
+// the slots come in arbitrary order; the combine puts them in row order). Rows whose token lies outside
+// [0, tokens) are left out.
+__global__ __launch_bounds__(256) void pf_rows_by_token_kernel(PrefillArgs a, const int64_t* row_token, int* cnt,
+                                                               int2* list, int tokens) {
+    for (int r = blockIdx.x * 256 + threadIdx.x; r < a.P; r += gridDim.x * 256) {
+        const int e = a.pe[r];
+        if (e < 0) continue;
+        const int64_t t = row_token[r];
+        if (t < 0 || t >= tokens) continue;
+        const int k = atomicAdd(cnt + t, 1);
+        if (k < PF_ROWS_PER_TOKEN) list[t * PF_ROWS_PER_TOKEN + k] = make_int2(r, e);
+    }
+}
+
+// One wave per (token t, 512 columns): the token's rows (at most PF_ROWS_PER_TOKEN) sorted by row index, then
+// out[t] += sum over them in that order of ((H(acc * dsc) * r) * svh_d) * w (fp32; deterministic, no atomics); out is
+// fp32 or bf16 (then rounded once, after the add). w = w32[r] or the fp16 w16[r].
+__global__ __launch_bounds__(256) void pf_combine_rows_kernel(PrefillArgs a, const int* cnt, const int2* list,
+                                                              int tokens) {
+    __shared__ int2 srt[4][PF_ROWS_PER_TOKEN];
+    const int wv = threadIdx.x >> 6;
+    const int t = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + wv));
+    if (t >= tokens) return;
+    const int lane = threadIdx.x & 63;
+    const int nr = min(cnt[t], PF_ROWS_PER_TOKEN);
+    int2 ent = make_int2(0x7FFFFFFF, 0);
+    if (lane < nr) ent = list[t * PF_ROWS_PER_TOKEN + lane];
+    int rank = 0;
+    for (int j = 0; j < nr; ++j) rank += __builtin_amdgcn_readlane(ent.x, j) < ent.x;
+    if (lane < nr) srt[wv][rank] = ent;
+    __builtin_amdgcn_s_waitcnt(0xc07f);                               // lgkmcnt(0): the wave's LDS writes landed
+    __builtin_amdgcn_wave_barrier();
+    const int col = blockIdx.y * 512 + 128 * (lane >> 4) + 8 * (lane & 15);
+    const bool live = blockIdx.y * 512 + 128 * (lane >> 4) < a.K;
+    const int colc = live ? col : 0;
+    float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < nr; k0 += 8) {
+        const int lk = min(k0 + (lane & 7), max(nr - 1, 0));
+        const int2 sl = srt[wv][lk];
+        const int pl = sl.x, el = sl.y;
+        const int okl = (int)(k0 + (lane & 7) < nr);
+        const float wl = a.w32 ? a.w32[pl] : (float)u16_as_h(a.w16[pl]);
+        const float dl = a.dsc ? a.dsc[pl] : 1.0f;
+        const int64_t svl = a.wt.d_svh[el];
+        f32x4 raw[8][2];
+        u32x4 sv[8];
+        bool ok[8];
+        float w[8], ds[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int pos = __builtin_amdgcn_readlane(pl, k);
+            ok[k] = __builtin_amdgcn_readlane(okl, k) != 0;
+            w[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k));
+            ds[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dl), k));
+            const uint64_t sp = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)svl, k)) |
+                                ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(svl >> 32), k) << 32);
+            const float* rp = a.contrib + (size_t)pos * a.K + colc;
+            raw[k][0] = *reinterpret_cast<const f32x4*>(rp);
+            raw[k][1] = *reinterpret_cast<const f32x4*>(rp + 4);
+            const uint16_t* svp = reinterpret_cast<const uint16_t*>(sp) + colc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[k][i] = *reinterpret_cast<const uint32_t*>(svp + 2 * i);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = raw[k][0][i];
+                v[4 + i] = raw[k][1][i];
+            }
+            if (a.dsc) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] *= ds[k];
+            }
+            fwht128_x16(v, lane);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t s2 = sv[k][i >> 1];
+                const float svf = (float)u16_as_h((i & 1) ? s2 >> 16 : s2 & 0xFFFFu);
+                if (ok[k]) sum[i] += v[i] * HAD_R * svf * w[k];
+            }
+        }
+    }
+    if (!live || nr == 0) return;
+    const size_t o = (size_t)t * a.out_stride + col;
+    if (a.odt == DT_F32) {
+        float* op = reinterpret_cast<float*>(a.out) + o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) op[i] = op[i] + sum[i];
+    } else {
+        uint16_t* op = reinterpret_cast<uint16_t*>(a.out) + o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) op[i] = f32_to_bf16(bf16_to_f32(op[i]) + sum[i]);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ launchers
 
 static bool g_pf_attr = false;
@@ -770,7 +939,8 @@ int prefill_setup() {
 int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
     if (prefill_setup()) return -1;
     const bool f8 = a.e4m3 != 0;
-    if (f8 && (a.K > 4 * 128 * PF_GATHER_PASSES || !a.asc || !a.dsc || !a.vd || !a.amaxd)) return -1;
+    if (f8 && (a.K > 4 * 128 * PF_GATHER_PASSES || !a.asc)) return -1;
+    if (f8 && (kernels & ~1) && (!a.dsc || !a.vd || !a.amaxd)) return -1;    // the gather alone needs only asc
     if (kernels & 1) {
         if (f8) hipLaunchKernelGGL(pf_gather8_kernel, dim3(4096), dim3(256), 0, st, a);
         else hipLaunchKernelGGL(pf_gather_kernel, dim3(4096), dim3(256), 0, st, a);
@@ -790,6 +960,39 @@ int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
         }
     }
     if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3((a.T + 3) / 4, (a.K + 511) / 512), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_zero_out(const PrefillArgs& a, hipStream_t st) {
+    const int64_t items = (int64_t)a.T * (a.K / 8);
+    if (items > 0)
+        hipLaunchKernelGGL(pf_zero_out_kernel, dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>(4096, (items + 255) / 256))),
+                           dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_prefill_rows_down(const PrefillArgs& a0, const int64_t* row_token, int tokens, int* cnt, int2* list,
+                             hipStream_t st) {
+    if (prefill_setup()) return -1;
+    PrefillArgs a = a0;
+    int* pe = const_cast<int*>(a.pe);
+    const int fill = std::max(1, std::min(2048, (std::max(a.P, tokens) + 255) / 256));
+    hipLaunchKernelGGL(pf_rows_init_kernel, dim3(fill), dim3(256), 0, st, a, pe, cnt, tokens);
+    hipLaunchKernelGGL(pf_seg_rows_kernel, dim3(a.S_cap), dim3(256), 0, st, a, pe);
+    const int sg = (a.S_cap + 7) / 8;
+    const dim3 dn(8 * (a.K / 256) * sg);
+    if (a.e4m3) {
+        // the e4m3 chain: gate/up (fp32 down inputs and their row maxima, which rows_init zeroed), quantization, down
+        hipLaunchKernelGGL(pf_gateup_kernel<true>, dim3(8 * (a.N / 128) * sg), dim3(PF_THREADS), PF_LDS, st, a);
+        hipLaunchKernelGGL(pf_quantd_kernel, dim3(4096), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(pf_down_kernel<true>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+    } else {
+        hipLaunchKernelGGL(pf_down_kernel<false>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+    }
+    hipLaunchKernelGGL(pf_rows_by_token_kernel, dim3(std::max(1, std::min(2048, (a.P + 255) / 256))), dim3(256), 0, st,
+                       a, row_token, cnt, list, tokens);
+    hipLaunchKernelGGL(pf_combine_rows_kernel, dim3((tokens + 3) / 4, (a.K + 511) / 512), dim3(256), 0, st, a, cnt,
+                       list, tokens);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -627,6 +627,41 @@ __global__ __launch_bounds__(1024) void route_counts_kernel(const int64_t* __res
     }
 }
 
+// Segment tables of rows grouped by expert (the e4m3 extension's seg_tables, code/fork/kernels/moe_e4m3.cu:2372-2400
+// and :3066-3083): expert e's rows start at the exclusive scan of counts[0 .. n); every expert with rows gets
+// ceil(count / tile) segments; num_rows = the total. One workgroup; n <= 4096.
+__global__ __launch_bounds__(1024) void seg_tables_kernel(const int64_t* __restrict__ counts64, int n, int tile,
+                                                          int max_segs, int* seg_expert, int* seg_row0, int* seg_rows,
+                                                          int* nseg, int* nrows) {
+    extern __shared__ int sh[];
+    __shared__ int tot[16];
+    int* cnt = sh;
+    int* start = sh + n;
+    int run = 0;
+    for (int base = 0; base < n; base += blockDim.x) {
+        const int e = base + threadIdx.x;
+        const int64_t c64 = e < n ? counts64[e] : 0;
+        const int c = c64 < 0 ? 0 : (c64 > (1 << 24) ? (1 << 24) : (int)c64);
+        int ctot;
+        const int cinc = block_scan_incl(c, tot, ctot);
+        if (e < n) {
+            cnt[e] = c;
+            start[e] = run + cinc - c;
+        }
+        run += ctot;
+    }
+    __syncthreads();
+    build_segments(cnt, start, n, 1 << 30, tile, max_segs, seg_expert, seg_row0, seg_rows, nseg, tot);
+    if (threadIdx.x == 0) nrows[0] = run;
+}
+
+int launch_seg_tables(const int64_t* counts, int n, int tile, int max_segs, int* se, int* sr0, int* sr, int* ns,
+                      int* nr, hipStream_t st) {
+    hipLaunchKernelGGL(seg_tables_kernel, dim3(1), dim3(1024), (size_t)2 * n * sizeof(int), st, counts, n, tile,
+                       max_segs, se, sr0, sr, ns, nr);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // Multi-block permutation for large P: (1) per-block counts, (2) one block scans them into per-block offsets
 // and builds the segments, (3) every block places its pairs (rank inside the block by pair index).
 constexpr int ROUTE_BLK = 1024;

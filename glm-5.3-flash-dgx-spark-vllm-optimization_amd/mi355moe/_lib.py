@@ -79,6 +79,20 @@ _SIGS = {
                                   _f, _int, _f, _c_p, _int, _i64, _c_p, _c_p, _c_p, _sz, _c_p]),
     "mi355moe_moe_layer_noalloc": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _c_p, _i64,
                                           _c_p, _i64, _f, _int, _f, _c_p, _int, _i64, _c_p, _c_p, _c_p]),
+    "mi355moe_e3_tile_rows": (_i64, []),
+    "mi355moe_e3_gather": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p]),
+    "mi355moe_e3_gateup": (_int, [_c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                  _i64, _c_p, _f, _c_p]),
+    "mi355moe_e3_down_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "mi355moe_e3_down": (_int, [_c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p,
+                                _c_p, _i64, _c_p, _c_p, _sz, _c_p]),
+    "mi355moe_e4m3_tile_rows": (_i64, []),
+    "mi355moe_e4m3_seg_tables": (_int, [_c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p]),
+    "mi355moe_e4m3_gather2": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p,
+                                     _int, _i64, _c_p]),
+    "mi355moe_e4m3_fused_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "mi355moe_e4m3_fused": (_int, [_c_p, _c_p, _c_p, _int, _i64, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                   _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _f, _c_p, _sz, _c_p]),
     "mi355moe_fp8_quant_rows": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _c_p]),
     "mi355moe_fp8_moe_workspace_bytes": (_i64, [ctypes.POINTER(Fp8LayerDesc), _i64, _i64]),
     "mi355moe_fp8_moe_forward_ids": (_int, [ctypes.POINTER(Fp8LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int, _c_p,

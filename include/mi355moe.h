@@ -183,6 +183,66 @@ int mi355moe_moe_layer_noalloc(const mi355moe_exl3_layer* layer, const void* x, 
                                int out_dtype, int64_t out_stride, int32_t* ids_out, float* weights_out,
                                hipStream_t stream);
 
+/* ---------------------------------------------------------------- the grouped (E3) trio over row tables */
+
+/* The three stages of the grouped fat-expert tier on caller-built device tables, the contract of
+ * exl3_fat_moe_gather / _gateup / _down (code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cuh:20-56), called by
+ * apply_exl3_grouped_fat (code/fork/docs/prod_exl3_reference.py:1364-1435) with the tables of
+ * build_grouped_fat_tables (:1316-1361): rows grouped by expert in a row buffer of rows_cap rows, row_token int64 /
+ * row_expert int32 / row_weight fp16 per row, segments (seg_expert, seg_row0, seg_rows) of at most
+ * mi355moe_e3_tile_rows() rows each, and the live counts num_rows / num_segs as int32 [1] device words (read by the
+ * kernels, so the host never synchronises). h13 fp16 [rows_cap][K] and h2 fp16 [rows_cap][N] are the stages'
+ * intermediates, in this library's staging order (k permuted within 16-element groups); they are only meant to be
+ * passed from one stage to the next. Numerics: the E3 rounding points (gather fp16(H(fp16(x * suh)) * r); gate/up
+ * with the limit before SiLU; down (H(acc) * r) * svh * w). The down stage ADDS each token's rows to out fp32
+ * [tokens][out_stride] in row order (deterministic, no atomics; at most 32 rows per token); its workspace (size from
+ * mi355moe_e3_down_workspace_bytes) holds the raw accumulators and the token row lists. Rows whose token is outside
+ * [0, tokens) or whose expert is outside [0, n) are skipped; segment entries outside the row buffer are skipped. */
+int64_t mi355moe_e3_tile_rows(void);
+int mi355moe_e3_gather(const void* x, int x_dtype, int64_t x_stride, int64_t tokens, int64_t K,
+                       const int64_t* row_token, const int32_t* row_expert, int64_t rows_cap, int64_t n,
+                       const int64_t* suh_table, void* h13, const int32_t* num_rows, hipStream_t stream);
+int mi355moe_e3_gateup(const void* h13, int64_t rows_cap, int64_t K, int64_t N, int64_t n,
+                       const int64_t* gate_trellis, const int64_t* up_trellis, const int64_t* gate_svh,
+                       const int64_t* up_svh, const int64_t* down_suh, void* h2, const int32_t* seg_expert,
+                       const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap, const int32_t* num_segs,
+                       float act_limit, hipStream_t stream);
+int64_t mi355moe_e3_down_workspace_bytes(int64_t rows_cap, int64_t K, int64_t tokens);
+int mi355moe_e3_down(const void* h2, int64_t rows_cap, int64_t K, int64_t N, int64_t n, const int64_t* down_trellis,
+                     const int64_t* down_svh, float* out, int64_t tokens, int64_t out_stride,
+                     const int64_t* row_token, const void* row_weight, const int32_t* seg_expert,
+                     const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap, const int32_t* num_segs,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------- the e4m3 extension's stages over row tables */
+
+/* The stage contract of the e4m3 extension the overlay's run() drives (code/fork/overlay/glm53_moe_e4m3.py:450-592
+ * -> code/fork/kernels/moe_e4m3.cu seg_tables :3066-3083, gather2 :245-310, fused :2721-2725), trellis-sourced e4m3
+ * numerics as mi355moe_e4m3_moe_forward_ids. seg_tables: segments of at most `tile` rows over the rows grouped by
+ * expert (counts int64 [n], max_segs >= ceil(rows_cap / tile) + n; tile = mi355moe_e4m3_tile_rows() for the fused
+ * stage). gather2: routed pair j = (token j / topk) with local expert local[j] (skipped unless 0 <= local < n) writes
+ * row pos[j] of a_rows (fp16 [T*topk][K]: the e4m3 values of the quantised rotated row, this library's staging
+ * order) and its scale asc[pos[j]]; a non-null out (fp32 or bf16 [T][out_stride]) is zeroed. fused: gate/up, the
+ * down-input quantisation and the down GEMM of every segment's rows, each token's rows (row_token) then ADDED to out
+ * in row order with the fp32 row_weight (deterministic); workspace from mi355moe_e4m3_fused_workspace_bytes. K <= 4096.
+ */
+int64_t mi355moe_e4m3_tile_rows(void);
+int mi355moe_e4m3_seg_tables(const int64_t* counts, int64_t n, int64_t tile, int64_t rows_cap, int32_t* seg_expert,
+                             int32_t* seg_row0, int32_t* seg_rows, int64_t max_segs, int32_t* num_segs,
+                             int32_t* num_rows, hipStream_t stream);
+int mi355moe_e4m3_gather2(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, const int32_t* local,
+                          const int32_t* pos, int64_t topk, int64_t n, const int64_t* gate_suh, void* a_rows,
+                          float* asc, void* out, int out_dtype, int64_t out_stride, hipStream_t stream);
+int64_t mi355moe_e4m3_fused_workspace_bytes(int64_t rows_cap, int64_t K, int64_t N, int64_t tokens);
+int mi355moe_e4m3_fused(const void* a_rows, const float* asc, void* out, int out_dtype, int64_t tokens,
+                        int64_t out_stride, int64_t K, int64_t N, int64_t n, const int64_t* gate_trellis,
+                        const int64_t* up_trellis, const int64_t* gate_svh, const int64_t* up_svh,
+                        const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                        const int64_t* row_token, const float* row_weight, int64_t rows_cap,
+                        const int32_t* seg_expert, const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap,
+                        const int32_t* num_segs, float limit, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
 /* ---------------------------------------------------------------- e4m3 expert variant */
 
 /* One layer of block-scaled e4m3 routed experts in vLLM's fp8 w8a8 block-quantised MoE layout (128x128 blocks):
