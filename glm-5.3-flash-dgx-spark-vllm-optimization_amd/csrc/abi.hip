@@ -48,7 +48,7 @@ struct Carve {
 int shared_flag(const mi355moe_exl3_layer* L) { return (L->flags & MI355MOE_LAYER_SHARED_W13_SUH) ? 1 : 0; }
 
 struct DecodePlan {
-    int rmax, seg, S_cap, sk_gu, sk_dn;
+    int rmax, seg, S_cap, sk_gu, sk_dn, kch_gu, kch_dn;
 };
 
 int pow2ceil(int64_t v) {
@@ -68,18 +68,20 @@ DecodePlan plan_decode(int64_t P, int64_t rows_bound, int64_t n, int64_t K, int6
     const int64_t target = 400;
     int64_t sk = 0;
     for (int64_t c : {1, 2, 4, 8, 16}) {
-        if (K % c || (K / c) % 256 || decode_lds_gateup(d.rmax, (int)K, (int)c, shared_suh) > DECODE_LDS_MAX) continue;
+        if (K % c || (K / c) % 256 || decode_lds_gateup(d.rmax, (int)(K / c), shared_suh) > DECODE_LDS_MAX) continue;
         sk = c;
         if (s_est * (N / 128) * c >= target) break;
     }
     d.sk_gu = (int)std::max<int64_t>(1, sk);
     int64_t nr = N;
     for (int64_t c : {1, 2, 4, 8}) {
-        if (N % c || (N / c) % 128 || decode_lds_down(d.rmax, (int)N, (int)c) > DECODE_LDS_MAX) continue;
+        if (N % c || (N / c) % 128 || decode_lds_down(d.rmax, (int)(N / c)) > DECODE_LDS_MAX) continue;
         nr = N / c;
         if (s_est * ((K + 511) / 512) * c >= target) break;   // 512-column down workgroups
     }
     d.sk_dn = (int)(N / nr);
+    d.kch_gu = (int)(K / d.sk_gu);
+    d.kch_dn = (int)nr;
     return d;
 }
 
@@ -109,12 +111,14 @@ void carve_decode(void* ws, int64_t P, int64_t n, int64_t K, int64_t N, const De
     r.loc = c.take<int>(P);
     r.blk_cnt = c.take<int>(((P + 1023) / 1024) * (n + 1));
     r.cnt_out = c.take<int>(n + 1);
-    d.cnt_gu = c.take<unsigned>((size_t)p.S_cap * (N / 128));
-    d.cnt_dn = c.take<unsigned>((size_t)p.S_cap * (K / 256));
-    r.zero = d.cnt_gu;                                               // both counter arrays, zeroed per call
+    d.cnt_gu = c.take<unsigned long long>((size_t)p.S_cap * (N / 128));
+    d.cnt_dn = c.take<unsigned long long>((size_t)p.S_cap * ((K + 511) / 512));
+    r.zero = reinterpret_cast<unsigned*>(d.cnt_gu);                  // both counter arrays, zeroed per call
     r.zero_words = (int64_t)((c.off - ((char*)d.cnt_gu - c.base)) / sizeof(unsigned));
-    d.zg = c.take<float>((size_t)p.sk_gu * 2 * P * N);
-    d.zd = c.take<float>((size_t)p.sk_dn * P * K);
+    // partial-sum slots: one per chunk of a fragmented tile (none when every tile is one fragment)
+    const int64_t zs_gu = K / p.kch_gu, zs_dn = N / p.kch_dn;
+    d.zg = c.take<float>(zs_gu > 1 ? (size_t)zs_gu * 2 * P * N : 1);
+    d.zd = c.take<float>(zs_dn > 1 ? (size_t)zs_dn * P * K : 1);
     d.xd = c.take<uint16_t>((size_t)P * N);
     d.contrib = with_contrib ? c.take<float>((size_t)P * K) : nullptr;
     w.bytes = c.off;
@@ -434,6 +438,8 @@ static int prep_decode(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     d.S_cap = p.S_cap;
     d.sk_gu = p.sk_gu;
     d.sk_dn = p.sk_dn;
+    d.kch_gu = p.kch_gu;
+    d.kch_dn = p.kch_dn;
     d.shared_suh = shared_flag(layer);
     d.limit = limit;
     d.out = out;
@@ -1069,6 +1075,8 @@ int mi355moe_exl3_moe(const mi355moe_exl3_layer* layer, const void* hidden, int6
     d.S_cap = p.S_cap;
     d.sk_gu = p.sk_gu;
     d.sk_dn = p.sk_dn;
+    d.kch_gu = p.kch_gu;
+    d.kch_dn = p.kch_dn;
     d.shared_suh = shared_flag(layer);
     d.limit = act_limit;
     d.out = out;

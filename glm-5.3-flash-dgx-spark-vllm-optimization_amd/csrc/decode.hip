@@ -256,21 +256,44 @@ constexpr int GU_WAVES = 8;      // gate/up workgroup: 4 column groups of 32 x 2
 constexpr int DN_WAVES = 8;      // down workgroup: 8 column groups of 32 (256 output columns) over the N range
 constexpr int ZS_ROWS = 16;
 
-// grid (N/128, K splits, segments), 512 threads: workgroup = 128 gate and up columns of one segment over one K range
-// (all of K unless small segment counts call for splits); wave (cg, kh) = columns 32cg..32cg+31 over half kh of the
-// range, DEPTH steps of loads in flight. The halves are added in LDS; with one split the epilogue follows directly,
-// with several each split stores its partial and the workgroup that arrives last adds them in split order.
-// The gate/up tile (column block cb, K split ks, segment s) of a 512-thread workgroup; smem: the dynamic LDS.
+// Arrival of a tile fragment of `len` chunks whose partial sums went to slot `slot`: one 64-bit atomic adds len to
+// the tile's chunk count (bits 0-31) and the slot's bit (bits 32-63). Returns true in the workgroup whose fragment
+// completes the tile's `total` chunks, with *mask = the slots of every fragment (every fragment's stores completed
+// before it arrived; the elected workgroup acquires before reading them).
+__device__ __forceinline__ bool arrive_fragment(unsigned long long* c, unsigned len, int slot, unsigned total,
+                                                unsigned* mask, int* flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long add = (unsigned long long)len | (1ull << (32 + slot));
+        const unsigned long long now =
+            __hip_atomic_fetch_add(c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+        *flag = (unsigned)now == total;
+        *mask = (unsigned)(now >> 32);
+    }
+    __syncthreads();
+    if (*flag == 0) return false;
+    acquire_agent();
+    return true;
+}
+
+// 512 threads: workgroup = 128 gate and up columns of one segment over one K range [kc0, kc1) in chunks of kch_gu;
+// wave (cg, kh) = columns 32cg..32cg+31 over half kh of the range, DEPTH steps of loads in flight. The halves are
+// added in LDS; a fragment covering all of K runs the epilogue directly, otherwise it stores its partial in slot
+// `slot` and the fragment that completes the tile adds the slots in order. smem: the dynamic LDS.
 template <int DEPTH, bool SHARED>
-__device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int ks, int s, unsigned char* smem) {
+__device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, int kc0, int kc1, int slot,
+                                            unsigned char* smem) {
     __shared__ int last_flag;
+    __shared__ unsigned slot_mask;
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int cg = wv & 3, kh = wv >> 2;
     const int K = a.K, N = a.N, NT = N >> 4;
-    const int KR = K / a.sk_gu, KH = KR >> 1, kbase = ks * KR, RSH = KR + XPAD;
+    const int KR = (kc1 - kc0) * a.kch_gu, KH = KR >> 1, kbase = kc0 * a.kch_gu, RSH = KR + XPAD;
+    const int KC = K / a.kch_gu;
     constexpr int NMAT = SHARED ? 1 : 2;
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);              // [NMAT][rn][RSH] halves, or
     uint32_t* xw = reinterpret_cast<uint32_t*>(smem);              // [rn][RSD] duplicated (SHARED, rn <= DUP_ROWS)
@@ -439,18 +462,21 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int ks,
     __syncthreads();
 
     const size_t P = a.P;
-    unsigned* cnt = a.cnt_gu + (size_t)s * (N >> 7) + cb;
-    if (a.sk_gu > 1) {
+    unsigned long long* cnt = a.cnt_gu + (size_t)s * (N >> 7) + cb;
+    const bool part = kc1 - kc0 < KC;
+    if (part) {
         for (int i = tid; i < 2 * rn * 128; i += GU_WAVES * 64) {
             const int mat = i / (rn * 128), rem = i - mat * rn * 128, r = rem >> 7, c = rem & 127;
-            st_coherent(a.zg + ((size_t)(ks * 2 + mat) * P + row0 + r) * N + cb * 128 + c,
+            st_coherent(a.zg + ((size_t)(slot * 2 + mat) * P + row0 + r) * N + cb * 128 + c,
                         zs[(mat * ZS_ROWS + r) * 128 + c]);
         }
-        if (!arrive_last(cnt, (unsigned)a.sk_gu, &last_flag)) return;
+        if (!arrive_fragment(cnt, (unsigned)(kc1 - kc0), slot, (unsigned)KC, &slot_mask, &last_flag)) return;
+        const unsigned mask = slot_mask;
         for (int i = tid; i < 2 * rn * 128; i += GU_WAVES * 64) {
             const int mat = i / (rn * 128), rem = i - mat * rn * 128, r = rem >> 7, c = rem & 127;
             float v = 0.f;
-            for (int k = 0; k < a.sk_gu; ++k) v += ld_coherent(a.zg + ((size_t)(k * 2 + mat) * P + row0 + r) * N + cb * 128 + c);
+            for (unsigned m = mask; m; m &= m - 1)                  // the slots in order (the chunks in K order)
+                v += ld_coherent(a.zg + ((size_t)(__builtin_ctz(m) * 2 + mat) * P + row0 + r) * N + cb * 128 + c);
             zs[(mat * ZS_ROWS + r) * 128 + c] = v;
         }
         __syncthreads();
@@ -496,14 +522,15 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int ks,
             *reinterpret_cast<u32x4*>(a.xd + (size_t)(row0 + rr) * N + colb) = o;
         }
     }
-    if (a.sk_gu > 1 && tid == 0) *cnt = 0u;
+    if (part && tid == 0) *cnt = 0ull;
 }
 
 template <int DEPTH, bool SHARED>
 __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_gateup_kernel(
     DecodeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    gateup_tile<DEPTH, SHARED>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+    // grid (N/128, K splits, segments): split ks is chunk ks (kch_gu = K / splits), its partials in slot ks
+    gateup_tile<DEPTH, SHARED>(a, blockIdx.x, blockIdx.z, blockIdx.y, blockIdx.y + 1, blockIdx.y, smem);
 }
 
 // grid (K/512, N splits, segments), 512 threads: workgroup = 512 output columns of one segment over one N range;
@@ -512,14 +539,17 @@ __global__ __launch_bounds__(GU_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4
 constexpr int DN_COLS = 512;
 // The down tile (column block cb, N split ks, segment s) of a 512-thread workgroup; smem: the dynamic LDS.
 template <int DEPTH>
-__device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int ks, int s, unsigned char* smem) {
+__device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int s, int kc0, int kc1, int slot,
+                                          unsigned char* smem) {
     __shared__ int last_flag;
+    __shared__ unsigned slot_mask;
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.K, N = a.N, KT = K >> 4;
-    const int NR = N / a.sk_dn, nbase = ks * NR, RSH = NR + XPAD;
+    const int NR = (kc1 - kc0) * a.kch_dn, nbase = kc0 * a.kch_dn, RSH = NR + XPAD;
+    const int NC = N / a.kch_dn;
     uint32_t* xw = reinterpret_cast<uint32_t*>(smem);              // [rn][RSD] inputs duplicated per n: (x, x)
     const int RSD = NR + 4;
 
@@ -620,20 +650,22 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int ks, i
 
     const size_t P = a.P;
     const int ncol = min(DN_COLS, K - cb * DN_COLS);                // 256 or 512
-    unsigned* cnt = a.cnt_dn + (size_t)s * ((K + DN_COLS - 1) / DN_COLS) + cb;
-    if (a.sk_dn > 1) {
+    unsigned long long* cnt = a.cnt_dn + (size_t)s * ((K + DN_COLS - 1) / DN_COLS) + cb;
+    const bool part = kc1 - kc0 < NC;
+    if (part) {
         for (int i = tid; i < rn * DN_COLS; i += DN_WAVES * 64) {
             const int r = i / DN_COLS, c = i % DN_COLS;
             if (c < ncol)
-                st_coherent(a.zd + ((size_t)ks * P + row0 + r) * K + cb * DN_COLS + c, zs[r * DN_COLS + c]);
+                st_coherent(a.zd + ((size_t)slot * P + row0 + r) * K + cb * DN_COLS + c, zs[r * DN_COLS + c]);
         }
-        if (!arrive_last(cnt, (unsigned)a.sk_dn, &last_flag)) return;
+        if (!arrive_fragment(cnt, (unsigned)(kc1 - kc0), slot, (unsigned)NC, &slot_mask, &last_flag)) return;
+        const unsigned mask = slot_mask;
         for (int i = tid; i < rn * DN_COLS; i += DN_WAVES * 64) {
             const int r = i / DN_COLS, c = i % DN_COLS;
             if (c >= ncol) continue;
             float v = 0.f;
-            for (int k = 0; k < a.sk_dn; ++k)
-                v += ld_coherent(a.zd + ((size_t)k * P + row0 + r) * K + cb * DN_COLS + c);
+            for (unsigned m = mask; m; m &= m - 1)                  // the slots in order (the chunks in N order)
+                v += ld_coherent(a.zd + ((size_t)__builtin_ctz(m) * P + row0 + r) * K + cb * DN_COLS + c);
             zs[r * DN_COLS + c] = v;
         }
         __syncthreads();
@@ -668,14 +700,15 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int ks, i
             }
         }
     }
-    if (a.sk_dn > 1 && tid == 0) *cnt = 0u;
+    if (part && tid == 0) *cnt = 0ull;
 }
 
 template <int DEPTH>
 __global__ __launch_bounds__(DN_WAVES * 64) __attribute__((amdgpu_waves_per_eu(4))) void dec_down_kernel(
     DecodeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    down_tile<DEPTH>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+    // grid (K/512, N splits, segments): split ks is chunk ks (kch_dn = N / splits), its partials in slot ks
+    down_tile<DEPTH>(a, blockIdx.x, blockIdx.z, blockIdx.y, blockIdx.y + 1, blockIdx.y, smem);
 }
 
 // grid (T, K/256), 128 threads x 2 columns: out[t] = sum over slots k (in order) of the valid pairs' contributions
@@ -728,15 +761,16 @@ int launch_rot_in(const void* x, int xdt, int64_t x_stride, const int* tok, cons
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-size_t decode_lds_gateup(int rmax, int K, int sk_gu, int shared_suh) {
-    size_t staged = (size_t)(shared_suh ? 1 : 2) * rmax * (K / sk_gu + XPAD) * 2;
-    if (shared_suh) staged = std::max(staged, (size_t)std::min(rmax, DUP_ROWS) * (K / sk_gu + 4) * 4);
+size_t decode_lds_gateup(int rmax, int kr, int shared_suh) {
+    size_t staged = (size_t)(shared_suh ? 1 : 2) * rmax * (kr + XPAD) * 2;
+    if (shared_suh) staged = std::max(staged, (size_t)std::min(rmax, DUP_ROWS) * (kr + 4) * 4);
     const size_t reduce = (size_t)(4 * 64 * 16 + 2 * ZS_ROWS * 128) * 4;
     return std::max(staged, reduce);
 }
-size_t decode_lds_down(int rmax, int N, int sk_dn) {
-    return std::max((size_t)rmax * (N / sk_dn + 4) * 4, (size_t)ZS_ROWS * DN_COLS * 4);
+size_t decode_lds_down(int rmax, int kr) {
+    return std::max((size_t)rmax * (kr + 4) * 4, (size_t)ZS_ROWS * DN_COLS * 4);
 }
+
 
 template <typename F>
 static int allow_lds(F* f) {
@@ -763,8 +797,8 @@ int launch_decode(const DecodeArgs& a0, int rmax, hipStream_t st, int kernels) {
     // load depth: four steps (of 64 k) when each wave's range holds a multiple of four, else two
     if (kernels & 1) {
         const dim3 grid(a.N / 128, a.sk_gu, a.S_cap);
-        const size_t lds = decode_lds_gateup(rmax, a.K, a.sk_gu, a.shared_suh);
-        const bool d4 = ((a.K / a.sk_gu / 2) >> 6) % 4 == 0;
+        const size_t lds = decode_lds_gateup(rmax, a.kch_gu, a.shared_suh);
+        const bool d4 = ((a.kch_gu / 2) >> 6) % 4 == 0;
         if (a.shared_suh) {
             if (d4) hipLaunchKernelGGL((dec_gateup_kernel<4, true>), grid, dim3(GU_WAVES * 64), lds, st, a);
             else hipLaunchKernelGGL((dec_gateup_kernel<2, true>), grid, dim3(GU_WAVES * 64), lds, st, a);
@@ -775,8 +809,8 @@ int launch_decode(const DecodeArgs& a0, int rmax, hipStream_t st, int kernels) {
     }
     if (kernels & 2) {
         const dim3 grid((a.K + DN_COLS - 1) / DN_COLS, a.sk_dn, a.S_cap);
-        const size_t lds = decode_lds_down(rmax, a.N, a.sk_dn);
-        if (((a.N / a.sk_dn) >> 6) % 4 == 0)
+        const size_t lds = decode_lds_down(rmax, a.kch_dn);
+        if ((a.kch_dn >> 6) % 4 == 0)
             hipLaunchKernelGGL(dec_down_kernel<4>, grid, dim3(DN_WAVES * 64), lds, st, a);
         else
             hipLaunchKernelGGL(dec_down_kernel<2>, grid, dim3(DN_WAVES * 64), lds, st, a);

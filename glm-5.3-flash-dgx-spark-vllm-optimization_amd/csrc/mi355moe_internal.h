@@ -69,17 +69,22 @@ struct DecodeArgs {
     const int* seg_rows;
     const int* nseg;
     int S_cap;
-    int sk_gu, sk_dn;       // K splits of the gate/up GEMV (over K) and the down GEMV (over N)
+    // Work decomposition: a tile is (row segment, column block); its reduction dimension (K for gate/up, N for
+    // down) is cut into sk_gu / sk_dn chunks of kch_gu / kch_dn elements, one workgroup per chunk (grid (column
+    // blocks, chunks, segments)). A tile computed in more than one chunk is summed by the chunk that arrives last,
+    // in chunk order.
+    int sk_gu, sk_dn;
+    int kch_gu, kch_dn;     // chunk length (K elements for gate/up, N elements for down)
     int rmax;               // rows per segment (<= 16)
     int shared_suh;         // gate and up share one input rotation (one staged copy)
     float limit;
     // workspace
-    float* zg;              // [sk_gu][2][P][N]
-    float* zd;              // [sk_dn][P][K]
+    float* zg;              // [K / kch_gu][2][P][N] partial sums, slot = the fragment's first chunk
+    float* zd;              // [N / kch_dn][P][K]
     uint16_t* xd;           // [P][N] fp16 bits
     float* contrib;         // [P][K] per-pair contribution (slot-order combine)
-    unsigned* cnt_gu;       // [S_cap][N/128], zero between calls
-    unsigned* cnt_dn;       // [S_cap][K/256], zero between calls
+    unsigned long long* cnt_gu;   // [S_cap][N/128]: chunks arrived (bits 0-31) | slots stored (bits 32-63); zero
+    unsigned long long* cnt_dn;   // [S_cap][ceil(K/512)]                                           between calls
     // output
     void* out;
     int odt;                // output dtype
@@ -197,9 +202,9 @@ int launch_route_counts(const int64_t* counts64, const int64_t* token_sorted, co
                         const RouteArgs& a, hipStream_t st);
 // kernels: bit 0 gate/up, bit 1 down, bit 2 combine
 int launch_decode(const DecodeArgs& a, int rmax, hipStream_t st, int kernels = 7);
-// LDS bytes of the decode GEMV workgroups (staged inputs)
-size_t decode_lds_gateup(int rmax, int K, int sk_gu, int shared_suh);
-size_t decode_lds_down(int rmax, int N, int sk_dn);
+// LDS bytes of the decode GEMV workgroups staging kr reduction elements (gate/up: K range, down: N range)
+size_t decode_lds_gateup(int rmax, int kr, int shared_suh);
+size_t decode_lds_down(int rmax, int kr);
 constexpr size_t DECODE_LDS_MAX = 81920;   // two 512-thread workgroups per CU
 int launch_dequant(const uint16_t* trellis, int kt, int nt, uint16_t* wq, hipStream_t st);
 int launch_rot_in(const void* x, int xdt, int64_t x_stride, const int* tok, const int* pe, const int64_t* suh_tab,
