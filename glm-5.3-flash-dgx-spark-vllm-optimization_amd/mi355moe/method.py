@@ -88,7 +88,7 @@ class Exl3MoEMethod:
     """FusedMoE quant method for EXL3 4-bit trellis routed experts (prod_exl3_reference.py:2030-2343)."""
 
     def __init__(self, bits: int = 4, swiglu_limit: float | None = None, e4m3: bool = False,
-                 max_num_tokens: int | None = None, topk: int = 8):
+                 max_num_tokens: int | None = None, topk: int = 8, tp_rank: int = 0, tp_size: int = 1):
         if bits != 4:
             raise ValueError("this build decodes 4-bit EXL3 trellis tiles only")
         self.bits = bits
@@ -99,6 +99,7 @@ class Exl3MoEMethod:
         # registration, code/fork/tf_exl3_moe.py:391-418)
         self.max_num_tokens = max_num_tokens
         self.topk = topk
+        self.tp_rank, self.tp_size = tp_rank, tp_size    # this rank's slice of N (gate/up columns, down rows)
 
     def create_weights(self, layer: torch.nn.Module, num_experts: int, hidden_size: int,
                        intermediate_size_per_partition: int, params_dtype=None, device=None, **_) -> None:
@@ -116,10 +117,24 @@ class Exl3MoEMethod:
             "w2_suh": ((n, N), torch.float16), "w2_svh": ((n, K), torch.float16), "w2_mcg": ((n, 1), torch.int32),
         }
         for name, (shape, dt) in shapes.items():
-            layer.register_parameter(name, P(torch.empty(shape, dtype=dt, **kw), requires_grad=False))
+            param = P(torch.empty(shape, dtype=dt, **kw), requires_grad=False)
+            layer.register_parameter(name, param)
+            param.weight_loader = self.weight_loader
+            param._mi355_owner = layer
         layer._exl3_hidden_size = K
         layer._exl3_intermediate_local = N
         layer._exl3_bits = self.bits
+
+    def weight_loader(self, param: torch.nn.Parameter, loaded_weight: torch.Tensor, weight_name: str,
+                      shard_id: str = "w1", expert_id: int = 0, return_success: bool = False):
+        """One checkpoint tensor of one expert (global id) into the stacked parameters, sliced for this rank
+        (prod_exl3_reference.py:2164-2221): shard_id w1 / w3 = gate / up (column slice), w2 = down (row slice).
+        Non-local experts (layer.expert_map, global -> local or -1) are skipped."""
+        from .loader import load_into
+        layer = param._mi355_owner
+        ok = load_into(layer, loaded_weight, weight_name, shard_id, expert_id, self.tp_rank, self.tp_size,
+                       getattr(layer, "expert_map", None))
+        return ok if return_success else None
 
     def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
         for name in ("w13_mcg", "w2_mcg"):
