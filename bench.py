@@ -354,6 +354,39 @@ def run_prefill(args, torch, dev):
                               f"experts, {n_layers} layers alternated, {steps} timed steps"}
 
 
+def run_prefill_zipf(args, torch, dev, caps=(0, 16, 32, 64, 128)):
+    """Prefill chunk T=8192 with Zipf(1.2)-skewed routing (top-8 of 288 drawn with probability ~ 1 / (rank + 1)^1.2
+    over a random ranking): the thin/fat split at several caps (0 = every expert on the grouped kernels; cap c: experts
+    with at most c rows on the decode kernels). Reports ms per layer call for each cap."""
+    from mi355moe import ops, synthetic
+    T = args.prefill_tokens
+    layer = synthetic.exl3_layer(E, K, N, seed=450, device=dev)
+    x = synthetic.activations(T, K, seed=451, device=dev)
+    ids = synthetic.zipf_ids(T, E, TOPK, seed=452, device=dev)
+    wts = synthetic.softmax_weights(T, TOPK, seed=453, device=dev)
+    out = torch.empty(T, K, dtype=torch.bfloat16, device=dev)
+    counts = torch.bincount(ids.reshape(-1).long(), minlength=E)
+    res = {}
+    for cap in caps:
+        for _ in range(2):
+            ops.moe_forward_ids_split(layer, x, ids, wts, cap, limit=LIMIT, out=out)
+        torch.cuda.synchronize()
+        steps = max(4, args.steps // 4)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            ops.moe_forward_ids_split(layer, x, ids, wts, cap, limit=LIMIT, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        res[str(cap)] = round(e0.elapsed_time(e1) / steps, 4)
+    best = min(res, key=lambda c: res[c])
+    return {"prefill_zipf_ms_by_cap": res, "prefill_zipf_best_cap": int(best),
+            "prefill_zipf_tokens_per_s": round(T / (res[best] / 1000.0), 1),
+            "prefill_zipf_config": f"T={T}, {E} experts, Zipf(1.2) top-{TOPK} (rows per expert "
+                                   f"{int(counts.min())}..{int(counts.max())}, {int((counts <= 64).sum())} experts "
+                                   "with <= 64 rows), EXL3 4-bit synthetic experts; ms per layer call by thin cap"}
+
+
 def run_fp8(args, torch, dev):
     """e4m3 expert variant, T=2048 (hidden 4096, 288 experts, top-8, intermediate 1024): block-scaled e4m3 experts
     (N(0, 0.02) weights, fp32 scale per 128x128 block), bf16 activations quantised per token, sigmoid top-8 x2.5 of
@@ -614,7 +647,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill", "fp8", "e4m3t", "stack"])
+    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill", "zipf", "fp8", "e4m3t", "stack"])
     ap.add_argument("--stack-layers", type=int, default=42)
     ap.add_argument("--prefill-tokens", type=int, default=8192)
     ap.add_argument("--fp8-tokens", type=int, default=2048)
@@ -635,7 +668,7 @@ def main():
     import mi355moe
     mi355moe._lib.lib()
     dev = torch.device("cuda", 0)
-    if args.workload in ("prefill", "fp8", "e4m3t", "stack"):
+    if args.workload in ("prefill", "zipf", "fp8", "e4m3t", "stack"):
         args.no_cpu_baseline = True
         res = run_decode(argparse.Namespace(**{**vars(args), "steps": 8, "warmup": 2}), torch, mi355moe, dev)
     else:
@@ -643,6 +676,9 @@ def main():
     if args.workload in ("all", "prefill"):
         log("[bench] prefill ...")
         res.update(run_prefill(args, torch, dev))
+    if args.workload in ("all", "prefill", "zipf"):
+        log("[bench] prefill, Zipf routing, thin/fat split ...")
+        res.update(run_prefill_zipf(args, torch, dev))
     if args.workload in ("all", "fp8"):
         log("[bench] fp8 ...")
         res.update(run_fp8(args, torch, dev))

@@ -553,6 +553,184 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
     return rc_launch(launch_decode(w.da, p.rmax, stream, stages >> 1));
 }
 
+// ---------------------------------------------------------------------------------------------- thin/fat split
+
+namespace {
+
+// Workspace of the thin/fat split: one permutation (tok, w16, inv) shared by two row sets -- experts with at most cap
+// rows (decode kernels, 16-row segments, pe_thin) and the rest (grouped kernels, 256-row segments, pe_fat) -- and one
+// contribution buffer both fill at sorted positions.
+struct SplitWs {
+    RouteArgs thin, fat;
+    DecodeArgs da;
+    PrefillArgs pa;
+    DecodePlan dp;
+    size_t bytes;
+};
+
+void carve_split(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t N, int64_t cap, int shared,
+                 SplitWs& w) {
+    Carve c(ws);
+    memset(&w.thin, 0, sizeof(w.thin));
+    memset(&w.da, 0, sizeof(w.da));
+    memset(&w.pa, 0, sizeof(w.pa));
+    DecodePlan& p = w.dp;
+    p = plan_decode(P, std::max<int64_t>(1, cap), n, K, N, shared);
+    p.S_cap = (int)std::min<int64_t>(p.S_cap, n * ((std::max<int64_t>(1, cap) + p.seg - 1) / p.seg));
+    const int S_fat = (int)(std::min(P, n) + (P + PREFILL_TM - 1) / PREFILL_TM);
+    RouteArgs& r = w.thin;
+    r.tok = c.take<int>(P);
+    r.w16 = c.take<uint16_t>(P);
+    r.inv = c.take<int>(P);
+    r.pe = c.take<int>(P);
+    r.seg_expert = c.take<int>(p.S_cap);
+    r.seg_row0 = c.take<int>(p.S_cap);
+    r.seg_rows = c.take<int>(p.S_cap);
+    r.nseg = c.take<int>(1);
+    r.counts = c.take<int>(n + 1);
+    r.loc = c.take<int>(P);
+    r.blk_cnt = c.take<int>(((P + 1023) / 1024) * (n + 1));
+    r.cnt_out = c.take<int>(n + 1);
+    r.S_cap = p.S_cap;
+    r.seg = p.seg;
+    w.fat = r;
+    w.fat.pe = c.take<int>(P);
+    w.fat.seg_expert = c.take<int>(S_fat);
+    w.fat.seg_row0 = c.take<int>(S_fat);
+    w.fat.seg_rows = c.take<int>(S_fat);
+    w.fat.nseg = c.take<int>(1);
+    w.fat.S_cap = S_fat;
+    w.fat.seg = PREFILL_TM;
+    DecodeArgs& d = w.da;
+    d.cnt_gu = c.take<unsigned long long>((size_t)p.S_cap * (N / 128));
+    d.cnt_dn = c.take<unsigned long long>((size_t)p.S_cap * ((K + 511) / 512));
+    r.zero = reinterpret_cast<unsigned*>(d.cnt_gu);
+    r.zero_words = (int64_t)((c.off - ((char*)d.cnt_gu - c.base)) / sizeof(unsigned));
+    const int64_t zs_gu = K / p.kch_gu, zs_dn = N / p.kch_dn;
+    d.zg = c.take<float>(zs_gu > 1 ? (size_t)zs_gu * 2 * P * N : 1);
+    d.zd = c.take<float>(zs_dn > 1 ? (size_t)zs_dn * P * K : 1);
+    d.xd = c.take<uint16_t>((size_t)P * N);
+    PrefillArgs& a = w.pa;
+    a.h13 = c.take<uint16_t>((size_t)P * K);
+    a.h2 = c.take<uint16_t>((size_t)P * N);
+    a.contrib = c.take<float>((size_t)P * K);
+    d.contrib = a.contrib;
+    w.bytes = c.off;
+}
+
+}  // namespace
+
+int64_t mi355moe_moe_split_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk,
+                                           int64_t thin_cap) {
+    if (layer_shape_ok(layer) || T < 0 || topk < 1 || topk > MAX_TOPK || thin_cap < 0) return -1;
+    SplitWs w;
+    carve_split(nullptr, std::max<int64_t>(1, T * topk), std::max<int64_t>(1, T), layer->n, layer->hidden,
+                layer->intermediate, thin_cap, shared_flag(layer), w);
+    return (int64_t)w.bytes;
+}
+
+int mi355moe_moe_forward_ids_split(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                   int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                   int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                   int out_dtype, int64_t out_stride, int64_t thin_cap, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+    if (int r = layer_shape_ok(layer)) return r;
+    if (!x || !ids || !weights || !out || !workspace) return MI355MOE_EINVAL;
+    if (dt_act(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;
+    if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
+    const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n;
+    if (T < 0 || topk < 1 || topk > MAX_TOPK || thin_cap < 0) return MI355MOE_ELIMIT;
+    if (x_stride < K || x_stride % 2 || out_stride < K || out_stride % 2) return MI355MOE_ESHAPE;
+    if (expert_map && n_global < 0) return MI355MOE_EINVAL;
+    if (!(layer->flags & MI355MOE_LAYER_SHARED_W13_SUH)) return MI355MOE_EUNSUPPORTED;
+    const int64_t P = T * topk;
+    if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (P == 0) return 0;
+    const int64_t cap = std::min(thin_cap, P);
+    SplitWs w;
+    carve_split(workspace, P, T, n, K, N, cap, shared_flag(layer), w);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    if (w.dp.S_cap > 65535) return MI355MOE_ELIMIT;
+    if (prefill_setup()) return rc_launch(-1);
+    for (RouteArgs* r : {&w.thin, &w.fat}) {
+        r->ids = ids;
+        r->ids64 = ids_dtype == MI355MOE_I64;
+        r->w = weights;
+        r->wdt = dt_w(weights_dtype);
+        r->emap = expert_map;
+        r->n_global = expert_map ? n_global : 0;
+        r->P = (int)P;
+        r->topk = (int)topk;
+        r->n = (int)n;
+    }
+    w.thin.R = (int)cap;                                             // thin: 0 < count <= cap
+    w.thin.Rmin = 0;
+    w.fat.R = 1 << 30;                                               // fat: count > cap
+    w.fat.Rmin = (int)cap;
+    w.fat.zero = nullptr;
+    w.fat.zero_words = 0;
+    // (the second permutation writes the same tok / w16 / inv as the first)
+    if (cap > 0)
+        if (int rc = launch_route(w.thin, stream)) return rc_launch(rc);
+    if (int rc = launch_route(w.fat, stream)) return rc_launch(rc);
+    if (cap > 0) {
+        DecodeArgs& d = w.da;
+        d.wt = tables(layer);
+        d.n = (int)n;
+        d.K = (int)K;
+        d.N = (int)N;
+        d.P = (int)P;
+        d.T = (int)T;
+        d.x = x;
+        d.xdt = dt_act(x_dtype);
+        d.x_stride = x_stride;
+        d.tok = w.thin.tok;
+        d.w16 = w.thin.w16;
+        d.pe = w.thin.pe;
+        d.inv = w.thin.inv;
+        d.seg_expert = w.thin.seg_expert;
+        d.seg_row0 = w.thin.seg_row0;
+        d.seg_rows = w.thin.seg_rows;
+        d.nseg = w.thin.nseg;
+        d.S_cap = w.dp.S_cap;
+        d.sk_gu = w.dp.sk_gu;
+        d.sk_dn = w.dp.sk_dn;
+        d.kch_gu = w.dp.kch_gu;
+        d.kch_dn = w.dp.kch_dn;
+        d.shared_suh = shared_flag(layer);
+        d.limit = limit;
+        d.accumulate = 0;
+        d.topk = (int)topk;
+        if (int rc = launch_decode(d, w.dp.rmax, stream, 1 | 2)) return rc_launch(rc);   // contributions, no combine
+    }
+    PrefillArgs& a = w.pa;
+    a.wt = tables(layer);
+    a.n = (int)n;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.P = (int)P;
+    a.T = (int)T;
+    a.x = x;
+    a.xdt = dt_act(x_dtype);
+    a.x_stride = x_stride;
+    a.tok = w.fat.tok;
+    a.w16 = w.fat.w16;
+    a.pe = w.fat.pe;
+    a.inv = w.fat.inv;
+    a.topk = (int)topk;
+    a.seg_expert = w.fat.seg_expert;
+    a.seg_row0 = w.fat.seg_row0;
+    a.seg_rows = w.fat.seg_rows;
+    a.nseg = w.fat.nseg;
+    a.S_cap = w.fat.S_cap;
+    a.limit = limit;
+    a.out = out;
+    a.odt = dt_w(out_dtype);
+    a.out_stride = out_stride;
+    a.pe_thin = cap > 0 ? w.thin.pe : nullptr;
+    return rc_launch(launch_prefill(a, stream, 1 | 2 | 4 | 8));
+}
+
 // ---------------------------------------------------------------------------------------------- e4m3 variant
 
 int64_t mi355moe_e4m3_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk) {

@@ -18,11 +18,12 @@ struct RouteArgs {
     const int64_t* emap;    // optional expert map [n_global] (global id -> local id or -1)
     int64_t n_global;
     int P, topk, n, R, seg, S_cap;
+    int Rmin;               // experts with count <= Rmin get no rows (pe = -1) and no segments (0: none excluded)
     // outputs (sorted position order unless noted)
     int* tok;               // [P] token of the pair at pos
     uint16_t* w16;          // [P] fp16 weight bits
     float* w32;             // optional [P] fp32 weight
-    int* pe;                // [P] local expert, -1 = skipped (sentinel or more than R rows)
+    int* pe;                // [P] local expert, -1 = skipped (sentinel, more than R or at most Rmin rows)
     int* inv;               // [P] pair j -> pos
     int* seg_expert;        // [S_cap]
     int* seg_row0;          // [S_cap]
@@ -131,6 +132,9 @@ struct PrefillArgs {
     const int* nrows;
     const int* pair_local;
     const int* pair_pos;
+    // thin/fat split: rows with pe < 0 and pe_thin >= 0 were computed by the decode kernels, whose contrib rows hold
+    // finished contributions (the combine adds them as they are); nullptr: no split
+    const int* pe_thin;
 };
 constexpr int PREFILL_TM = 256;
 constexpr int PF_ROWS_PER_TOKEN = 32;   // rows of one token the row-table combine handles (topk <= 32)

@@ -722,18 +722,21 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
         const int lk = k0 + (lane & 7);
         const int pl = a.inv[t * a.topk + min(lk, a.topk - 1)];
         const int el = a.pe[pl];
-        const int okl = (int)(lk < a.topk) & (int)(el >= 0);
+        // thin/fat split: a row this path skipped but the decode kernels computed holds a finished contribution
+        const int thl = (int)(lk < a.topk && el < 0 && a.pe_thin && a.pe_thin[pl] >= 0);
+        const int okl = (int)(lk < a.topk) & (int)(el >= 0 || thl);
         const float wl = a.w32 ? a.w32[pl] : (float)u16_as_h(a.w16[pl]);
         const float dl = a.dsc ? a.dsc[pl] : 1.0f;                   // e4m3 variant: the down input's row scale
         const int64_t svl = a.wt.d_svh[max(el, 0)];
         f32x4 raw[8][2];
         u32x4 sv[8];
-        bool ok[8];
+        bool ok[8], thin[8];
         float w[8], ds[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {                                 // unconditional loads (no joins between them)
             const int pos = __builtin_amdgcn_readlane(pl, k);
             ok[k] = __builtin_amdgcn_readlane(okl, k) != 0;
+            thin[k] = __builtin_amdgcn_readlane(thl, k) != 0;
             w[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k));
             ds[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dl), k));
             const uint64_t sp = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)svl, k)) |
@@ -752,6 +755,11 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
             for (int i = 0; i < 4; ++i) {
                 v[i] = raw[k][0][i];
                 v[4 + i] = raw[k][1][i];
+            }
+            if (thin[k]) {                                           // uniform: one slot per wave
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sum[i] += v[i];
+                continue;
             }
             if (a.dsc) {
 #pragma unroll

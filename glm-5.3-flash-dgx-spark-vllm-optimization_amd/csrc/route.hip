@@ -256,15 +256,15 @@ __device__ __forceinline__ int block_scan_incl(int v, int* tot, int& total) {
 }
 
 // Segment table from per-expert counts held in `cnt` (shared, [n]) and their starts: every expert with
-// 0 < c <= R gets ceil(c / seg) segments (expert, first row, rows). Called by every thread of the block.
+// max(0, Rmin) < c <= R gets ceil(c / seg) segments (expert, first row, rows). Called by every thread of the block.
 __device__ void build_segments(const int* cnt, const int* start, int n, int R, int seg, int S_cap,
                                int* __restrict__ seg_expert, int* __restrict__ seg_row0, int* __restrict__ seg_rows,
-                               int* __restrict__ nseg_out, int* tot) {
+                               int* __restrict__ nseg_out, int* tot, int Rmin = 0) {
     int run = 0;
     for (int base = 0; base < n; base += blockDim.x) {
         const int e = base + threadIdx.x;
         const int c = e < n ? cnt[e] : 0;
-        const bool elig = e < n && c > 0 && c <= R;
+        const bool elig = e < n && c > Rmin && c > 0 && c <= R;
         const int ns = elig ? (c + seg - 1) / seg : 0;
         int stot;
         const int sinc = block_scan_incl(ns, tot, stot);
@@ -321,7 +321,7 @@ __device__ void route_small_body(const RouteArgs& a, int* sh) {
     __syncthreads();
     if (a.counts)
         for (int e = threadIdx.x; e <= a.n; e += blockDim.x) a.counts[e] = cnt[e];
-    build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot);
+    build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot, a.Rmin);
     for (int j = threadIdx.x; j < a.P; j += blockDim.x) {
         const int l = loc[j];
         int rank = 0;                                                // earlier pairs with the same local id
@@ -336,7 +336,7 @@ __device__ void route_small_body(const RouteArgs& a, int* sh) {
         a.tok[pos] = j / a.topk;
         a.w16[pos] = weight_f16(a.w, a.wdt, j);
         if (a.w32) a.w32[pos] = weight_f32(a.w, a.wdt, j);
-        a.pe[pos] = (l < a.n && cnt[l] <= a.R) ? l : -1;
+        a.pe[pos] = (l < a.n && cnt[l] <= a.R && cnt[l] > a.Rmin) ? l : -1;
         a.inv[j] = pos;
     }
 }
@@ -395,7 +395,7 @@ __device__ void route_wave64(const RouteArgs& a) {
     const uint64_t smask = __ballot(start);
     const uint64_t above = lane == 63 ? 0ull : smask >> (lane + 1);
     const int c = (above ? lane + 1 + __builtin_ctzll(above) : a.P) - lane;   // run length, at run starts
-    const bool elig = start && l < a.n && c <= a.R;
+    const bool elig = start && l < a.n && c <= a.R && c > a.Rmin;
     const uint64_t emask = __ballot(elig);
     const uint64_t upto = smask & (lane == 63 ? ~0ull : ((1ull << (lane + 1)) - 1));
     const int rs = upto ? 63 - __builtin_clzll(upto) : 0;           // this lane's run start
@@ -715,7 +715,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(RouteArgs a, int nblk)
         if (a.counts) a.counts[e] = cnt[e];
         a.cnt_out[e] = cnt[e];
     }
-    build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot);
+    build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot, a.Rmin);
 }
 
 __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
@@ -733,7 +733,7 @@ __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
     a.tok[pos] = j / a.topk;
     a.w16[pos] = weight_f16(a.w, a.wdt, j);
     if (a.w32) a.w32[pos] = weight_f32(a.w, a.wdt, j);
-    a.pe[pos] = (l < a.n && a.cnt_out[l] <= a.R) ? l : -1;
+    a.pe[pos] = (l < a.n && a.cnt_out[l] <= a.R && a.cnt_out[l] > a.Rmin) ? l : -1;
     a.inv[j] = pos;
 }
 

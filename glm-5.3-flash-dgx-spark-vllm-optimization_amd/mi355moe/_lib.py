@@ -79,6 +79,10 @@ _SIGS = {
                                   _f, _int, _f, _c_p, _int, _i64, _c_p, _c_p, _c_p, _sz, _c_p]),
     "mi355moe_moe_layer_noalloc": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _c_p, _i64,
                                           _c_p, _i64, _f, _int, _f, _c_p, _int, _i64, _c_p, _c_p, _c_p]),
+    "mi355moe_moe_split_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64, _i64, _i64]),
+    "mi355moe_moe_forward_ids_split": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int,
+                                              _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _i64, _c_p, _sz,
+                                              _c_p]),
     "mi355moe_e3_tile_rows": (_i64, []),
     "mi355moe_e3_gather": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p]),
     "mi355moe_e3_gateup": (_int, [_c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,

@@ -244,6 +244,38 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
     return out
 
 
+def moe_forward_ids_split(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor,
+                          topk_weights: torch.Tensor, thin_cap: int, limit: float = 10.0,
+                          expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                          out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The thin/fat split of a prefill-size call (code/fork/docs/prod_exl3_reference.py:1659-1679 with the cap of
+    code/fork/glm53_prefill_cap.py): experts routed at most thin_cap rows on the decode kernels, the rest on the
+    grouped kernels, one slot-order combine; output [T, K] written. thin_cap = 0: all experts grouped."""
+    dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
+    if dev != experts.device:
+        raise ValueError(f"activations on {dev}, experts on {experts.device}")
+    if x.dim() != 2 or x.shape[1] != experts.K or x.stride(1) != 1:
+        raise ValueError(f"x must be [T, {experts.K}] with unit column stride")
+    T = x.shape[0]
+    ids = topk_ids.reshape(T, -1).contiguous()
+    w = topk_weights.reshape(T, -1).contiguous()
+    topk = ids.shape[1]
+    if out is None:
+        out = torch.empty(T, experts.K, dtype=out_dtype or x.dtype, device=dev)
+    L = _lib.lib()
+    nb = L.mi355moe_moe_split_workspace_bytes(ctypes.byref(experts.desc), T, topk, int(thin_cap))
+    if nb < 0:
+        raise ValueError("mi355moe_moe_split_workspace_bytes rejected the shape")
+    ws = workspace(dev, nb)
+    em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
+    _lib.check("mi355moe_moe_forward_ids_split", L.mi355moe_moe_forward_ids_split(
+        ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
+        ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em), 0 if em is None else em.numel(),
+        float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), int(thin_cap), _p(ws), ws.numel(),
+        _stream(dev)))
+    return out
+
+
 def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                          limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
                          out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL) -> torch.Tensor:

@@ -160,6 +160,17 @@ def zipf_logits(T: int, E: int, seed: int, s: float = 1.2, noise: torch.Tensor |
     return lg
 
 
+def zipf_ids(T: int, n: int, topk: int, seed: int, s: float = 1.2, device="cuda") -> torch.Tensor:
+    """Top-k picks with Zipf(s)-skewed expert popularity: every token draws topk distinct experts with probability
+    proportional to 1 / (rank + 1)^s over a random ranking of the experts (int32 [T, topk])."""
+    g = _gen(seed, torch.device("cpu"))
+    p = 1.0 / (torch.arange(n, dtype=torch.float64) + 1.0) ** s
+    probs = torch.empty(n, dtype=torch.float64)
+    probs[torch.randperm(n, generator=g)] = p
+    ids = torch.multinomial(probs.expand(T, n), topk, replacement=False, generator=g) if T else torch.zeros(0, topk)
+    return ids.to(torch.int32).to(device)
+
+
 def zipf_router(E: int, K: int, seed: int, rank_seed: int, device="cuda", s: float = 1.2,
                 c0: float = 8.0) -> tuple[torch.Tensor, torch.Tensor]:
     """A router (W, bias) whose GEMM itself produces Zipf(s)-skewed expert popularity: column 0 of W is

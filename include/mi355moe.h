@@ -138,6 +138,20 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
                                 int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, int path,
                                 int stages, hipStream_t stream);
 
+/* The thin/fat split of a prefill-size call (production's E3 branch, code/fork/docs/prod_exl3_reference.py:1659-1679,
+ * with the cap of code/fork/glm53_prefill_cap.py): experts routed at most thin_cap rows run on the decode kernels
+ * (16-row segments, limit after SiLU), the others on the grouped kernels (256-row tiles, limit before SiLU); both
+ * write per-pair contributions at the same sorted positions and every token's slots are summed in slot order, out
+ * WRITTEN in out_dtype. thin_cap = 0: every expert on the grouped kernels. The layer needs
+ * MI355MOE_LAYER_SHARED_W13_SUH. Arguments otherwise as mi355moe_moe_forward_ids. */
+int64_t mi355moe_moe_split_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk,
+                                           int64_t thin_cap);
+int mi355moe_moe_forward_ids_split(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                   int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                   int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                   int out_dtype, int64_t out_stride, int64_t thin_cap, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+
 /* The fused-experts op exllamav3_ext.exl3_moe (code/fork/docs/ref/xl_exl3_moe.cu:93-130, called by
  * prod_exl3_reference.py:1490-1537): hidden fp16 [B][K]; out fp32 [B][K] ACCUMULATED into; expert_count int64
  * [n+1] (last = sentinel bucket, ignored); token_sorted int64 [P]; weight_sorted fp16 [P]; experts with more
