@@ -289,6 +289,20 @@ def run_decode(args, torch, mi355moe, dev):
     return res
 
 
+def _time_calls(torch, fn, n_layers, warmup, steps):
+    """ms per call of fn(layer index), layers alternated, event-bracketed on the current stream."""
+    for w in range(warmup):
+        fn(w % n_layers)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for k in range(steps):
+        fn(k % n_layers)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def run_prefill(args, torch, dev):
     """Prefill MoE chunk, T=8192 (same layer shapes), uniform-random router logits; the grouped MFMA path."""
     from mi355moe import _lib, ops, synthetic
@@ -336,6 +350,13 @@ def run_prefill(args, torch, dev):
         gu.append((a, b))
     torch.cuda.synchronize()
     gu_ms = sum(a.elapsed_time(b) for a, b in gu) / len(gu)
+
+    def step_fold(l):
+        # bf16 down accumulators, routed sum added into out (which stands for the shared experts' bf16 output)
+        ids, wts = ops.router_topk(logits[l], TOPK, None, routed_scale=SCALE)
+        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], accumulate=True, bf16_contrib=True)
+
+    ms_fold = _time_calls(torch, step_fold, n_layers, 2, steps)
     P = sum(pairs) / len(pairs)
     flops = 2.0 * P * (K * 2 * N + N * K)
     gu_flops = 2.0 * P * K * 2 * N
@@ -344,6 +365,7 @@ def run_prefill(args, torch, dev):
         extra["cpu_baseline_prefill"] = cpu_baseline_prefill(torch, layers[0], x, info[0][0], info[0][1],
                                                              min(16, os.cpu_count() or 1))
     return {**extra, "prefill_tokens_per_s": round(T / (ms / 1000.0), 1), "prefill_ms_per_layer": round(ms, 4),
+            "prefill_bf16acc_fold_ms_per_layer": round(ms_fold, 4),
             "prefill_tflops": round(flops / (ms / 1000.0) / 1e12, 2),
             "roofline_prefill": {"bound": "mfma", "kernel": "pf_gateup_kernel (includes the gather launch)",
                                  "achieved": round(gu_flops / (gu_ms / 1000.0) / 1e12, 2),
@@ -487,8 +509,16 @@ def run_e4m3_trellis(args, torch, dev):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+
+    def step_fold(l):
+        ids, wts = ops.router_topk(logits[l], TOPK, None, routed_scale=SCALE)
+        ops.moe_forward_ids_e4m3(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], accumulate=True,
+                                 bf16_contrib=True)
+
+    ms_fold = _time_calls(torch, step_fold, n_layers, 2, steps)
     P = T * TOPK
     return {"e4m3t_tokens_per_s": round(T / (ms / 1000.0), 1), "e4m3t_ms_per_layer": round(ms, 4),
+            "e4m3t_bf16acc_fold_ms_per_layer": round(ms_fold, 4),
             "e4m3t_tflops": round(2.0 * P * 3 * K * N / (ms / 1000.0) / 1e12, 2),
             "e4m3t_config": f"T={T}, {E} EXL3 4-bit experts, trellis-sourced e4m3 numerics (per-row e4m3 activations, "
                             f"weights rounded to e4m3, fp32 sums), sigmoid top-{TOPK} x{SCALE} of uniform-random "

@@ -456,7 +456,7 @@ static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dt
                        const void* ids, int ids_dtype, const void* weights, int weights_dtype, int64_t topk,
                        const int64_t* expert_map, int64_t n_global, float limit, void* out, int out_dtype,
                        int64_t out_stride, void* workspace, size_t workspace_bytes, int stages, bool e4m3,
-                       hipStream_t stream) {
+                       int options, hipStream_t stream) {
     const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n, P = T * topk;
     RouteArgs r;
     PrefillWs w;
@@ -491,6 +491,8 @@ static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     d.odt = dt_w(out_dtype);
     d.out_stride = out_stride;
     d.e4m3 = e4m3 ? 1 : 0;
+    d.contrib_bf16 = (options & MI355MOE_OPT_BF16_CONTRIB) ? 1 : 0;
+    d.out_accumulate = (options & MI355MOE_OPT_ACCUMULATE) ? 1 : 0;
     if (prefill_setup()) return rc_launch(-1);
     r.ids = ids;
     r.ids64 = ids_dtype == MI355MOE_I64;
@@ -516,10 +518,24 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
                                 int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
                                 int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, int path,
                                 int stages, hipStream_t stream) {
+    return mi355moe_moe_forward_ids_opt(layer, x, x_dtype, x_stride, T, ids, ids_dtype, weights, weights_dtype, topk,
+                                        expert_map, n_global, limit, out, out_dtype, out_stride, workspace,
+                                        workspace_bytes, path, stages, 0, stream);
+}
+
+int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                 int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                 int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                 int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, int path,
+                                 int stages, int options, hipStream_t stream) {
     if (int r = layer_shape_ok(layer)) return r;
     if (!x || !ids || !weights || !out || !workspace) return MI355MOE_EINVAL;
     if (stages <= 0 || stages > MI355MOE_STAGE_ALL) return MI355MOE_EINVAL;
     if (path < MI355MOE_PATH_AUTO || path > MI355MOE_PATH_PREFILL) return MI355MOE_EINVAL;
+    if (options & ~(MI355MOE_OPT_ACCUMULATE | MI355MOE_OPT_BF16_CONTRIB | MI355MOE_OPT_E4M3)) return MI355MOE_EINVAL;
+    const bool e4m3 = (options & MI355MOE_OPT_E4M3) != 0;
+    if (e4m3 && path == MI355MOE_PATH_DECODE) return MI355MOE_EINVAL;      // e4m3 numerics run on the grouped tier
+    if (e4m3 && layer && layer->hidden > 4096) return MI355MOE_EUNSUPPORTED;
     if (dt_act(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;
     if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
     const int64_t K = layer->hidden, N = layer->intermediate, n = layer->n;
@@ -529,13 +545,13 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
     const int64_t P = T * topk;
     if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
     if (P == 0) return 0;
-    const int use = choose_path(layer, P, path);
+    const int use = e4m3 ? MI355MOE_PATH_PREFILL : choose_path(layer, P, path);
     if (use == MI355MOE_PATH_PREFILL && !(layer->flags & MI355MOE_LAYER_SHARED_W13_SUH))
         return MI355MOE_EUNSUPPORTED;                   // the grouped tier gathers once with the gate's suh
     if (use == MI355MOE_PATH_PREFILL)
         return run_grouped(layer, x, x_dtype, x_stride, T, ids, ids_dtype, weights, weights_dtype, topk, expert_map,
-                           n_global, limit, out, out_dtype, out_stride, workspace, workspace_bytes, stages, false,
-                           stream);
+                           n_global, limit, out, out_dtype, out_stride, workspace, workspace_bytes, stages, e4m3,
+                           options, stream);
     DecodePlan p;
     DecodeWs w;
     if (int rc = prep_decode(layer, x, x_dtype, x_stride, T, topk, limit, out, out_dtype, out_stride, workspace,
@@ -550,6 +566,7 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
     r.n_global = expert_map ? n_global : 0;
     if (stages & MI355MOE_STAGE_ROUTE)
         if (int rc = launch_route(r, stream)) return rc_launch(rc);
+    w.da.out_accumulate = (options & MI355MOE_OPT_ACCUMULATE) ? 1 : 0;
     return rc_launch(launch_decode(w.da, p.rmax, stream, stages >> 1));
 }
 
@@ -761,7 +778,8 @@ int mi355moe_e4m3_moe_forward_ids(const mi355moe_exl3_layer* layer, const void* 
     if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
     if (P == 0) return 0;
     return run_grouped(layer, x, x_dtype, x_stride, T, ids, ids_dtype, weights, weights_dtype, topk, expert_map,
-                       n_global, limit, out, out_dtype, out_stride, workspace, workspace_bytes, stages, true, stream);
+                       n_global, limit, out, out_dtype, out_stride, workspace, workspace_bytes, stages, true, 0,
+                       stream);
 }
 
 // ---------------------------------------------------------------------------------------------- whole layer

@@ -737,6 +737,18 @@ __global__ __launch_bounds__(128) void combine_kernel(DecodeArgs a) {
             }
     }
     const size_t o = (size_t)t * a.out_stride + col;
+    if (a.out_accumulate) {                                          // out += the routed sum (one rounding)
+        if (a.odt == DT_F32) {
+            s0 += reinterpret_cast<const float*>(a.out)[o];
+            s1 += reinterpret_cast<const float*>(a.out)[o + 1];
+        } else if (a.odt == DT_BF16) {
+            s0 += bf16_to_f32(reinterpret_cast<const uint16_t*>(a.out)[o]);
+            s1 += bf16_to_f32(reinterpret_cast<const uint16_t*>(a.out)[o + 1]);
+        } else {
+            s0 += (float)reinterpret_cast<const _Float16*>(a.out)[o];
+            s1 += (float)reinterpret_cast<const _Float16*>(a.out)[o + 1];
+        }
+    }
     if (a.odt == DT_F32) {
         *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.out) + o) = make_float2(s0, s1);
     } else if (a.odt == DT_BF16) {

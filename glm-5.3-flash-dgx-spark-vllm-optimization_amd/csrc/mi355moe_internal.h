@@ -92,6 +92,7 @@ struct DecodeArgs {
     int64_t out_stride;
     int accumulate;         // 1: out (fp32) += contributions with atomics; 0: out = slot-order sum
     int topk;
+    int out_accumulate;     // with accumulate 0: out += the slot-order sum (the shared-expert fold)
 };
 
 // The prefill-path kernels (gather, fp16 MFMA grouped GEMMs over 256-row expert tiles).
@@ -135,6 +136,8 @@ struct PrefillArgs {
     // thin/fat split: rows with pe < 0 and pe_thin >= 0 were computed by the decode kernels, whose contrib rows hold
     // finished contributions (the combine adds them as they are); nullptr: no split
     const int* pe_thin;
+    int contrib_bf16;       // the down kernel stores its raw accumulators as bf16 (contrib viewed as bf16 [P][K])
+    int out_accumulate;     // the combine adds the routed sum to out's current values (the shared-expert fold)
 };
 constexpr int PREFILL_TM = 256;
 constexpr int PF_ROWS_PER_TOKEN = 32;   // rows of one token the row-table combine handles (topk <= 32)

@@ -690,7 +690,26 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     // this kernel's MFMAs). Lane n of block s holds column 16 (n / 8) + n % 8 + 8 s of the wave.
     const int lane = threadIdx.x & 63;
     const int n = lane & 31;
-    float* o = a.contrib + (size_t)row0 * K + cb * 256 + 64 * wv + 16 * (n >> 3) + (n & 7);
+    const size_t c0 = (size_t)row0 * K + cb * 256 + 64 * wv + 16 * (n >> 3) + (n & 7);
+    if (a.contrib_bf16) {
+        // bf16 raw accumulators: lanes n, n ^ 1 hold adjacent columns; they trade values (DPP lane ^ 1) so the even
+        // lane stores the pair (c, c + 1) of block 0 and the odd lane the pair (c - 1 + 8, c + 8) of block 1
+        uint16_t* ob = reinterpret_cast<uint16_t*>(a.contrib) + c0 + ((n & 1) ? 7 : 0);
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const float mine = (n & 1) ? acc[rb][1][r] : acc[rb][0][r];
+                const float give = (n & 1) ? acc[rb][0][r] : acc[rb][1][r];
+                const float got = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, give),
+                                                                                     0xB1, 0xF, 0xF, true));
+                const uint32_t lo = f32_to_bf16((n & 1) ? got : mine), hi = f32_to_bf16((n & 1) ? mine : got);
+                if (trow < rn) *reinterpret_cast<uint32_t*>(ob + (size_t)trow * K) = lo | (hi << 16);
+            }
+        return;
+    }
+    float* o = a.contrib + c0;
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
@@ -741,9 +760,15 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
             ds[k] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dl), k));
             const uint64_t sp = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)svl, k)) |
                                 ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(svl >> 32), k) << 32);
-            const float* rp = a.contrib + (size_t)pos * a.K + colc;
-            raw[k][0] = *reinterpret_cast<const f32x4*>(rp);
-            raw[k][1] = *reinterpret_cast<const f32x4*>(rp + 4);
+            if (a.contrib_bf16) {                                    // 8 bf16 in the first vector's place
+                const u32x4 rb16 = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.contrib) +
+                                                                   (size_t)pos * a.K + colc);
+                raw[k][0] = __builtin_bit_cast(f32x4, rb16);
+            } else {
+                const float* rp = a.contrib + (size_t)pos * a.K + colc;
+                raw[k][0] = *reinterpret_cast<const f32x4*>(rp);
+                raw[k][1] = *reinterpret_cast<const f32x4*>(rp + 4);
+            }
             const uint16_t* svp = reinterpret_cast<const uint16_t*>(sp) + colc;
 #pragma unroll
             for (int i = 0; i < 4; ++i) sv[k][i] = *reinterpret_cast<const uint32_t*>(svp + 2 * i);
@@ -751,10 +776,19 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             float v[8];
+            if (a.contrib_bf16 && !thin[k]) {
+                const u32x4 rb16 = __builtin_bit_cast(u32x4, raw[k][0]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[i] = raw[k][0][i];
-                v[4 + i] = raw[k][1][i];
+                for (int i = 0; i < 4; ++i) {
+                    v[2 * i] = bf16_to_f32((uint16_t)(rb16[i] & 0xFFFFu));
+                    v[2 * i + 1] = bf16_to_f32((uint16_t)(rb16[i] >> 16));
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[i] = raw[k][0][i];
+                    v[4 + i] = raw[k][1][i];
+                }
             }
             if (thin[k]) {                                           // uniform: one slot per wave
 #pragma unroll
@@ -776,6 +810,21 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     }
     if (!live) return;
     const size_t o = (size_t)t * a.out_stride + col;
+    if (a.out_accumulate) {                                          // out += the routed sum (one rounding)
+        float prev[8];
+        if (a.odt == DT_F32) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) prev[i] = reinterpret_cast<const float*>(a.out)[o + i];
+        } else if (a.odt == DT_BF16) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) prev[i] = bf16_to_f32(reinterpret_cast<const uint16_t*>(a.out)[o + i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) prev[i] = (float)reinterpret_cast<const _Float16*>(a.out)[o + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum[i] = prev[i] + sum[i];
+    }
     if (a.odt == DT_F32) {
         float* op = reinterpret_cast<float*>(a.out) + o;
 #pragma unroll
@@ -981,7 +1030,7 @@ int launch_zero_out(const PrefillArgs& a, hipStream_t st) {
 
 int launch_prefill_rows_down(const PrefillArgs& a0, const int64_t* row_token, int tokens, int* cnt, int2* list,
                              hipStream_t st) {
-    if (prefill_setup()) return -1;
+    if (prefill_setup() || a0.contrib_bf16) return -1;           // the row-table combine reads fp32 accumulators
     PrefillArgs a = a0;
     int* pe = const_cast<int*>(a.pe);
     const int fill = std::max(1, std::min(2048, (std::max(a.P, tokens) + 255) / 256));

@@ -15,6 +15,7 @@ ABI_VERSION = 1
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
 STAGE_ROUTE, STAGE_GATEUP, STAGE_DOWN, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 8, 15
 PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
+OPT_ACCUMULATE, OPT_BF16_CONTRIB, OPT_E4M3 = 1, 2, 4
 LAYER_SHARED_W13_SUH = 1
 PREFILL_MIN_PAIRS = 4096
 NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -69,6 +70,9 @@ _SIGS = {
     "mi355moe_moe_forward_ids_ex": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int,
                                            _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int, _int,
                                            _c_p]),
+    "mi355moe_moe_forward_ids_opt": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int,
+                                            _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int,
+                                            _int, _int, _c_p]),
     "mi355moe_e4m3_moe_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64, _i64]),
     "mi355moe_e4m3_moe_forward_ids": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int,
                                              _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int,

@@ -211,10 +211,16 @@ def rot_in(x: torch.Tensor, tok: torch.Tensor, pe: torch.Tensor, suh_table: torc
 def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                     limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
                     out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL,
-                    path: int = _lib.PATH_AUTO) -> torch.Tensor:
-    """Routed-expert output [T, K] (x's dtype unless out/out_dtype say otherwise), written (not accumulated).
+                    path: int = _lib.PATH_AUTO, accumulate: bool = False,
+                    bf16_contrib: bool = False) -> torch.Tensor:
+    """Routed-expert output [T, K] (x's dtype unless out/out_dtype say otherwise), written, or with accumulate added
+    to out's values (the shared-expert fold: out holds the shared experts' output; fp32 sum, one rounding).
     path: _lib.PATH_AUTO (decode kernels for few pairs, the grouped MFMA prefill kernels for many), or forced.
-    stages: a subset of the call's launches (_lib.STAGE_*), for timing one kernel; the default runs them all."""
+    stages: a subset of the call's launches (_lib.STAGE_*), for timing one kernel; the default runs them all.
+    bf16_contrib: the grouped path keeps its per-pair down accumulators in bf16 (half the contribution traffic;
+    code/fork/docs/OPT_MOE.md:13)."""
+    if accumulate and out is None:
+        raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
     if dev != experts.device:
         raise ValueError(f"activations on {dev}, experts on {experts.device}")
@@ -236,11 +242,12 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
         raise ValueError("mi355moe_moe_workspace_bytes rejected the shape")
     ws = workspace(dev, nb)
     em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
-    _lib.check("mi355moe_moe_forward_ids", L.mi355moe_moe_forward_ids_ex(
+    opts = (_lib.OPT_ACCUMULATE if accumulate else 0) | (_lib.OPT_BF16_CONTRIB if bf16_contrib else 0)
+    _lib.check("mi355moe_moe_forward_ids", L.mi355moe_moe_forward_ids_opt(
         ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
         ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em), 0 if em is None else em.numel(),
         float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), int(path),
-        int(stages), _stream(dev)))
+        int(stages), opts, _stream(dev)))
     return out
 
 
@@ -278,11 +285,15 @@ def moe_forward_ids_split(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch
 
 def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                          limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                         out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL) -> torch.Tensor:
+                         out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL,
+                         accumulate: bool = False, bf16_contrib: bool = False) -> torch.Tensor:
     """The trellis-sourced e4m3 variant of the routed experts (code/fork/overlay/glm53_moe_e4m3.py:484-592 run(),
     numerics of spec_ffn :666-674 with DOWN16 off): activations quantized per row to e4m3 after the input rotation,
     EXL3 weights rounded to e4m3, fp32 sums; output [T, K] written like moe_forward_ids. The layer needs gate and up
-    sharing one suh and hidden <= 4096."""
+    sharing one suh and hidden <= 4096. accumulate / bf16_contrib: the ACC=bf16 and FOLD_SHARED knobs
+    (code/fork/docs/OPT_MOE.md:9-21) as in moe_forward_ids."""
+    if accumulate and out is None:
+        raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
     if dev != experts.device:
         raise ValueError(f"activations on {dev}, experts on {experts.device}")
@@ -304,6 +315,15 @@ def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.
         raise ValueError("mi355moe_e4m3_moe_workspace_bytes rejected the shape")
     ws = workspace(dev, nb)
     em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
+    if accumulate or bf16_contrib:
+        opts = (_lib.OPT_E4M3 | (_lib.OPT_ACCUMULATE if accumulate else 0) |
+                (_lib.OPT_BF16_CONTRIB if bf16_contrib else 0))
+        _lib.check("mi355moe_moe_forward_ids_opt", L.mi355moe_moe_forward_ids_opt(
+            ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
+            ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em),
+            0 if em is None else em.numel(), float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0),
+            _p(ws), ws.numel(), _lib.PATH_PREFILL, int(stages), opts, _stream(dev)))
+        return out
     _lib.check("mi355moe_e4m3_moe_forward_ids", L.mi355moe_e4m3_moe_forward_ids(
         ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
         ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em), 0 if em is None else em.numel(),

@@ -138,6 +138,27 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
                                 int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, int path,
                                 int stages, hipStream_t stream);
 
+/* mi355moe_moe_forward_ids_ex with an options mask (the reference's opt-in prefill knobs, code/fork/docs/
+ * OPT_MOE.md:9-21, and its e4m3 numerics):
+ *   MI355MOE_OPT_ACCUMULATE   out += the routed output instead of out = (the FOLD_SHARED knob: out holds the shared
+ *                             experts' output, and the sum is added to it in fp32 with one rounding to out_dtype, so
+ *                             the separate shared + routed add is not needed); both paths.
+ *   MI355MOE_OPT_BF16_CONTRIB the grouped path keeps its per-pair down accumulators in bf16 (half the bytes of the
+ *                             contribution buffer; the ACC=bf16 knob's traffic saving). The combine still applies
+ *                             the rotation, svh and router weight in fp32 and adds a token's slots in slot order, so
+ *                             the result stays deterministic; each contribution carries one bf16 rounding of its raw
+ *                             accumulators (relative error about 2^-9 per element). No effect on the decode path.
+ *   MI355MOE_OPT_E4M3         the trellis-sourced e4m3 numerics of mi355moe_e4m3_moe_forward_ids (grouped path
+ *                             only: path DECODE is refused; hidden <= 4096).
+ * Unknown bits: MI355MOE_EINVAL. Workspace sizes as mi355moe_moe_workspace_bytes_path (with MI355MOE_OPT_E4M3:
+ * mi355moe_e4m3_moe_workspace_bytes). */
+enum { MI355MOE_OPT_ACCUMULATE = 1, MI355MOE_OPT_BF16_CONTRIB = 2, MI355MOE_OPT_E4M3 = 4 };
+int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
+                                 int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
+                                 int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
+                                 int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, int path,
+                                 int stages, int options, hipStream_t stream);
+
 /* The thin/fat split of a prefill-size call (production's E3 branch, code/fork/docs/prod_exl3_reference.py:1659-1679,
  * with the cap of code/fork/glm53_prefill_cap.py): experts routed at most thin_cap rows run on the decode kernels
  * (16-row segments, limit after SiLU), the others on the grouped kernels (256-row tiles, limit before SiLU); both

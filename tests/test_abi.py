@@ -80,6 +80,17 @@ def test_argument_errors_before_any_launch():
     assert L.mi355moe_exl3_moe(*args, 0, 4, 4, 4, 1, 1, 1, 0, 1, 0, *tail[3:]) == 6   # mul1 codebook
 
 
+def test_forward_options_are_checked_before_any_launch():
+    from mi355moe import _lib
+    L = _lib.lib()
+    d = _fake_desc()
+    p = ctypes.c_void_p(0x1000)
+    args = [ctypes.byref(d), p, _lib.BF16, 1024, 4, p, _lib.I32, p, _lib.F32, 8, None, 0, 10.0, p, _lib.BF16, 1024,
+            p, 1 << 30]
+    assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_AUTO, _lib.STAGE_ALL, 8, None) == 1          # unknown bit
+    assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_DECODE, _lib.STAGE_ALL, _lib.OPT_E4M3, None) == 1
+
+
 def test_python_layer_rejects_cpu_tensors_and_bad_shapes():
     from mi355moe import ops
     with pytest.raises(ValueError):
