@@ -308,7 +308,7 @@ def run_prefill(args, torch, dev):
     from mi355moe import _lib, ops, synthetic
     T = args.prefill_tokens
     n_layers = 2
-    layers = [synthetic.exl3_layer(E, K, N, seed=400 + l, device=dev) for l in range(n_layers)]
+    layers = [synthetic.exl3_layer(E, K, N, seed=400 + l, device=dev, uniform_suh=True) for l in range(n_layers)]
     x = synthetic.activations(T, K, seed=500, device=dev)
     g = torch.Generator(device=dev)
     g.manual_seed(501)
@@ -373,7 +373,8 @@ def run_prefill(args, torch, dev):
                                  "frac": round(gu_flops / (gu_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
                                  "avg_launch_us": round(gu_ms * 1000.0, 1)},
             "prefill_config": f"T={T}, {E} experts, top-{TOPK}, uniform-random router logits, EXL3 4-bit synthetic "
-                              f"experts, {n_layers} layers alternated, {steps} timed steps"}
+                              f"experts sharing one w13 suh as the real checkpoints' layers do (one gathered row "
+                              f"per token), {n_layers} layers alternated, {steps} timed steps"}
 
 
 def run_prefill_zipf(args, torch, dev, caps=(0, 16, 32, 64, 128)):
@@ -382,7 +383,7 @@ def run_prefill_zipf(args, torch, dev, caps=(0, 16, 32, 64, 128)):
     with at most c rows on the decode kernels). Reports ms per layer call for each cap."""
     from mi355moe import ops, synthetic
     T = args.prefill_tokens
-    layer = synthetic.exl3_layer(E, K, N, seed=450, device=dev)
+    layer = synthetic.exl3_layer(E, K, N, seed=450, device=dev, uniform_suh=True)
     x = synthetic.activations(T, K, seed=451, device=dev)
     ids = synthetic.zipf_ids(T, E, TOPK, seed=452, device=dev)
     wts = synthetic.softmax_weights(T, TOPK, seed=453, device=dev)
@@ -487,7 +488,7 @@ def run_e4m3_trellis(args, torch, dev):
     from mi355moe import ops, synthetic
     T = args.fp8_tokens
     n_layers = 2
-    layers = [synthetic.exl3_layer(E, K, N, seed=640 + l, device=dev) for l in range(n_layers)]
+    layers = [synthetic.exl3_layer(E, K, N, seed=640 + l, device=dev, uniform_suh=True) for l in range(n_layers)]
     x = synthetic.activations(T, K, seed=660, device=dev)
     g = torch.Generator(device=dev)
     g.manual_seed(661)

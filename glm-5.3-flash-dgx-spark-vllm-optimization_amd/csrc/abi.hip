@@ -46,6 +46,10 @@ struct Carve {
 
 // The decode plan for P pairs.
 int shared_flag(const mi355moe_exl3_layer* L) { return (L->flags & MI355MOE_LAYER_SHARED_W13_SUH) ? 1 : 0; }
+// one w13 suh for every expert (and gate == up): the grouped path gathers one row per token
+int tok_rows_flag(const mi355moe_exl3_layer* L) {
+    return (L->flags & MI355MOE_LAYER_SHARED_W13_SUH) && (L->flags & MI355MOE_LAYER_UNIFORM_W13_SUH) ? 1 : 0;
+}
 
 struct DecodePlan {
     int rmax, seg, S_cap, sk_gu, sk_dn, kch_gu, kch_dn;
@@ -491,6 +495,7 @@ static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     d.odt = dt_w(out_dtype);
     d.out_stride = out_stride;
     d.e4m3 = e4m3 ? 1 : 0;
+    d.tok_rows = tok_rows_flag(layer);
     d.contrib_bf16 = (options & MI355MOE_OPT_BF16_CONTRIB) ? 1 : 0;
     d.out_accumulate = (options & MI355MOE_OPT_ACCUMULATE) ? 1 : 0;
     if (prefill_setup()) return rc_launch(-1);
@@ -731,6 +736,7 @@ int mi355moe_moe_forward_ids_split(const mi355moe_exl3_layer* layer, const void*
     a.xdt = dt_act(x_dtype);
     a.x_stride = x_stride;
     a.tok = w.fat.tok;
+    a.tok_rows = tok_rows_flag(layer);
     a.w16 = w.fat.w16;
     a.pe = w.fat.pe;
     a.inv = w.fat.inv;

@@ -36,6 +36,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Two fp32 values rounded to bf16 (round to nearest even, gfx950's v_cvt_pk_bf16_f32), packed lo | hi << 16.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // The codebook value of one 16-bit state (s < 2^16).
 __device__ __forceinline__ _Float16 mcg_value(uint32_t s) {
     const uint32_t x = ((s * MCG_MUL) & MCG_MASK) ^ MCG_FLIP;

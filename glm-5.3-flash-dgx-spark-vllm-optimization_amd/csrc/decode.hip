@@ -752,7 +752,7 @@ __global__ __launch_bounds__(128) void combine_kernel(DecodeArgs a) {
     if (a.odt == DT_F32) {
         *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.out) + o) = make_float2(s0, s1);
     } else if (a.odt == DT_BF16) {
-        const uint32_t v = (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);
+        const uint32_t v = pack_bf16x2(s0, s1);
         *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + o) = v;
     } else {
         *reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o) = h2{(_Float16)s0, (_Float16)s1};

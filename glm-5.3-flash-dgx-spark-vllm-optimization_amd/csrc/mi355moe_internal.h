@@ -136,6 +136,8 @@ struct PrefillArgs {
     // thin/fat split: rows with pe < 0 and pe_thin >= 0 were computed by the decode kernels, whose contrib rows hold
     // finished contributions (the combine adds them as they are); nullptr: no split
     const int* pe_thin;
+    // every expert shares one w13 suh: h13 (and, e4m3, asc) hold one row per token, row pos reads token tok[pos]'s
+    int tok_rows;
     int contrib_bf16;       // the down kernel stores its raw accumulators as bf16 (contrib viewed as bf16 [P][K])
     int out_accumulate;     // the combine adds the routed sum to out's current values (the shared-expert fold)
 };

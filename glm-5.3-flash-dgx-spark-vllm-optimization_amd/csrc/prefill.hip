@@ -61,6 +61,11 @@ __device__ __forceinline__ void pf_store_group(_Float16* grp, const uint32_t (&w
 // Work item i of a gather: the row it writes, the token it reads and the expert whose suh it applies; false when the
 // item is skipped (see PrefillArgs: sorted positions with pe/tok, caller row tables with tok64, or routed pairs).
 __device__ __forceinline__ bool pf_gather_item(const PrefillArgs& a, int i, int& pos, int& tok, int& e) {
+    if (a.tok_rows) {                                                 // one row per token, the layer's one suh
+        pos = tok = i;
+        e = 0;
+        return true;
+    }
     if (a.pair_pos) {
         e = a.pair_local[i];
         if (e < 0 || e >= a.n) return false;
@@ -83,10 +88,12 @@ __device__ __forceinline__ bool pf_gather_item(const PrefillArgs& a, int i, int&
 }
 // Number of work items of a gather (a device row count caps the caller's row tables).
 __device__ __forceinline__ int pf_gather_items(const PrefillArgs& a) {
+    if (a.tok_rows) return a.T;
     return a.nrows ? min(a.P, __builtin_amdgcn_readfirstlane(a.nrows[0])) : a.P;
 }
 
-// h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0. One wave per row
+// h13[pos] = rotated x[tok[pos]] with expert pe[pos]'s gate suh, for every row with pe >= 0 (tok_rows: h13[t] =
+// rotated x[t] with the suh every expert shares, for every token t). One wave per row
 // (grid-stride): a pass rotates four 128-blocks at once (16 lanes per block, lane c holding elements 8c .. 8c + 7,
 // DPP Hadamard); the loads of all passes of the row are issued before the first rotation.
 constexpr int PF_GATHER_PASSES = 8;                 // passes of 4 blocks in flight (K up to 4096 in one round)
@@ -177,7 +184,8 @@ __device__ __forceinline__ float e4m3_row_scale(float amax) {
     return sc > 0.0f ? sc : 1.0f;
 }
 
-// The e4m3 variant's gather (code/fork/kernels/moe_e4m3.cu:245-310, gather2): per row, v = H(x16 * suh) * r in fp32
+// The e4m3 variant's gather (code/fork/kernels/moe_e4m3.cu:245-310, gather2; with tok_rows one row per token, its
+// gather_tok): per row, v = H(x16 * suh) * r in fp32
 // (x rounded to fp16 first, the product and the butterflies in fp32, r applied after the transform), s = amax|v| /
 // 448, q = e4m3(clamp(v / s)) stored as the fp16 of each e4m3 value in h13's permuted order, asc[pos] = s; the row's
 // down-input maximum amaxd[pos] is zeroed for the gate/up epilogue. One wave per row; the whole row (K <= 4096) stays
@@ -251,9 +259,11 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
         }
         if (lane == 0) {
             a.asc[pos] = sc;
-            if (a.amaxd) a.amaxd[pos] = 0u;
+            if (a.amaxd && !a.tok_rows) a.amaxd[pos] = 0u;
         }
     }
+    if (a.amaxd && a.tok_rows)                                       // rows, not tokens: zeroed by a grid-stride loop
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < a.P; i += gridDim.x * blockDim.x) a.amaxd[i] = 0u;
 }
 
 // The e4m3 variant's down-input quantization: per row, s = amaxd / 448 (the maximum over the whole row, gathered by
@@ -287,7 +297,8 @@ __global__ __launch_bounds__(256) void pf_quantd_kernel(PrefillArgs a) {
 // columns = four trellis column tiles. MFMA column n of block s is column 16 (n / 8) + n % 8 + 8 s of the wave.
 // A rows come from `a_rows` (row stride kdim, k permuted as stored), clamped to rn - 1.
 struct PfTile {
-    const uint16_t* a_rows;       // first row of the segment
+    const uint16_t* a_rows;       // first row of the segment (a_tok: row 0 of the token-row buffer)
+    const int* a_tok;             // nullptr, or the segment's rows' tokens: row r is a_rows[a_tok[r]]
     int rn, kdim;
     const uint32_t* btr;          // this wave's trellis matrix
     int btiles_n;                 // tiles per trellis row (the matrix's column tiles)
@@ -409,7 +420,8 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     for (int i = 0; i < CPR; ++i) {
         const int R = 64 * wv + (64 / CPR) * i + lane / CPR;
         const int chunk = (lane % CPR) ^ pf_swz(R);
-        asrc[i] = t.a_rows + (size_t)min(R, t.rn - 1) * t.kdim + 8 * chunk;
+        const int rr = min(R, t.rn - 1);
+        asrc[i] = t.a_rows + (size_t)(t.a_tok ? t.a_tok[rr] : rr) * t.kdim + 8 * chunk;
     }
     // raw-word DMA sources: instruction i, lane -> k tile 2i + lane / 32, column tile (lane / 8) % 4, piece lane % 8
     const uint32_t* wsrc = t.btr + ((size_t)(lane >> 5) * t.btiles_n + t.bcol0 + ((lane >> 3) & 3)) * 32 + 4 * (lane & 7);
@@ -563,7 +575,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     const int K = a.K, N = a.N;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     PfTile t;                                                        // waves 0, 1: gate columns; 2, 3: up columns
-    t.a_rows = a.h13 + (size_t)row0 * K;
+    t.a_rows = a.tok_rows ? a.h13 : a.h13 + (size_t)row0 * K;       // tok_rows: the rows' tokens index h13
+    t.a_tok = a.tok_rows ? a.tok + row0 : nullptr;
     t.rn = rn;
     t.kdim = K;
     t.btr = reinterpret_cast<const uint32_t*>(wv < 2 ? a.wt.g_tr[e] : a.wt.u_tr[e]);
@@ -612,7 +625,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
                 u[i] = u4.x, u[i + 1] = u4.y, u[i + 2] = u4.z, u[i + 3] = u4.w;
             }
             if (E4M3) {                                              // dequantise: times the row's activation scale
-                const float rs = a.asc[row0 + min(trow, rn - 1)];
+                const int ar = row0 + min(trow, rn - 1);
+                const float rs = a.asc[a.tok_rows ? a.tok[ar] : ar];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     g[i] *= rs;
@@ -676,6 +690,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     PfTile t;
     t.a_rows = a.h2 + (size_t)row0 * N;
+    t.a_tok = nullptr;
     t.rn = rn;
     t.kdim = N;
     t.btr = reinterpret_cast<const uint32_t*>(a.wt.d_tr[e]);
@@ -691,35 +706,61 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
     const int n = lane & 31;
     const size_t c0 = (size_t)row0 * K + cb * 256 + 64 * wv + 16 * (n >> 3) + (n & 7);
+    // row blocks wholly inside the segment store unguarded (uniform test); only the block holding row rn is masked
     if (a.contrib_bf16) {
-        // bf16 raw accumulators: lanes n, n ^ 1 hold adjacent columns; they trade values (DPP lane ^ 1) so the even
-        // lane stores the pair (c, c + 1) of block 0 and the odd lane the pair (c - 1 + 8, c + 8) of block 1
+        // bf16 raw accumulators: lane n holds columns c (block 0) and c + 8 (block 1), its partner n ^ 1 columns
+        // c + 1 and c + 9 (n even). Each lane packs its own two values, takes the partner's pack (DPP lane ^ 1) and
+        // keeps one column pair: the even lane (c, c + 1), the odd lane (c + 8, c + 9), one 4-byte store each.
         uint16_t* ob = reinterpret_cast<uint16_t*>(a.contrib) + c0 + ((n & 1) ? 7 : 0);
+        const uint32_t sel = (n & 1) ? 0x03020706u : 0x05040100u;  // bytes of {partner, own}: odd hi halves, even lo
+        auto put = [&](int rb, int r) {
+            const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const uint32_t own = pack_bf16x2(acc[rb][0][r], acc[rb][1][r]);
+            const uint32_t par = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xB1, 0xF, 0xF, true);
+            return std::pair<uint32_t*, uint32_t>(reinterpret_cast<uint32_t*>(ob + (size_t)trow * K),
+                                                  __builtin_amdgcn_perm(par, own, sel));
+        };
 #pragma unroll
-        for (int rb = 0; rb < 8; ++rb)
+        for (int rb = 0; rb < 8; ++rb) {
+            if (32 * rb >= rn) break;
+            if (32 * rb + 32 <= rn) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const float mine = (n & 1) ? acc[rb][1][r] : acc[rb][0][r];
-                const float give = (n & 1) ? acc[rb][0][r] : acc[rb][1][r];
-                const float got = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, give),
-                                                                                     0xB1, 0xF, 0xF, true));
-                const uint32_t lo = f32_to_bf16((n & 1) ? got : mine), hi = f32_to_bf16((n & 1) ? mine : got);
-                if (trow < rn) *reinterpret_cast<uint32_t*>(ob + (size_t)trow * K) = lo | (hi << 16);
+                for (int r = 0; r < 16; ++r) {
+                    const auto pv = put(rb, r);
+                    *pv.first = pv.second;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const auto pv = put(rb, r);                       // (the DPP runs with every lane active)
+                    if (32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3) < rn) *pv.first = pv.second;
+                }
             }
+        }
         return;
     }
     float* o = a.contrib + c0;
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb)
+    for (int rb = 0; rb < 8; ++rb) {
+        if (32 * rb >= rn) break;
+        if (32 * rb + 32 <= rn) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (trow < rn) {
+            for (int r = 0; r < 16; ++r) {
+                const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 o[(size_t)trow * K] = acc[rb][0][r];
                 o[(size_t)trow * K + 8] = acc[rb][1][r];
             }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (trow < rn) {
+                    o[(size_t)trow * K] = acc[rb][0][r];
+                    o[(size_t)trow * K + 8] = acc[rb][1][r];
+                }
+            }
         }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ combine
@@ -832,7 +873,7 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     } else if (a.odt == DT_BF16) {
         uint32_t* op = reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + o);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) op[i] = (uint32_t)f32_to_bf16(sum[2 * i]) | ((uint32_t)f32_to_bf16(sum[2 * i + 1]) << 16);
+        for (int i = 0; i < 4; ++i) op[i] = pack_bf16x2(sum[2 * i], sum[2 * i + 1]);
     } else {
         h2* op = reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o);
 #pragma unroll

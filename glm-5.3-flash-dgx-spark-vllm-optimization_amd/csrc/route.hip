@@ -122,84 +122,6 @@ __global__ __launch_bounds__(1024) void router_logits_kernel(const uint16_t* __r
 constexpr int TOPK_MAX_E = 1024;   // experts per token row
 constexpr int TOPK_MAX_K = 32;
 
-// 1024 threads per token: scores s = sigmoid(logit) (through double exp) and choice keys s + bias go to
-// LDS; every candidate's rank = the number of candidates with a larger key, or an equal key and a lower id (ranks
-// are distinct and follow the reference's order: largest first, lower id on ties). Q = 1024 / E16 threads share a
-// candidate, each counting over a slice of the keys; the topk lowest ranks write themselves to their slot and the
-// renormalising total is summed sequentially in pick order. blockDim.x = 512 or 1024 >= E16.
-__device__ __forceinline__ void topk_body(const float* __restrict__ lrow, int E, const float* __restrict__ bias,
-                                          int topk, float scale, int renorm, int32_t* __restrict__ ids_row,
-                                          float* __restrict__ wts_row) {
-    __shared__ __align__(16) float key[TOPK_MAX_E];
-    __shared__ float sco[TOPK_MAX_E];
-    __shared__ int part[1024];
-    __shared__ int pick_e[TOPK_MAX_K];
-    __shared__ float pick_s[TOPK_MAX_K];
-    const int tid = threadIdx.x;
-    const int E16 = (E + 15) & ~15;                                  // keys padded with -inf (never ahead of a key)
-    const int BD = blockDim.x;                                       // 512 or 1024; E16 <= BD
-    for (int e = tid; e < E16; e += BD) {
-        float sv = 0.f, kv = -__builtin_inff();
-        if (e < E) {
-            const float lg = lrow[e];
-            sv = (float)(1.0 / (1.0 + exp(-(double)lg)));
-            kv = sv + (bias ? bias[e] : 0.f);
-        }
-        sco[e] = sv;
-        key[e] = kv;
-    }
-    __syncthreads();
-    const int Q = E16 <= BD / 4 ? 4 : (E16 <= BD / 2 ? 2 : 1);
-    const int c = tid / Q, p = tid - c * Q;
-    const int slice = E16 / Q;                                       // a multiple of 4 (E16 % 16 == 0)
-    int greater = 0, tie = 0;
-    if (c < E) {
-        const float v = key[c];
-        const f32x4* k4 = reinterpret_cast<const f32x4*>(key + p * slice);
-        int equal = 0;
-        for (int j4 = 0; j4 < slice / 4; ++j4) {
-            const f32x4 u = k4[j4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                greater += u[i] > v;
-                equal += u[i] == v;
-            }
-        }
-        if (c >= p * slice && c < p * slice + slice) --equal;       // the candidate itself
-        if (equal)                                                   // rare: equal keys, lower ids come first
-            for (int j = p * slice; j < p * slice + slice && j < c; ++j) tie += key[j] == v;
-    }
-    part[tid] = greater + tie;
-    __syncthreads();
-    if (p == 0 && c < E) {
-        int rank = 0;
-        for (int i = 0; i < Q; ++i) rank += part[tid + i];
-        if (rank < topk) {
-            pick_e[rank] = c;
-            pick_s[rank] = sco[c];
-        }
-    }
-    __syncthreads();
-    if (tid < topk) {
-        float total = 0.f;
-        for (int k = 0; k < topk; ++k) total = total + pick_s[k];
-        float wv = pick_s[tid];
-        if (renorm) wv = __fdiv_rn(wv, total + 1e-20f);
-        wv = wv * scale;
-        ids_row[tid] = pick_e[tid];
-        wts_row[tid] = wv;
-    }
-}
-
-// grid T, 1024 threads: one token's top-k per workgroup
-__global__ __launch_bounds__(1024) void router_topk_kernel(const float* __restrict__ logits, int T, int E,
-                                                           const float* __restrict__ bias, int topk, float scale,
-                                                           int renorm, int32_t* __restrict__ ids,
-                                                           float* __restrict__ wts) {
-    const int t = blockIdx.x;
-    topk_body(logits + (size_t)t * E, E, bias, topk, scale, renorm, ids + (size_t)t * topk, wts + (size_t)t * topk);
-}
-
 // ------------------------------------------------------------------------------------------------ permutation
 
 template <typename IT>
@@ -440,9 +362,10 @@ __device__ __forceinline__ uint64_t topk_order(float key, int e) {
 }
 
 // One wave's top-k of one token (E <= 1024 candidates, lane l holding candidates l + 64 j): topk rounds of "largest
-// order key" (the lane-local best, then a butterfly max over the wave); the owner of the winner drops it. Scores s
-// (sigmoid through double exp, as topk_body) go to sco [E] for the weights; weights are renormalised over the picks
-// summed in pick order and scaled, as topk_body.
+// order key" (the lane-local best, then a butterfly max over the wave); the owner of the winner drops it, so picks
+// come largest first, lower id on ties (the reference's order). Scores s = sigmoid(logit) (through double exp) go to
+// sco [E] for the weights; weights are the picks' scores renormalised over their total (summed sequentially in pick
+// order, + 1e-20, correctly rounded division) and scaled.
 // Maximum of a 64-bit value over the wave, returned in every lane: rotations by 1, 2, 4, 8 inside each 16-lane row
 // (DPP, no LDS), then the four row maxima by readlane.
 template <int CTRL>
@@ -514,6 +437,22 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E,
         ids_sh[lane] = mine_e;
         wts_sh[lane] = wv * scale;
     }
+}
+
+// One wave per token, four tokens per 256-thread workgroup: topk_wave over the token's logits (scores in LDS).
+template <int J>
+__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T, int E,
+                                                          const float* __restrict__ bias, int topk, float scale,
+                                                          int renorm, int32_t* __restrict__ ids,
+                                                          float* __restrict__ wts) {
+    __shared__ float sco[4 * 64 * J];
+    __shared__ int ids_sh[4 * TOPK_MAX_K];
+    __shared__ float wts_sh[4 * TOPK_MAX_K];
+    const int wv = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wv;
+    if (t >= T) return;                                              // uniform over the wave (no block barrier)
+    topk_wave<J>(logits + (size_t)t * E, E, bias, topk, scale, renorm, sco + wv * 64 * J, ids + (size_t)t * topk,
+                 wts + (size_t)t * topk, ids_sh + wv * TOPK_MAX_K, wts_sh + wv * TOPK_MAX_K);
 }
 
 // The decode-size front end in one workgroup (P = T topk <= ROUTE_SMALL_MAX_P): wave w of the workgroup's nw takes
@@ -747,9 +686,11 @@ int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w,
 
 int launch_router_topk(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
                        int32_t* ids, float* wts, hipStream_t st) {
-    if (T > 0)
-        hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(1024), 0, st, logits, T, E, bias, topk, scale, renorm,
-                           ids, wts);
+    if (E > TOPK_MAX_E || topk > TOPK_MAX_K) return -1;
+    const dim3 g((T + 3) / 4);
+    if (T <= 0) return 0;
+    if (E <= 320) hipLaunchKernelGGL(router_topk_kernel<5>, g, dim3(256), 0, st, logits, T, E, bias, topk, scale, renorm, ids, wts);
+    else hipLaunchKernelGGL(router_topk_kernel<16>, g, dim3(256), 0, st, logits, T, E, bias, topk, scale, renorm, ids, wts);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -17,6 +17,7 @@ STAGE_ROUTE, STAGE_GATEUP, STAGE_DOWN, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 8, 15
 PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
 OPT_ACCUMULATE, OPT_BF16_CONTRIB, OPT_E4M3 = 1, 2, 4
 LAYER_SHARED_W13_SUH = 1
+LAYER_UNIFORM_W13_SUH = 2
 PREFILL_MIN_PAIRS = 4096
 NOALLOC_SCRATCH_BYTES = 32 << 20
 ESCRATCH = 7

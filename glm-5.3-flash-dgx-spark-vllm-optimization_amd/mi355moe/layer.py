@@ -79,6 +79,9 @@ class Exl3Experts:
         }
         # gate and up share one input rotation (production's _exl3_shared_w13_suh, prod_exl3_reference.py:2243-2245)
         self.shared_suh = bool(torch.equal(self.w13_suh[:, 0], self.w13_suh[:, 1]))
+        # ... and every expert the same one (the reference's TOKGATHER condition, code/fork/docs/OPT_MOE.md:14)
+        self.uniform_suh = self.shared_suh and bool(torch.equal(self.w13_suh[:, 0],
+                                                                self.w13_suh[:1, 0].expand(n, K)))
         self.desc = self.make_desc(self.tables)
 
     def make_desc(self, tables: dict) -> _lib.Exl3LayerDesc:
@@ -86,7 +89,8 @@ class Exl3Experts:
         d.n, d.hidden, d.intermediate = self.n, self.K, self.N
         for k, v in tables.items():
             setattr(d, k, ctypes.c_void_p(v.data_ptr()))
-        d.flags = _lib.LAYER_SHARED_W13_SUH if self.shared_suh else 0
+        d.flags = ((_lib.LAYER_SHARED_W13_SUH if self.shared_suh else 0) |
+                   (_lib.LAYER_UNIFORM_W13_SUH if self.uniform_suh else 0))
         return d
 
     @property
@@ -121,12 +125,15 @@ def _check_aligned(name: str, t: torch.Tensor, n: int) -> None:
     _CHECKED_TABLES.add(key)
 
 
-def tables_desc(n: int, K: int, N: int, tables: dict, shared_suh: bool = False) -> _lib.Exl3LayerDesc:
+def tables_desc(n: int, K: int, N: int, tables: dict, shared_suh: bool = False,
+                uniform_suh: bool = False) -> _lib.Exl3LayerDesc:
     """Descriptor from caller-built pointer tables (the exl3_moe contract passes them directly); every table entry is
-    checked for 16-byte alignment the first time the table is seen."""
+    checked for 16-byte alignment the first time the table is seen. uniform_suh (every expert the same w13 suh)
+    implies shared_suh."""
     d = _lib.Exl3LayerDesc()
     d.n, d.hidden, d.intermediate = n, K, N
-    d.flags = _lib.LAYER_SHARED_W13_SUH if shared_suh else 0
+    d.flags = ((_lib.LAYER_SHARED_W13_SUH if shared_suh or uniform_suh else 0) |
+               (_lib.LAYER_UNIFORM_W13_SUH if uniform_suh else 0))
     for k in ("gate_trellis", "gate_suh", "gate_svh", "up_trellis", "up_suh", "up_svh", "down_trellis", "down_suh",
               "down_svh"):
         t = tables[k]

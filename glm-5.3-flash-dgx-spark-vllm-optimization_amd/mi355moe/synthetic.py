@@ -25,15 +25,19 @@ def _signs(shape, g, device) -> torch.Tensor:
 
 
 def exl3_layer(n: int, K: int, N: int, seed: int, device="cuda", svh_scale: float = 0.01,
-               svh_d_scale: float | None = None, shared_suh: bool = True) -> Exl3Experts:
+               svh_d_scale: float | None = None, shared_suh: bool = True,
+               uniform_suh: bool = False) -> Exl3Experts:
     """One layer of n random EXL3 4-bit experts in production's stacked layout. shared_suh: gate and up share
     one input rotation, as production's checkpoints do (its grouped prefill tier requires it,
-    code/fork/docs/prod_exl3_reference.py:376)."""
+    code/fork/docs/prod_exl3_reference.py:376). uniform_suh: every expert the same w13 suh too, as in the real
+    checkpoints' layers (code/fork/docs/OPT_MOE.md:14)."""
     device = torch.device(device)
     g = _gen(seed, device)
     w13_trellis = torch.randint(-32768, 32768, (n, 2, K // 16, N // 16, 64), generator=g, device=device,
                                 dtype=torch.int32).to(torch.int16)
     w13_suh = _signs((n, 2, K), g, device).to(torch.float16)
+    if uniform_suh:
+        w13_suh.copy_(w13_suh[:1, :1].clone().expand(n, 2, K))
     if shared_suh:
         w13_suh[:, 1].copy_(w13_suh[:, 0])
     w13_svh = (_signs((n, 2, N), g, device) * torch.randn((n, 2, N), generator=g, device=device).abs()
@@ -64,13 +68,14 @@ def _scaled_signs(shape, scale, g, device) -> torch.Tensor:
 
 
 def calibrated_layer(n: int, K: int, N: int, seed: int, device="cuda", g_std: float = 5.0, svh_d: float = 0.001,
-                     shared_suh: bool = True) -> Exl3Experts:
+                     shared_suh: bool = True, uniform_suh: bool = False) -> Exl3Experts:
     """n random EXL3 4-bit experts with scales calibrated as the reference's test harness does
     (code/fork/tests/harness.py:178-200): suh, svh and down suh are random signs x (1 +- 25 %) x a scale, the gate/up
     svh scale chosen so that the gate and up pre-activations have standard deviation g_std for x ~ N(0, 1)
     (std(g) = sqrt(K) * codebook std * E|suh| * E|svh|); with g_std = 5 and the SwiGLU limit 10 about 5 % of the
     gate values are clamped. Down suh ~ 8 / sqrt(N) as there; the down svh scale (svh_d; the reference uses 1.0, which
-    gives routed outputs of RMS ~200) is 0.001 by default, for routed outputs of RMS ~0.2."""
+    gives routed outputs of RMS ~200) is 0.001 by default, for routed outputs of RMS ~0.2. uniform_suh: every expert
+    the same w13 suh (as in the real checkpoints' layers)."""
     device = torch.device(device)
     g = _gen(seed, device)
     mag_rms = math.sqrt(1 + 0.25 ** 2 / 3)
@@ -78,6 +83,8 @@ def calibrated_layer(n: int, K: int, N: int, seed: int, device="cuda", g_std: fl
     w13_trellis = torch.randint(-32768, 32768, (n, 2, K // 16, N // 16, 64), generator=g, device=device,
                                 dtype=torch.int32).to(torch.int16)
     w13_suh = _scaled_signs((n, 2, K), 1.0, g, device)
+    if uniform_suh:
+        w13_suh.copy_(w13_suh[:1, :1].clone().expand(n, 2, K))
     if shared_suh:
         w13_suh[:, 1].copy_(w13_suh[:, 0])
     w13_svh = _scaled_signs((n, 2, N), s_svh, g, device)

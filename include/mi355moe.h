@@ -64,6 +64,11 @@ typedef struct mi355moe_exl3_layer {
 /* gate and up share one input rotation (w13_suh[:, 0] == w13_suh[:, 1], production's _exl3_shared_w13_suh,
  * code/fork/docs/prod_exl3_reference.py:2243-2245); the grouped prefill path requires it (:376) */
 #define MI355MOE_LAYER_SHARED_W13_SUH 1
+/* every expert of the layer has the same w13 suh (with MI355MOE_LAYER_SHARED_W13_SUH): the rotated gate/up input
+ * does not depend on the expert, so the grouped path gathers one row per token instead of one per routed pair and
+ * its gate/up GEMM reads A rows through the rows' tokens (the reference's TOKGATHER, code/fork/docs/OPT_MOE.md:14;
+ * true of the real checkpoints' layers). Same results bit for bit; the flag only changes the schedule. */
+#define MI355MOE_LAYER_UNIFORM_W13_SUH 2
 
 int mi355moe_abi_version(void);
 const char* mi355moe_strerror(int code);

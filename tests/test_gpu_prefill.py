@@ -138,3 +138,51 @@ def test_prefill_full_size_vs_decode_path(cuda):
     r = (torch.linalg.norm((a - b).double()) / torch.linalg.norm(b.double())).item()
     _say(f"prefill vs decode rel_l2 {r:.3e}")
     assert r <= 5e-3
+
+
+@pytest.mark.parametrize("numerics,T,n,K,N", [("e3", 700, 16, 1024, 512), ("e4m3", 700, 16, 1024, 512),
+                                              ("e3", 8192, 288, 4096, 1024), ("split", 2000, 64, 1024, 512)])
+def test_token_rows_gather_bit_exact(cuda, numerics, T, n, K, N):
+    """Experts sharing one w13 suh (MI355MOE_LAYER_UNIFORM_W13_SUH): the grouped path gathers one row per token and
+    the gate/up GEMM reads rows through their tokens. The output equals the per-pair gather's (the same layer with the
+    flag cleared) bit for bit, for E3 and e4m3 numerics and the thin/fat split; E3 is also checked against the
+    oracle's rounding points on sampled tokens."""
+    from mi355moe import _lib, ops, synthetic
+    _say(f"token-row gather {numerics} T={T} n={n} K={K} N={N}")
+    ex = synthetic.calibrated_layer(n, K, N, seed=T + n, device=cuda, uniform_suh=True)
+    assert ex.uniform_suh and ex.desc.flags == _lib.LAYER_SHARED_W13_SUH | _lib.LAYER_UNIFORM_W13_SUH
+    x = synthetic.activations(T, K, seed=T + 1, device=cuda)
+    ids = (synthetic.zipf_ids(T, n, 8, seed=T + 2, device=cuda) if numerics == "split" else
+           synthetic.random_ids(T, n, 8, seed=T + 2, device=cuda))
+    ids[1, 2] = -1
+    w = synthetic.softmax_weights(T, 8, seed=T + 3, device=cuda)
+
+    def run():
+        if numerics == "e4m3":
+            return ops.moe_forward_ids_e4m3(ex, x, ids, w, out_dtype=torch.float32)
+        if numerics == "split":
+            return ops.moe_forward_ids_split(ex, x, ids, w, 16, out_dtype=torch.float32)
+        return ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+
+    a = run()
+    ex.desc.flags = _lib.LAYER_SHARED_W13_SUH
+    b = run()
+    ex.desc.flags = _lib.LAYER_SHARED_W13_SUH | _lib.LAYER_UNIFORM_W13_SUH
+    torch.cuda.synchronize()
+    assert torch.isfinite(a).all()
+    assert torch.equal(a, b)
+    if numerics == "e3":
+        sample = np.array([0, 1, 2, T // 2, T - 1])
+        sel_t = torch.from_numpy(sample).to(cuda)
+        ids_s, w_s = ids[sel_t].cpu().numpy(), w[sel_t].cpu().numpy()
+        used = np.unique(ids_s[ids_s >= 0])
+        remap = {int(e): i for i, e in enumerate(used)}
+        local = np.vectorize(lambda v: remap.get(int(v), len(used)))(ids_s)
+        sel = torch.as_tensor(used, dtype=torch.long, device=cuda)
+        lay = {k: getattr(ex, k).index_select(0, sel).cpu().numpy() for k in
+               ("w13_trellis", "w13_suh", "w13_svh", "w2_trellis", "w2_suh", "w2_svh")}
+        tok, exx, w16 = moe.pairs_from_routing(local, w_s, len(used), 8)
+        ref_k = moe.forward(lay, x[sel_t].to(torch.float16).cpu().numpy(), tok, exx, w16, 10.0, "e3")
+        r = _rel(a[sel_t].cpu().numpy(), ref_k)
+        _say(f"  rel_l2 vs E3 rounding points {r:.3e}")
+        assert r <= 5e-4, r

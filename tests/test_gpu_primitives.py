@@ -100,15 +100,17 @@ def test_router_picks_4096_tokens(cuda):
     assert np.array_equal(wts[:64].cpu().numpy(), rw)
 
 
-@pytest.mark.parametrize("T,E,topk", [(64, 288, 8), (5, 32, 4), (3, 1024, 32)])
+@pytest.mark.parametrize("T,E,topk", [(64, 288, 8), (5, 32, 4), (3, 1024, 32), (8193, 288, 8), (7, 320, 8),
+                                      (6, 321, 8), (2, 1, 1)])
 def test_router_topk_bit_exact(cuda, T, E, topk):
     from mi355moe import ops
     _say(f"router_topk T={T} E={E} topk={topk}")
     g = torch.Generator().manual_seed(T + E)
     lg = torch.randn(T, E, generator=g) * 2
     b = torch.randn(E, generator=g) * 0.01
-    lg[0, 7] = lg[0, 9]
-    b[7] = b[9]                                   # an exact tie
+    if E > 9:
+        lg[0, 7] = lg[0, 9]
+        b[7] = b[9]                               # an exact tie
     ids, w = ops.router_topk(lg.to(cuda), topk, b.to(cuda), routed_scale=2.5)
     rid, rw = routing.topk_sigmoid_bias(lg.numpy(), b.numpy(), topk, 2.5)
     assert np.array_equal(ids.cpu().numpy(), rid)
