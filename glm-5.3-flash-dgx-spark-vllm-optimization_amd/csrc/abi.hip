@@ -537,8 +537,10 @@ int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x
     if (!x || !ids || !weights || !out || !workspace) return MI355MOE_EINVAL;
     if (stages <= 0 || stages > MI355MOE_STAGE_ALL) return MI355MOE_EINVAL;
     if (path < MI355MOE_PATH_AUTO || path > MI355MOE_PATH_PREFILL) return MI355MOE_EINVAL;
-    if (options & ~(MI355MOE_OPT_ACCUMULATE | MI355MOE_OPT_BF16_CONTRIB | MI355MOE_OPT_E4M3)) return MI355MOE_EINVAL;
+    if (options & ~(MI355MOE_OPT_ACCUMULATE | MI355MOE_OPT_BF16_CONTRIB | MI355MOE_OPT_E4M3 | MI355MOE_OPT_PERSISTENT))
+        return MI355MOE_EINVAL;
     const bool e4m3 = (options & MI355MOE_OPT_E4M3) != 0;
+    if (options & MI355MOE_OPT_PERSISTENT) return MI355MOE_EUNSUPPORTED;      // switched off (see the header)
     if (e4m3 && path == MI355MOE_PATH_DECODE) return MI355MOE_EINVAL;      // e4m3 numerics run on the grouped tier
     if (e4m3 && layer && layer->hidden > 4096) return MI355MOE_EUNSUPPORTED;
     if (dt_act(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;

@@ -15,7 +15,7 @@ ABI_VERSION = 1
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
 STAGE_ROUTE, STAGE_GATEUP, STAGE_DOWN, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 8, 15
 PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
-OPT_ACCUMULATE, OPT_BF16_CONTRIB, OPT_E4M3 = 1, 2, 4
+OPT_ACCUMULATE, OPT_BF16_CONTRIB, OPT_E4M3, OPT_PERSISTENT = 1, 2, 4, 8
 LAYER_SHARED_W13_SUH = 1
 LAYER_UNIFORM_W13_SUH = 2
 PREFILL_MIN_PAIRS = 4096

@@ -212,13 +212,14 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
                     limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
                     out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL,
                     path: int = _lib.PATH_AUTO, accumulate: bool = False,
-                    bf16_contrib: bool = False) -> torch.Tensor:
+                    bf16_contrib: bool = False, persistent: bool = False) -> torch.Tensor:
     """Routed-expert output [T, K] (x's dtype unless out/out_dtype say otherwise), written, or with accumulate added
     to out's values (the shared-expert fold: out holds the shared experts' output; fp32 sum, one rounding).
     path: _lib.PATH_AUTO (decode kernels for few pairs, the grouped MFMA prefill kernels for many), or forced.
     stages: a subset of the call's launches (_lib.STAGE_*), for timing one kernel; the default runs them all.
     bf16_contrib: the grouped path keeps its per-pair down accumulators in bf16 (half the contribution traffic;
-    code/fork/docs/OPT_MOE.md:13)."""
+    code/fork/docs/OPT_MOE.md:13). persistent: the one-launch ticket-ordered schedule of the grouped path
+    (code/fork/kernels/moe_e4m3.cu:867-897); not available in this build (the library refuses it)."""
     if accumulate and out is None:
         raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
@@ -242,7 +243,8 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
         raise ValueError("mi355moe_moe_workspace_bytes rejected the shape")
     ws = workspace(dev, nb)
     em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
-    opts = (_lib.OPT_ACCUMULATE if accumulate else 0) | (_lib.OPT_BF16_CONTRIB if bf16_contrib else 0)
+    opts = ((_lib.OPT_ACCUMULATE if accumulate else 0) | (_lib.OPT_BF16_CONTRIB if bf16_contrib else 0) |
+            (_lib.OPT_PERSISTENT if persistent else 0))
     _lib.check("mi355moe_moe_forward_ids", L.mi355moe_moe_forward_ids_opt(
         ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
         ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em), 0 if em is None else em.numel(),

@@ -155,9 +155,12 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
  *                             accumulators (relative error about 2^-9 per element). No effect on the decode path.
  *   MI355MOE_OPT_E4M3         the trellis-sourced e4m3 numerics of mi355moe_e4m3_moe_forward_ids (grouped path
  *                             only: path DECODE is refused; hidden <= 4096).
+ *   MI355MOE_OPT_PERSISTENT   reserved for a one-launch, ticket-ordered gate/up + down schedule of the grouped path
+ *                             (the reference's code/fork/kernels/moe_e4m3.cu:867-897); not available in this build:
+ *                             every call with it returns MI355MOE_EUNSUPPORTED before any launch.
  * Unknown bits: MI355MOE_EINVAL. Workspace sizes as mi355moe_moe_workspace_bytes_path (with MI355MOE_OPT_E4M3:
  * mi355moe_e4m3_moe_workspace_bytes). */
-enum { MI355MOE_OPT_ACCUMULATE = 1, MI355MOE_OPT_BF16_CONTRIB = 2, MI355MOE_OPT_E4M3 = 4 };
+enum { MI355MOE_OPT_ACCUMULATE = 1, MI355MOE_OPT_BF16_CONTRIB = 2, MI355MOE_OPT_E4M3 = 4, MI355MOE_OPT_PERSISTENT = 8 };
 int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
                                  int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
                                  int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,

@@ -1,0 +1,84 @@
+"""GPU checks of the one-launch ticket-ordered schedule of the grouped path (MI355MOE_OPT_PERSISTENT): gate/up and
+down tiles taken from per-XCD ticket queues, a down tile waiting on its segment's gate/up count. Same kernels per
+tile, so the output equals the separate launches' bit for bit: uniform and Zipf routing, full size, fewer segments
+than queues, one-block routing, bf16 accumulators, and stage-split calls that rely on the control words being left at
+zero."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skip(reason="the one-launch schedule took a GPU memory fault on its first run and no cause "
+                                      "was found by reading it; the library refuses MI355MOE_OPT_PERSISTENT until "
+                                      "one is")]
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+@pytest.mark.parametrize("n,K,N,T,routing,uniform", [(16, 1024, 512, 700, "uniform", False),
+                                                     (64, 1024, 512, 4096, "zipf", True),
+                                                     (4, 1024, 256, 20, "uniform", False),
+                                                     (16, 1024, 512, 100, "zipf", False),
+                                                     (288, 4096, 1024, 8192, "uniform", True)])
+def test_persistent_equals_separate_launches(cuda, n, K, N, T, routing, uniform):
+    from mi355moe import _lib, ops, synthetic
+    _say(f"persistent schedule n={n} K={K} N={N} T={T} {routing} uniform_suh={uniform}")
+    ex = synthetic.calibrated_layer(n, K, N, seed=n + T, device=cuda, uniform_suh=uniform)
+    topk = min(8, n)
+    x = synthetic.activations(T, K, seed=T + 1, device=cuda)
+    ids = (synthetic.zipf_ids(T, n, topk, seed=T + 2, device=cuda) if routing == "zipf" else
+           synthetic.random_ids(T, n, topk, seed=T + 2, device=cuda))
+    ids[0, 1] = -1
+    w = synthetic.softmax_weights(T, topk, seed=T + 3, device=cuda)
+    for b16 in (False, True):
+        ref = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL, bf16_contrib=b16)
+        got = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL, bf16_contrib=b16,
+                                  persistent=True)
+        again = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL,
+                                    bf16_contrib=b16, persistent=True)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got).all()
+        assert torch.equal(got, ref), (got - ref).abs().max().item()
+        assert torch.equal(again, ref)
+
+
+def test_persistent_stage_split_calls(cuda):
+    """Route once, then the gate/up + down + combine stages twice with new activations: the second launch finds its
+    tickets and segment counts back at zero (left so by the first) and equals the separate launches."""
+    from mi355moe import _lib, ops, synthetic
+    _say("persistent schedule, stage-split calls")
+    n, K, N, T = 32, 1024, 512, 1500
+    ex = synthetic.calibrated_layer(n, K, N, seed=5, device=cuda)
+    ids = synthetic.random_ids(T, n, 8, seed=6, device=cuda)
+    w = synthetic.softmax_weights(T, 8, seed=7, device=cuda)
+    kw = dict(path=_lib.PATH_PREFILL, persistent=True)
+    out = torch.empty(T, K, dtype=torch.float32, device=cuda)
+    x0 = synthetic.activations(T, K, seed=8, device=cuda)
+    ops.moe_forward_ids(ex, x0, ids, w, out=out, stages=_lib.STAGE_ROUTE, **kw)
+    for seed in (9, 10):
+        x = synthetic.activations(T, K, seed=seed, device=cuda)
+        ops.moe_forward_ids(ex, x, ids, w, out=out, stages=_lib.STAGE_GATEUP | _lib.STAGE_DOWN | _lib.STAGE_COMBINE,
+                            **kw)
+        ref = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+
+
+def test_persistent_refused_with_e4m3(cuda):
+    from mi355moe import _lib, ops, synthetic
+    ex = synthetic.calibrated_layer(8, 1024, 256, seed=1, device=cuda)
+    x = synthetic.activations(64, 1024, seed=2, device=cuda)
+    ids = synthetic.random_ids(64, 8, 4, seed=3, device=cuda)
+    w = synthetic.softmax_weights(64, 4, seed=4, device=cuda)
+    out = torch.empty(64, 1024, dtype=torch.float32, device=cuda)
+    L = _lib.lib()
+    import ctypes
+    ws = ops.workspace(cuda, L.mi355moe_e4m3_moe_workspace_bytes(ctypes.byref(ex.desc), 64, 4))
+    rc = L.mi355moe_moe_forward_ids_opt(
+        ctypes.byref(ex.desc), ops._p(x), ops.act_dtype_code(x.dtype), x.stride(0), 64, ops._p(ids), _lib.I32,
+        ops._p(w), _lib.F32, 4, None, 0, 10.0, ops._p(out), _lib.F32, out.stride(0), ops._p(ws), ws.numel(),
+        _lib.PATH_PREFILL, _lib.STAGE_ALL, _lib.OPT_E4M3 | _lib.OPT_PERSISTENT, ops._stream(cuda))
+    assert rc == 6                                                # MI355MOE_EUNSUPPORTED, before any launch
