@@ -111,6 +111,55 @@ __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int6
     }
 }
 
+// Large-T router GEMM on the float64 matrix cores (v_mfma_f64_16x16x4_f64): a wave computes 16 tokens x 32 experts
+// (two 16 x 16 blocks) over all of K. The bf16 inputs are widened exactly to float64 and every product and sum of the
+// MFMA is float64, so -- the terms spanning far fewer binades than float64 holds, as in logits_body -- the sums are the
+// exact dot products whatever their order, and the logits equal the GEMV kernel's bit for bit. The reduction order is
+// free, so lane group g = lane / 16 (the MFMA's k index) walks its own contiguous quarter of K, k = g K / 4 + j,
+// with 16-byte loads of 8 consecutive bf16. MFMA layouts (16 x 16 x 4, float64): A[i][k] from lane i + 16 k, B[k][j]
+// from lane j + 16 k, D[i][j] in lane j + 16 (i % 4), element i / 4 (rows interleaved by 4, unlike the 16 x 16
+// layouts of the narrower types).
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+constexpr int RG_TOK = 16, RG_EXP = 32;   // tokens x experts per wave
+__global__ __launch_bounds__(256) void router_gemm_f64_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                              const uint16_t* __restrict__ w, int T, int K, int E,
+                                                              float* __restrict__ logits) {
+    const int lane = threadIdx.x & 63;
+    const int tiles_e = (E + RG_EXP - 1) / RG_EXP;
+    const int tile = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int t0 = (tile / tiles_e) * RG_TOK, e0 = (tile % tiles_e) * RG_EXP;
+    if (t0 >= T) return;                                             // uniform over the wave (no block barrier)
+    const int g = lane >> 4, r = lane & 15;
+    const int kq = K >> 2;
+    const uint16_t* xa = x + (size_t)min(t0 + r, T - 1) * x_stride + (size_t)g * kq;
+    const uint16_t* wb0 = w + (size_t)min(e0 + r, E - 1) * K + (size_t)g * kq;
+    const uint16_t* wb1 = w + (size_t)min(e0 + 16 + r, E - 1) * K + (size_t)g * kq;
+    f64x4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+    for (int k = 0; k < kq; k += 8) {
+        const u32x4 av = *reinterpret_cast<const u32x4*>(xa + k);
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(wb0 + k);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(wb1 + k);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int sh = (q & 1) ? 0 : 16;                         // element q of a dword pair: low half first
+            const uint32_t m = 0xFFFF0000u;
+            const double a = (double)__builtin_bit_cast(float, (av[q >> 1] << sh) & m);
+            const double c0 = (double)__builtin_bit_cast(float, (b0[q >> 1] << sh) & m);
+            const double c1 = (double)__builtin_bit_cast(float, (b1[q >> 1] << sh) & m);
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, c0, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, c1, acc1, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int t = t0 + g + 4 * v;
+        if (t >= T) continue;
+        if (e0 + r < E) logits[(size_t)t * E + e0 + r] = router_round(acc0[v]);
+        if (e0 + 16 + r < E) logits[(size_t)t * E + e0 + 16 + r] = router_round(acc1[v]);
+    }
+}
+constexpr int RG_MIN_T = 256;   // from this many tokens the MFMA GEMM beats the GEMV kernel
+
 __global__ __launch_bounds__(1024) void router_logits_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
                                                              const uint16_t* __restrict__ w, int T, int K, int E,
                                                              float* __restrict__ logits) {
@@ -680,7 +729,14 @@ __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
 
 int launch_router_logits(const uint16_t* x, int64_t x_stride, const uint16_t* w, int T, int K, int E, float* logits,
                          hipStream_t st) {
-    hipLaunchKernelGGL(router_logits_kernel, dim3(E), dim3(64 * (K / 512)), 0, st, x, x_stride, w, T, K, E, logits);
+    if (T >= RG_MIN_T) {
+        const int64_t waves = (int64_t)((T + RG_TOK - 1) / RG_TOK) * ((E + RG_EXP - 1) / RG_EXP);
+        hipLaunchKernelGGL(router_gemm_f64_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, x_stride, w,
+                           T, K, E, logits);
+    } else {
+        hipLaunchKernelGGL(router_logits_kernel, dim3(E), dim3(64 * (K / 512)), 0, st, x, x_stride, w, T, K, E,
+                           logits);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -81,6 +81,28 @@ def test_router_logits_bit_exact(cuda, T):
     assert np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("T,E,K", [(255, 288, 4096), (256, 288, 4096), (1000, 100, 1024), (4097, 17, 512),
+                                   (300, 1, 8192)])
+def test_router_logits_large_t_bit_exact(cuda, T, E, K):
+    """From 256 tokens the logits come from the float64 MFMA GEMM (16 tokens x 32 experts per wave, each lane group
+    walking its own quarter of K): ragged tokens and experts, the smallest and largest K, bit for bit against the
+    oracle, and the constructed midpoint cases in the first rows."""
+    from mi355moe import ops, synthetic
+    _say(f"router_logits T={T} E={E} K={K}")
+    w, _ = synthetic.router(E, K, seed=E + K, device="cpu")
+    x = synthetic.activations(T, K, seed=T, device="cpu")
+    x[:2] = 0
+    w[0] = 0
+    x[0, :3] = torch.tensor([1.0, 2.0 ** -8, 2.0 ** -15])
+    x[1, K - 3:] = torch.tensor([1.0, 2.0 ** -8, 2.0 ** -15])      # in the last lane group's quarter of K
+    w[0, :3] = torch.tensor([1.0, 1.0, 2.0 ** -15])
+    w[0, K - 3:] = torch.tensor([1.0, 1.0, 2.0 ** -7])
+    got = ops.router_logits(x.to(cuda), w.to(cuda)).cpu().numpy()
+    ref = routing.router_logits(x.float().numpy(), w.float().numpy())
+    assert got[0, 0] == 1.0 and got[1, 0] == 1.0 + 2.0 ** -7
+    assert np.array_equal(got, ref)
+
+
 def test_router_picks_4096_tokens(cuda):
     """Top-8 sets of 4,096 tokens from the GPU router (logits + top-k) against the top-8 of the reference's router
     oracle, bf16(float64 dot) (code/fork/tests/router_topk_agreement.py:82): ids in pick order bit for bit (largest
