@@ -357,6 +357,13 @@ def run_prefill(args, torch, dev):
         ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], accumulate=True, bf16_contrib=True)
 
     ms_fold = _time_calls(torch, step_fold, n_layers, 2, steps)
+    # the whole routed layer from the hidden states: router GEMM (float64 matrix cores), top-k, permutation, experts
+    w_r, b_r = synthetic.router(E, K, seed=502, device=dev)
+
+    def step_layer(l):
+        ops.moe_layer(layers[l], x, router_w=w_r, topk=TOPK, bias=b_r, routed_scale=SCALE, limit=LIMIT, out=outs[l])
+
+    ms_layer = _time_calls(torch, step_layer, n_layers, 2, steps)
     P = sum(pairs) / len(pairs)
     flops = 2.0 * P * (K * 2 * N + N * K)
     gu_flops = 2.0 * P * K * 2 * N
@@ -366,6 +373,7 @@ def run_prefill(args, torch, dev):
                                                              min(16, os.cpu_count() or 1))
     return {**extra, "prefill_tokens_per_s": round(T / (ms / 1000.0), 1), "prefill_ms_per_layer": round(ms, 4),
             "prefill_bf16acc_fold_ms_per_layer": round(ms_fold, 4),
+            "prefill_layer_with_router_ms": round(ms_layer, 4),
             "prefill_tflops": round(flops / (ms / 1000.0) / 1e12, 2),
             "roofline_prefill": {"bound": "mfma", "kernel": "pf_gateup_kernel (includes the gather launch)",
                                  "achieved": round(gu_flops / (gu_ms / 1000.0) / 1e12, 2),

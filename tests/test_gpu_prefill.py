@@ -186,3 +186,45 @@ def test_token_rows_gather_bit_exact(cuda, numerics, T, n, K, N):
         r = _rel(a[sel_t].cpu().numpy(), ref_k)
         _say(f"  rel_l2 vs E3 rounding points {r:.3e}")
         assert r <= 5e-4, r
+
+
+@pytest.mark.parametrize("case", ["one_token", "t17", "eight_experts_hold_every_row", "half_non_local"])
+def test_prefill_edge_cases(cuda, case):
+    """Edge cases of the reference's accumulator tests (code/fork/docs/OPT_MOE.md:25-27: T=1 and 17, one expert
+    holding every row, half the experts non-local) on the grouped path, against the oracle's E3 rounding points
+    (rel_l2 <= 5e-4) and float64 (bf16 elementwise rtol 2e-2 / atol 1e-3); tokens with no local expert get exact
+    zeros."""
+    from mi355moe import _lib, ops, synthetic
+    _say(f"prefill edge case {case}")
+    n, K, N, topk = 16, 1024, 512, 8
+    T = {"one_token": 1, "t17": 17, "eight_experts_hold_every_row": 700, "half_non_local": 600}[case]
+    ex = synthetic.calibrated_layer(n, K, N, seed=31 + T, device=cuda, uniform_suh=(case == "t17"))
+    x = synthetic.activations(T, K, seed=T + 5, device=cuda)
+    w = synthetic.softmax_weights(T, topk, seed=T + 6, device=cuda)
+    emap = None
+    if case == "eight_experts_hold_every_row":
+        ids = torch.arange(topk, dtype=torch.int32, device=cuda).repeat(T, 1)      # 700 rows in each of 8 experts
+    elif case == "half_non_local":
+        n_global = 2 * n                                                           # 32 global experts, 16 local
+        ids = synthetic.random_ids(T, n_global, topk, seed=T + 7, device=cuda)
+        ids[:5] = torch.arange(0, 2 * topk, 2, dtype=torch.int32, device=cuda)     # tokens 0..4: no local expert
+        em = torch.full((n_global,), -1, dtype=torch.int64)
+        em[1::2] = torch.arange(n)                                                 # odd global ids are local
+        emap = em.to(cuda)
+    else:
+        ids = synthetic.random_ids(T, n, topk, seed=T + 7, device=cuda)
+    out32 = ops.moe_forward_ids(ex, x, ids, w, expert_map=emap, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+    out_bf = ops.moe_forward_ids(ex, x, ids, w, expert_map=emap, out_dtype=torch.bfloat16, path=_lib.PATH_PREFILL)
+    torch.cuda.synchronize()
+    lay = _np_layer(ex)
+    local = routing.map_topk_to_local(ids.cpu().numpy(), n, None if emap is None else emap.cpu().numpy())
+    tok, exx, w16 = moe.pairs_from_routing(local, w.cpu().numpy(), n, topk)
+    x16 = x.to(torch.float16).cpu().numpy()
+    ref_k = moe.forward(lay, x16, tok, exx, w16, 10.0, "e3")
+    ref64 = moe.forward(lay, x16, tok, exx, w16, 10.0, "f64_pre")
+    got = out32.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert _rel(got, ref_k) <= 5e-4, _rel(got, ref_k)
+    assert np.allclose(out_bf.float().cpu().numpy(), ref64, rtol=2e-2, atol=1e-3)
+    if case == "half_non_local":
+        assert not got[:5].any()
