@@ -698,7 +698,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+              "(the layer's tensor- and expert-parallel sharding is designed, not run)", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
