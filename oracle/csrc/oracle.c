@@ -208,6 +208,66 @@ void orc_rot_in(const uint16_t* x16, const uint16_t* suh16, int n, uint16_t* out
 /* sigmoid as this build defines it: 1 / (1 + (float)exp(-(double)g)), IEEE fp32 division */
 static inline float sigm(float g) { return 1.0f / (1.0f + (float)exp(-(double)g)); }
 
+/* ---------------------------------------------------------------- the reference's default (TF_PARITY=1) epilogues
+ * code/fork/kernels/exl3.cu:31-32 (TF_PARITY defaults to 1), :351-357 (fp16 SiLU), :371-436 (gate/up epilogue),
+ * :455-496 (down epilogue). fp16 arithmetic is IEEE binary16 with one rounding per operation: a product or a sum of
+ * two fp16 values is exact in double, so rounding that double once is the correctly rounded fp16 result. The
+ * reference's SiLU uses the CUDA half intrinsics h2exp / h2rcp; here exp and the reciprocal are the correctly
+ * rounded fp16 values of the exact functions (libm exp and a division in double, each then rounded once to fp16),
+ * so an element can differ from the reference by an ulp where an intrinsic is not correctly rounded (the
+ * reference's own stage test, code/fork/docs/DESIGN.md:553-554, allows 1 fp16 ulp on 1 % of elements there). */
+static inline float h_add(float a, float b) { return orc_h2f(orc_d2h((double)a + (double)b)); }
+static inline float h_exp(float a) { return orc_h2f(orc_d2h(exp((double)a))); }
+static inline float h_rcp(float a) { return orc_h2f(orc_d2h(1.0 / (double)a)); }
+static inline float h_min(float a, float b) { return b < a ? b : a; }
+static inline float h_max(float a, float b) { return b > a ? b : a; }
+
+/* x * (1 / (1 + exp(-x))) in fp16, x an fp16 value (exl3.cu:351-357) */
+float orc_silu_h(float x) {
+    const float e = h_exp(-x);
+    const float r = h_rcp(h_add(1.0f, e));
+    return hmul(x, r);
+}
+
+/* Gate/up epilogue of one pair row with the reference's default rounding points (exl3.cu:371-436): the fp32 GEMV
+ * sums zg / zu [N] rounded to fp16, rotated per 128 block in fp32, times r rounded to fp16, times svh in fp16,
+ * g = silu_h(g), then (L != 0) u clamped to [fp16(-L), fp16(L)] and g to at most fp16(L), a = g * u * suh_d in
+ * fp16, rotated in fp32 and stored as fp16(H(a) * r) into xd [N]. zg / zu are not modified. */
+void orc_gateup_epilogue_tf(const float* zg, const float* zu, const uint16_t* svh_g, const uint16_t* svh_u,
+                            const uint16_t* suh_d, int N, float limit, uint16_t* xd) {
+    float g[128], u[128], v[128];
+    const float lo = rh(-limit), hi = rh(limit);
+    for (int b0 = 0; b0 < N; b0 += 128) {
+        for (int i = 0; i < 128; ++i) { g[i] = rh(zg[b0 + i]); u[i] = rh(zu[b0 + i]); }
+        orc_fwht128(g);
+        orc_fwht128(u);
+        for (int i = 0; i < 128; ++i) {
+            float gh = hmul(rh(g[i] * HAD_R), orc_h2f(svh_g[b0 + i]));
+            float uh = hmul(rh(u[i] * HAD_R), orc_h2f(svh_u[b0 + i]));
+            gh = orc_silu_h(gh);
+            if (limit != 0.0f) {
+                uh = h_min(h_max(uh, lo), hi);
+                gh = h_min(gh, hi);
+            }
+            v[i] = hmul(hmul(gh, uh), orc_h2f(suh_d[b0 + i]));
+        }
+        orc_fwht128(v);
+        for (int i = 0; i < 128; ++i) xd[b0 + i] = orc_f2h(v[i] * HAD_R);
+    }
+}
+
+/* Down epilogue of one pair row with the reference's default rounding points (exl3.cu:455-496): the fp32 sums
+ * zd [K] rounded to fp16, rotated per 128 block in fp32, times (r * w) and then svh_d in fp32, into out [K]. */
+void orc_down_epilogue_tf(const float* zd, const uint16_t* svh_d, uint16_t w16, int K, float* out) {
+    float v[128];
+    const float rs = HAD_R * orc_h2f(w16);
+    for (int b0 = 0; b0 < K; b0 += 128) {
+        for (int i = 0; i < 128; ++i) v[i] = rh(zd[b0 + i]);
+        orc_fwht128(v);
+        for (int i = 0; i < 128; ++i) out[b0 + i] = v[i] * rs * orc_h2f(svh_d[b0 + i]);
+    }
+}
+
 /* ---------------------------------------------------------------- one layer of routed experts */
 
 typedef struct {
@@ -230,6 +290,8 @@ typedef struct {
  * mode 3: float64 reference with the limit before SiLU iff L != 0 (production's python loop, prod:961-1006).
  * mode 4: mode 0 with every weight taken as fp16(lo) + fp16(hi) of its codebook word without the final fp16
  *         rounding (the decode GEMV feeds both halves to the matrix cores, whose fp32 sum is exact).
+ * mode 5: the reference's default decode numerics (TF_PARITY=1, exl3.cu:31-32): fp32 GEMV sums over fp16 weights
+ *         and inputs, with orc_gateup_epilogue_tf / orc_down_epilogue_tf as the epilogues.
  * out[T][K] (fp32, or double for modes 2/3 through out64) is accumulated into in pair order per token.
  * Returns 0, or -1 on a bad argument.
  */
@@ -240,7 +302,7 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
     if (K % 128 || N % 128 || T < 0 || P < 0) return -1;
     const int KT = K / 16, NT = N / 16;
     const int f64 = mode == 2 || mode == 3;
-    if (mode < 0 || mode > 4) return -1;
+    if (mode < 0 || mode > 5) return -1;
     orc_init();
     const float* cbt = mode == 4 ? g_cbx : g_cbf;
     /* per-pair contribution rows, summed per token in pair order afterwards (deterministic) */
@@ -295,7 +357,8 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
                         for (int c = 0; c < N; ++c) { zg[c] += a * rg[c]; zu[c] += b * ru[c]; }
                     }
                     float* act = tmp + 2 * N;
-                    for (int b0 = 0; b0 < N; b0 += 128) {
+                    if (mode == 5) orc_gateup_epilogue_tf(zg, zu, svh_g, svh_u, suh_d, N, limit, xdd);
+                    else for (int b0 = 0; b0 < N; b0 += 128) {
                         orc_fwht128(zg + b0);
                         orc_fwht128(zu + b0);
                         for (int i = 0; i < 128; ++i) {
@@ -330,7 +393,8 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
                     const float w = orc_h2f(pair_w16[j]);
                     const float rs = HAD_R * w;
                     float* dst = c32 + (size_t)j * K;
-                    for (int b0 = 0; b0 < K; b0 += 128) {
+                    if (mode == 5) orc_down_epilogue_tf(zd, svh_d, pair_w16[j], K, dst);
+                    else for (int b0 = 0; b0 < K; b0 += 128) {
                         orc_fwht128(zd + b0);
                         for (int i = 0; i < 128; ++i) {
                             float v;

@@ -9,6 +9,11 @@ module loads it with ctypes and exposes:
                           mode "f64_pre" : float64 reference, limit before SiLU (code/fork/docs/prod_exl3_reference.py:961-1006)
                           mode "decode_x": "decode" with every weight fp16(lo) + fp16(hi) unrounded (the decode GEMV
                                            feeds both codebook halves to the matrix cores)
+                          mode "tf_parity": the reference's default decode numerics (TF_PARITY=1,
+                                           code/fork/kernels/exl3.cu:31-32, :351-496): fp16 roundings of the GEMV
+                                           sums, fp16 svh / SiLU / limit / suh_d products, correctly rounded fp16
+                                           exp and reciprocal in the SiLU
+  silu_h / gateup_epilogue_tf / down_epilogue_tf   the "tf_parity" epilogues on their own
   pairs_from_routing      (token, local expert, fp16 weight) per routed pair, invalid ids skipped
 """
 from __future__ import annotations
@@ -22,7 +27,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _SO = os.path.join(_HERE, "_build", "liboracle.so")
 _LIB = None
-MODES = {"decode": 0, "e3": 1, "f64": 2, "f64_pre": 3, "decode_x": 4}
+MODES = {"decode": 0, "e3": 1, "f64": 2, "f64_pre": 3, "decode_x": 4, "tf_parity": 5}
 
 
 class _Layer(ctypes.Structure):
@@ -55,6 +60,11 @@ def lib() -> ctypes.CDLL:
         L.orc_fwht128.argtypes = [ctypes.c_void_p]
         L.orc_rot_in.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
         L.orc_expf_via_double.restype = ctypes.c_float
+        L.orc_silu_h.restype = ctypes.c_float
+        L.orc_silu_h.argtypes = [ctypes.c_float]
+        L.orc_gateup_epilogue_tf.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p]
+        L.orc_down_epilogue_tf.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint16, ctypes.c_int,
+                                           ctypes.c_void_p]
         L.orc_expf_via_double.argtypes = [ctypes.c_float]
         L.orc_moe_forward.restype = ctypes.c_int
         L.orc_moe_forward.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
@@ -108,6 +118,40 @@ def rot_in_c(x16: np.ndarray, suh16: np.ndarray) -> np.ndarray:
     return out
 
 
+def silu_h(x16: np.ndarray) -> np.ndarray:
+    """fp16 SiLU of the reference's default numerics, elementwise over fp16 values."""
+    x = np.asarray(x16, np.float16).ravel()
+    f = lib().orc_silu_h
+    return np.array([f(float(v)) for v in x], np.float32).astype(np.float16).reshape(np.shape(x16))
+
+
+def gateup_epilogue_tf(zg: np.ndarray, zu: np.ndarray, svh_g: np.ndarray, svh_u: np.ndarray, suh_d: np.ndarray,
+                       limit: float) -> np.ndarray:
+    """One pair row: fp32 GEMV sums zg / zu [N] -> the down GEMV's fp16 input [N] (exl3.cu:371-436, TF_PARITY=1)."""
+    zg = np.ascontiguousarray(zg, np.float32)
+    zu = np.ascontiguousarray(zu, np.float32)
+    args = [np.ascontiguousarray(a, np.float16) for a in (svh_g, svh_u, suh_d)]
+    N = zg.size
+    if N % 128 or zu.size != N or any(a.size != N for a in args):
+        raise ValueError("gateup_epilogue_tf: rows of one length, a multiple of 128")
+    out = np.zeros(N, np.float16)
+    lib().orc_gateup_epilogue_tf(_p(zg), _p(zu), *[_p(a) for a in args], N, float(limit), _p(out))
+    return out
+
+
+def down_epilogue_tf(zd: np.ndarray, svh_d: np.ndarray, w16) -> np.ndarray:
+    """One pair row: fp32 down GEMV sums zd [K] -> the pair's fp32 contribution (exl3.cu:455-496, TF_PARITY=1)."""
+    zd = np.ascontiguousarray(zd, np.float32)
+    sv = np.ascontiguousarray(svh_d, np.float16)
+    K = zd.size
+    if K % 128 or sv.size != K:
+        raise ValueError("down_epilogue_tf: rows of one length, a multiple of 128")
+    out = np.zeros(K, np.float32)
+    w = int(np.asarray(w16, np.float16).view(np.uint16))
+    lib().orc_down_epilogue_tf(_p(zd), _p(sv), w, K, _p(out))
+    return out
+
+
 def pairs_from_routing(local: np.ndarray, weights: np.ndarray, n: int, topk: int):
     """(token, expert, fp16 weight) of every routed pair j = t*topk + k in pair order; the sentinel (local id n)
     and invalid ids keep expert -1 so the forward skips them."""
@@ -121,8 +165,8 @@ def pairs_from_routing(local: np.ndarray, weights: np.ndarray, n: int, topk: int
 
 def forward(layer: dict, x16: np.ndarray, pair_token: np.ndarray, pair_expert: np.ndarray, pair_w16: np.ndarray,
             limit: float, mode: str = "decode", threads: int = 0) -> np.ndarray:
-    """Routed output [T, K] (float32 for the kernel modes, float64 for the f64 modes), summed per token in pair
-    order. layer: numpy arrays w13_trellis int16 [n,2,K/16,N/16,64], w13_suh/w13_svh fp16 [n,2,K]/[n,2,N],
+    """Routed output [T, K] (float32 for the kernel and tf_parity modes, float64 for the f64 modes), summed per
+    token in pair order. layer: numpy arrays w13_trellis int16 [n,2,K/16,N/16,64], w13_suh/w13_svh fp16 [n,2,K]/[n,2,N],
     w2_trellis int16 [n,N/16,K/16,64], w2_suh fp16 [n,N], w2_svh fp16 [n,K]."""
     arrs = {k: np.ascontiguousarray(layer[k]) for k in
             ("w13_trellis", "w13_suh", "w13_svh", "w2_trellis", "w2_suh", "w2_svh")}

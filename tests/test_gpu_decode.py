@@ -97,6 +97,32 @@ def test_sentinels_map_and_duplicates(cuda, layer32):
     assert torch.count_nonzero(z).item() == 0
 
 
+@pytest.mark.parametrize("limit", [10.0, 1.0])
+def test_decode_within_reference_bar_of_its_default_numerics(cuda, limit):
+    """The decode kernels round at fp32 points (the reference's NATIVE epilogues); the reference's production build
+    rounds to fp16 at more points (TF_PARITY=1, code/fork/kernels/exl3.cu:31-32, the oracle's "tf_parity" mode).
+    Bound: the reference's own bar between its build and production (code/fork/docs/DESIGN.md:520-523: global
+    rel_l2 <= 2e-3, per row <= 1e-2), on a layer calibrated so that the L = 10 clamp fires (harness.py:178-186),
+    plus the elementwise rtol 2e-2 / atol 1e-3 on the bf16 output."""
+    from mi355moe import ops, synthetic
+    n, T, topk = 32, 8, 8
+    _say(f"decode vs tf_parity limit={limit}")
+    ex = synthetic.calibrated_layer(n, K, N, seed=41, device=cuda, shared_suh=False)
+    lay = _np_layer(ex)
+    x = synthetic.activations(T, K, seed=42, device=cuda)
+    ids = synthetic.random_ids(T, n, topk, seed=43, device=cuda)
+    w = synthetic.softmax_weights(T, topk, seed=44, device=cuda)
+    got = ops.moe_forward_ids(ex, x, ids, w, limit=limit, out_dtype=torch.float32).cpu().numpy()
+    gb = ops.moe_forward_ids(ex, x, ids, w, limit=limit, out_dtype=torch.bfloat16).float().cpu().numpy()
+    tf = _oracle(lay, x, ids, w, n, limit, "tf_parity").astype(np.float64)
+    rel = _rel(got, tf)
+    rows = np.linalg.norm(got - tf, axis=1) / np.linalg.norm(tf, axis=1)
+    _say(f"  rel_l2 {rel:.3e}, worst row {rows.max():.3e}")
+    assert rel <= 2e-3, rel
+    assert rows.max() <= 1e-2, rows.max()
+    assert np.allclose(gb, tf, rtol=2e-2, atol=1e-3)
+
+
 def test_deterministic_and_graph_replay(cuda, layer32):
     from mi355moe import ops, synthetic
     ex, _ = layer32
