@@ -707,7 +707,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(RouteArgs a, int nblk)
 }
 
 __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
-    __shared__ int loc[ROUTE_BLK];
+    __shared__ __align__(16) int loc[ROUTE_BLK];
     const int j0 = blockIdx.x * ROUTE_BLK;
     const int j = j0 + threadIdx.x;
     const int nj = min(ROUTE_BLK, a.P - j0);
@@ -715,8 +715,23 @@ __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
     __syncthreads();
     if (threadIdx.x >= nj) return;
     const int l = loc[threadIdx.x];
+    // rank among the block's earlier pairs with the same id: the earlier waves' pairs (a bound uniform over the
+    // wave, four per LDS read), then this wave's earlier lanes
+    const int w0 = threadIdx.x & ~63;
+    const int4* l4 = reinterpret_cast<const int4*>(loc);
     int rank = 0;
-    for (int i = 0; i < (int)threadIdx.x; ++i) rank += loc[i] == l;
+#pragma unroll 8
+    for (int i4 = 0; i4 < (w0 >> 2); ++i4) {
+        const int4 v = l4[i4];
+        rank += (v.x == l) + (v.y == l) + (v.z == l) + (v.w == l);
+    }
+    const int me = threadIdx.x;
+#pragma unroll
+    for (int i4 = w0 >> 2; i4 < (w0 >> 2) + 16; ++i4) {
+        const int4 v = l4[i4];
+        const int i = 4 * i4;
+        rank += (i < me && v.x == l) + (i + 1 < me && v.y == l) + (i + 2 < me && v.z == l) + (i + 3 < me && v.w == l);
+    }
     const int pos = a.blk_cnt[(size_t)blockIdx.x * (a.n + 1) + l] + rank;
     a.tok[pos] = j / a.topk;
     a.w16[pos] = weight_f16(a.w, a.wdt, j);
