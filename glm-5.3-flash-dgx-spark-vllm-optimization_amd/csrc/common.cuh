@@ -82,24 +82,31 @@ __device__ __forceinline__ int opaque_lane() {
     return l;
 }
 
-// One stage of fwht128_x16 across lanes: partner = the value of lane l ^ m (m = 1, 2, 8 via DPP control CTRL);
-// the lower lane of the pair keeps own + partner, the upper partner - own (fma with +-1: exact, one rounding).
-template <int CTRL>
-__device__ __forceinline__ void fwht_xstage(float (&v)[8], bool upper) {
-    const float sg = upper ? -1.0f : 1.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float p = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v[i]), CTRL, 0xF,
-                                                                           0xF, true));
-        v[i] = __builtin_fmaf(v[i], sg, p);
-    }
-}
+// v[i] += c * v[i] of lane l ^ m for the 8 values, one v_fmac_f32 with a DPP source per value (control CTL:
+// quad_perm [1,0,3,2] for m = 1, [2,3,0,1] for m = 2, row_ror:8 for m = 8). s_nop 1 gives the two wait states a DPP
+// read needs after a VALU write of its source; inside the block each source was written eight instructions earlier.
+#define MI355_FMAC_DPP8(v, c, CTL)                                                                                   \
+    asm("s_nop 1\n\t"                                                                                             \
+        "v_fmac_f32_dpp %0, %0, %8 " CTL " row_mask:0xf bank_mask:0xf\n\t"                                         \
+        "v_fmac_f32_dpp %1, %1, %8 " CTL " row_mask:0xf bank_mask:0xf\n\t"                                         \
+        "v_fmac_f32_dpp %2, %2, %8 " CTL " row_mask:0xf bank_mask:0xf\n\t"                                         \
+        "v_fmac_f32_dpp %3, %3, %8 " CTL " row_mask:0xf bank_mask:0xf\n\t"                                         \
+        "v_fmac_f32_dpp %4, %4, %8 " CTL " row_mask:0xf bank_mask:0xf\n\t"                                         \
+        "v_fmac_f32_dpp %5, %5, %8 " CTL " row_mask:0xf bank_mask:0xf\n\t"                                         \
+        "v_fmac_f32_dpp %6, %6, %8 " CTL " row_mask:0xf bank_mask:0xf\n\t"                                         \
+        "v_fmac_f32_dpp %7, %7, %8 " CTL " row_mask:0xf bank_mask:0xf"                                               \
+        : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])        \
+        : "v"(c))
 
 // 128-point Walsh-Hadamard of four blocks per wave held 8 consecutive elements per lane (block = lane / 16, elements
-// 8 (lane % 16) .. + 7): the butterfly order of fwht128_w64 (element strides 1, 2, 4 in registers, then 8, 16, 32,
-// 64 across lanes xor 1, 2, 4, 8 inside each 16-lane row, by DPP), the lower element of every pair keeping a + b
-// and the upper a - b, so the results are bit-identical.
-__device__ __forceinline__ void fwht128_x16(float (&v)[8], int lane) {
+// 8 (lane % 16) .. + 7), in the butterfly order of fwht128_w64 (element strides 1, 2, 4 in registers, then 8, 16, 32,
+// 64 across lanes xor 1, 2, 4, 8 inside each 16-lane row, by DPP), each value returned times the lane's sign
+// fwht_sign(lane) = (-1)^popcount(lane % 16). The butterfly's upper element is a - b; a cross-lane stage here keeps
+// own + c * partner with c = -1 on the upper lane of a pair (for lanes xor 1, 2, 8 one v_fmac_f32 with a DPP source
+// per value), i.e. the upper result negated. Round-to-nearest is symmetric, so every value is the butterfly's, bit for
+// bit, up to that sign; the caller folds the sign into its next multiply (an exact +-1 factor).
+__device__ __forceinline__ float fwht_sign(int lane) { return (__builtin_popcount(lane & 15) & 1) ? -1.0f : 1.0f; }
+__device__ __forceinline__ void fwht128_x16s(float (&v)[8], int lane) {
 #pragma unroll
     for (int h = 1; h < 8; h <<= 1) {
 #pragma unroll
@@ -110,20 +117,18 @@ __device__ __forceinline__ void fwht128_x16(float (&v)[8], int lane) {
                 v[i + h] = a - b;
             }
     }
-    fwht_xstage<0xB1>(v, lane & 1);                                  // quad_perm [1,0,3,2]: lane ^ 1
-    fwht_xstage<0x4E>(v, lane & 2);                                  // quad_perm [2,3,0,1]: lane ^ 2
-    {
-        // lane ^ 4: row_ror:12 reads lane + 4 (lanes 0-3, 8-11 of a row), row_ror:4 lane - 4 (banks 1 and 3)
-        const float sg = (lane & 4) ? -1.0f : 1.0f;
+    const float c1 = (lane & 1) ? -1.0f : 1.0f, c2 = (lane & 2) ? -1.0f : 1.0f, c4 = (lane & 4) ? -1.0f : 1.0f,
+                c8 = (lane & 8) ? -1.0f : 1.0f;
+    MI355_FMAC_DPP8(v, c1, "quad_perm:[1,0,3,2]");
+    MI355_FMAC_DPP8(v, c2, "quad_perm:[2,3,0,1]");
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int x = __builtin_bit_cast(int, v[i]);
-            const int lo = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0xF, true);
-            const float p = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(lo, x, 0x124, 0xF, 0xA, false));
-            v[i] = __builtin_fmaf(v[i], sg, p);
-        }
+    for (int i = 0; i < 8; ++i) {                                     // lane ^ 4: row_ror:12 reads lane + 4 (banks 0, 2),
+        const int x = __builtin_bit_cast(int, v[i]);                  // row_ror:4 lane - 4 (banks 1, 3)
+        const int lo = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0xF, true);
+        const float p = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(lo, x, 0x124, 0xF, 0xA, false));
+        v[i] = __builtin_fmaf(p, c4, v[i]);                           // exact product, one rounding
     }
-    fwht_xstage<0x128>(v, lane & 8);                                 // row_ror:8: lane ^ 8
+    MI355_FMAC_DPP8(v, c8, "row_ror:8");
 }
 
 // The value of lane l ^ M (M = 1, 2, 4, 8, 16, 32) without LDS: quad permutes (1, 2), two row rotations with bank

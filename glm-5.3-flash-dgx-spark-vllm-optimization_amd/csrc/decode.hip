@@ -107,7 +107,7 @@ __device__ __forceinline__ int xa_pos(int k) {
 
 // Staged-input preparation, four 128-blocks per wave (one per 16-lane row, 8 consecutive inputs per lane):
 // rot8_load fetches a lane's 8 inputs and 8 suh values, rot8_scale forms fp16(x * suh) as floats (bf16 inputs are
-// first rounded to fp16, as x.half() does), fwht128_x16 rotates, and the stores write fp16(v * r) into the staged
+// first rounded to fp16, as x.half() does), fwht128_x16s rotates, and the stores write fp16(v * r) into the staged
 // row in the matrix-core order (xa_pos), plain or duplicated.
 struct RotIn8 {
     uint32_t x[4];
@@ -149,18 +149,18 @@ __device__ __forceinline__ uint32_t dup16(_Float16 h) {
 }
 // 8 consecutive values at local k0 (a multiple of 8) of a staged row: value j goes to position xa_pos(k0 + j) =
 // 16 (k0 / 16) + 4 (j / 2) + j % 2 + 2 ((k0 / 8) % 2), as halves (plain) or duplicated dwords
-__device__ __forceinline__ void stage8_store(const float (&p)[8], uint16_t* row, int k0) {
+__device__ __forceinline__ void stage8_store(const float (&p)[8], float hr, uint16_t* row, int k0) {
     uint16_t* d = row + (k0 & ~15) + 2 * ((k0 >> 3) & 1);
 #pragma unroll
     for (int m = 0; m < 4; ++m)
-        *reinterpret_cast<h2*>(d + 4 * m) = h2{(_Float16)(p[2 * m] * HAD_R), (_Float16)(p[2 * m + 1] * HAD_R)};
+        *reinterpret_cast<h2*>(d + 4 * m) = h2{(_Float16)(p[2 * m] * hr), (_Float16)(p[2 * m + 1] * hr)};
 }
-__device__ __forceinline__ void stage8_store_dup(const float (&p)[8], uint32_t* row, int k0) {
+__device__ __forceinline__ void stage8_store_dup(const float (&p)[8], float hr, uint32_t* row, int k0) {
     uint32_t* d = row + (k0 & ~15) + 2 * ((k0 >> 3) & 1);
 #pragma unroll
     for (int m = 0; m < 4; ++m)
         *reinterpret_cast<uint2*>(d + 4 * m) =
-            make_uint2(dup16((_Float16)(p[2 * m] * HAD_R)), dup16((_Float16)(p[2 * m + 1] * HAD_R)));
+            make_uint2(dup16((_Float16)(p[2 * m] * hr)), dup16((_Float16)(p[2 * m + 1] * hr)));
 }
 
 // Segments of up to DUP_ROWS rows stage each input duplicated into a dword (x, x) at dword xa_pos(k) of the row,
@@ -320,11 +320,12 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
     auto task_store = [&](int task, const RotIn8& vv) {
         float p[8];
         rot8_scale(vv, a.xdt, p);
-        fwht128_x16(p, lane);
+        fwht128_x16s(p, lane);
+        const float hr = HAD_R * fwht_sign(lane);                    // r and the sign fwht128_x16s leaves
         const int r = task / (NMAT * nb), rem = task - r * NMAT * nb, mat = rem / nb, b = rem - mat * nb;
         if (task < ntask) {
-            if (dup) stage8_store_dup(p, xw + (size_t)r * RSD, b * 128 + 8 * l16);
-            else stage8_store(p, xs + (size_t)(mat * rn + r) * RSH, b * 128 + 8 * l16);
+            if (dup) stage8_store_dup(p, hr, xw + (size_t)r * RSD, b * 128 + 8 * l16);
+            else stage8_store(p, hr, xs + (size_t)(mat * rn + r) * RSH, b * 128 + 8 * l16);
         }
     };
     constexpr int QB = 1;                                            // quads per wave per batch
@@ -499,12 +500,13 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
         *reinterpret_cast<float4*>(g + 4) = *reinterpret_cast<const float4*>(zs + r * 128 + 8 * el16 + 4);
         *reinterpret_cast<float4*>(u) = *reinterpret_cast<const float4*>(zs + (ZS_ROWS + r) * 128 + 8 * el16);
         *reinterpret_cast<float4*>(u + 4) = *reinterpret_cast<const float4*>(zs + (ZS_ROWS + r) * 128 + 8 * el16 + 4);
-        fwht128_x16(g, ln);
-        fwht128_x16(u, ln);
+        fwht128_x16s(g, ln);
+        fwht128_x16s(u, ln);
+        const float hr = HAD_R * fwht_sign(ln);                      // r and the sign fwht128_x16s leaves
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float gv = g[i] * HAD_R * (float)half(svg, i);
-            float uv = u[i] * HAD_R * (float)half(svu, i);
+            const float gv = g[i] * hr * (float)half(svg, i);
+            float uv = u[i] * hr * (float)half(svu, i);
             float sv = gv * sigmoid_dexp(gv);
             if (L != 0.0f) {
                 sv = fminf(sv, L);
@@ -513,12 +515,12 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
             const _Float16 a16 = (_Float16)(sv * uv);
             bv[i] = (float)(_Float16)(a16 * half(sud, i));
         }
-        fwht128_x16(bv, ln);
+        fwht128_x16s(bv, ln);
         if (rr < rn) {
             u32x4 o;
 #pragma unroll
             for (int m = 0; m < 4; ++m)
-                o[m] = h_as_u16((_Float16)(bv[2 * m] * HAD_R)) | (h_as_u16((_Float16)(bv[2 * m + 1] * HAD_R)) << 16);
+                o[m] = h_as_u16((_Float16)(bv[2 * m] * hr)) | (h_as_u16((_Float16)(bv[2 * m + 1] * hr)) << 16);
             *reinterpret_cast<u32x4*>(a.xd + (size_t)(row0 + rr) * N + colb) = o;
         }
     }
@@ -684,8 +686,8 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int s, in
         float v[8];
         *reinterpret_cast<float4*>(v) = *reinterpret_cast<const float4*>(zs + r * DN_COLS + hb * 128 + 8 * l16);
         *reinterpret_cast<float4*>(v + 4) = *reinterpret_cast<const float4*>(zs + r * DN_COLS + hb * 128 + 8 * l16 + 4);
-        fwht128_x16(v, ln);
-        const float rs = HAD_R * (float)u16_as_h(a.w16[row]);
+        fwht128_x16s(v, ln);
+        const float rs = HAD_R * fwht_sign(ln) * (float)u16_as_h(a.w16[row]);   // with the sign fwht128_x16s leaves
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = v[i] * rs * (float)u16_as_h(svd[i >> 1] >> (16 * (i & 1)));
         if (task < ntk && a.pe[row] >= 0) {                          // pe < 0: a row whose token id was out of range

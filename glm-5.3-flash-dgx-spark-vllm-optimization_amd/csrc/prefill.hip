@@ -145,11 +145,12 @@ __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
                     p[2 * i] = (float)(_Float16)(h0 * u16_as_h(sw & 0xFFFFu));
                     p[2 * i + 1] = (float)(_Float16)(h1 * u16_as_h(sw >> 16));
                 }
-                fwht128_x16(p, lane);
+                fwht128_x16s(p, lane);
+                const float hr = HAD_R * fwht_sign(lane);
                 uint32_t wm[4];
 #pragma unroll
                 for (int m = 0; m < 4; ++m)
-                    wm[m] = __builtin_bit_cast(uint32_t, h2{(_Float16)(p[2 * m] * HAD_R), (_Float16)(p[2 * m + 1] * HAD_R)});
+                    wm[m] = __builtin_bit_cast(uint32_t, h2{(_Float16)(p[2 * m] * hr), (_Float16)(p[2 * m + 1] * hr)});
                 if (blk < nb) pf_store_group(dst0 + blk * 128, wm, c);
             }
         }
@@ -234,11 +235,12 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
                 v[j][2 * i] = (float)h0 * (float)u16_as_h(sw & 0xFFFFu);
                 v[j][2 * i + 1] = (float)h1 * (float)u16_as_h(sw >> 16);
             }
-            fwht128_x16(v[j], lane);
+            fwht128_x16s(v[j], lane);
             const bool live = 4 * j + q < nb;
+            const float hr = HAD_R * fwht_sign(lane);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                v[j][i] = v[j][i] * HAD_R;
+                v[j][i] = v[j][i] * hr;
                 if (live) m = fmaxf(m, fabsf(v[j][i]));
             }
         }
@@ -606,6 +608,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     // storage of the lane's pairs m = 0..3 (columns 8c + 2m, + 1): k pair j = 4 (c % 2) + m of group c / 2
     const int grp0 = cb * 128 + 16 * (c >> 1);                      // the lane's 16-group of the block
     const float L = a.limit;
+    const float hr = HAD_R * fwht_sign(lane);                        // r and the sign fwht128_x16s leaves
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb) {
         if (32 * rb >= rn) break;                                    // uniform over the workgroup
@@ -633,12 +636,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
                     u[i] *= rs;
                 }
             }
-            fwht128_x16(g, lane);
-            fwht128_x16(u, lane);
+            fwht128_x16s(g, lane);
+            fwht128_x16s(u, lane);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                float gv = g[i] * HAD_R * svg[i];
-                float uv = u[i] * HAD_R * svu[i];
+                float gv = g[i] * hr * svg[i];
+                float uv = u[i] * hr * svu[i];
                 if (L != 0.0f) {
                     gv = fminf(gv, L);
                     uv = fminf(fmaxf(uv, -L), L);
@@ -646,12 +649,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
                 const float act = sigmoid_fast(gv) * gv * uv;
                 b[i] = E4M3 ? (float)(_Float16)act * (float)sud[i] : (float)(_Float16)((_Float16)act * sud[i]);
             }
-            fwht128_x16(b, lane);
+            fwht128_x16s(b, lane);
             if (E4M3) {                                              // fp32 down input and its row maximum
                 float m = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    b[i] = b[i] * HAD_R;
+                    b[i] = b[i] * hr;
                     m = fmaxf(m, fabsf(b[i]));
                 }
                 m = fmaxf(m, xor_lane<1>(m, lane));
@@ -668,7 +671,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
                 uint32_t wm[4];
 #pragma unroll
                 for (int m = 0; m < 4; ++m)
-                    wm[m] = __builtin_bit_cast(uint32_t, h2{(_Float16)(b[2 * m] * HAD_R), (_Float16)(b[2 * m + 1] * HAD_R)});
+                    wm[m] = __builtin_bit_cast(uint32_t, h2{(_Float16)(b[2 * m] * hr), (_Float16)(b[2 * m + 1] * hr)});
                 pf_store_group(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow) * N + grp0, wm, c);
             }
         }
@@ -773,6 +776,7 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
     const int t = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
     if (t >= a.T) return;
     const int lane = threadIdx.x & 63;
+    const float hr = HAD_R * fwht_sign(lane);                        // r and the sign fwht128_x16s leaves
     const int col = blockIdx.y * 512 + 128 * (lane >> 4) + 8 * (lane & 15);
     const bool live = blockIdx.y * 512 + 128 * (lane >> 4) < a.K;    // whole 16-lane groups
     const int colc = live ? col : 0;
@@ -840,12 +844,12 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[i] *= ds[k];
             }
-            fwht128_x16(v, lane);
+            fwht128_x16s(v, lane);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const uint32_t s2 = sv[k][i >> 1];
                 const float svf = (float)u16_as_h((i & 1) ? s2 >> 16 : s2 & 0xFFFFu);
-                if (ok[k]) sum[i] += v[i] * HAD_R * svf * w[k];
+                if (ok[k]) sum[i] += v[i] * hr * svf * w[k];
             }
         }
     }
@@ -945,6 +949,7 @@ __global__ __launch_bounds__(256) void pf_combine_rows_kernel(PrefillArgs a, con
     const int t = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + wv));
     if (t >= tokens) return;
     const int lane = threadIdx.x & 63;
+    const float hr = HAD_R * fwht_sign(lane);                        // r and the sign fwht128_x16s leaves
     const int nr = min(cnt[t], PF_ROWS_PER_TOKEN);
     int2 ent = make_int2(0x7FFFFFFF, 0);
     if (lane < nr) ent = list[t * PF_ROWS_PER_TOKEN + lane];
@@ -996,12 +1001,12 @@ __global__ __launch_bounds__(256) void pf_combine_rows_kernel(PrefillArgs a, con
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[i] *= ds[k];
             }
-            fwht128_x16(v, lane);
+            fwht128_x16s(v, lane);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const uint32_t s2 = sv[k][i >> 1];
                 const float svf = (float)u16_as_h((i & 1) ? s2 >> 16 : s2 & 0xFFFFu);
-                if (ok[k]) sum[i] += v[i] * HAD_R * svf * w[k];
+                if (ok[k]) sum[i] += v[i] * hr * svf * w[k];
             }
         }
     }
