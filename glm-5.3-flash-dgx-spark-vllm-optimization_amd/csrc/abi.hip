@@ -234,6 +234,13 @@ int mi355moe_exl3_dequant(const void* trellis, int64_t k_tiles, int64_t n_tiles,
                                     static_cast<uint16_t*>(wq), stream));
 }
 
+int mi355moe_sigmoid(const float* g, int64_t n, int variant, float* out, hipStream_t stream) {
+    if (!g || !out || (variant != 0 && variant != 1)) return MI355MOE_EINVAL;
+    if (n < 0) return MI355MOE_ESHAPE;
+    if (n == 0) return 0;
+    return rc_launch(launch_sigmoid(g, n, variant, out, stream));
+}
+
 int mi355moe_router_logits(const void* x, int64_t T, int64_t K, int64_t x_stride, const void* w, int64_t E,
                            float* logits, hipStream_t stream) {
     if (!x || !w || !logits) return MI355MOE_EINVAL;

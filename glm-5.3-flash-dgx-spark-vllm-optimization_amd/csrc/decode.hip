@@ -761,7 +761,23 @@ __global__ __launch_bounds__(128) void combine_kernel(DecodeArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------ sigmoid
+
+// The epilogues' logistic sigmoid on n values (grid-stride): variant 0 = sigmoid_dexp (decode epilogue), 1 =
+// sigmoid_fast (grouped prefill epilogues).
+__global__ __launch_bounds__(256) void sigmoid_kernel(const float* __restrict__ g, int64_t n, int variant,
+                                                      float* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        out[i] = variant ? sigmoid_fast(g[i]) : sigmoid_dexp(g[i]);
+}
+
 // ------------------------------------------------------------------------------------------------ launchers
+
+int launch_sigmoid(const float* g, int64_t n, int variant, float* out, hipStream_t st) {
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 8192));
+    hipLaunchKernelGGL(sigmoid_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g, n, variant, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 int launch_dequant(const uint16_t* trellis, int kt, int nt, uint16_t* wq, hipStream_t st) {
     hipLaunchKernelGGL(dequant_kernel, dim3(nt / 8, kt), dim3(64), 0, st, reinterpret_cast<const u32x4*>(trellis), nt,

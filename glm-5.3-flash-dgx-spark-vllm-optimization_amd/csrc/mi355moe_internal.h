@@ -216,6 +216,7 @@ size_t decode_lds_gateup(int rmax, int kr, int shared_suh);
 size_t decode_lds_down(int rmax, int kr);
 constexpr size_t DECODE_LDS_MAX = 81920;   // two 512-thread workgroups per CU
 int launch_dequant(const uint16_t* trellis, int kt, int nt, uint16_t* wq, hipStream_t st);
+int launch_sigmoid(const float* g, int64_t n, int variant, float* out, hipStream_t st);
 int launch_rot_in(const void* x, int xdt, int64_t x_stride, const int* tok, const int* pe, const int64_t* suh_tab,
                   int P, int K, uint16_t* out, hipStream_t st);
 

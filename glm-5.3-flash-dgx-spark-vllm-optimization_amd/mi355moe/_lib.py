@@ -58,6 +58,7 @@ _SIGS = {
     "mi355moe_abi_version": (_int, []),
     "mi355moe_strerror": (ctypes.c_char_p, [_int]),
     "mi355moe_exl3_dequant": (_int, [_c_p, _i64, _i64, _c_p, _c_p]),
+    "mi355moe_sigmoid": (_int, [_c_p, _i64, _int, _c_p, _c_p]),
     "mi355moe_router_logits": (_int, [_c_p, _i64, _i64, _i64, _c_p, _i64, _c_p, _c_p]),
     "mi355moe_router_topk": (_int, [_c_p, _i64, _i64, _c_p, _i64, _f, _int, _c_p, _c_p, _c_p]),
     "mi355moe_route_workspace_bytes": (_i64, [_i64, _i64]),

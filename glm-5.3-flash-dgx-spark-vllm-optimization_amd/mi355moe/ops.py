@@ -136,6 +136,18 @@ def dequant(trellis: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def sigmoid(g: torch.Tensor, variant: int = 0) -> torch.Tensor:
+    """The SwiGLU epilogues' sigmoid of fp32 g (any shape): variant 0 = the decode epilogue's
+    1 / (1 + (float)exp(-(double)g)) (E3's formula, exl3_fat_moe.cu:366-369), 1 = the grouped prefill epilogues'."""
+    dev = _need_cuda(g)
+    if g.dtype != torch.float32:
+        raise ValueError("g must be float32")
+    t = g.contiguous()
+    out = torch.empty_like(t)
+    _lib.check("mi355moe_sigmoid", _lib.lib().mi355moe_sigmoid(_p(t), t.numel(), int(variant), _p(out), _stream(dev)))
+    return out
+
+
 def router_logits(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """fp32 [T, E] holding bf16(x bf16 [T, K] @ w bf16 [E, K]^T): the exact (float64) dot products rounded to bf16
     through fp32, what F.linear(x, w).to(torch.float32) returns (code/fork/docs/BF16_GEMV.md:27,38)."""

@@ -78,6 +78,12 @@ const char* mi355moe_strerror(int code);
  * code/fork/tests/test_layout_equiv.py:1-46). n_tiles must be a multiple of 8. */
 int mi355moe_exl3_dequant(const void* trellis, int64_t k_tiles, int64_t n_tiles, void* wq, hipStream_t stream);
 
+/* The logistic sigmoid of the SwiGLU epilogues on n fp32 values (stage entry): variant 0 = the decode epilogue's
+ * 1 / (1 + (float)exp(-(double)g)) with an IEEE division, E3's formula (code/fork/docs/ref/mia_exl3-fat-kernel/
+ * exl3_fat_moe.cu:366-369); variant 1 = the grouped prefill epilogues' fp32 form (v_exp_f32 of the rounded
+ * exponent with its residual, one v_rcp_f32), a few ulp from variant 0. g and out fp32 device arrays of n. */
+int mi355moe_sigmoid(const float* g, int64_t n, int variant, float* out, hipStream_t stream);
+
 /* Router logits fp32 [T][E] = x bf16 [T][K] (row stride x_stride) times W bf16 [E][K]^T, each the bf16 rounding
  * (through fp32, nearest even) of the float64 sum of the bf16 products, as F.linear(x, W).to(torch.float32)
  * returns it (code/fork/docs/BF16_GEMV.md:27,38; reference oracle (X.double() @ W.t()).to(bfloat16),

@@ -15,6 +15,28 @@ def _say(*a):
     print(*a, flush=True)
 
 
+def test_sigmoid_against_the_e3_formula(cuda):
+    """The epilogues' sigmoid over every float32 in [-87, 87] whose low 6 mantissa bits are zero (35 M values, every
+    binade): variant 0 (decode epilogue) equals E3's 1 / (1 + (float)exp(-(double)g)) with IEEE float32 add and
+    division (exl3_fat_moe.cu:366-369; exp from the host's libm, rounded once to float32) bit for bit; variant 1
+    (grouped prefill epilogues) stays within 4 ulp of it."""
+    from mi355moe import ops
+    top = int(np.array([87.0], np.float32).view(np.uint32)[0])
+    pos = np.arange(0, top + 1, 64, dtype=np.uint32).view(np.float32)
+    g = np.concatenate([pos, -pos[1:]])
+    _say(f"sigmoid over {g.size} values")
+    e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    ref = (np.float32(1.0) / (np.float32(1.0) + e)).astype(np.float32)
+    gt = torch.from_numpy(g).to(cuda)
+    got0 = ops.sigmoid(gt, 0).cpu().numpy()
+    bad = np.count_nonzero(got0.view(np.uint32) != ref.view(np.uint32))
+    assert bad == 0, (bad, g[got0 != ref][:8])
+    got1 = ops.sigmoid(gt, 1).cpu().numpy()
+    ulp = np.abs(got1.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))   # both positive
+    _say(f"  fast variant: max {ulp.max()} ulp, {np.mean(ulp > 0):.3%} of values differ")
+    assert ulp.max() <= 4, ulp.max()
+
+
 @pytest.mark.parametrize("kt,nt", [(1, 8), (16, 64), (256, 64), (64, 256)])
 def test_dequant_bit_exact(cuda, kt, nt):
     from mi355moe import ops
