@@ -706,6 +706,45 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(RouteArgs a, int nblk)
     build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot, a.Rmin);
 }
 
+// route_scan_kernel with the per-block counts staged in LDS (nblk <= 64 blocks, (n + 1) * nblk ints): one coalesced
+// read of blk_cnt, the scans over blocks in LDS (one wave per local id, lane = block), one coalesced write of the
+// offsets, so no global load waits on a store. Same tables as route_scan_kernel.
+constexpr size_t ROUTE_SCAN_LDS_MAX = 120 * 1024;
+__global__ __launch_bounds__(1024) void route_scan_lds_kernel(RouteArgs a, int nblk) {
+    extern __shared__ int sh[];
+    __shared__ int tot[16];
+    const int n1 = a.n + 1, cells = n1 * nblk;
+    int* cnt = sh;
+    int* start = sh + n1;
+    int* stage = sh + 2 * n1;                                         // [nblk][n1]
+    for (int i = threadIdx.x; i < cells; i += blockDim.x) stage[i] = a.blk_cnt[i];
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int e = wv; e < n1; e += nw) {
+        const int v = lane < nblk ? stage[lane * n1 + e] : 0;
+        const int incl = wave_scan_incl(v);
+        if (lane < nblk) stage[lane * n1 + e] = incl - v;             // this id's pairs in earlier blocks
+        if (lane == 63) cnt[e] = incl;
+    }
+    __syncthreads();
+    int run = 0;
+    for (int base = 0; base <= a.n; base += blockDim.x) {
+        const int e = base + threadIdx.x;
+        const int c = e <= a.n ? cnt[e] : 0;
+        int ctot;
+        const int cinc = block_scan_incl(c, tot, ctot);
+        if (e <= a.n) start[e] = run + cinc - c;
+        run += ctot;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < cells; i += blockDim.x) a.blk_cnt[i] = start[i % n1] + stage[i];
+    for (int e = threadIdx.x; e <= a.n; e += blockDim.x) {
+        if (a.counts) a.counts[e] = cnt[e];
+        a.cnt_out[e] = cnt[e];
+    }
+    build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot, a.Rmin);
+}
+
 __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
     __shared__ __align__(16) int loc[ROUTE_BLK];
     const int j0 = blockIdx.x * ROUTE_BLK;
@@ -826,7 +865,18 @@ int launch_route(const RouteArgs& a, hipStream_t st) {
     const size_t shm1 = (size_t)(a.n + 1) * sizeof(int);
     if (a.ids64) hipLaunchKernelGGL(route_hist_kernel<int64_t>, dim3(nblk), dim3(ROUTE_BLK), shm1, st, a);
     else hipLaunchKernelGGL(route_hist_kernel<int32_t>, dim3(nblk), dim3(ROUTE_BLK), shm1, st, a);
-    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 2 * shm1, st, a, nblk);
+    const size_t shm_lds = (size_t)(a.n + 1) * (2 + nblk) * sizeof(int);
+    static bool lds_attr = false;
+    if (nblk <= 64 && shm_lds <= ROUTE_SCAN_LDS_MAX && !lds_attr) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(route_scan_lds_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)ROUTE_SCAN_LDS_MAX) != hipSuccess)
+            return -1;
+        lds_attr = true;
+    }
+    if (nblk <= 64 && shm_lds <= ROUTE_SCAN_LDS_MAX)
+        hipLaunchKernelGGL(route_scan_lds_kernel, dim3(1), dim3(1024), shm_lds, st, a, nblk);
+    else
+        hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 2 * shm1, st, a, nblk);
     hipLaunchKernelGGL(route_place_kernel, dim3(nblk), dim3(ROUTE_BLK), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

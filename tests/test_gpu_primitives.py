@@ -163,7 +163,8 @@ def test_router_topk_bit_exact(cuda, T, E, topk):
 
 @pytest.mark.parametrize("T,topk,n,seg,ids64,emap", [(8, 8, 288, 8, False, False), (1, 8, 288, 1, True, False),
                                                      (64, 8, 288, 16, False, True), (2048, 8, 288, 256, False, False),
-                                                     (8192, 8, 288, 256, True, False), (130, 8, 64, 16, True, True)])
+                                                     (8192, 8, 288, 256, True, False), (130, 8, 64, 16, True, True),
+                                                     (2048, 8, 4000, 64, False, False)])
 def test_route_bit_exact(cuda, T, topk, n, seg, ids64, emap):
     from mi355moe import ops
     _say(f"route T={T} topk={topk} n={n} seg={seg}")
