@@ -254,6 +254,12 @@ __device__ __forceinline__ void dma16(const void* src_lane, unsigned char* lds_w
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src_lane)
                  : "memory", "m0");
 }
+// The same marked non-temporal (data read once, e.g. streamed weights).
+__device__ __forceinline__ void dma16_nt(const void* src_lane, unsigned char* lds_wave) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(m0), "v"(src_lane)
+                 : "memory", "m0");
+}
 // The same with 4 bytes per lane: lane l -> LDS bytes lds_wave + 4 l (global_load_lds_dword).
 __device__ __forceinline__ void dma4(const void* src_lane, unsigned char* lds_wave) {
     const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;

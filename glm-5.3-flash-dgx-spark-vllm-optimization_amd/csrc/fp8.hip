@@ -143,7 +143,10 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     const int ldsw = wv * (GU_INST * 8) * 128;                       // this wave's first stage row
     auto issue = [&](unsigned char* st, int kb) {
 #pragma unroll
-        for (int j = 0; j < GU_INST; ++j) dma16(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+        for (int j = 0; j < GU_INST; ++j) {                           // weight rows (read once) non-temporal
+            if (wv * (GU_INST * 8) + j * 8 < 256) dma16_nt(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+            else dma16(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+        }
     };
 
     // the block scales of this column block (gate then up) go to LDS before any staged load is issued, so the
@@ -232,7 +235,10 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
     const int ldsw = wv * (DN_INST * 8) * 128;
     auto issue = [&](unsigned char* st, int kb) {
 #pragma unroll
-        for (int j = 0; j < DN_INST; ++j) dma16(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+        for (int j = 0; j < DN_INST; ++j) {                           // weight rows (read once) non-temporal
+            if (wv * (DN_INST * 8) + j * 8 < 128) dma16_nt(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+            else dma16(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+        }
     };
     for (int i = threadIdx.x; i < nkb; i += 256) scl[i] = a.w2s[((size_t)e * (K / 128) + cb) * nkb + i];
     __syncthreads();
