@@ -11,8 +11,10 @@
 //   down     q_a, s_a = quant(a16 row); y = (same GEMM with the down scales) * s_a; contribution w * y per pair;
 //            out[token] = the token's contributions summed in slot order (fp32), then the output dtype
 //
-// Work decomposition: a workgroup (4 waves) owns one 64-row segment of one expert and 128 output columns; wave w
-// owns 32 of them for both 32-row tiles (and, in gate/up, for gate and up, so the SwiGLU is local to the lane).
+// Work decomposition: a workgroup (4 waves) owns one 64-row segment of one expert and 64 output columns of gate and
+// up (wave w: 32-row tile w / 2, columns 32 (w % 2) .. + 31 of both, so the SwiGLU is local to the lane; two
+// workgroups per CU, which keeps more weight bytes in flight) or 128 output columns of down (wave w owns 32 of them
+// for both 32-row tiles).
 // Per 128-k block the workgroup stages its weight rows and activation rows in LDS with asynchronous
 // global-to-LDS loads (three stages, two blocks in flight), each wave instruction reading whole 128-byte lines;
 // lane half h = lane/32 then takes k 64h..64h+63 of its row from LDS, and v_mfma_scale_f32_32x32x64_f8f6f4 #1
@@ -109,13 +111,14 @@ __device__ __forceinline__ int tile_row(int r, int lane) { return 8 * (r >> 2) +
 
 
 constexpr int FP8_MAX_KB = 128;           // 128-k blocks per row (hidden and intermediate <= 16384)
-constexpr int GU_ROWS = 320;              // 128 gate + 128 up weight rows + 64 activation rows per stage
-constexpr int GU_INST = GU_ROWS / 8 / 4;  // wave instructions per stage per wave (10)
+constexpr int GU_ROWS = 192;              // 64 gate + 64 up weight rows + 64 activation rows per stage
+constexpr int GU_INST = GU_ROWS / 8 / 4;  // wave instructions per stage per wave (6)
 constexpr int DN_ROWS = 192;              // 128 weight rows + 64 activation rows
 constexpr int DN_INST = DN_ROWS / 8 / 4;  // 6
 
-// grid (N/128, segments), 256 threads: the 64-row segment's gate and up outputs of 128 columns, SwiGLU -> a16.
-// Three LDS stages of 40 KB; the loads for block kb + 2 are issued while block kb is multiplied.
+// grid (N/64, segments), 256 threads: the 64-row segment's gate and up outputs of 64 columns, SwiGLU -> a16.
+// Three LDS stages of 24 KB (two workgroups per CU); the loads for block kb + 2 are issued while block kb is
+// multiplied.
 __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     __shared__ __align__(16) unsigned char st0[GU_ROWS * 128];
     __shared__ __align__(16) unsigned char st1[GU_ROWS * 128];
@@ -129,22 +132,22 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     const int K = a.K, N = a.N;
     const int nkb = K >> 7;
 
-    // this lane's source rows for its ten stage instructions (swizzled chunk offset included)
+    // this lane's source rows for its six stage instructions (swizzled chunk offset included)
     const uint8_t* src[GU_INST];
 #pragma unroll
     for (int j = 0; j < GU_INST; ++j) {
         const int R = wv * (GU_INST * 8) + j * 8 + (lane >> 3);
         const uint8_t* rowp;
-        if (R < 128) rowp = a.w13 + ((size_t)e * 2 * N + cb * 128 + R) * K;
-        else if (R < 256) rowp = a.w13 + ((size_t)e * 2 * N + N + cb * 128 + (R - 128)) * K;
-        else rowp = a.qx + (size_t)a.tok[row0 + min(R - 256, rn - 1)] * K;
+        if (R < 64) rowp = a.w13 + ((size_t)e * 2 * N + cb * 64 + R) * K;
+        else if (R < 128) rowp = a.w13 + ((size_t)e * 2 * N + N + cb * 64 + (R - 64)) * K;
+        else rowp = a.qx + (size_t)a.tok[row0 + min(R - 128, rn - 1)] * K;
         src[j] = rowp + (((lane & 7) ^ swz(R)) << 4);
     }
     const int ldsw = wv * (GU_INST * 8) * 128;                       // this wave's first stage row
     auto issue = [&](unsigned char* st, int kb) {
 #pragma unroll
         for (int j = 0; j < GU_INST; ++j) {                           // weight rows (read once) non-temporal
-            if (wv * (GU_INST * 8) + j * 8 < 256) dma16_nt(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
+            if (wv * (GU_INST * 8) + j * 8 < 128) dma16_nt(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
             else dma16(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
         }
     };
@@ -152,21 +155,19 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     // the block scales of this column block (gate then up) go to LDS before any staged load is issued, so the
     // loop reads no global memory of its own
     for (int i = threadIdx.x; i < 2 * nkb; i += 256)
-        scl[i] = a.w13s[((size_t)e * (2 * N / 128) + (i < nkb ? 0 : N / 128) + cb) * nkb + (i < nkb ? i : i - nkb)];
+        scl[i] = a.w13s[((size_t)e * (2 * N / 128) + (i < nkb ? 0 : N / 128) + cb / 2) * nkb + (i < nkb ? i : i - nkb)];
     __syncthreads();
     const int h = lane >> 5, c = lane & 31;
-    f32x16 g0 = {}, g1 = {}, u0 = {}, u1 = {};
+    const int rt = wv >> 1, ct = wv & 1;
+    f32x16 g0 = {}, u0 = {};
     auto compute = [&](const unsigned char* st, int kb) {
-        u32x4 wg[4], wu[4], x0[4], x1[4];
-        frag64(st, wv * 32 + c, h, wg);
-        frag64(st, 128 + wv * 32 + c, h, wu);
-        frag64(st, 256 + c, h, x0);
-        frag64(st, 288 + c, h, x1);
+        u32x4 wg[4], wu[4], x0[4];
+        frag64(st, ct * 32 + c, h, wg);
+        frag64(st, 64 + ct * 32 + c, h, wu);
+        frag64(st, 128 + rt * 32 + c, h, x0);
         const float fg = scl[kb], fu = scl[nkb + kb];
         block_acc(x0, wg, fg, g0);
-        block_acc(x1, wg, fg, g1);
         block_acc(x0, wu, fu, u0);
-        block_acc(x1, wu, fu, u1);
     };
     // one pipeline step on stage buffer `cur` (block kb): wait for it, barrier, refill `nxt` (the buffer read in
     // the previous step) with block kb + 2, multiply
@@ -186,23 +187,20 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     }
 
     const float L = a.limit;
-    const int col = cb * 128 + wv * 32 + c;
+    const int col = cb * 64 + ct * 32 + c;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = 32 * t + tile_row(r, lane);
-            if (row < rn) {
-                const int pos = row0 + row;
-                const float sxv = a.sx[a.tok[pos]];
-                float gv = (t ? g1[r] : g0[r]) * sxv, uv = (t ? u1[r] : u0[r]) * sxv;
-                if (L != 0.0f) {
-                    gv = fminf(gv, L);
-                    uv = fminf(fmaxf(uv, -L), L);
-                }
-                const float act = __fdiv_rn(gv, 1.0f + (float)exp(-(double)gv)) * uv;
-                a.a16[(size_t)pos * N + col] = (uint16_t)h_as_u16((_Float16)act);
+    for (int r = 0; r < 16; ++r) {
+        const int row = 32 * rt + tile_row(r, lane);
+        if (row < rn) {
+            const int pos = row0 + row;
+            const float sxv = a.sx[a.tok[pos]];
+            float gv = g0[r] * sxv, uv = u0[r] * sxv;
+            if (L != 0.0f) {
+                gv = fminf(gv, L);
+                uv = fminf(fmaxf(uv, -L), L);
             }
+            const float act = __fdiv_rn(gv, 1.0f + (float)exp(-(double)gv)) * uv;
+            a.a16[(size_t)pos * N + col] = (uint16_t)h_as_u16((_Float16)act);
         }
     }
 }
@@ -319,7 +317,7 @@ int launch_fp8(const Fp8Args& a, hipStream_t st, int kernels) {
     if (kernels & 1)
         if (a.T > 0) hipLaunchKernelGGL(quant_rows_kernel, dim3(a.T), dim3(256), 0, st, a.x, a.xdt, a.x_stride, a.K,
                                         a.qx, a.sx);
-    if (kernels & 2) hipLaunchKernelGGL(fp8_gateup_kernel, dim3(a.N / 128, a.S_cap), dim3(256), 0, st, a);
+    if (kernels & 2) hipLaunchKernelGGL(fp8_gateup_kernel, dim3(a.N / 64, a.S_cap), dim3(256), 0, st, a);
     if (kernels & 4) {
         hipLaunchKernelGGL(quant_rows_kernel, dim3(a.P), dim3(256), 0, st, (const void*)a.a16, (int)DT_F16,
                            (int64_t)a.N, a.N, a.qa, a.sa);
