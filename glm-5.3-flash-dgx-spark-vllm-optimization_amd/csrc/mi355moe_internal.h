@@ -156,7 +156,8 @@ int launch_prefill_rows_down(const PrefillArgs& a, const int64_t* row_token, int
 int launch_zero_out(const PrefillArgs& a, hipStream_t st);
 int prefill_setup();
 
-// The block-scaled e4m3 expert path: per-token e4m3 activations, grouped fp8 MFMA GEMMs over 64-row segments.
+// The block-scaled e4m3 expert path: per-token e4m3 activations, grouped GEMMs over 64-row segments (e4m3 operands
+// converted to fp16, exact products, fp32 block sums on the fp16 matrix cores).
 struct Fp8Args {
     int n, K, N, P, T;
     const uint8_t* w13;     // [n][2N][K] e4m3, gate rows then up rows

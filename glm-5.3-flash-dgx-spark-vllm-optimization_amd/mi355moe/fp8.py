@@ -1,5 +1,5 @@
 """The e4m3 expert variant: block-scaled e4m3 routed experts (vLLM's fp8 w8a8 block-quantised MoE layout, 128x128
-blocks) with per-token dynamic e4m3 activations, on gfx950's fp8 matrix cores.
+blocks) with per-token dynamic e4m3 activations; exact products on gfx950's fp16 matrix cores, fp32 block sums.
 
   Fp8Experts          one layer's experts: w13 e4m3 [n, 2I, H] (gate rows then up rows), w13_scale fp32
                       [n, 2I/128, H/128], w2 e4m3 [n, H, I], w2_scale fp32 [n, H/128, I/128]

@@ -1,11 +1,13 @@
 """GPU parity of the e4m3 expert variant (mi355moe.fp8) against the oracle (oracle/e4m3.py, oracle/csrc/fp8.c):
 
   - the per-row e4m3 quantiser is bit-exact (codes and scales);
-  - the layer forward agrees with the oracle's fp32 and float64 modes to rel_l2 <= 5e-3, the reference's own e4m3
-    tolerance (code/fork/overlay/glm53_moe_e4m3.py:110). The bound is not tighter because gfx950's fp8 matrix core
-    does not add its products in fp32: measured, it aligns each group of 8 consecutive-k products to the largest and
-    keeps about 12 significant bits (448 + 63 * 2^-9 comes out 448 + 56 * 2^-9), which moves a 4096-term dot
-    product by ~1e-3 relative. Elementwise the bf16 output stays within rtol 2e-2 plus 1e-2 of the output scale.
+  - the layer forward agrees with the oracle's fp32 mode (the spec's exact e4m3 products summed in fp32 per
+    128-k block) to rel_l2 <= 1e-6 and with float64 to rel_l2 <= 1e-4 (the reference's own e4m3 tolerance is 5e-3,
+    code/fork/overlay/glm53_moe_e4m3.py:110): the kernels form every block sum from exact products on the fp16
+    matrix cores (measured 2-4e-8 and <= 8.4e-6). The bf16 output is elementwise within rtol 2e-2 / atol 1e-3 of the
+    fp32 oracle. Against float64 only rel_l2 <= 5e-3 holds in general: the float64 layer rounds its own intermediate
+    to fp16 before the per-row requantisation, and one fp16 ulp on a row's largest element changes that row's e4m3
+    scale and so every code of the row (token 77 of the full configuration: 1 % of its row).
   - at the full e4m3 configuration (T=2048, 288 experts, hidden 4096, intermediate 1024, top-8) a sample of tokens
     is checked against the oracle evaluated for those tokens only (the output of a token depends only on its own
     pairs).
@@ -74,11 +76,11 @@ def test_forward_vs_oracle(cuda, n, K, N, T, topk, limit):
     tok, exs, pw = e4m3.pairs_fp32(local, w, n)
     ref_k = e4m3.forward(lay, xf, tok, exs, pw, limit, "kernel")
     ref64 = e4m3.forward(lay, xf, tok, exs, pw, limit, "f64")
-    assert _rel(got, ref_k) <= 5e-3, _rel(got, ref_k)
-    assert _rel(got, ref64) <= 5e-3, _rel(got, ref64)
+    assert _rel(got, ref_k) <= 1e-6, _rel(got, ref_k)
+    assert _rel(got, ref64) <= 1e-4, _rel(got, ref64)
     outb = fp8.moe_forward_ids(ex, x, torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), limit=limit)
     assert outb.dtype == torch.bfloat16
-    assert np.allclose(outb.float().cpu().numpy(), ref64, rtol=2e-2, atol=1e-2 * float(np.abs(ref64).max()))
+    assert np.allclose(outb.float().cpu().numpy(), ref_k, rtol=2e-2, atol=1e-3)
 
 
 def test_expert_map_and_stages(cuda):
@@ -124,6 +126,9 @@ def test_full_configuration_token_sample(cuda):
     lay = _host_layer(ex, used)
     xs = x[torch.from_numpy(sample).cuda()].float().cpu().numpy()
     ref = e4m3.forward(lay, xs, tok, exs, pw, 10.0, "kernel")
+    ref64 = e4m3.forward(lay, xs, tok, exs, pw, 10.0, "f64")
     got = out[torch.from_numpy(sample).cuda()].cpu().numpy()
-    assert _rel(got, ref) <= 5e-3, _rel(got, ref)
+    assert _rel(got, ref) <= 1e-6, _rel(got, ref)
+    assert np.allclose(torch.from_numpy(got).to(torch.bfloat16).float().numpy(), ref, rtol=2e-2, atol=1e-3)
+    assert _rel(got, ref64) <= 5e-3, _rel(got, ref64)
     assert np.isfinite(out.cpu().numpy()).all()
