@@ -734,7 +734,7 @@ def main():
                     help="after the workload, copy a tensor of this many MiB three times (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
+        print(f"bench.py: this benchmark runs on one MI355X; --gpus {args.gpus} is not supported "
               "(the layer's tensor- and expert-parallel sharding is designed, not run)", file=sys.stderr)
         sys.exit(2)
     import torch

@@ -90,7 +90,7 @@ class Exl3MoEMethod:
     def __init__(self, bits: int = 4, swiglu_limit: float | None = None, e4m3: bool = False,
                  max_num_tokens: int | None = None, topk: int = 8, tp_rank: int = 0, tp_size: int = 1):
         if bits != 4:
-            raise ValueError("this build decodes 4-bit EXL3 trellis tiles only")
+            raise ValueError("only 4-bit EXL3 trellis tiles are supported")
         self.bits = bits
         self.swiglu_limit = swiglu_limit
         self.e4m3 = e4m3                  # the overlay's e4m3 expert numerics instead of the fp16 paths

@@ -231,7 +231,7 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
     stages: a subset of the call's launches (_lib.STAGE_*), for timing one kernel; the default runs them all.
     bf16_contrib: the grouped path keeps its per-pair down accumulators in bf16 (half the contribution traffic;
     code/fork/docs/OPT_MOE.md:13). persistent: the one-launch ticket-ordered schedule of the grouped path
-    (code/fork/kernels/moe_e4m3.cu:867-897); not available in this build (the library refuses it)."""
+    (code/fork/kernels/moe_e4m3.cu:867-897); not available (the library refuses it)."""
     if accumulate and out is None:
         raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)

@@ -162,7 +162,7 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
  *   MI355MOE_OPT_E4M3         the trellis-sourced e4m3 numerics of mi355moe_e4m3_moe_forward_ids (grouped path
  *                             only: path DECODE is refused; hidden <= 4096).
  *   MI355MOE_OPT_PERSISTENT   reserved for a one-launch, ticket-ordered gate/up + down schedule of the grouped path
- *                             (the reference's code/fork/kernels/moe_e4m3.cu:867-897); not available in this build:
+ *                             (the reference's code/fork/kernels/moe_e4m3.cu:867-897); not available in this library:
  *                             every call with it returns MI355MOE_EUNSUPPORTED before any launch.
  * Unknown bits: MI355MOE_EINVAL. Workspace sizes as mi355moe_moe_workspace_bytes_path (with MI355MOE_OPT_E4M3:
  * mi355moe_e4m3_moe_workspace_bytes). */

@@ -1,8 +1,8 @@
 """CPU oracle for the routed-MoE hot path -- TEST INFRASTRUCTURE ONLY.
 
-This package is the checker that the HIP kernels are measured against. Only ``tests/``,
-``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import it, and only as the checker or as
-the timed CPU baseline, never as a product code path. The shipped package (``mi355moe``) never imports it and
+This package is the reference the HIP kernels' results are compared with. Only ``tests/``,
+``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import it, and only for that comparison or
+as the timed CPU baseline, never as a product code path. The shipped package (``mi355moe``) never imports it and
 fails loudly when its HIP library is missing.
 
 Contents (each function cites the reference file:line it restates):

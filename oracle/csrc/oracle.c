@@ -1,6 +1,6 @@
 /*
- * CPU oracle for the routed-MoE hot path. TEST INFRASTRUCTURE ONLY: the checker the HIP kernels are compared
- * against (tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg). The shipped library never links it.
+ * CPU oracle for the routed-MoE hot path. TEST INFRASTRUCTURE ONLY: the reference the HIP kernels' results are
+ * compared with (tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg). The shipped library never links it.
  *
  * Plain C restatement of the reference's arithmetic:
  *   - EXL3 4-bit trellis format and decode: code/fork/kernels/exl3_format_ref.py:13-27 (closed form), :70-97
@@ -11,7 +11,7 @@
  *     code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu:95-126).
  *   - decode-path epilogues (exl3_moe semantics, SiLU then the limit: code/fork/docs/ref/xl_hadamard_inner.cuh:
  *     280-400, exl3.cu:371-449) and E3 prefill epilogues (limit then SiLU, sigmoid = 1/(1+(float)exp(-(double)g)):
- *     exl3_fat_moe.cu:340-378, 443-457), each evaluated at the rounding points this build's kernels use.
+ *     exl3_fat_moe.cu:340-378, 443-457), each evaluated at the rounding points the HIP kernels use.
  *   - float64 layer reference y = ((((x*suh) H) Wq) H) * svh (exl3_format_ref.py:127-131,
  *     code/fork/tests/test_e2e_vs_f64.py:52-75).
  * Threads: OpenMP over experts (one decoded expert per thread at a time).
@@ -205,7 +205,7 @@ void orc_rot_in(const uint16_t* x16, const uint16_t* suh16, int n, uint16_t* out
     }
 }
 
-/* sigmoid as this build defines it: 1 / (1 + (float)exp(-(double)g)), IEEE fp32 division */
+/* sigmoid as the HIP kernels define it: 1 / (1 + (float)exp(-(double)g)), IEEE fp32 division */
 static inline float sigm(float g) { return 1.0f / (1.0f + (float)exp(-(double)g)); }
 
 /* ---------------------------------------------------------------- the reference's default (TF_PARITY=1) epilogues
@@ -479,5 +479,5 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
     return 0;
 }
 
-/* exp as this build's kernels round it: (float)exp((double)a) */
+/* exp as the HIP kernels round it: (float)exp((double)a) */
 float orc_expf_via_double(float a) { return (float)exp((double)a); }
