@@ -140,6 +140,8 @@ struct PrefillArgs {
     int tok_rows;
     int contrib_bf16;       // the down kernel stores its raw accumulators as bf16 (contrib viewed as bf16 [P][K])
     int out_accumulate;     // the combine adds the routed sum to out's current values (the shared-expert fold)
+    int small_rows;         // > 0: segments of at most this many rows go to the small-tile GEMMs, larger ones to the
+                            // 256-row GEMMs (set by launch_prefill; 0: one kind takes every segment)
 };
 constexpr int PREFILL_TM = 256;
 constexpr int PF_ROWS_PER_TOKEN = 32;   // rows of one token the row-table combine handles (topk <= 32)

@@ -16,6 +16,8 @@
 //            the token's contributions summed in slot order (fp32), then the output dtype. The down kernel stores the
 //            raw accumulators acc_d; the combine applies H, r, svh_d and w16 before summing.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 #include "common.cuh"
 #include "mi355moe_internal.h"
@@ -33,8 +35,9 @@ constexpr int PF_RB = 32 * PF_KT;               // bytes of one A row in a stage
 constexpr int PF_ASB = PF_TM * PF_RB;           // one A stage: 256 rows x 16 PF_KT k
 constexpr int PF_WWB = 512 * PF_KT;             // one wave's raw words of a step: PF_KT k tiles x 4 column tiles x 128 B
 constexpr int PF_WSB = 4 * PF_WWB;              // one raw-word stage (4 waves)
-constexpr int PF_DMA = PF_RB / 16 + PF_KT / 2;  // DMA instructions per wave per step
 constexpr size_t PF_LDS = (size_t)PF_NS * (PF_ASB + PF_WSB);   // 163,840 bytes (the whole LDS)
+constexpr int PF_TMS = 64;                      // rows per tile of the small-tile kernels (two per CU)
+constexpr size_t PF_LDS_S = (size_t)PF_NS * (PF_TMS * PF_RB + PF_WSB);   // 65,536 bytes
 constexpr int PF_CLD = 260;                     // epilogue staging row stride (floats): [32][PF_CLD] fp32
 
 // Rotated activations (h13, h2) are stored with k permuted inside every group of 16: storage pair p (halves 2p,
@@ -408,19 +411,26 @@ __device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p
 // sourced e4m3 variant's operand; the products with e4m3 activations are then exact and summed in fp32.
 // NRB: the 32-row blocks of the tile that are multiplied (a compile-time count: tiles of up to 32 NRB rows skip the
 // MFMAs and A reads of the other blocks, whose accumulators stay zero and are never stored; the decode is the same).
-template <bool E4M3 = false, int NRB = 8>
+// TM: the A rows staged per step (256, or 64 for the small-tile kernels, whose stages then take 64 KB of LDS).
+template <bool E4M3 = false, int NRB = 8, int TM = PF_TM>
 __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[8][2]) {
-    unsigned char* Ast = smem;                                        // [PF_NS][256 rows][PF_RB]
-    unsigned char* Wst = smem + PF_NS * PF_ASB;                       // [PF_NS][4 waves][PF_KT k tiles][4 tiles][128 B]
+    static_assert(32 * NRB <= TM && TM % 32 == 0, "the multiplied row blocks are staged");
+    constexpr int ASB = TM * PF_RB;                                   // one A stage
+    constexpr int CPR = PF_RB / 16;                                   // 16-byte chunks per A row
+    constexpr int RPW = TM / 4;                                       // A rows staged by each wave
+    constexpr int RPI = 64 / CPR;                                     // A rows per DMA instruction
+    constexpr int NA = RPW / RPI;                                     // A DMA instructions per wave per step
+    constexpr int NDMA = NA + PF_KT / 2;                              // DMA instructions per wave per step
+    unsigned char* Ast = smem;                                        // [PF_NS][TM rows][PF_RB]
+    unsigned char* Wst = smem + PF_NS * ASB;                          // [PF_NS][4 waves][PF_KT k tiles][4 tiles][128 B]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    constexpr int CPR = PF_RB / 16;                                   // 16-byte chunks per A row
     const int steps = t.kdim / (16 * PF_KT);
-    // A DMA sources: instruction i of this wave = rows 64 wv + (64 / CPR) i + lane / CPR, slot lane % CPR
-    const uint16_t* asrc[CPR];
+    // A DMA sources: instruction i of this wave = rows RPW wv + RPI i + lane / CPR, slot lane % CPR
+    const uint16_t* asrc[NA];
 #pragma unroll
-    for (int i = 0; i < CPR; ++i) {
-        const int R = 64 * wv + (64 / CPR) * i + lane / CPR;
+    for (int i = 0; i < NA; ++i) {
+        const int R = RPW * wv + RPI * i + lane / CPR;
         const int chunk = (lane % CPR) ^ pf_swz(R);
         const int rr = min(R, t.rn - 1);
         asrc[i] = t.a_rows + (size_t)(t.a_tok ? t.a_tok[rr] : rr) * t.kdim + 8 * chunk;
@@ -437,14 +447,14 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     auto issue_one = [&](int k, int sa, int sw) {                     // DMA instruction k of the batch (A(sa), W(sw))
         sa = min(sa, steps - 1);
         sw = min(sw, steps - 1);
-        if (k < CPR)
-            dma16(asrc[k] + (size_t)sa * 16 * PF_KT, Ast + (sa % PF_NS) * PF_ASB + wv * 64 * PF_RB + k * 1024);
+        if (k < NA)
+            dma16(asrc[k] + (size_t)sa * 16 * PF_KT, Ast + (sa % PF_NS) * ASB + wv * RPW * PF_RB + k * 1024);
         else
-            dma16(wsrc + (size_t)sw * wstep + (k - CPR) * wins, Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB + (k - CPR) * 1024);
+            dma16(wsrc + (size_t)sw * wstep + (k - NA) * wins, Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB + (k - NA) * 1024);
     };
     auto issue = [&](int sa, int sw) {                                // the whole batch
 #pragma unroll
-        for (int k = 0; k < PF_DMA; ++k) issue_one(k, sa, sw);
+        for (int k = 0; k < NDMA; ++k) issue_one(k, sa, sw);
     };
     auto words = [&](int sw, uint32_t (&w)[PF_KT][3]) {              // this lane's raw words of step sw
         const unsigned char* wr = Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB;
@@ -471,12 +481,12 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     // step it, each pair with one fp16 pair's decode for step it + 1 between them (VALU work issued while the MFMAs
     // run), the A fragments read four MFMA pairs ahead.
     constexpr int NF = 8 * PF_KT;                                     // A fragments (and decoded pairs) per step
-    constexpr int DMA_EVERY = NF / PF_DMA;                            // MFMA pairs between DMA instructions
+    constexpr int DMA_EVERY = NF / NDMA;                              // MFMA pairs between DMA instructions
     auto step = [&](int it, const h8 (&bc)[PF_KT][2], h8 (&bn)[PF_KT][2]) {
-        WAIT_VM(PF_DMA * (PF_NS - 2));                                // A(it) and words(it + 1): the oldest batch
+        WAIT_VM(NDMA * (PF_NS - 2));                                  // A(it) and words(it + 1): the oldest batch
         LDS_BARRIER();
         __builtin_amdgcn_sched_barrier(0);
-        const unsigned char* as = Ast + (it % PF_NS) * PF_ASB;
+        const unsigned char* as = Ast + (it % PF_NS) * ASB;
         uint32_t w[PF_KT][3];
         words(it + 1, w);                                             // step it + 1 (past the end: never used)
         h8 af[NF];
@@ -490,7 +500,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         for (int i = 0; i < NF; ++i) {
             // the next batch's DMA instructions spread over the step (the CU's address path takes them one at a
             // time; issued together after the barrier they would stall every wave behind each other)
-            if (i % DMA_EVERY == 0 && i / DMA_EVERY < PF_DMA) issue_one(i / DMA_EVERY, it + PF_NS - 1, it + PF_NS);
+            if (i % DMA_EVERY == 0 && i / DMA_EVERY < NDMA) issue_one(i / DMA_EVERY, it + PF_NS - 1, it + PF_NS);
             if (i + 4 < NF && ((i + 4) & 7) < NRB) af[i + 4] = afrag(as, i + 4);
             const int kt = i >> 3, rb = i & 7;
             // pair i's products after the first MFMA, pair i - 1's values after the second: no VALU instruction
@@ -516,7 +526,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     issue_w(0);
 #pragma unroll
     for (int j = 0; j < PF_NS - 1; ++j) issue(j, j + 1);
-    WAIT_VM(PF_DMA * (PF_NS - 1));                                    // the step-0 words (this wave's own)
+    WAIT_VM(NDMA * (PF_NS - 1));                                      // the step-0 words (this wave's own)
     h8 bA[PF_KT][2], bB[PF_KT][2];
     {
         uint32_t w[PF_KT][3], q[PF_KT][8];
@@ -525,7 +535,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         for (int i = 0; i < NF; ++i) q[i >> 3][i & 7] = pf_decode_pair(w[i >> 3], i & 7);
         operands(q, bA);
     }
-    static_assert(PF_DMA * (PF_NS - 1) <= 63 && PF_KT % 2 == 0, "stages within the vmcnt range");
+    static_assert(NDMA * (PF_NS - 1) <= 63 && PF_KT % 2 == 0, "stages within the vmcnt range");
     for (int it = 0; it < steps; it += 2) {                           // steps is even (kdim % (32 PF_KT) == 0)
         step(it, bA, bB);
         step(it + 1, bB, bA);
@@ -566,13 +576,15 @@ __device__ __forceinline__ void pf_tile_of(int b, int ncb, int& s, int& cb) {
 // E4M3: the trellis-sourced e4m3 variant (weights rounded to e4m3 in the GEMM; accumulators times the row's
 // activation scale before the output Hadamard; the down input H(a16 * suh_d) * r kept in fp32 in vd, its row maxima
 // gathered in amaxd for pf_quantd_kernel). code/fork/overlay/glm53_moe_e4m3.py:654-674 (spec_proj, spec_ffn).
-template <bool E4M3>
-__global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    int s, cb;
-    pf_tile_of(blockIdx.x, a.N >> 7, s, cb);
-    if (s >= a.nseg[0]) return;
-    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
+// SMALL: the tile is rows 64 quarter .. 64 quarter + 63 of the segment, staged as 64 rows (the small-tile kernels).
+template <bool E4M3, bool SMALL>
+__device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int quarter, int cb, unsigned char* smem) {
+    const int e = a.seg_expert[s];
+    int row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
+    if (SMALL) {
+        row0 += PF_TMS * quarter;
+        rn = min(rn - PF_TMS * quarter, PF_TMS);
+    }
     if (rn <= 0 || row0 < 0 || row0 + rn > a.P || e < 0 || e >= a.n) return;   // (caller-built tables)
     const int K = a.K, N = a.N;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -585,7 +597,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     t.btiles_n = N >> 4;
     t.bcol0 = cb * 8 + 4 * (wv & 1);
     f16v acc[8][2];
-    if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);                   // uniform: small tiles multiply two row blocks
+    if (SMALL) pf_gemm<E4M3, 2, PF_TMS>(t, smem, acc);
+    else if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);              // uniform: small tiles multiply two row blocks
     else pf_gemm<E4M3, 8>(t, smem, acc);
 
     // epilogue, 32 rows at a time through LDS; a wave finishes 4 rows at once: 16 lanes per row, lane c holding
@@ -610,7 +623,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     const float L = a.limit;
     const float hr = HAD_R * fwht_sign(lane);                        // r and the sign fwht128_x16s leaves
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb) {
+    for (int rb = 0; rb < (SMALL ? 2 : 8); ++rb) {
         if (32 * rb >= rn) break;                                    // uniform over the workgroup
         pf_stage_rows(acc, Cs, rb);
         __syncthreads();
@@ -679,15 +692,50 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     }
 }
 
-// ------------------------------------------------------------------------------------------------ down
+// Workgroup b of a small-tile grid (8 ncb ceil(4 S_cap / 8) workgroups): tile (virtual segment v, column block cb)
+// as pf_tile_of orders them, v = quarter S_cap + s, so the first quarters of all segments come first (at small row
+// counts the only ones with rows) and the later quarters' workgroups, mostly empty, come last.
+__device__ __forceinline__ bool pf_small_tile_of(const PrefillArgs& a, int ncb, int& s, int& quarter, int& cb) {
+    int v;
+    pf_tile_of(blockIdx.x, ncb, v, cb);
+    if (a.S_cap <= 0 || v >= 4 * a.S_cap) return false;
+    quarter = v / a.S_cap;
+    s = v - quarter * a.S_cap;
+    return s < a.nseg[0];
+}
 
 template <bool E4M3>
-__global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     int s, cb;
-    pf_tile_of(blockIdx.x, a.K >> 8, s, cb);
-    if (s >= a.nseg[0]) return;
-    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
+    pf_tile_of(blockIdx.x, a.N >> 7, s, cb);
+    if (s >= a.nseg[0] || (a.small_rows > 0 && a.seg_rows[s] <= a.small_rows)) return;
+    pf_gateup_tile<E4M3, false>(a, s, 0, cb, smem);
+}
+
+// The same GEMM for segments of few rows: 64-row tiles with 64 KB of LDS and at most 256 registers per wave, so two
+// workgroups share a CU and one's waits are covered by the other's work (a tile's weight decode does not shrink
+// with its rows, so at ~60 rows per expert the decode, not the MFMA, bounds the GEMM).
+template <bool E4M3>
+__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void pf_gateup_small_kernel(
+    PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    int s, quarter, cb;
+    if (!pf_small_tile_of(a, a.N >> 7, s, quarter, cb)) return;
+    if (a.small_rows > 0 && a.seg_rows[s] > a.small_rows) return;
+    pf_gateup_tile<E4M3, true>(a, s, quarter, cb, smem);
+}
+
+// ------------------------------------------------------------------------------------------------ down
+
+template <bool E4M3, bool SMALL>
+__device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int quarter, int cb, unsigned char* smem) {
+    const int e = a.seg_expert[s];
+    int row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
+    if (SMALL) {
+        row0 += PF_TMS * quarter;
+        rn = min(rn - PF_TMS * quarter, PF_TMS);
+    }
     if (rn <= 0 || row0 < 0 || row0 + rn > a.P || e < 0 || e >= a.n) return;   // (caller-built tables)
     const int K = a.K, N = a.N;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -700,7 +748,8 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     t.btiles_n = K >> 4;
     t.bcol0 = cb * 16 + 4 * wv;
     f16v acc[8][2];
-    if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);
+    if (SMALL) pf_gemm<E4M3, 2, PF_TMS>(t, smem, acc);
+    else if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);
     else pf_gemm<E4M3, 8>(t, smem, acc);
 
     // epilogue: the raw accumulators (rows < rn) straight from registers into contrib; the output rotation, svh and
@@ -724,7 +773,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
                                                   __builtin_amdgcn_perm(par, own, sel));
         };
 #pragma unroll
-        for (int rb = 0; rb < 8; ++rb) {
+        for (int rb = 0; rb < (SMALL ? 2 : 8); ++rb) {
             if (32 * rb >= rn) break;
             if (32 * rb + 32 <= rn) {
 #pragma unroll
@@ -744,7 +793,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     }
     float* o = a.contrib + c0;
 #pragma unroll
-    for (int rb = 0; rb < 8; ++rb) {
+    for (int rb = 0; rb < (SMALL ? 2 : 8); ++rb) {
         if (32 * rb >= rn) break;
         if (32 * rb + 32 <= rn) {
 #pragma unroll
@@ -764,6 +813,25 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
             }
         }
     }
+}
+
+template <bool E4M3>
+__global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    int s, cb;
+    pf_tile_of(blockIdx.x, a.K >> 8, s, cb);
+    if (s >= a.nseg[0] || (a.small_rows > 0 && a.seg_rows[s] <= a.small_rows)) return;
+    pf_down_tile<E4M3, false>(a, s, 0, cb, smem);
+}
+
+template <bool E4M3>
+__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void pf_down_small_kernel(
+    PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    int s, quarter, cb;
+    if (!pf_small_tile_of(a, a.K >> 8, s, quarter, cb)) return;
+    if (a.small_rows > 0 && a.seg_rows[s] > a.small_rows) return;
+    pf_down_tile<E4M3, true>(a, s, quarter, cb, smem);
 }
 
 // ------------------------------------------------------------------------------------------------ combine
@@ -1035,12 +1103,38 @@ int prefill_setup() {
                          reinterpret_cast<const void*>(pf_down_kernel<true>)};
     for (const void* k : ks)
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS) != hipSuccess) return -1;
+    const void* kss[4] = {reinterpret_cast<const void*>(pf_gateup_small_kernel<false>),
+                          reinterpret_cast<const void*>(pf_gateup_small_kernel<true>),
+                          reinterpret_cast<const void*>(pf_down_small_kernel<false>),
+                          reinterpret_cast<const void*>(pf_down_small_kernel<true>)};
+    for (const void* k : kss)
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_S) != hipSuccess) return -1;
     g_pf_attr = true;
     return 0;
 }
 
-int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
+// Which grouped GEMMs a call runs. The small-tile kernels take a call whose routed experts average at most
+// PF_SMALL_ROWS rows (P <= 128 n): two workgroups per CU keep the VALU-bound weight decode busier, which outweighs
+// decoding a segment's weights once per 64-row quarter (measured at 288 experts, top-8: T = 2048, ~57 rows per
+// expert, 21 % faster; T = 4096, ~114 rows, 6 % faster; T = 8192, ~228 rows, 47 % slower). Larger calls run the
+// 256-row tiles. "hybrid" splits one call by segment size (segments of at most PF_SMALL_ROWS rows on the small
+// tiles, larger ones on the 256-row tiles: 2 % faster on Zipf-skewed routing at T = 8192, 6 % slower on uniform
+// routing, where the few small segments add a serial launch). The environment variable MI355MOE_PREFILL_TILES =
+// "small", "large" or "hybrid" forces a choice; all three give bit-identical results (a row's arithmetic does not
+// depend on the tile that holds it).
+constexpr int PF_SMALL_ROWS = 128;
+enum { PF_TILES_SMALL = 1, PF_TILES_LARGE = 2, PF_TILES_BOTH = 3 };
+static int pf_tiles(const PrefillArgs& a) {
+    const char* f = getenv("MI355MOE_PREFILL_TILES");
+    if (f && !strcmp(f, "small")) return PF_TILES_SMALL;
+    if (f && !strcmp(f, "large")) return PF_TILES_LARGE;
+    if (f && !strcmp(f, "hybrid")) return PF_TILES_BOTH;
+    return (a.n > 0 && (int64_t)a.P <= (int64_t)PF_SMALL_ROWS * a.n) ? PF_TILES_SMALL : PF_TILES_LARGE;
+}
+
+int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     if (prefill_setup()) return -1;
+    PrefillArgs a = a0;
     const bool f8 = a.e4m3 != 0;
     if (f8 && (a.K > 4 * 128 * PF_GATHER_PASSES || !a.asc)) return -1;
     if (f8 && (kernels & ~1) && (!a.dsc || !a.vd || !a.amaxd)) return -1;    // the gather alone needs only asc
@@ -1050,16 +1144,29 @@ int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels) {
     }
     const int sg = (a.S_cap + 7) / 8;                               // segment groups of 8 (one per XCD)
     const dim3 gu(8 * (a.N / 128) * sg), dn(8 * (a.K / 256) * sg);
+    const int sgs = (4 * a.S_cap + 7) / 8;                          // small tiles: four quarters per segment
+    const dim3 gus(8 * (a.N / 128) * sgs), dns(8 * (a.K / 256) * sgs);
+    const int tiles = pf_tiles(a0);
+    a.small_rows = tiles == PF_TILES_BOTH ? PF_SMALL_ROWS : 0;
     if (kernels & 2) {
-        if (f8) hipLaunchKernelGGL(pf_gateup_kernel<true>, gu, dim3(PF_THREADS), PF_LDS, st, a);
-        else hipLaunchKernelGGL(pf_gateup_kernel<false>, gu, dim3(PF_THREADS), PF_LDS, st, a);
+        if (tiles & PF_TILES_LARGE) {
+            if (f8) hipLaunchKernelGGL(pf_gateup_kernel<true>, gu, dim3(PF_THREADS), PF_LDS, st, a);
+            else hipLaunchKernelGGL(pf_gateup_kernel<false>, gu, dim3(PF_THREADS), PF_LDS, st, a);
+        }
+        if (tiles & PF_TILES_SMALL) {
+            if (f8) hipLaunchKernelGGL(pf_gateup_small_kernel<true>, gus, dim3(PF_THREADS), PF_LDS_S, st, a);
+            else hipLaunchKernelGGL(pf_gateup_small_kernel<false>, gus, dim3(PF_THREADS), PF_LDS_S, st, a);
+        }
     }
     if (kernels & 4) {
-        if (f8) {
-            hipLaunchKernelGGL(pf_quantd_kernel, dim3(4096), dim3(256), 0, st, a);
-            hipLaunchKernelGGL(pf_down_kernel<true>, dn, dim3(PF_THREADS), PF_LDS, st, a);
-        } else {
-            hipLaunchKernelGGL(pf_down_kernel<false>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+        if (f8) hipLaunchKernelGGL(pf_quantd_kernel, dim3(4096), dim3(256), 0, st, a);
+        if (tiles & PF_TILES_LARGE) {
+            if (f8) hipLaunchKernelGGL(pf_down_kernel<true>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+            else hipLaunchKernelGGL(pf_down_kernel<false>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+        }
+        if (tiles & PF_TILES_SMALL) {
+            if (f8) hipLaunchKernelGGL(pf_down_small_kernel<true>, dns, dim3(PF_THREADS), PF_LDS_S, st, a);
+            else hipLaunchKernelGGL(pf_down_small_kernel<false>, dns, dim3(PF_THREADS), PF_LDS_S, st, a);
         }
     }
     if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3((a.T + 3) / 4, (a.K + 511) / 512), dim3(256), 0, st, a);

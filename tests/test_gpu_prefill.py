@@ -228,3 +228,72 @@ def test_prefill_edge_cases(cuda, case):
     assert np.allclose(out_bf.float().cpu().numpy(), ref64, rtol=2e-2, atol=1e-3)
     if case == "half_non_local":
         assert not got[:5].any()
+
+
+def _hot_ids(T, n, topk, seed, cuda):
+    """Random distinct experts per token with expert 0 in every token's slot 0 (expert 0 then holds T rows, so a
+    small-tile call runs its later 64-row quarters too)."""
+    from mi355moe import synthetic
+    ids = synthetic.random_ids(T, n, topk, seed=seed, device=cuda).cpu().numpy()
+    for t in range(T):
+        row = list(ids[t])
+        if 0 in row:
+            j = row.index(0)
+            row[0], row[j] = row[j], row[0]
+        else:
+            row[0] = 0
+        ids[t] = row
+    return torch.from_numpy(ids).to(cuda)
+
+
+@pytest.mark.parametrize("numerics,n,K,N,T,topk", [("e3", 16, 1024, 512, 200, 4), ("e4m3", 16, 1024, 512, 200, 4),
+                                                   ("e3", 32, 2048, 256, 300, 2), ("e4m3", 8, 4096, 1024, 130, 3)])
+def test_small_tiles_bit_equal_to_large_tiles(cuda, monkeypatch, numerics, n, K, N, T, topk):
+    """The grouped GEMMs on 64-row tiles (two workgroups per CU; chosen when the routed experts average at most 128
+    rows), on 256-row tiles, and split between the two by segment size (segments of at most 128 rows on the small
+    tiles), forced with MI355MOE_PREFILL_TILES: bit-identical outputs, including a hot expert whose 130..300 rows
+    span up to four 64-row quarters."""
+    from mi355moe import _lib, ops, synthetic
+    _say(f"small vs large tiles: {numerics} n={n} K={K} N={N} T={T} topk={topk}")
+    ex = synthetic.calibrated_layer(n, K, N, seed=n + K + T, device=cuda)
+    x = synthetic.activations(T, K, seed=T + 11, device=cuda)
+    ids = _hot_ids(T, n, topk, T + 12, cuda)
+    w = synthetic.softmax_weights(T, topk, seed=T + 13, device=cuda)
+    outs = []
+    for kind in ("small", "large", "hybrid"):
+        monkeypatch.setenv("MI355MOE_PREFILL_TILES", kind)
+        if numerics == "e3":
+            o = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+        else:
+            o = ops.moe_forward_ids_e4m3(ex, x, ids, w, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        outs.append(o)
+    assert torch.isfinite(outs[0]).all()
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[0], outs[2])
+
+
+def test_small_tiles_vs_oracle(cuda):
+    """The automatic choice at ~27 rows per expert (P = 432 <= 128 n) with a hot expert of 144 rows (three quarters):
+    fp32 output against the E3 rounding points (rel_l2 <= 5e-4) and float64 (rel_l2 <= 5e-3), bf16 elementwise
+    rtol 2e-2 / atol 1e-3."""
+    from mi355moe import _lib, ops, synthetic
+    n, K, N, T, topk, limit = 16, 1024, 512, 144, 3, 10.0
+    _say(f"small tiles vs oracle n={n} K={K} N={N} T={T} topk={topk}")
+    ex = synthetic.calibrated_layer(n, K, N, seed=77, device=cuda)
+    x = synthetic.activations(T, K, seed=78, device=cuda)
+    ids = _hot_ids(T, n, topk, 79, cuda)
+    w = synthetic.softmax_weights(T, topk, seed=80, device=cuda)
+    out32 = ops.moe_forward_ids(ex, x, ids, w, limit=limit, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+    out_bf = ops.moe_forward_ids(ex, x, ids, w, limit=limit, out_dtype=torch.bfloat16, path=_lib.PATH_PREFILL)
+    torch.cuda.synchronize()
+    lay = _np_layer(ex)
+    local = routing.map_topk_to_local(ids.cpu().numpy(), n)
+    tok, exx, w16 = moe.pairs_from_routing(local, w.cpu().numpy(), n, topk)
+    x16 = x.to(torch.float16).cpu().numpy()
+    ref_k = moe.forward(lay, x16, tok, exx, w16, limit, "e3")
+    ref64 = moe.forward(lay, x16, tok, exx, w16, limit, "f64_pre")
+    got = out32.cpu().numpy()
+    assert _rel(got, ref_k) <= 5e-4, _rel(got, ref_k)
+    assert _rel(got, ref64) <= 5e-3, _rel(got, ref64)
+    assert np.allclose(out_bf.float().cpu().numpy(), ref64, rtol=2e-2, atol=1e-3)
