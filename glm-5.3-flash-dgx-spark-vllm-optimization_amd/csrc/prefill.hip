@@ -38,6 +38,13 @@ constexpr int PF_WSB = 4 * PF_WWB;              // one raw-word stage (4 waves)
 constexpr size_t PF_LDS = (size_t)PF_NS * (PF_ASB + PF_WSB);   // 163,840 bytes (the whole LDS)
 constexpr int PF_TMS = 64;                      // rows per tile of the small-tile kernels (two per CU)
 constexpr size_t PF_LDS_S = (size_t)PF_NS * (PF_TMS * PF_RB + PF_WSB);   // 65,536 bytes
+constexpr int PF_TMM = 128;                     // rows per tile of the mid-tile kernels (two per CU)
+constexpr int PF_NSM = 3;                       // their staged steps
+constexpr size_t PF_LDS_M = (size_t)PF_NSM * (PF_TMM * PF_RB + PF_WSB);  // 73,728 bytes
+// Tile kinds of the grouped GEMMs: the rows of a segment (at most 256) taken whole, in 64-row quarters or in
+// 128-row halves.
+enum { PF_LARGE = 0, PF_SMALL = 1, PF_MID = 2 };
+__host__ __device__ constexpr int pf_sub_rows(int kind) { return kind == PF_SMALL ? PF_TMS : kind == PF_MID ? PF_TMM : PF_TM; }
 constexpr int PF_CLD = 260;                     // epilogue staging row stride (floats): [32][PF_CLD] fp32
 
 // Rotated activations (h13, h2) are stored with k permuted inside every group of 16: storage pair p (halves 2p,
@@ -411,8 +418,9 @@ __device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p
 // sourced e4m3 variant's operand; the products with e4m3 activations are then exact and summed in fp32.
 // NRB: the 32-row blocks of the tile that are multiplied (a compile-time count: tiles of up to 32 NRB rows skip the
 // MFMAs and A reads of the other blocks, whose accumulators stay zero and are never stored; the decode is the same).
-// TM: the A rows staged per step (256, or 64 for the small-tile kernels, whose stages then take 64 KB of LDS).
-template <bool E4M3 = false, int NRB = 8, int TM = PF_TM>
+// TM: the A rows staged per step (256; 128 or 64 for the mid- and small-tile kernels). NS: staged steps (loads of
+// step it + NS - 1 are issued while step it is multiplied).
+template <bool E4M3 = false, int NRB = 8, int TM = PF_TM, int NS = PF_NS>
 __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[8][2]) {
     static_assert(32 * NRB <= TM && TM % 32 == 0, "the multiplied row blocks are staged");
     constexpr int ASB = TM * PF_RB;                                   // one A stage
@@ -421,8 +429,8 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     constexpr int RPI = 64 / CPR;                                     // A rows per DMA instruction
     constexpr int NA = RPW / RPI;                                     // A DMA instructions per wave per step
     constexpr int NDMA = NA + PF_KT / 2;                              // DMA instructions per wave per step
-    unsigned char* Ast = smem;                                        // [PF_NS][TM rows][PF_RB]
-    unsigned char* Wst = smem + PF_NS * ASB;                          // [PF_NS][4 waves][PF_KT k tiles][4 tiles][128 B]
+    unsigned char* Ast = smem;                                        // [NS][TM rows][PF_RB]
+    unsigned char* Wst = smem + NS * ASB;                          // [NS][4 waves][PF_KT k tiles][4 tiles][128 B]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int steps = t.kdim / (16 * PF_KT);
@@ -440,7 +448,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     const size_t wstep = (size_t)PF_KT * t.btiles_n * 32;             // words per step (PF_KT k tiles)
     const size_t wins = (size_t)2 * t.btiles_n * 32;                  // words between a wave's W instructions
     auto issue_w = [&](int sw) {
-        unsigned char* wd = Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB;
+        unsigned char* wd = Wst + (sw % NS) * PF_WSB + wv * PF_WWB;
 #pragma unroll
         for (int i = 0; i < PF_KT / 2; ++i) dma16(wsrc + (size_t)sw * wstep + i * wins, wd + i * 1024);
     };
@@ -448,16 +456,16 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         sa = min(sa, steps - 1);
         sw = min(sw, steps - 1);
         if (k < NA)
-            dma16(asrc[k] + (size_t)sa * 16 * PF_KT, Ast + (sa % PF_NS) * ASB + wv * RPW * PF_RB + k * 1024);
+            dma16(asrc[k] + (size_t)sa * 16 * PF_KT, Ast + (sa % NS) * ASB + wv * RPW * PF_RB + k * 1024);
         else
-            dma16(wsrc + (size_t)sw * wstep + (k - NA) * wins, Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB + (k - NA) * 1024);
+            dma16(wsrc + (size_t)sw * wstep + (k - NA) * wins, Wst + (sw % NS) * PF_WSB + wv * PF_WWB + (k - NA) * 1024);
     };
     auto issue = [&](int sa, int sw) {                                // the whole batch
 #pragma unroll
         for (int k = 0; k < NDMA; ++k) issue_one(k, sa, sw);
     };
     auto words = [&](int sw, uint32_t (&w)[PF_KT][3]) {              // this lane's raw words of step sw
-        const unsigned char* wr = Wst + (sw % PF_NS) * PF_WSB + wv * PF_WWB;
+        const unsigned char* wr = Wst + (sw % NS) * PF_WSB + wv * PF_WWB;
 #pragma unroll
         for (int kt = 0; kt < PF_KT; ++kt) pf_load_words(wr + kt * 512, lane, w[kt]);
     };
@@ -483,10 +491,10 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     constexpr int NF = 8 * PF_KT;                                     // A fragments (and decoded pairs) per step
     constexpr int DMA_EVERY = NF / NDMA;                              // MFMA pairs between DMA instructions
     auto step = [&](int it, const h8 (&bc)[PF_KT][2], h8 (&bn)[PF_KT][2]) {
-        WAIT_VM(NDMA * (PF_NS - 2));                                  // A(it) and words(it + 1): the oldest batch
+        WAIT_VM(NDMA * (NS - 2));                                  // A(it) and words(it + 1): the oldest batch
         LDS_BARRIER();
         __builtin_amdgcn_sched_barrier(0);
-        const unsigned char* as = Ast + (it % PF_NS) * ASB;
+        const unsigned char* as = Ast + (it % NS) * ASB;
         uint32_t w[PF_KT][3];
         words(it + 1, w);                                             // step it + 1 (past the end: never used)
         h8 af[NF];
@@ -500,7 +508,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         for (int i = 0; i < NF; ++i) {
             // the next batch's DMA instructions spread over the step (the CU's address path takes them one at a
             // time; issued together after the barrier they would stall every wave behind each other)
-            if (i % DMA_EVERY == 0 && i / DMA_EVERY < NDMA) issue_one(i / DMA_EVERY, it + PF_NS - 1, it + PF_NS);
+            if (i % DMA_EVERY == 0 && i / DMA_EVERY < NDMA) issue_one(i / DMA_EVERY, it + NS - 1, it + NS);
             if (i + 4 < NF && ((i + 4) & 7) < NRB) af[i + 4] = afrag(as, i + 4);
             const int kt = i >> 3, rb = i & 7;
             // pair i's products after the first MFMA, pair i - 1's values after the second: no VALU instruction
@@ -521,12 +529,12 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         for (int s = 0; s < 2; ++s)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[rb][s][r] = 0.f;
-    // prologue: raw words of step 0 first, then the batches that steps 0 .. PF_NS - 2 of the loop would have issued
-    // (A(0 .. PF_NS - 2), words(1 .. PF_NS - 1)); decode step 0
+    // prologue: raw words of step 0 first, then the batches that steps 0 .. NS - 2 of the loop would have issued
+    // (A(0 .. NS - 2), words(1 .. NS - 1)); decode step 0
     issue_w(0);
 #pragma unroll
-    for (int j = 0; j < PF_NS - 1; ++j) issue(j, j + 1);
-    WAIT_VM(NDMA * (PF_NS - 1));                                      // the step-0 words (this wave's own)
+    for (int j = 0; j < NS - 1; ++j) issue(j, j + 1);
+    WAIT_VM(NDMA * (NS - 1));                                      // the step-0 words (this wave's own)
     h8 bA[PF_KT][2], bB[PF_KT][2];
     {
         uint32_t w[PF_KT][3], q[PF_KT][8];
@@ -535,7 +543,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
         for (int i = 0; i < NF; ++i) q[i >> 3][i & 7] = pf_decode_pair(w[i >> 3], i & 7);
         operands(q, bA);
     }
-    static_assert(NDMA * (PF_NS - 1) <= 63 && PF_KT % 2 == 0, "stages within the vmcnt range");
+    static_assert(NDMA * (NS - 1) <= 63 && PF_KT % 2 == 0, "stages within the vmcnt range");
     for (int it = 0; it < steps; it += 2) {                           // steps is even (kdim % (32 PF_KT) == 0)
         step(it, bA, bB);
         step(it + 1, bB, bA);
@@ -576,14 +584,15 @@ __device__ __forceinline__ void pf_tile_of(int b, int ncb, int& s, int& cb) {
 // E4M3: the trellis-sourced e4m3 variant (weights rounded to e4m3 in the GEMM; accumulators times the row's
 // activation scale before the output Hadamard; the down input H(a16 * suh_d) * r kept in fp32 in vd, its row maxima
 // gathered in amaxd for pf_quantd_kernel). code/fork/overlay/glm53_moe_e4m3.py:654-674 (spec_proj, spec_ffn).
-// SMALL: the tile is rows 64 quarter .. 64 quarter + 63 of the segment, staged as 64 rows (the small-tile kernels).
-template <bool E4M3, bool SMALL>
-__device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int quarter, int cb, unsigned char* smem) {
+// KIND: the tile is part `part` of the segment's rows in pf_sub_rows(KIND)-row parts (PF_LARGE: the whole segment).
+template <bool E4M3, int KIND>
+__device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int part, int cb, unsigned char* smem) {
+    constexpr int SUB = pf_sub_rows(KIND);
     const int e = a.seg_expert[s];
     int row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
-    if (SMALL) {
-        row0 += PF_TMS * quarter;
-        rn = min(rn - PF_TMS * quarter, PF_TMS);
+    if (KIND != PF_LARGE) {
+        row0 += SUB * part;
+        rn = min(rn - SUB * part, SUB);
     }
     if (rn <= 0 || row0 < 0 || row0 + rn > a.P || e < 0 || e >= a.n) return;   // (caller-built tables)
     const int K = a.K, N = a.N;
@@ -597,7 +606,9 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
     t.btiles_n = N >> 4;
     t.bcol0 = cb * 8 + 4 * (wv & 1);
     f16v acc[8][2];
-    if (SMALL) pf_gemm<E4M3, 2, PF_TMS>(t, smem, acc);
+    if (KIND == PF_SMALL) pf_gemm<E4M3, 2, PF_TMS>(t, smem, acc);
+    else if (KIND == PF_MID && rn <= 64) pf_gemm<E4M3, 2, PF_TMM, PF_NSM>(t, smem, acc);
+    else if (KIND == PF_MID) pf_gemm<E4M3, 4, PF_TMM, PF_NSM>(t, smem, acc);
     else if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);              // uniform: small tiles multiply two row blocks
     else pf_gemm<E4M3, 8>(t, smem, acc);
 
@@ -623,7 +634,7 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
     const float L = a.limit;
     const float hr = HAD_R * fwht_sign(lane);                        // r and the sign fwht128_x16s leaves
 #pragma unroll
-    for (int rb = 0; rb < (SMALL ? 2 : 8); ++rb) {
+    for (int rb = 0; rb < SUB / 32; ++rb) {
         if (32 * rb >= rn) break;                                    // uniform over the workgroup
         pf_stage_rows(acc, Cs, rb);
         __syncthreads();
@@ -692,15 +703,15 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
     }
 }
 
-// Workgroup b of a small-tile grid (8 ncb ceil(4 S_cap / 8) workgroups): tile (virtual segment v, column block cb)
-// as pf_tile_of orders them, v = quarter S_cap + s, so the first quarters of all segments come first (at small row
-// counts the only ones with rows) and the later quarters' workgroups, mostly empty, come last.
-__device__ __forceinline__ bool pf_small_tile_of(const PrefillArgs& a, int ncb, int& s, int& quarter, int& cb) {
+// Workgroup b of a grid of segment parts (8 ncb ceil(parts S_cap / 8) workgroups): tile (virtual segment v, column
+// block cb) as pf_tile_of orders them, v = part S_cap + s, so the first parts of all segments come first and the
+// later parts' workgroups, empty for segments of fewer rows, come last.
+__device__ __forceinline__ bool pf_part_tile_of(const PrefillArgs& a, int ncb, int parts, int& s, int& part, int& cb) {
     int v;
     pf_tile_of(blockIdx.x, ncb, v, cb);
-    if (a.S_cap <= 0 || v >= 4 * a.S_cap) return false;
-    quarter = v / a.S_cap;
-    s = v - quarter * a.S_cap;
+    if (a.S_cap <= 0 || v >= parts * a.S_cap) return false;
+    part = v / a.S_cap;
+    s = v - part * a.S_cap;
     return s < a.nseg[0];
 }
 
@@ -710,7 +721,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a)
     int s, cb;
     pf_tile_of(blockIdx.x, a.N >> 7, s, cb);
     if (s >= a.nseg[0] || (a.small_rows > 0 && a.seg_rows[s] <= a.small_rows)) return;
-    pf_gateup_tile<E4M3, false>(a, s, 0, cb, smem);
+    pf_gateup_tile<E4M3, PF_LARGE>(a, s, 0, cb, smem);
 }
 
 // The same GEMM for segments of few rows: 64-row tiles with 64 KB of LDS and at most 256 registers per wave, so two
@@ -721,20 +732,33 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     int s, quarter, cb;
-    if (!pf_small_tile_of(a, a.N >> 7, s, quarter, cb)) return;
+    if (!pf_part_tile_of(a, a.N >> 7, 4, s, quarter, cb)) return;
     if (a.small_rows > 0 && a.seg_rows[s] > a.small_rows) return;
-    pf_gateup_tile<E4M3, true>(a, s, quarter, cb, smem);
+    pf_gateup_tile<E4M3, PF_SMALL>(a, s, quarter, cb, smem);
+}
+
+// The same GEMM on 128-row halves of the segments (73,728 bytes of LDS in three stages, at most 256 registers per
+// wave, two workgroups per CU): each weight is decoded twice per 256-row segment, and one workgroup's epilogue and
+// waits are covered by the other's main loop.
+template <bool E4M3>
+__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void pf_gateup_mid_kernel(
+    PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    int s, half, cb;
+    if (!pf_part_tile_of(a, a.N >> 7, 2, s, half, cb)) return;
+    pf_gateup_tile<E4M3, PF_MID>(a, s, half, cb, smem);
 }
 
 // ------------------------------------------------------------------------------------------------ down
 
-template <bool E4M3, bool SMALL>
-__device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int quarter, int cb, unsigned char* smem) {
+template <bool E4M3, int KIND>
+__device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int part, int cb, unsigned char* smem) {
+    constexpr int SUB = pf_sub_rows(KIND);
     const int e = a.seg_expert[s];
     int row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
-    if (SMALL) {
-        row0 += PF_TMS * quarter;
-        rn = min(rn - PF_TMS * quarter, PF_TMS);
+    if (KIND != PF_LARGE) {
+        row0 += SUB * part;
+        rn = min(rn - SUB * part, SUB);
     }
     if (rn <= 0 || row0 < 0 || row0 + rn > a.P || e < 0 || e >= a.n) return;   // (caller-built tables)
     const int K = a.K, N = a.N;
@@ -748,7 +772,9 @@ __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int qu
     t.btiles_n = K >> 4;
     t.bcol0 = cb * 16 + 4 * wv;
     f16v acc[8][2];
-    if (SMALL) pf_gemm<E4M3, 2, PF_TMS>(t, smem, acc);
+    if (KIND == PF_SMALL) pf_gemm<E4M3, 2, PF_TMS>(t, smem, acc);
+    else if (KIND == PF_MID && rn <= 64) pf_gemm<E4M3, 2, PF_TMM, PF_NSM>(t, smem, acc);
+    else if (KIND == PF_MID) pf_gemm<E4M3, 4, PF_TMM, PF_NSM>(t, smem, acc);
     else if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);
     else pf_gemm<E4M3, 8>(t, smem, acc);
 
@@ -773,7 +799,7 @@ __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int qu
                                                   __builtin_amdgcn_perm(par, own, sel));
         };
 #pragma unroll
-        for (int rb = 0; rb < (SMALL ? 2 : 8); ++rb) {
+        for (int rb = 0; rb < SUB / 32; ++rb) {
             if (32 * rb >= rn) break;
             if (32 * rb + 32 <= rn) {
 #pragma unroll
@@ -793,7 +819,7 @@ __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int qu
     }
     float* o = a.contrib + c0;
 #pragma unroll
-    for (int rb = 0; rb < (SMALL ? 2 : 8); ++rb) {
+    for (int rb = 0; rb < SUB / 32; ++rb) {
         if (32 * rb >= rn) break;
         if (32 * rb + 32 <= rn) {
 #pragma unroll
@@ -821,7 +847,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     int s, cb;
     pf_tile_of(blockIdx.x, a.K >> 8, s, cb);
     if (s >= a.nseg[0] || (a.small_rows > 0 && a.seg_rows[s] <= a.small_rows)) return;
-    pf_down_tile<E4M3, false>(a, s, 0, cb, smem);
+    pf_down_tile<E4M3, PF_LARGE>(a, s, 0, cb, smem);
 }
 
 template <bool E4M3>
@@ -829,9 +855,18 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     int s, quarter, cb;
-    if (!pf_small_tile_of(a, a.K >> 8, s, quarter, cb)) return;
+    if (!pf_part_tile_of(a, a.K >> 8, 4, s, quarter, cb)) return;
     if (a.small_rows > 0 && a.seg_rows[s] > a.small_rows) return;
-    pf_down_tile<E4M3, true>(a, s, quarter, cb, smem);
+    pf_down_tile<E4M3, PF_SMALL>(a, s, quarter, cb, smem);
+}
+
+template <bool E4M3>
+__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void pf_down_mid_kernel(
+    PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    int s, half, cb;
+    if (!pf_part_tile_of(a, a.K >> 8, 2, s, half, cb)) return;
+    pf_down_tile<E4M3, PF_MID>(a, s, half, cb, smem);
 }
 
 // ------------------------------------------------------------------------------------------------ combine
@@ -1109,27 +1144,41 @@ int prefill_setup() {
                           reinterpret_cast<const void*>(pf_down_small_kernel<true>)};
     for (const void* k : kss)
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_S) != hipSuccess) return -1;
+    const void* ksm[4] = {reinterpret_cast<const void*>(pf_gateup_mid_kernel<false>),
+                          reinterpret_cast<const void*>(pf_gateup_mid_kernel<true>),
+                          reinterpret_cast<const void*>(pf_down_mid_kernel<false>),
+                          reinterpret_cast<const void*>(pf_down_mid_kernel<true>)};
+    for (const void* k : ksm)
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_M) != hipSuccess) return -1;
     g_pf_attr = true;
     return 0;
 }
 
-// Which grouped GEMMs a call runs. The small-tile kernels take a call whose routed experts average at most
-// PF_SMALL_ROWS rows (P <= 128 n): two workgroups per CU keep the VALU-bound weight decode busier, which outweighs
-// decoding a segment's weights once per 64-row quarter (measured at 288 experts, top-8: T = 2048, ~57 rows per
-// expert, 21 % faster; T = 4096, ~114 rows, 6 % faster; T = 8192, ~228 rows, 47 % slower). Larger calls run the
-// 256-row tiles. "hybrid" splits one call by segment size (segments of at most PF_SMALL_ROWS rows on the small
-// tiles, larger ones on the 256-row tiles: 2 % faster on Zipf-skewed routing at T = 8192, 6 % slower on uniform
-// routing, where the few small segments add a serial launch). The environment variable MI355MOE_PREFILL_TILES =
-// "small", "large" or "hybrid" forces a choice; all three give bit-identical results (a row's arithmetic does not
-// depend on the tile that holds it).
+// Which grouped GEMMs a call runs. Tiles of few rows are bound by the weight decode on the VALU, and the 256-row
+// kernels run one workgroup per CU (160 KB of staging, 256 accumulator registers), which leaves the VALU idle at
+// every barrier and load wait. The mid- and small-tile kernels run two workgroups per CU, at the price of decoding
+// a segment's weights once per 128-row half or 64-row quarter. Measured at 288 experts, top-8 (E3 numerics /
+// trellis-sourced e4m3), against the 256-row kernels:
+//   T = 2048 (~57 rows per expert):  mid 27 % faster / small 18 % faster (mid 3 % slower);
+//   T = 4096 (~114 rows):            mid 29 % faster / mid 21 % faster (small 3 % slower);
+//   T = 6144 (~171 rows):            mid 4 % slower;
+//   T = 8192 (~228 rows):            mid 8 % slower, small 47 % slower; Zipf-skewed routing: mid 4 % faster.
+// Hence: P <= 64 n: mid (small for e4m3); P <= 128 n: mid; larger calls: the 256-row kernels. "hybrid" splits a
+// call by segment size (segments of at most PF_SMALL_ROWS rows on the small tiles, larger ones on the 256-row
+// tiles). The environment variable MI355MOE_PREFILL_TILES = "small", "mid", "large" or "hybrid" forces a choice;
+// all give bit-identical results (a row's arithmetic does not depend on the tile that holds it).
 constexpr int PF_SMALL_ROWS = 128;
-enum { PF_TILES_SMALL = 1, PF_TILES_LARGE = 2, PF_TILES_BOTH = 3 };
+enum { PF_TILES_SMALL = 1, PF_TILES_LARGE = 2, PF_TILES_BOTH = 3, PF_TILES_MID = 4 };
 static int pf_tiles(const PrefillArgs& a) {
     const char* f = getenv("MI355MOE_PREFILL_TILES");
+    if (f && !strcmp(f, "mid")) return PF_TILES_MID;
     if (f && !strcmp(f, "small")) return PF_TILES_SMALL;
     if (f && !strcmp(f, "large")) return PF_TILES_LARGE;
     if (f && !strcmp(f, "hybrid")) return PF_TILES_BOTH;
-    return (a.n > 0 && (int64_t)a.P <= (int64_t)PF_SMALL_ROWS * a.n) ? PF_TILES_SMALL : PF_TILES_LARGE;
+    if (a.n <= 0) return PF_TILES_LARGE;
+    const int64_t P = a.P, n = a.n;
+    if (P <= 64 * n) return a.e4m3 ? PF_TILES_SMALL : PF_TILES_MID;
+    return P <= 128 * n ? PF_TILES_MID : PF_TILES_LARGE;
 }
 
 int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
@@ -1146,6 +1195,8 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     const dim3 gu(8 * (a.N / 128) * sg), dn(8 * (a.K / 256) * sg);
     const int sgs = (4 * a.S_cap + 7) / 8;                          // small tiles: four quarters per segment
     const dim3 gus(8 * (a.N / 128) * sgs), dns(8 * (a.K / 256) * sgs);
+    const int sgm = (2 * a.S_cap + 7) / 8;                          // mid tiles: two halves per segment
+    const dim3 gum(8 * (a.N / 128) * sgm), dnm(8 * (a.K / 256) * sgm);
     const int tiles = pf_tiles(a0);
     a.small_rows = tiles == PF_TILES_BOTH ? PF_SMALL_ROWS : 0;
     if (kernels & 2) {
@@ -1157,6 +1208,10 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
             if (f8) hipLaunchKernelGGL(pf_gateup_small_kernel<true>, gus, dim3(PF_THREADS), PF_LDS_S, st, a);
             else hipLaunchKernelGGL(pf_gateup_small_kernel<false>, gus, dim3(PF_THREADS), PF_LDS_S, st, a);
         }
+        if (tiles & PF_TILES_MID) {
+            if (f8) hipLaunchKernelGGL(pf_gateup_mid_kernel<true>, gum, dim3(PF_THREADS), PF_LDS_M, st, a);
+            else hipLaunchKernelGGL(pf_gateup_mid_kernel<false>, gum, dim3(PF_THREADS), PF_LDS_M, st, a);
+        }
     }
     if (kernels & 4) {
         if (f8) hipLaunchKernelGGL(pf_quantd_kernel, dim3(4096), dim3(256), 0, st, a);
@@ -1167,6 +1222,10 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
         if (tiles & PF_TILES_SMALL) {
             if (f8) hipLaunchKernelGGL(pf_down_small_kernel<true>, dns, dim3(PF_THREADS), PF_LDS_S, st, a);
             else hipLaunchKernelGGL(pf_down_small_kernel<false>, dns, dim3(PF_THREADS), PF_LDS_S, st, a);
+        }
+        if (tiles & PF_TILES_MID) {
+            if (f8) hipLaunchKernelGGL(pf_down_mid_kernel<true>, dnm, dim3(PF_THREADS), PF_LDS_M, st, a);
+            else hipLaunchKernelGGL(pf_down_mid_kernel<false>, dnm, dim3(PF_THREADS), PF_LDS_M, st, a);
         }
     }
     if (kernels & 8) hipLaunchKernelGGL(pf_combine_kernel, dim3((a.T + 3) / 4, (a.K + 511) / 512), dim3(256), 0, st, a);

@@ -248,19 +248,19 @@ def _hot_ids(T, n, topk, seed, cuda):
 
 @pytest.mark.parametrize("numerics,n,K,N,T,topk", [("e3", 16, 1024, 512, 200, 4), ("e4m3", 16, 1024, 512, 200, 4),
                                                    ("e3", 32, 2048, 256, 300, 2), ("e4m3", 8, 4096, 1024, 130, 3)])
-def test_small_tiles_bit_equal_to_large_tiles(cuda, monkeypatch, numerics, n, K, N, T, topk):
-    """The grouped GEMMs on 64-row tiles (two workgroups per CU; chosen when the routed experts average at most 128
-    rows), on 256-row tiles, and split between the two by segment size (segments of at most 128 rows on the small
-    tiles), forced with MI355MOE_PREFILL_TILES: bit-identical outputs, including a hot expert whose 130..300 rows
-    span up to four 64-row quarters."""
+def test_tile_kinds_bit_equal(cuda, monkeypatch, numerics, n, K, N, T, topk):
+    """The grouped GEMMs on 64-row tiles and on 128-row tiles (two workgroups per CU; chosen when the routed experts
+    average at most 128 rows), on 256-row tiles, and split between small and 256-row tiles by segment size, forced
+    with MI355MOE_PREFILL_TILES: bit-identical outputs, including a hot expert whose 130..300 rows span up to four
+    64-row quarters or three 128-row halves of its segments."""
     from mi355moe import _lib, ops, synthetic
-    _say(f"small vs large tiles: {numerics} n={n} K={K} N={N} T={T} topk={topk}")
+    _say(f"tile kinds: {numerics} n={n} K={K} N={N} T={T} topk={topk}")
     ex = synthetic.calibrated_layer(n, K, N, seed=n + K + T, device=cuda)
     x = synthetic.activations(T, K, seed=T + 11, device=cuda)
     ids = _hot_ids(T, n, topk, T + 12, cuda)
     w = synthetic.softmax_weights(T, topk, seed=T + 13, device=cuda)
     outs = []
-    for kind in ("small", "large", "hybrid"):
+    for kind in ("small", "large", "hybrid", "mid"):
         monkeypatch.setenv("MI355MOE_PREFILL_TILES", kind)
         if numerics == "e3":
             o = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
@@ -271,15 +271,16 @@ def test_small_tiles_bit_equal_to_large_tiles(cuda, monkeypatch, numerics, n, K,
     assert torch.isfinite(outs[0]).all()
     assert torch.equal(outs[0], outs[1])
     assert torch.equal(outs[0], outs[2])
+    assert torch.equal(outs[0], outs[3])
 
 
-def test_small_tiles_vs_oracle(cuda):
-    """The automatic choice at ~27 rows per expert (P = 432 <= 128 n) with a hot expert of 144 rows (three quarters):
-    fp32 output against the E3 rounding points (rel_l2 <= 5e-4) and float64 (rel_l2 <= 5e-3), bf16 elementwise
-    rtol 2e-2 / atol 1e-3."""
+def test_few_row_tiles_vs_oracle(cuda):
+    """The automatic choice at ~27 rows per expert (P = 432 <= 64 n: the mid-tile kernels, 128-row halves) with a hot
+    expert of 144 rows (two halves): fp32 output against the E3 rounding points (rel_l2 <= 5e-4) and float64
+    (rel_l2 <= 5e-3), bf16 elementwise rtol 2e-2 / atol 1e-3."""
     from mi355moe import _lib, ops, synthetic
     n, K, N, T, topk, limit = 16, 1024, 512, 144, 3, 10.0
-    _say(f"small tiles vs oracle n={n} K={K} N={N} T={T} topk={topk}")
+    _say(f"few-row tiles vs oracle n={n} K={K} N={N} T={T} topk={topk}")
     ex = synthetic.calibrated_layer(n, K, N, seed=77, device=cuda)
     x = synthetic.activations(T, K, seed=78, device=cuda)
     ids = _hot_ids(T, n, topk, 79, cuda)
