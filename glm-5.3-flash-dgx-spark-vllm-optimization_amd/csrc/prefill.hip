@@ -1,12 +1,14 @@
 // Prefill-path kernels (many rows per expert, the E3 grouped tier): gather + input rotation, the gate/up grouped
-// GEMM and the down grouped GEMM on fp16 MFMA (v_mfma_f32_32x32x16_f16) with the EXL3 trellis decoded into LDS.
+// GEMM and the down grouped GEMM on fp16 MFMA (v_mfma_f32_32x32x16_f16) with the EXL3 trellis decoded in registers.
 //
 // Tiles: a workgroup of 4 waves (one per SIMD) owns a 256-row segment of one expert (rows sorted by expert) and one
 // column block; each wave multiplies all 256 rows by its own 64 columns:
 //   gate/up: 128 columns of gate (waves 0, 1) and the same 128 of up (waves 2, 3);
 //   down:    256 output columns.
 // The A rows are staged in LDS (shared by the 4 waves); each wave decodes its own trellis words straight into MFMA
-// operands, so every weight value is decoded once per 256-row tile and never goes through LDS.
+// operands, so every weight value is decoded once per tile and never goes through LDS. Calls with few rows per
+// expert run the same GEMM on 128- or 64-row parts of the segments instead (the mid- and small-tile kernels: two
+// workgroups per CU, see pf_tiles).
 // Numerics (oracle/csrc/oracle.c mode 1 = the E3 kernels, code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu):
 //   gather   h13 = fp16(H(fp16(x * suh_g)) * r)                                         (exl3_fat_moe.cu:95-126)
 //   gate/up  g = (H(acc_g) * r) * svh_g, u likewise; iff L != 0: g = min(g, L), u = clamp(u, -L, L);
