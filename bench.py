@@ -452,6 +452,34 @@ def run_prefill_zipf(args, torch, dev, caps=(0, 16, 32, 64, 128)):
                                    "with <= 64 rows), EXL3 4-bit synthetic experts; ms per layer call by thin cap"}
 
 
+def run_prefill_chunks(args, torch, dev, sizes=(2048, 4096)):
+    """Smaller prefill chunks (uniform-random router logits, the T=8192 workload's layer shapes): ms per layer call
+    of the grouped path at each chunk size. At ~57 and ~114 rows per expert these run the mid-tile GEMMs (128-row
+    halves of the segments, two workgroups per CU)."""
+    from mi355moe import _lib, ops, synthetic
+    layer = synthetic.exl3_layer(E, K, N, seed=470, device=dev, uniform_suh=True)
+    res = {}
+    for T in sizes:
+        x = synthetic.activations(T, K, seed=471, device=dev)
+        g = torch.Generator(device=dev)
+        g.manual_seed(472)
+        ids, wts = ops.router_topk(torch.rand(T, E, generator=g, device=dev) * 4 - 2, TOPK, None, routed_scale=SCALE)
+        out = torch.empty(T, K, dtype=torch.bfloat16, device=dev)
+        call = lambda: ops.moe_forward_ids(layer, x, ids, wts, limit=LIMIT, out=out, path=_lib.PATH_PREFILL)
+        settle(torch, call, 20.0)
+        steps = max(4, args.steps // 2)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        res[str(T)] = round(e0.elapsed_time(e1) / steps, 4)
+    return {"prefill_chunk_ms_by_tokens": res,
+            "prefill_chunk_config": f"{E} experts, top-{TOPK}, uniform-random router logits, EXL3 4-bit synthetic "
+                                    "experts sharing one w13 suh; grouped path, ms per layer call by chunk tokens"}
+
+
 def run_fp8(args, torch, dev):
     """e4m3 expert variant, T=2048 (hidden 4096, 288 experts, top-8, intermediate 1024): block-scaled e4m3 experts
     (N(0, 0.02) weights, fp32 scale per 128x128 block), bf16 activations quantised per token, sigmoid top-8 x2.5 of
@@ -755,6 +783,9 @@ def main():
     if args.workload in ("all", "prefill", "zipf"):
         log("[bench] prefill, Zipf routing, thin/fat split ...")
         res.update(run_prefill_zipf(args, torch, dev))
+    if args.workload in ("all", "prefill"):
+        log("[bench] prefill chunks T=2048, 4096 ...")
+        res.update(run_prefill_chunks(args, torch, dev))
     if args.workload in ("all", "fp8"):
         log("[bench] fp8 ...")
         res.update(run_fp8(args, torch, dev))
