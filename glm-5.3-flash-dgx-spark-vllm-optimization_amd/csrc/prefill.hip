@@ -1250,15 +1250,12 @@ int launch_prefill_rows_down(const PrefillArgs& a0, const int64_t* row_token, in
     const int fill = std::max(1, std::min(2048, (std::max(a.P, tokens) + 255) / 256));
     hipLaunchKernelGGL(pf_rows_init_kernel, dim3(fill), dim3(256), 0, st, a, pe, cnt, tokens);
     hipLaunchKernelGGL(pf_seg_rows_kernel, dim3(a.S_cap), dim3(256), 0, st, a, pe);
-    const int sg = (a.S_cap + 7) / 8;
-    const dim3 dn(8 * (a.K / 256) * sg);
+    // the grouped GEMMs as launch_prefill runs them (the same tile choice); e4m3: gate/up (fp32 down inputs and their
+    // row maxima, which rows_init zeroed), quantization, down
     if (a.e4m3) {
-        // the e4m3 chain: gate/up (fp32 down inputs and their row maxima, which rows_init zeroed), quantization, down
-        hipLaunchKernelGGL(pf_gateup_kernel<true>, dim3(8 * (a.N / 128) * sg), dim3(PF_THREADS), PF_LDS, st, a);
-        hipLaunchKernelGGL(pf_quantd_kernel, dim3(4096), dim3(256), 0, st, a);
-        hipLaunchKernelGGL(pf_down_kernel<true>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+        if (launch_prefill(a, st, 2 | 4)) return -1;
     } else {
-        hipLaunchKernelGGL(pf_down_kernel<false>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+        if (launch_prefill(a, st, 4)) return -1;
     }
     hipLaunchKernelGGL(pf_rows_by_token_kernel, dim3(std::max(1, std::min(2048, (a.P + 255) / 256))), dim3(256), 0, st,
                        a, row_token, cnt, list, tokens);
