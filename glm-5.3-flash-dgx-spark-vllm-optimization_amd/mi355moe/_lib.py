@@ -18,7 +18,7 @@ PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
 OPT_ACCUMULATE, OPT_BF16_CONTRIB, OPT_E4M3, OPT_PERSISTENT = 1, 2, 4, 8
 LAYER_SHARED_W13_SUH = 1
 LAYER_UNIFORM_W13_SUH = 2
-PREFILL_MIN_PAIRS = 4096
+PREFILL_MIN_PAIRS = 5120
 NOALLOC_SCRATCH_BYTES = 32 << 20
 ESCRATCH = 7
 

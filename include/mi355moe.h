@@ -127,8 +127,9 @@ int mi355moe_rot_in(const void* x, int x_dtype, int64_t x_stride, int64_t K, con
  * Pairs P = T*topk <= 65536. */
 enum { MI355MOE_PATH_AUTO = 0, MI355MOE_PATH_DECODE = 1, MI355MOE_PATH_PREFILL = 2 };
 /* The automatic choice: the prefill path when P >= MI355MOE_PREFILL_MIN_PAIRS and the layer has
- * MI355MOE_LAYER_SHARED_W13_SUH, else the decode path. */
-#define MI355MOE_PREFILL_MIN_PAIRS 4096
+ * MI355MOE_LAYER_SHARED_W13_SUH, else the decode path (measured at 288 experts, hidden 4096, intermediate 1024: the
+ * decode path is faster up to ~4,700 pairs, the grouped path beyond). */
+#define MI355MOE_PREFILL_MIN_PAIRS 5120
 int64_t mi355moe_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk);
 int64_t mi355moe_moe_workspace_bytes_path(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk, int path);
 

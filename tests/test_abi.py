@@ -55,7 +55,7 @@ def test_workspace_planners_answer_without_a_gpu():
     bad = _fake_desc(K=4000)
     assert L.mi355moe_moe_workspace_bytes(ctypes.byref(bad), 8, 8) == -1
     assert L.mi355moe_route_workspace_bytes(65536, 288) > 0
-    # the automatic choice: prefill layout (rotated rows + fp32 accumulator) above 4096 pairs with shared suh
+    # the automatic choice: prefill layout (rotated rows + fp32 accumulator) from 5120 pairs with shared suh
     big = L.mi355moe_moe_workspace_bytes(ctypes.byref(d), 8192, 8)
     assert big >= 8192 * 8 * (4096 + 1024) * 2 + 8192 * 4096 * 4
     assert L.mi355moe_moe_workspace_bytes_path(ctypes.byref(d), 8192, 8, 1) != big      # forced decode layout
