@@ -317,6 +317,87 @@ int mi355moe_route(const void* ids, int ids_dtype, const void* weights, int weig
     return rc_launch(launch_route(a, stream));
 }
 
+int64_t mi355moe_route_rows_workspace_bytes(int64_t P, int64_t n) {
+    if (P < 0 || n < 0) return -1;
+    Carve c(nullptr);
+    const int64_t S = std::min(P, n) + (P + PREFILL_TM - 1) / PREFILL_TM;
+    c.take<int>(P);                  // tok
+    c.take<uint16_t>(P);             // w16
+    c.take<float>(P);                // w32
+    c.take<int>(P);                  // pe
+    c.take<int>(P);                  // inv
+    c.take<int>(3 * S + 1);          // segments (unused) and their count
+    c.take<int>(n + 1);              // counts
+    c.take<int>(P);                  // multi-block scratch
+    c.take<int>(((P + 1023) / 1024) * (n + 1));
+    c.take<int>(n + 1);
+    return (int64_t)c.off;
+}
+
+int mi355moe_route_rows(const void* ids, int ids_dtype, const void* weights, int weights_dtype, int64_t T,
+                        int64_t topk, const int64_t* expert_map, int64_t n_global, int64_t n, int32_t* local,
+                        int32_t* pos, int64_t* row_token, float* row_weight, int32_t* row_expert, int64_t* counts,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!ids || !weights || !local || !pos || !row_token || !row_weight || !row_expert || !counts || !workspace)
+        return MI355MOE_EINVAL;
+    if (ids_dtype != MI355MOE_I32 && ids_dtype != MI355MOE_I64) return MI355MOE_EDTYPE;
+    if (dt_w(weights_dtype) < 0) return MI355MOE_EDTYPE;
+    if (T < 0 || topk < 1 || topk > MAX_TOPK || n < 1 || n > MAX_EXPERTS) return MI355MOE_ELIMIT;
+    if (expert_map && n_global < 0) return MI355MOE_EINVAL;
+    const int64_t P = T * topk;
+    if (P > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if ((int64_t)workspace_bytes < mi355moe_route_rows_workspace_bytes(P, n)) return MI355MOE_EWORKSPACE;
+    if (P == 0) return 0;
+    const int64_t S = std::min(P, n) + (P + PREFILL_TM - 1) / PREFILL_TM;
+    RouteArgs a;
+    memset(&a, 0, sizeof(a));
+    Carve c(workspace);
+    a.tok = c.take<int>(P);
+    a.w16 = c.take<uint16_t>(P);
+    a.w32 = c.take<float>(P);
+    a.pe = c.take<int>(P);
+    a.inv = c.take<int>(P);
+    a.seg_expert = c.take<int>(3 * S + 1);
+    a.seg_row0 = a.seg_expert + S;
+    a.seg_rows = a.seg_row0 + S;
+    a.nseg = a.seg_rows + S;
+    a.counts = c.take<int>(n + 1);
+    a.loc = c.take<int>(P);
+    a.blk_cnt = c.take<int>(((P + 1023) / 1024) * (n + 1));
+    a.cnt_out = c.take<int>(n + 1);
+    a.ids = ids;
+    a.ids64 = ids_dtype == MI355MOE_I64;
+    a.w = weights;
+    a.wdt = dt_w(weights_dtype);
+    a.emap = expert_map;
+    a.n_global = expert_map ? n_global : 0;
+    a.P = (int)P;
+    a.topk = (int)topk;
+    a.n = (int)n;
+    a.R = 1 << 30;
+    a.seg = PREFILL_TM;
+    a.S_cap = (int)S;
+    return rc_launch(launch_route_rows(a, local, pos, row_token, row_weight, row_expert, counts, stream));
+}
+
+int mi355moe_e3_fat_tables(const int64_t* counts, int64_t n, int64_t cap, const int64_t* token_sorted,
+                           const void* weight_sorted, int64_t rows_cap, int64_t tile, int32_t* seg_expert,
+                           int32_t* seg_row0, int32_t* seg_rows, int64_t max_segs, int32_t* num_segs,
+                           int32_t* num_rows, int32_t* row_expert, int64_t* row_token, void* row_weight,
+                           int32_t* scratch, hipStream_t stream) {
+    if (!counts || !token_sorted || !weight_sorted || !seg_expert || !seg_row0 || !seg_rows || !num_segs ||
+        !num_rows || !row_expert || !row_token || !row_weight || !scratch)
+        return MI355MOE_EINVAL;
+    if (n < 1 || n > MAX_EXPERTS || rows_cap < 0 || rows_cap > MAX_PAIRS || cap < 0) return MI355MOE_ELIMIT;
+    if (tile < 16 || tile > PREFILL_TM) return MI355MOE_ESHAPE;
+    if (max_segs < (rows_cap + tile - 1) / tile + n) return MI355MOE_ESHAPE;
+    return rc_launch(launch_fat_tables(counts, (int)n, (int)std::min<int64_t>(cap, 1 << 30), token_sorted,
+                                       static_cast<const uint16_t*>(weight_sorted), (int)rows_cap, (int)tile,
+                                       (int)std::min<int64_t>(max_segs, 1 << 30), seg_expert, seg_row0, seg_rows,
+                                       num_segs, num_rows, row_expert, row_token,
+                                       static_cast<uint16_t*>(row_weight), scratch, stream));
+}
+
 int mi355moe_rot_in(const void* x, int x_dtype, int64_t x_stride, int64_t K, const int32_t* tok, const int32_t* pe,
                     int64_t P, const int64_t* suh_table, void* out, hipStream_t stream) {
     if (!x || !tok || !pe || !suh_table || !out) return MI355MOE_EINVAL;
@@ -505,6 +586,10 @@ static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     d.tok_rows = tok_rows_flag(layer);
     d.contrib_bf16 = (options & MI355MOE_OPT_BF16_CONTRIB) ? 1 : 0;
     d.out_accumulate = (options & MI355MOE_OPT_ACCUMULATE) ? 1 : 0;
+    if (e4m3 && (options & MI355MOE_OPT_DOWN16)) {   // fp16 down operands: no down-input quantisation or its scale
+        d.down16 = 1;
+        d.dsc = nullptr;
+    }
     if (prefill_setup()) return rc_launch(-1);
     r.ids = ids;
     r.ids64 = ids_dtype == MI355MOE_I64;
@@ -544,9 +629,11 @@ int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x
     if (!x || !ids || !weights || !out || !workspace) return MI355MOE_EINVAL;
     if (stages <= 0 || stages > MI355MOE_STAGE_ALL) return MI355MOE_EINVAL;
     if (path < MI355MOE_PATH_AUTO || path > MI355MOE_PATH_PREFILL) return MI355MOE_EINVAL;
-    if (options & ~(MI355MOE_OPT_ACCUMULATE | MI355MOE_OPT_BF16_CONTRIB | MI355MOE_OPT_E4M3 | MI355MOE_OPT_PERSISTENT))
+    if (options & ~(MI355MOE_OPT_ACCUMULATE | MI355MOE_OPT_BF16_CONTRIB | MI355MOE_OPT_E4M3 | MI355MOE_OPT_PERSISTENT |
+                    MI355MOE_OPT_DOWN16))
         return MI355MOE_EINVAL;
     const bool e4m3 = (options & MI355MOE_OPT_E4M3) != 0;
+    if ((options & MI355MOE_OPT_DOWN16) && !e4m3) return MI355MOE_EINVAL;
     if (options & MI355MOE_OPT_PERSISTENT) return MI355MOE_EUNSUPPORTED;      // switched off (see the header)
     if (e4m3 && path == MI355MOE_PATH_DECODE) return MI355MOE_EINVAL;      // e4m3 numerics run on the grouped tier
     if (e4m3 && layer && layer->hidden > 4096) return MI355MOE_EUNSUPPORTED;
@@ -951,9 +1038,10 @@ int mi355moe_e3_gateup(const void* h13, int64_t rows_cap, int64_t K, int64_t N, 
 }
 
 namespace {
-// Workspace of the row-table down stages: row experts [rows], raw down accumulators [rows][K], token row counts
-// [tokens] and lists [tokens][PF_ROWS_PER_TOKEN]; with e4m3 also the fp32 down inputs [rows][N], their row maxima
-// [rows], their e4m3 values [rows][N] (fp16) and row scales [rows].
+// Workspace of the row-table stages: row experts [rows], raw down accumulators [rows][K], token row counts [tokens]
+// and lists [tokens][PF_ROWS_PER_TOKEN]; with e4m3 also the fp32 down inputs [rows][N], their row maxima [rows], their
+// e4m3 values [rows][N] (fp16) and row scales [rows], the rows' tokens [rows] and the widened gate/up input rows
+// [max(rows, tokens)][K] (fp16).
 struct RowsWs {
     int* pe;
     float* contrib;
@@ -963,6 +1051,8 @@ struct RowsWs {
     unsigned* amaxd;
     uint16_t* h2;
     float* dsc;
+    int* tok32;
+    uint16_t* h13;
     size_t bytes;
 };
 RowsWs carve_rows(void* ws, int64_t rows, int64_t K, int64_t N, int64_t tokens, bool e4m3) {
@@ -978,6 +1068,8 @@ RowsWs carve_rows(void* ws, int64_t rows, int64_t K, int64_t N, int64_t tokens, 
         w.amaxd = c.take<unsigned>(std::max<int64_t>(1, rows));
         w.h2 = c.take<uint16_t>((size_t)std::max<int64_t>(1, rows) * N);
         w.dsc = c.take<float>(std::max<int64_t>(1, rows));
+        w.tok32 = c.take<int>(std::max<int64_t>(1, rows));
+        w.h13 = c.take<uint16_t>((size_t)std::max<int64_t>(1, std::max(rows, tokens)) * K);
     }
     w.bytes = c.off;
     return w;
@@ -1025,7 +1117,15 @@ int mi355moe_e3_down(const void* h2, int64_t rows_cap, int64_t K, int64_t N, int
     a.out = out;
     a.odt = DT_F32;
     a.out_stride = out_stride;
-    return rc_launch(launch_prefill_rows_down(a, row_token, (int)tokens, w.cnt, w.list, stream));
+    RowsPlan rp;
+    memset(&rp, 0, sizeof(rp));
+    rp.pe = w.pe;
+    rp.row_token = row_token;
+    rp.tokens = (int)tokens;
+    rp.cnt = w.cnt;
+    rp.list = w.list;
+    rp.kernels = 4;
+    return rc_launch(launch_prefill_rows(a, rp, stream));
 }
 
 int64_t mi355moe_e4m3_tile_rows(void) { return PREFILL_TM; }
@@ -1034,30 +1134,35 @@ int mi355moe_e4m3_seg_tables(const int64_t* counts, int64_t n, int64_t tile, int
                              int32_t* seg_row0, int32_t* seg_rows, int64_t max_segs, int32_t* num_segs,
                              int32_t* num_rows, hipStream_t stream) {
     if (!counts || !seg_expert || !seg_row0 || !seg_rows || !num_segs || !num_rows) return MI355MOE_EINVAL;
-    if (n < 1 || n > MAX_EXPERTS || tile < 16 || tile > 4096 || rows_cap < 0 || rows_cap > MAX_PAIRS)
-        return MI355MOE_ELIMIT;
+    if (n < 1 || n > MAX_EXPERTS || rows_cap < 0 || rows_cap > MAX_PAIRS) return MI355MOE_ELIMIT;
+    if (tile < 16 || tile > PREFILL_TM) return MI355MOE_ESHAPE;         // the GEMMs take at most PREFILL_TM rows
     if (max_segs < (rows_cap + tile - 1) / tile + n) return MI355MOE_ESHAPE;
     return rc_launch(launch_seg_tables(counts, (int)n, (int)tile, (int)std::min<int64_t>(max_segs, 1 << 30), seg_expert,
                                        seg_row0, seg_rows, num_segs, num_rows, stream));
 }
 
-int mi355moe_e4m3_gather2(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, const int32_t* local,
-                          const int32_t* pos, int64_t topk, int64_t n, const int64_t* gate_suh, void* a_rows,
-                          float* asc, void* out, int out_dtype, int64_t out_stride, hipStream_t stream) {
-    if (!x || !local || !pos || !gate_suh || !a_rows || !asc) return MI355MOE_EINVAL;
+namespace {
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// The e4m3 gathers (per routed pair, or one row per token): validated arguments -> launch.
+int e4m3_gather(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, const int32_t* local,
+                const int32_t* pos, int64_t topk, int64_t n, const int64_t* gate_suh, uint8_t* a8, int64_t a8_rows,
+                float* asc, void* out, int out_dtype, int64_t out_stride, hipStream_t stream) {
+    if (!x || !gate_suh || !a8 || !asc || (!local) != (!pos)) return MI355MOE_EINVAL;
     if (dt_act(x_dtype) < 0) return MI355MOE_EDTYPE;
     if (out && out_dtype != MI355MOE_F32 && out_dtype != MI355MOE_BF16) return MI355MOE_EDTYPE;
-    if (K < 256 || K % 256 || K > 4096 || x_stride < K || x_stride % 2 || (out && out_stride < K))
+    if (K < 256 || K % 256 || K > 4096 || x_stride < K || x_stride % 2 || (out && out_stride < K) || !al16(a8))
         return MI355MOE_ESHAPE;
     if (T < 0 || topk < 1 || topk > MAX_TOPK || T * topk > MAX_PAIRS || n < 1 || n > MAX_EXPERTS)
         return MI355MOE_ELIMIT;
+    if (a8_rows < (local ? T * topk : T)) return MI355MOE_ESHAPE;    // pos[j] < T * topk rows / one row per token
     if (T == 0) return 0;
     PrefillArgs a;
     memset(&a, 0, sizeof(a));
     a.wt.g_suh = gate_suh;
     a.n = (int)n;
     a.K = (int)K;
-    a.P = (int)(T * topk);
+    a.P = (int)(local ? T * topk : T);
     a.T = (int)T;
     a.topk = (int)topk;
     a.x = x;
@@ -1065,7 +1170,8 @@ int mi355moe_e4m3_gather2(const void* x, int x_dtype, int64_t x_stride, int64_t 
     a.x_stride = x_stride;
     a.pair_local = local;
     a.pair_pos = pos;
-    a.h13 = static_cast<uint16_t*>(a_rows);
+    a.tok_rows = local ? 0 : 1;
+    a.a8out = a8;
     a.asc = asc;
     a.e4m3 = 1;
     if (out) {
@@ -1078,33 +1184,179 @@ int mi355moe_e4m3_gather2(const void* x, int x_dtype, int64_t x_stride, int64_t 
     return rc_launch(launch_prefill(a, stream, 1));
 }
 
-int64_t mi355moe_e4m3_fused_workspace_bytes(int64_t rows_cap, int64_t K, int64_t N, int64_t tokens) {
+// The common checks and argument block of the row-table e4m3 stages (rows_cap rows, seg_cap segment entries).
+int e4m3_rows_args(int64_t rows_cap, int64_t K, int64_t N, int64_t n, int64_t seg_cap, const int32_t* seg_row0,
+                   const int32_t* seg_rows, const int32_t* num_segs, int64_t chunk, int64_t nchunks, PrefillArgs& a) {
+    if (!seg_row0 || !seg_rows || !num_segs) return MI355MOE_EINVAL;
+    if (K < 256 || K % 256 || K > 4096 || N < 128 || N % 128 || N > 4096) return MI355MOE_ESHAPE;
+    if (rows_cap < 0 || rows_cap > MAX_PAIRS || n < 1 || n > MAX_EXPERTS || seg_cap < 0 || seg_cap > 65535)
+        return MI355MOE_ELIMIT;
+    if (nchunks < 1 || chunk < 0 || chunk >= nchunks || nchunks > 65535) return MI355MOE_EINVAL;
+    memset(&a, 0, sizeof(a));
+    a.n = (int)n;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.P = (int)rows_cap;
+    a.seg_row0 = seg_row0;
+    a.seg_rows = seg_rows;
+    a.nseg = num_segs;
+    a.S_cap = (int)seg_cap;
+    a.chunk = (int)chunk;
+    a.nchunks = (int)nchunks;
+    a.e4m3 = 1;
+    return 0;
+}
+}  // namespace
+
+int mi355moe_e4m3_gather2(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, const int32_t* local,
+                          const int32_t* pos, int64_t topk, int64_t n, const int64_t* gate_suh, uint8_t* a8,
+                          int64_t a8_rows, float* asc, void* out, int out_dtype, int64_t out_stride,
+                          hipStream_t stream) {
+    if (!local || !pos) return MI355MOE_EINVAL;
+    return e4m3_gather(x, x_dtype, x_stride, T, K, local, pos, topk, n, gate_suh, a8, a8_rows, asc, out, out_dtype,
+                       out_stride, stream);
+}
+
+int mi355moe_e4m3_gather_tok(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K,
+                             const int64_t* gate_suh, uint8_t* a8, int64_t a8_rows, float* asc, void* out,
+                             int out_dtype, int64_t out_stride, hipStream_t stream) {
+    return e4m3_gather(x, x_dtype, x_stride, T, K, nullptr, nullptr, 1, 1, gate_suh, a8, a8_rows, asc, out, out_dtype,
+                       out_stride, stream);
+}
+
+int64_t mi355moe_e4m3_stage_workspace_bytes(int64_t rows_cap, int64_t K, int64_t N, int64_t tokens) {
     if (rows_cap < 0 || K < 0 || N < 0 || tokens < 0) return -1;
     return (int64_t)carve_rows(nullptr, rows_cap, K, N, tokens, true).bytes;
 }
 
-int mi355moe_e4m3_fused(const void* a_rows, const float* asc, void* out, int out_dtype, int64_t tokens,
-                        int64_t out_stride, int64_t K, int64_t N, int64_t n, const int64_t* gate_trellis,
-                        const int64_t* up_trellis, const int64_t* gate_svh, const int64_t* up_svh,
-                        const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
-                        const int64_t* row_token, const float* row_weight, int64_t rows_cap,
-                        const int32_t* seg_expert, const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap,
-                        const int32_t* num_segs, float limit, void* workspace, size_t workspace_bytes,
-                        hipStream_t stream) {
-    if (!a_rows || !asc || !out || !gate_trellis || !up_trellis || !gate_svh || !up_svh || !down_trellis ||
-        !down_suh || !down_svh || !row_token || !row_weight || !seg_expert || !seg_row0 || !seg_rows || !num_segs ||
-        !workspace)
+int mi355moe_e4m3_gateup(const uint8_t* a8, const float* asc, int64_t rows_cap, int64_t K, int64_t N, int64_t n,
+                         const int64_t* gate_trellis, const int64_t* up_trellis, const int64_t* gate_svh,
+                         const int64_t* up_svh, void* a16, const int32_t* seg_expert, const int32_t* seg_row0,
+                         const int32_t* seg_rows, int64_t seg_cap, const int32_t* num_segs, float limit, int64_t chunk,
+                         int64_t nchunks, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!a8 || !asc || !gate_trellis || !up_trellis || !gate_svh || !up_svh || !a16 || !seg_expert || !workspace)
         return MI355MOE_EINVAL;
-    if (out_dtype != MI355MOE_F32 && out_dtype != MI355MOE_BF16) return MI355MOE_EDTYPE;
-    if (K < 256 || K % 256 || K > 4096 || N < 128 || N % 128 || out_stride < K) return MI355MOE_ESHAPE;
-    if (rows_cap < 0 || rows_cap > MAX_PAIRS || n < 1 || n > MAX_EXPERTS || seg_cap < 0 || seg_cap > 65535 ||
-        tokens < 0 || tokens > (1 << 24))
-        return MI355MOE_ELIMIT;
+    PrefillArgs a;
+    if (int rc = e4m3_rows_args(rows_cap, K, N, n, seg_cap, seg_row0, seg_rows, num_segs, chunk, nchunks, a)) return rc;
+    if (!al16(a8) || !al16(a16)) return MI355MOE_ESHAPE;
+    if (rows_cap == 0 || seg_cap == 0) return 0;
+    const RowsWs w = carve_rows(workspace, rows_cap, K, N, 0, true);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    a.wt.g_tr = gate_trellis;
+    a.wt.u_tr = up_trellis;
+    a.wt.g_svh = gate_svh;
+    a.wt.u_svh = up_svh;
+    a.seg_expert = seg_expert;
+    a.limit = limit;
+    a.h13 = w.h13;
+    a.asc = const_cast<float*>(asc);
+    a.a16out = static_cast<uint16_t*>(a16);
+    RowsPlan rp;
+    memset(&rp, 0, sizeof(rp));
+    rp.pe = w.pe;
+    rp.a8 = a8;
+    rp.a8_rows = (int)rows_cap;
+    rp.a8_cols = (int)K;
+    rp.a8_dst = w.h13;
+    rp.kernels = 2;
+    return rc_launch(launch_prefill_rows(a, rp, stream));
+}
+
+int mi355moe_e4m3_actq(const void* a16, int64_t rows_cap, int64_t N, const int32_t* row_expert, int64_t n,
+                       const int64_t* down_suh, uint8_t* a8d, float* dsc, const int32_t* seg_row0,
+                       const int32_t* seg_rows, int64_t seg_cap, const int32_t* num_segs, int64_t chunk,
+                       int64_t nchunks, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!a16 || !row_expert || !down_suh || !a8d || !dsc || !workspace) return MI355MOE_EINVAL;
+    PrefillArgs a;
+    if (int rc = e4m3_rows_args(rows_cap, 256, N, n, seg_cap, seg_row0, seg_rows, num_segs, chunk, nchunks, a))
+        return rc;
+    if (!al16(a16) || !al16(a8d)) return MI355MOE_ESHAPE;
+    if (rows_cap == 0 || seg_cap == 0) return 0;
+    const RowsWs w = carve_rows(workspace, rows_cap, 256, N, 0, true);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    // the gather's quantiser over the marked rows: row r reads a16 row r (K = N wide) with expert row_expert[r]'s
+    // down suh, writes a8d row r and dsc[r]
+    a.K = (int)N;
+    a.x = a16;
+    a.xdt = DT_F16;
+    a.x_stride = N;
+    a.wt.g_suh = down_suh;
+    a.row_expert = row_expert;
+    a.a8out = a8d;
+    a.asc = dsc;
+    RowsPlan rp;
+    memset(&rp, 0, sizeof(rp));
+    rp.pe = w.pe;
+    rp.kernels = 1;
+    return rc_launch(launch_prefill_rows(a, rp, stream));
+}
+
+int mi355moe_e4m3_down(const uint8_t* a8d, const float* dsc, int64_t rows_cap, int64_t K, int64_t N, int64_t n,
+                       const int64_t* down_trellis, const int64_t* down_svh, float* out, int64_t tokens,
+                       int64_t out_stride, const int64_t* row_token, const float* row_weight,
+                       const int32_t* seg_expert, const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap,
+                       const int32_t* num_segs, int64_t chunk, int64_t nchunks, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+    if (!a8d || !dsc || !down_trellis || !down_svh || !out || !row_token || !row_weight || !seg_expert || !workspace)
+        return MI355MOE_EINVAL;
+    PrefillArgs a;
+    if (int rc = e4m3_rows_args(rows_cap, K, N, n, seg_cap, seg_row0, seg_rows, num_segs, chunk, nchunks, a)) return rc;
+    if (!al16(a8d) || out_stride < K) return MI355MOE_ESHAPE;
+    if (tokens < 0 || tokens > (1 << 24)) return MI355MOE_ELIMIT;
     if (rows_cap == 0 || seg_cap == 0 || tokens == 0) return 0;
     const RowsWs w = carve_rows(workspace, rows_cap, K, N, tokens, true);
     if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    a.T = (int)tokens;
+    a.wt.d_tr = down_trellis;
+    a.wt.d_svh = down_svh;
+    a.seg_expert = seg_expert;
+    a.h2 = w.h2;
+    a.contrib = w.contrib;
+    a.asc = const_cast<float*>(dsc);                 // (the e4m3 checks want a gate/up scale; unused here)
+    a.dsc = const_cast<float*>(dsc);
+    a.w32 = row_weight;
+    a.out = out;
+    a.odt = DT_F32;
+    a.out_stride = out_stride;
+    RowsPlan rp;
+    memset(&rp, 0, sizeof(rp));
+    rp.pe = w.pe;
+    rp.row_token = row_token;
+    rp.tokens = (int)tokens;
+    rp.cnt = w.cnt;
+    rp.list = w.list;
+    rp.a8 = a8d;
+    rp.a8_rows = (int)rows_cap;
+    rp.a8_cols = (int)N;
+    rp.a8_dst = w.h2;
+    rp.kernels = 4 | PF_NO_QUANTD;
+    return rc_launch(launch_prefill_rows(a, rp, stream));
+}
+
+int mi355moe_e4m3_fused(const uint8_t* a8, const float* asc, int64_t a8_rows, uint8_t* a8d, float* dsc, void* a16,
+                        void* out, int out_dtype, int64_t tokens, int64_t out_stride, int64_t K, int64_t N, int64_t n,
+                        const int64_t* gate_trellis, const int64_t* up_trellis, const int64_t* gate_svh,
+                        const int64_t* up_svh, const int64_t* down_trellis, const int64_t* down_suh,
+                        const int64_t* down_svh, const int64_t* row_token, const float* row_weight, int64_t rows_cap,
+                        const int32_t* seg_expert, const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap,
+                        const int32_t* num_segs, float limit, int variant, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+    if (!a8 || !asc || !out || !gate_trellis || !up_trellis || !gate_svh || !up_svh || !down_trellis || !down_suh ||
+        !down_svh || !row_token || !row_weight || !seg_expert || !workspace || (!a8d) != (!dsc))
+        return MI355MOE_EINVAL;
+    if (variant & ~(MI355MOE_E4M3_DOWN16 | MI355MOE_E4M3_TOKEN_ROWS | MI355MOE_E4M3_LEAN_MAINLOOP))
+        return MI355MOE_EINVAL;
+    if (out_dtype != MI355MOE_F32 && out_dtype != MI355MOE_BF16) return MI355MOE_EDTYPE;
     PrefillArgs a;
-    memset(&a, 0, sizeof(a));
+    if (int rc = e4m3_rows_args(rows_cap, K, N, n, seg_cap, seg_row0, seg_rows, num_segs, 0, 1, a)) return rc;
+    const bool tok_rows = (variant & MI355MOE_E4M3_TOKEN_ROWS) != 0, down16 = (variant & MI355MOE_E4M3_DOWN16) != 0;
+    if (!al16(a8) || (a8d && !al16(a8d)) || (a16 && !al16(a16)) || out_stride < K) return MI355MOE_ESHAPE;
+    if (tokens < 0 || tokens > (1 << 24)) return MI355MOE_ELIMIT;
+    if (a8_rows < (tok_rows ? tokens : rows_cap)) return MI355MOE_ESHAPE;
+    if (rows_cap == 0 || seg_cap == 0 || tokens == 0) return 0;
+    const RowsWs w = carve_rows(workspace, rows_cap, K, N, tokens, true);
+    if (workspace_bytes < w.bytes) return MI355MOE_EWORKSPACE;
+    a.T = (int)tokens;
     a.wt.g_tr = gate_trellis;
     a.wt.u_tr = up_trellis;
     a.wt.g_svh = gate_svh;
@@ -1112,31 +1364,43 @@ int mi355moe_e4m3_fused(const void* a_rows, const float* asc, void* out, int out
     a.wt.d_tr = down_trellis;
     a.wt.d_suh = down_suh;
     a.wt.d_svh = down_svh;
-    a.n = (int)n;
-    a.K = (int)K;
-    a.N = (int)N;
-    a.P = (int)rows_cap;
-    a.T = (int)tokens;
     a.seg_expert = seg_expert;
-    a.seg_row0 = seg_row0;
-    a.seg_rows = seg_rows;
-    a.nseg = num_segs;
-    a.S_cap = (int)seg_cap;
     a.limit = limit;
-    a.h13 = const_cast<uint16_t*>(static_cast<const uint16_t*>(a_rows));
+    a.h13 = w.h13;
     a.h2 = w.h2;
-    a.pe = w.pe;
     a.contrib = w.contrib;
-    a.e4m3 = 1;
     a.asc = const_cast<float*>(asc);
-    a.dsc = w.dsc;
-    a.vd = w.vd;
-    a.amaxd = w.amaxd;
+    a.down16 = down16 ? 1 : 0;
+    a.a16out = static_cast<uint16_t*>(a16);
+    if (!down16) {                                    // e4m3 down: fp32 down inputs, their maxima and quantisation
+        a.vd = w.vd;
+        a.amaxd = w.amaxd;
+        a.dsc = dsc ? dsc : w.dsc;
+        a.a8dout = a8d;
+    }
     a.w32 = row_weight;
     a.out = out;
     a.odt = dt_w(out_dtype);
     a.out_stride = out_stride;
-    return rc_launch(launch_prefill_rows_down(a, row_token, (int)tokens, w.cnt, w.list, stream));
+    if (tok_rows) {                                   // row r's gate/up input is a8 row row_token[r]
+        a.tok_rows = 1;
+        a.tok = w.tok32;
+    }
+    RowsPlan rp;
+    memset(&rp, 0, sizeof(rp));
+    rp.pe = w.pe;
+    rp.row_token = row_token;
+    rp.tokens = (int)tokens;
+    rp.cnt = w.cnt;
+    rp.list = w.list;
+    rp.tok32 = tok_rows ? w.tok32 : nullptr;
+    rp.a8 = a8;
+    rp.a8_rows = (int)(tok_rows ? tokens : rows_cap);
+    rp.a8_cols = (int)K;
+    rp.a8_all = tok_rows ? 1 : 0;
+    rp.a8_dst = w.h13;
+    rp.kernels = 2 | 4;
+    return rc_launch(launch_prefill_rows(a, rp, stream));
 }
 
 }  // extern "C"

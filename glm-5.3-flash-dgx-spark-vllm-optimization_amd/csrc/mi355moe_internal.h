@@ -142,18 +142,44 @@ struct PrefillArgs {
     int out_accumulate;     // the combine adds the routed sum to out's current values (the shared-expert fold)
     int small_rows;         // > 0: segments of at most this many rows go to the small-tile GEMMs, larger ones to the
                             // 256-row GEMMs (set by launch_prefill; 0: one kind takes every segment)
+    // the e4m3 extension's stage entries (caller-owned buffers in that extension's byte layout: one e4m3 code per
+    // element, columns in the staging order of h13 / h2)
+    uint8_t* a8out;         // e4m3 gathers: the rows' e4m3 codes [rows][K] instead of their fp16 values in h13
+    uint8_t* a8dout;        // e4m3 down-input quantization: also the codes [P][N] of the down inputs
+    uint16_t* a16out;       // e4m3 gate/up: also the fp16 SwiGLU output [P][N] in plain column order
+    int down16;             // e4m3 gate/up writes the fp16 rotated down input h2 for an fp16 down GEMM (the
+                            // extension's DOWN16 variant) instead of vd / amaxd
+    int chunk, nchunks;     // nchunks > 1: the GEMMs and row kernels take only the segments
+                            // [ns chunk / nchunks, ns (chunk + 1) / nchunks) of the ns = nseg[0] live ones
+    const int* row_expert;  // optional: the row-table setup marks row r with row_expert[r] instead of its segment's
 };
 constexpr int PREFILL_TM = 256;
 constexpr int PF_ROWS_PER_TOKEN = 32;   // rows of one token the row-table combine handles (topk <= 32)
 
-// kernels: bit 0 gather, bit 1 gate/up, bit 2 down, bit 3 slot-order combine into the output dtype
+// kernels: bit 0 gather, bit 1 gate/up, bit 2 down (e4m3: the down-input quantization, then the down GEMM), bit 3
+// slot-order combine into the output dtype; PF_NO_QUANTD with bit 2: h2 already holds the down inputs
+constexpr int PF_NO_QUANTD = 16;
 int launch_prefill(const PrefillArgs& a, hipStream_t st, int kernels);
-// The down half over caller-built row tables (rows a.P = rows_cap, segments a.seg_*/a.nseg): row experts from the
-// segments into a.pe, (e4m3: the gate/up GEMM too, then the down-input quantization,) the down GEMM, then every
-// token's rows (row_token) summed in row order and ADDED to out (fp32 or bf16 [tokens][K], row stride a.out_stride);
-// router weights a.w32 (fp32) or a.w16 (fp16) per row. cnt [tokens] and list [tokens][PF_ROWS_PER_TOKEN] are scratch.
-int launch_prefill_rows_down(const PrefillArgs& a, const int64_t* row_token, int tokens, int* cnt, int2* list,
-                             hipStream_t st);
+// A call over caller-built row tables (rows a.P = rows_cap, segments a.seg_* / a.nseg, chunk a.chunk / a.nchunks):
+// the rows the live segments cover are marked in pe (their segment's expert, or a.row_expert[r]), every other row -1;
+// then optionally e4m3 code rows widened into the GEMMs' fp16 staging (a8 -> a8_dst: every row < a8_rows, or only the
+// marked ones), launch_prefill's `kernels` over the marked rows, and with tokens > 0 every token's marked rows
+// (row_token) summed in row order and ADDED to out (fp32 or bf16 [tokens][K], row stride a.out_stride) with the row
+// weights a.w32 (fp32) or a.w16 (fp16). tok32 (optional): [P] the rows' tokens as int32 (outside [0, tokens): 0), for
+// token-row A operands. cnt [tokens], list [tokens][PF_ROWS_PER_TOKEN] and pe [P] are scratch.
+struct RowsPlan {
+    int* pe;
+    const int64_t* row_token;
+    int tokens;
+    int* cnt;
+    int2* list;
+    int* tok32;
+    const uint8_t* a8;
+    int a8_rows, a8_cols, a8_all;
+    uint16_t* a8_dst;
+    int kernels;
+};
+int launch_prefill_rows(const PrefillArgs& a, const RowsPlan& p, hipStream_t st);
 // out[t][0 .. K) = 0 for t < a.T (a.out, a.odt F32 or BF16, a.out_stride)
 int launch_zero_out(const PrefillArgs& a, hipStream_t st);
 int prefill_setup();
@@ -203,6 +229,14 @@ int launch_route(const RouteArgs& a, hipStream_t st);
 // segment tables of rows grouped by expert from int64 counts [n] (n <= 4096), ceil(count / tile) segments each
 int launch_seg_tables(const int64_t* counts, int n, int tile, int max_segs, int* se, int* sr0, int* sr, int* ns,
                       int* nr, hipStream_t st);
+// fat-expert row tables of the grouped tier (counts > cap, back to back in expert order); sc: int scratch [2 n]
+int launch_fat_tables(const int64_t* counts, int n, int cap, const int64_t* token_sorted,
+                      const uint16_t* weight_sorted, int rows_cap, int tile, int max_segs, int* se, int* sr0, int* sr,
+                      int* ns, int* nr, int* row_expert, int64_t* row_token, uint16_t* row_weight, int* sc,
+                      hipStream_t st);
+// the permutation (a.w32, a.counts required) and the e4m3 extension's plan tables from it
+int launch_route_rows(const RouteArgs& a, int* local, int* pos, int64_t* row_token, float* row_weight,
+                      int* row_expert, int64_t* counts64, hipStream_t st);
 // top-k of T tokens' logits and the permutation of the picks in one workgroup (P <= ROUTE_SMALL_MAX_P, a.ids = ids)
 int launch_topk_route(const float* logits, int T, int E, const float* bias, int topk, float scale, int renorm,
                       int32_t* ids, float* wts, const RouteArgs& a, hipStream_t st);

@@ -67,6 +67,17 @@ __device__ __forceinline__ void pf_store_group(_Float16* grp, const uint32_t (&w
     const u32x4 v = hi ? u32x4{r0, wm[2], r1, wm[3]} : u32x4{wm[0], r0, wm[1], r1};
     *reinterpret_cast<u32x4*>(grp + 8 * (c & 1)) = v;
 }
+// The same placement for one byte per element (e4m3 codes): q[m] holds the lane's pair m as two codes in its low 16
+// bits; lane h of the pair of lanes writes storage pairs 4h .. 4h + 3 as 8 contiguous bytes. grp: the 16-group's
+// first byte.
+__device__ __forceinline__ void pf_store_group8(uint8_t* grp, const uint32_t (&q)[4], int c) {
+    const bool hi = c & 1;
+    const uint32_t s = hi ? (q[0] | (q[1] << 16)) : (q[2] | (q[3] << 16));
+    const uint32_t r = (uint32_t)__builtin_amdgcn_mov_dpp((int)s, 0xB1, 0xF, 0xF, true);   // lane ^ 1
+    const uint2 v = hi ? make_uint2((r & 0xFFFFu) | (q[2] << 16), (r >> 16) | (q[3] << 16))
+                       : make_uint2(q[0] | (r << 16), q[1] | (r & 0xFFFF0000u));
+    *reinterpret_cast<uint2*>(grp + 8 * (c & 1)) = v;
+}
 
 // ------------------------------------------------------------------------------------------------ gather
 
@@ -94,7 +105,7 @@ __device__ __forceinline__ bool pf_gather_item(const PrefillArgs& a, int i, int&
         if (t < 0 || t >= a.T) return false;                         // (caller-built tables)
         tok = (int)t;
     } else {
-        tok = a.tok[i];
+        tok = a.tok ? a.tok[i] : i;                                   // no token table: row i reads x row i
     }
     return true;
 }
@@ -180,17 +191,20 @@ __device__ __forceinline__ uint32_t e4m3_round_h2(uint32_t d) {
     asm("v_cvt_scalef32_pk_f16_fp8 %0, %1, %2" : "=v"(r) : "v"(f8), "v"(one));
     return r;
 }
-// Two fp32 values already divided by their row scale -> the fp16 pair of e4m3(clamp(v, -448, 448)) (round to nearest
-// even, the reference's quantiser).
-__device__ __forceinline__ uint32_t e4m3_quant_h2(float a, float b) {
+// Two fp32 values already divided by their row scale -> the codes of e4m3(clamp(v, -448, 448)) in the low 16 bits
+// (round to nearest even, the reference's quantiser); e4m3_h2 widens two codes to the fp16 pair of their values.
+__device__ __forceinline__ uint32_t e4m3_quant_f8(float a, float b) {
     a = __builtin_amdgcn_fmed3f(a, -448.0f, 448.0f);
     b = __builtin_amdgcn_fmed3f(b, -448.0f, 448.0f);
-    const uint32_t f8 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+__device__ __forceinline__ uint32_t e4m3_h2(uint32_t f8) {
     const float one = 1.0f;
     uint32_t r;
     asm("v_cvt_scalef32_pk_f16_fp8 %0, %1, %2" : "=v"(r) : "v"(f8), "v"(one));
     return r;
 }
+__device__ __forceinline__ uint32_t e4m3_quant_h2(float a, float b) { return e4m3_h2(e4m3_quant_f8(a, b)); }
 // Row scale of the e4m3 activations: amax / 448 (IEEE division), 1 for an all-zero row.
 __device__ __forceinline__ float e4m3_row_scale(float amax) {
     const float sc = __fdiv_rn(amax, 448.0f);
@@ -198,11 +212,12 @@ __device__ __forceinline__ float e4m3_row_scale(float amax) {
 }
 
 // The e4m3 variant's gather (code/fork/kernels/moe_e4m3.cu:245-310, gather2; with tok_rows one row per token, its
-// gather_tok): per row, v = H(x16 * suh) * r in fp32
+// gather_tok; over rows with pe >= 0 and no token table, its actq :440-488 with x = the SwiGLU output and suh = the
+// down suh): per row, v = H(x16 * suh) * r in fp32
 // (x rounded to fp16 first, the product and the butterflies in fp32, r applied after the transform), s = amax|v| /
-// 448, q = e4m3(clamp(v / s)) stored as the fp16 of each e4m3 value in h13's permuted order, asc[pos] = s; the row's
-// down-input maximum amaxd[pos] is zeroed for the gate/up epilogue. One wave per row; the whole row (K <= 4096) stays
-// in registers between the amax and the quantization.
+// 448, q = e4m3(clamp(v / s)) stored as the fp16 of each e4m3 value in h13's permuted order (a8out: as the e4m3 codes,
+// one byte each, in that order), asc[pos] = s; the row's down-input maximum amaxd[pos] is zeroed for the gate/up
+// epilogue. One wave per row; the whole row (K <= 4096) stays in registers between the amax and the quantization.
 __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
@@ -260,6 +275,7 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
         for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         const float sc = e4m3_row_scale(m);
         _Float16* dst0 = reinterpret_cast<_Float16*>(a.h13) + (size_t)pos * a.K + 16 * (c >> 1);
+        uint8_t* dst8 = a.a8out + (size_t)pos * a.K + 16 * (c >> 1);
 #pragma unroll
         for (int j = 0; j < PF_GATHER_PASSES; ++j) {
             const int blk = 4 * j + q;
@@ -267,8 +283,14 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
                 uint32_t wm[4];
 #pragma unroll
                 for (int mm = 0; mm < 4; ++mm)
-                    wm[mm] = e4m3_quant_h2(__fdiv_rn(v[j][2 * mm], sc), __fdiv_rn(v[j][2 * mm + 1], sc));
-                pf_store_group(dst0 + blk * 128, wm, c);
+                    wm[mm] = e4m3_quant_f8(__fdiv_rn(v[j][2 * mm], sc), __fdiv_rn(v[j][2 * mm + 1], sc));
+                if (a.a8out) {                                       // the codes (the extension's byte layout)
+                    pf_store_group8(dst8 + blk * 128, wm, c);
+                } else {
+#pragma unroll
+                    for (int mm = 0; mm < 4; ++mm) wm[mm] = e4m3_h2(wm[mm]);
+                    pf_store_group(dst0 + blk * 128, wm, c);
+                }
             }
         }
         if (lane == 0) {
@@ -281,8 +303,8 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
 }
 
 // The e4m3 variant's down-input quantization: per row, s = amaxd / 448 (the maximum over the whole row, gathered by
-// the gate/up epilogues), h2 = the fp16 of e4m3(clamp(vd / s)) in the permuted order, dsc[pos] = s. One wave per row,
-// four 128-blocks per pass.
+// the gate/up epilogues), h2 = the fp16 of e4m3(clamp(vd / s)) in the permuted order (a8dout: also the codes, one
+// byte each, in that order), dsc[pos] = s. One wave per row, four 128-blocks per pass.
 __global__ __launch_bounds__(256) void pf_quantd_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
@@ -292,14 +314,19 @@ __global__ __launch_bounds__(256) void pf_quantd_kernel(PrefillArgs a) {
         const float sc = e4m3_row_scale(__builtin_bit_cast(float, a.amaxd[pos]));
         const float* src = a.vd + (size_t)pos * a.N + 8 * c;
         _Float16* dst0 = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos * a.N + 16 * (c >> 1);
+        uint8_t* dst8 = a.a8dout + (size_t)pos * a.N + 16 * (c >> 1);
         for (int blk = q; blk < (a.N >> 7); blk += 4) {
             const float4 lo = *reinterpret_cast<const float4*>(src + blk * 128);
             const float4 hi = *reinterpret_cast<const float4*>(src + blk * 128 + 4);
             const float w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            uint32_t wm[4];
+            uint32_t f8[4], wm[4];
 #pragma unroll
-            for (int mm = 0; mm < 4; ++mm) wm[mm] = e4m3_quant_h2(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
+            for (int mm = 0; mm < 4; ++mm) {
+                f8[mm] = e4m3_quant_f8(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
+                wm[mm] = e4m3_h2(f8[mm]);
+            }
             pf_store_group(dst0 + blk * 128, wm, c);
+            if (a.a8dout) pf_store_group8(dst8 + blk * 128, f8, c);
         }
         if (lane == 0) a.dsc[pos] = sc;
     }
@@ -581,6 +608,20 @@ __device__ __forceinline__ void pf_tile_of(int b, int ncb, int& s, int& cb) {
     s = 8 * (q / ncb) + x;
 }
 
+// The segments a launch takes: [lo, hi) = chunk `chunk` of `nchunks` equal shares of the live segments (all of them
+// with one chunk; the reference's chunked schedule, code/fork/kernels/moe_e4m3.cu:479-481), never past the S_cap
+// table entries. A grid's virtual segment s is segment lo + s.
+__device__ __forceinline__ void pf_seg_range(const PrefillArgs& a, int& lo, int& hi) {
+    const int ns = min(a.nseg[0], a.S_cap);
+    if (a.nchunks <= 1) {
+        lo = 0;
+        hi = ns;
+        return;
+    }
+    lo = (int)((int64_t)ns * a.chunk / a.nchunks);
+    hi = (int)((int64_t)ns * (a.chunk + 1) / a.nchunks);
+}
+
 // ------------------------------------------------------------------------------------------------ gate/up
 
 // E4M3: the trellis-sourced e4m3 variant (weights rounded to e4m3 in the GEMM; accumulators times the row's
@@ -622,11 +663,13 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
     const int col = cb * 128 + 8 * c;
     float svg[8], svu[8];
     _Float16 sud[8];
+    // no down suh table: the SwiGLU output (a16out) is the epilogue's only output
+    const _Float16* dsp = a.wt.d_suh ? reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) : nullptr;
 #pragma unroll
     for (int i = 0; i < 8; i += 2) {
         const h2 g2 = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + col + i);
         const h2 u2 = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + col + i);
-        const h2 d2 = *reinterpret_cast<const h2*>(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + col + i);
+        const h2 d2 = dsp ? *reinterpret_cast<const h2*>(dsp + col + i) : h2{(_Float16)1.0f, (_Float16)1.0f};
         svg[i] = (float)g2.x, svg[i + 1] = (float)g2.y;
         svu[i] = (float)u2.x, svu[i + 1] = (float)u2.y;
         sud[i] = d2.x, sud[i + 1] = d2.y;
@@ -664,6 +707,7 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
             }
             fwht128_x16s(g, lane);
             fwht128_x16s(u, lane);
+            _Float16 av[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 float gv = g[i] * hr * svg[i];
@@ -672,11 +716,15 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
                     gv = fminf(gv, L);
                     uv = fminf(fmaxf(uv, -L), L);
                 }
-                const float act = sigmoid_fast(gv) * gv * uv;
-                b[i] = E4M3 ? (float)(_Float16)act * (float)sud[i] : (float)(_Float16)((_Float16)act * sud[i]);
+                av[i] = (_Float16)(sigmoid_fast(gv) * gv * uv);
+                b[i] = E4M3 ? (float)av[i] * (float)sud[i] : (float)(_Float16)(av[i] * sud[i]);
             }
+            if (E4M3 && a.a16out && trow < rn)                       // the fp16 SwiGLU output, plain column order
+                *reinterpret_cast<h8*>(a.a16out + (size_t)(row0 + trow) * N + col) =
+                    h8{av[0], av[1], av[2], av[3], av[4], av[5], av[6], av[7]};
+            if (E4M3 && !a.down16 && !a.vd) continue;                // (uniform) a16 was the only output
             fwht128_x16s(b, lane);
-            if (E4M3) {                                              // fp32 down input and its row maximum
+            if (E4M3 && !a.down16) {                                 // fp32 down input and its row maximum
                 float m = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
@@ -709,20 +757,24 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
 // block cb) as pf_tile_of orders them, v = part S_cap + s, so the first parts of all segments come first and the
 // later parts' workgroups, empty for segments of fewer rows, come last.
 __device__ __forceinline__ bool pf_part_tile_of(const PrefillArgs& a, int ncb, int parts, int& s, int& part, int& cb) {
-    int v;
+    int v, lo, hi;
     pf_tile_of(blockIdx.x, ncb, v, cb);
     if (a.S_cap <= 0 || v >= parts * a.S_cap) return false;
     part = v / a.S_cap;
     s = v - part * a.S_cap;
-    return s < a.nseg[0];
+    pf_seg_range(a, lo, hi);
+    s += lo;
+    return s < hi;
 }
 
 template <bool E4M3>
 __global__ __launch_bounds__(PF_THREADS, 1) void pf_gateup_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    int s, cb;
+    int s, cb, lo, hi;
     pf_tile_of(blockIdx.x, a.N >> 7, s, cb);
-    if (s >= a.nseg[0] || (a.small_rows > 0 && a.seg_rows[s] <= a.small_rows)) return;
+    pf_seg_range(a, lo, hi);
+    s += lo;
+    if (s >= hi || (a.small_rows > 0 && a.seg_rows[s] <= a.small_rows)) return;
     pf_gateup_tile<E4M3, PF_LARGE>(a, s, 0, cb, smem);
 }
 
@@ -846,9 +898,11 @@ __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int pa
 template <bool E4M3>
 __global__ __launch_bounds__(PF_THREADS, 1) void pf_down_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    int s, cb;
+    int s, cb, lo, hi;
     pf_tile_of(blockIdx.x, a.K >> 8, s, cb);
-    if (s >= a.nseg[0] || (a.small_rows > 0 && a.seg_rows[s] <= a.small_rows)) return;
+    pf_seg_range(a, lo, hi);
+    s += lo;
+    if (s >= hi || (a.small_rows > 0 && a.seg_rows[s] <= a.small_rows)) return;
     pf_down_tile<E4M3, PF_LARGE>(a, s, 0, cb, smem);
 }
 
@@ -994,11 +1048,17 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
 
 // Rows of caller-built tables: pe[r] = -1 for every row and cnt[t] = 0 for every token, then pe[r] = the expert of the
 // segment covering row r (segments s < nseg[0]); rows no segment covers stay skipped.
-__global__ __launch_bounds__(256) void pf_rows_init_kernel(PrefillArgs a, int* pe, int* cnt, int tokens) {
+// tok32 (optional): tok32[r] = row_token[r] as int32, 0 where it lies outside [0, tokens).
+__global__ __launch_bounds__(256) void pf_rows_init_kernel(PrefillArgs a, int* pe, int* cnt, int tokens, int* tok32,
+                                                           const int64_t* row_token) {
     for (int i = blockIdx.x * 256 + threadIdx.x; i < max(a.P, tokens); i += gridDim.x * 256) {
         if (i < a.P) {
             pe[i] = -1;
             if (a.amaxd) a.amaxd[i] = 0u;
+            if (tok32) {
+                const int64_t t = row_token[i];
+                tok32[i] = (t >= 0 && t < tokens) ? (int)t : 0;
+            }
         }
         if (i < tokens) cnt[i] = 0;
     }
@@ -1020,13 +1080,44 @@ __global__ __launch_bounds__(256) void pf_zero_out_kernel(PrefillArgs a) {
         }
     }
 }
+// One workgroup per segment of the launch's range (pf_seg_range); with a.row_expert the rows are marked with their own
+// row_expert entries (the segment's expert is not read).
 __global__ __launch_bounds__(256) void pf_seg_rows_kernel(PrefillArgs a, int* pe) {
-    const int s = blockIdx.x;
-    if (s >= a.nseg[0]) return;
-    const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PREFILL_TM);
+    int lo, hi;
+    pf_seg_range(a, lo, hi);
+    const int s = lo + (int)blockIdx.x;
+    if (s >= hi) return;
+    const int e = a.row_expert ? 0 : a.seg_expert[s], row0 = a.seg_row0[s], rn = min(a.seg_rows[s], PREFILL_TM);
     if (e < 0 || e >= a.n) return;                                    // (the GEMM kernels skip such segments too)
     for (int i = threadIdx.x; i < rn; i += 256)
-        if (row0 + i >= 0 && row0 + i < a.P) pe[row0 + i] = e;
+        if (row0 + i >= 0 && row0 + i < a.P) pe[row0 + i] = a.row_expert ? a.row_expert[row0 + i] : e;
+}
+
+// e4m3 code rows (one byte per element, in the staging order of h13 / h2) widened to the fp16 staging rows the GEMMs
+// read: dst[r][k] = the fp16 of the e4m3 value src[r][k] (exact: every e4m3 value is an fp16), for every row r < rows
+// (pe == nullptr) or those with pe[r] >= 0. One wave per row, 16 codes per lane per pass; cols % 16 == 0.
+__global__ __launch_bounds__(256) void pf_widen8_kernel(const uint8_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                        int cols, int rows, const int* __restrict__ pe) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+    for (int r = wave; r < rows; r += gridDim.x * 4) {
+        if (pe && pe[r] < 0) continue;                               // uniform: one row per wave
+        const uint8_t* sr = src + (size_t)r * cols;
+        uint16_t* dr = dst + (size_t)r * cols;
+        for (int c = 16 * lane; c < cols; c += 1024) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(sr + c);
+            u32x4 o0, o1;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                o0[2 * i] = e4m3_h2(v[i] & 0xFFFFu);
+                o0[2 * i + 1] = e4m3_h2(v[i] >> 16);
+                o1[2 * i] = e4m3_h2(v[i + 2] & 0xFFFFu);
+                o1[2 * i + 1] = e4m3_h2(v[i + 2] >> 16);
+            }
+            *reinterpret_cast<u32x4*>(dr + c) = o0;
+            *reinterpret_cast<u32x4*>(dr + c + 8) = o1;
+        }
+    }
 }
 
 // Every computed row r claims a slot of its token's list: list[t][k] = (r, expert) with k from an atomic counter (so
@@ -1188,7 +1279,13 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     PrefillArgs a = a0;
     const bool f8 = a.e4m3 != 0;
     if (f8 && (a.K > 4 * 128 * PF_GATHER_PASSES || !a.asc)) return -1;
-    if (f8 && (kernels & ~1) && (!a.dsc || !a.vd || !a.amaxd)) return -1;    // the gather alone needs only asc
+    // e4m3 gate/up writes a16out, h2 (down16) or vd + amaxd; the down-input quantization needs vd, amaxd and dsc, the
+    // e4m3 down GEMM's combine dsc
+    if (f8 && (kernels & 2) && !a.down16 && !a.a16out && (!a.vd || !a.amaxd)) return -1;
+    const bool quantd = f8 && !a.down16 && (kernels & 4) && !(kernels & PF_NO_QUANTD);
+    if (quantd && (!a.vd || !a.amaxd || !a.dsc)) return -1;
+    if (f8 && !a.down16 && (kernels & 8) && !a.dsc) return -1;
+    const bool f8dn = f8 && !a.down16;                              // the down GEMM rounds its weights to e4m3
     if (kernels & 1) {
         if (f8) hipLaunchKernelGGL(pf_gather8_kernel, dim3(4096), dim3(256), 0, st, a);
         else hipLaunchKernelGGL(pf_gather_kernel, dim3(4096), dim3(256), 0, st, a);
@@ -1216,17 +1313,17 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
         }
     }
     if (kernels & 4) {
-        if (f8) hipLaunchKernelGGL(pf_quantd_kernel, dim3(4096), dim3(256), 0, st, a);
+        if (quantd) hipLaunchKernelGGL(pf_quantd_kernel, dim3(4096), dim3(256), 0, st, a);
         if (tiles & PF_TILES_LARGE) {
-            if (f8) hipLaunchKernelGGL(pf_down_kernel<true>, dn, dim3(PF_THREADS), PF_LDS, st, a);
+            if (f8dn) hipLaunchKernelGGL(pf_down_kernel<true>, dn, dim3(PF_THREADS), PF_LDS, st, a);
             else hipLaunchKernelGGL(pf_down_kernel<false>, dn, dim3(PF_THREADS), PF_LDS, st, a);
         }
         if (tiles & PF_TILES_SMALL) {
-            if (f8) hipLaunchKernelGGL(pf_down_small_kernel<true>, dns, dim3(PF_THREADS), PF_LDS_S, st, a);
+            if (f8dn) hipLaunchKernelGGL(pf_down_small_kernel<true>, dns, dim3(PF_THREADS), PF_LDS_S, st, a);
             else hipLaunchKernelGGL(pf_down_small_kernel<false>, dns, dim3(PF_THREADS), PF_LDS_S, st, a);
         }
         if (tiles & PF_TILES_MID) {
-            if (f8) hipLaunchKernelGGL(pf_down_mid_kernel<true>, dnm, dim3(PF_THREADS), PF_LDS_M, st, a);
+            if (f8dn) hipLaunchKernelGGL(pf_down_mid_kernel<true>, dnm, dim3(PF_THREADS), PF_LDS_M, st, a);
             else hipLaunchKernelGGL(pf_down_mid_kernel<false>, dnm, dim3(PF_THREADS), PF_LDS_M, st, a);
         }
     }
@@ -1242,25 +1339,27 @@ int launch_zero_out(const PrefillArgs& a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_prefill_rows_down(const PrefillArgs& a0, const int64_t* row_token, int tokens, int* cnt, int2* list,
-                             hipStream_t st) {
-    if (prefill_setup() || a0.contrib_bf16) return -1;           // the row-table combine reads fp32 accumulators
+int launch_prefill_rows(const PrefillArgs& a0, const RowsPlan& p, hipStream_t st) {
+    if (prefill_setup()) return -1;
+    if (p.tokens > 0 && (a0.contrib_bf16 || !p.row_token || !p.cnt || !p.list)) return -1;   // fp32 accumulators
+    if (p.tok32 && !p.row_token) return -1;
     PrefillArgs a = a0;
-    int* pe = const_cast<int*>(a.pe);
-    const int fill = std::max(1, std::min(2048, (std::max(a.P, tokens) + 255) / 256));
-    hipLaunchKernelGGL(pf_rows_init_kernel, dim3(fill), dim3(256), 0, st, a, pe, cnt, tokens);
-    hipLaunchKernelGGL(pf_seg_rows_kernel, dim3(a.S_cap), dim3(256), 0, st, a, pe);
-    // the grouped GEMMs as launch_prefill runs them (the same tile choice); e4m3: gate/up (fp32 down inputs and their
-    // row maxima, which rows_init zeroed), quantization, down
-    if (a.e4m3) {
-        if (launch_prefill(a, st, 2 | 4)) return -1;
-    } else {
-        if (launch_prefill(a, st, 4)) return -1;
+    a.pe = p.pe;
+    const int fill = std::max(1, std::min(2048, (std::max(a.P, p.tokens) + 255) / 256));
+    hipLaunchKernelGGL(pf_rows_init_kernel, dim3(fill), dim3(256), 0, st, a, p.pe, p.cnt, std::max(p.tokens, 0),
+                       p.tok32, p.row_token);
+    if (a.S_cap > 0) hipLaunchKernelGGL(pf_seg_rows_kernel, dim3(a.S_cap), dim3(256), 0, st, a, p.pe);
+    if (p.a8 && p.a8_rows > 0)
+        hipLaunchKernelGGL(pf_widen8_kernel, dim3(std::max(1, std::min(4096, (p.a8_rows + 3) / 4))), dim3(256), 0, st,
+                           p.a8, p.a8_dst, p.a8_cols, p.a8_rows, p.a8_all ? nullptr : p.pe);
+    if (p.kernels)
+        if (launch_prefill(a, st, p.kernels)) return -1;
+    if (p.tokens > 0) {
+        hipLaunchKernelGGL(pf_rows_by_token_kernel, dim3(std::max(1, std::min(2048, (a.P + 255) / 256))), dim3(256), 0,
+                           st, a, p.row_token, p.cnt, p.list, p.tokens);
+        hipLaunchKernelGGL(pf_combine_rows_kernel, dim3((p.tokens + 3) / 4, (a.K + 511) / 512), dim3(256), 0, st, a,
+                           p.cnt, p.list, p.tokens);
     }
-    hipLaunchKernelGGL(pf_rows_by_token_kernel, dim3(std::max(1, std::min(2048, (a.P + 255) / 256))), dim3(256), 0, st,
-                       a, row_token, cnt, list, tokens);
-    hipLaunchKernelGGL(pf_combine_rows_kernel, dim3((tokens + 3) / 4, (a.K + 511) / 512), dim3(256), 0, st, a, cnt,
-                       list, tokens);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

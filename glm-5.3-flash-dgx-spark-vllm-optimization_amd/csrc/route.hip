@@ -10,6 +10,8 @@
 //                stable sorted position of every pair (pairs grouped by local id, the sentinel group last, inside a
 //                group by pair index; code/fork/kernels/exl3.cu:742-775), plus the row-segment table
 //                (code/fork/kernels/exl3.cu:529-566) with a caller-chosen segment height.
+#include <algorithm>
+
 #include "common.cuh"
 #include "mi355moe_internal.h"
 
@@ -647,6 +649,112 @@ int launch_seg_tables(const int64_t* counts, int n, int tile, int max_segs, int*
                       int* nr, hipStream_t st) {
     hipLaunchKernelGGL(seg_tables_kernel, dim3(1), dim3(1024), (size_t)2 * n * sizeof(int), st, counts, n, tile,
                        max_segs, se, sr0, sr, ns, nr);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Row tables of the grouped tier's fat experts (the contract of code/fork/docs/prod_exl3_reference.py:1316-1361): the
+// experts with more than `cap` pairs (counts int64 [n], the pairs sorted by expert) laid out back to back in expert
+// order, segments of at most `tile` rows. fat_scan_kernel (one workgroup): the exclusive scans of the counts (each
+// expert's first sorted position) and of the fat counts (its first row), the segment table (build_segments with the
+// thin experts excluded), num_rows, and per expert (first row, first sorted position) into sc [2 n].
+__global__ __launch_bounds__(1024) void fat_scan_kernel(const int64_t* __restrict__ counts64, int n, int cap, int tile,
+                                                        int max_segs, int* seg_expert, int* seg_row0, int* seg_rows,
+                                                        int* nseg, int* nrows, int* sc) {
+    extern __shared__ int sh[];
+    __shared__ int tot[16];
+    int* cnt = sh;
+    int* row0 = sh + n;
+    int run = 0, frun = 0;
+    for (int base = 0; base < n; base += blockDim.x) {
+        const int e = base + threadIdx.x;
+        const int64_t c64 = e < n ? counts64[e] : 0;
+        const int c = c64 < 0 ? 0 : (c64 > (1 << 24) ? (1 << 24) : (int)c64);
+        const int f = c > cap ? c : 0;
+        int ctot, ftot;
+        const int cinc = block_scan_incl(c, tot, ctot);
+        const int finc = block_scan_incl(f, tot, ftot);
+        if (e < n) {
+            cnt[e] = c;
+            row0[e] = frun + finc - f;
+            sc[e] = row0[e];
+            sc[n + e] = run + cinc - c;
+        }
+        run += ctot;
+        frun += ftot;
+    }
+    __syncthreads();
+    build_segments(cnt, row0, n, 1 << 30, tile, max_segs, seg_expert, seg_row0, seg_rows, nseg, tot, cap);
+    if (threadIdx.x == 0) nrows[0] = frun;
+}
+
+// fat_rows_kernel: workgroup e < n writes the rows of fat expert e (row sc[e] + i = sorted position sc[n + e] + i: its
+// token and weight, and e); the workgroups past n mark the rows no fat expert fills (expert -1, token 0, weight 0).
+// Rows past rows_cap and sorted positions past the arrays (inconsistent counts) are left out.
+__global__ __launch_bounds__(256) void fat_rows_kernel(const int64_t* __restrict__ counts64, int n, int cap,
+                                                       const int64_t* __restrict__ token_sorted,
+                                                       const uint16_t* __restrict__ weight_sorted, int rows_cap,
+                                                       const int* __restrict__ sc, const int* __restrict__ nrows,
+                                                       int* row_expert, int64_t* row_token, uint16_t* row_weight) {
+    const int b = blockIdx.x;
+    if (b < n) {
+        const int64_t c = counts64[b];
+        if (c <= cap) return;
+        const int r0 = sc[b], p0 = sc[n + b];
+        for (int i = threadIdx.x; i < c; i += 256) {
+            const int r = r0 + i, p = p0 + i;
+            if (r >= rows_cap || p >= rows_cap) break;
+            row_expert[r] = b;
+            row_token[r] = token_sorted[p];
+            row_weight[r] = weight_sorted[p];
+        }
+        return;
+    }
+    for (int r = nrows[0] + (b - n) * 256 + threadIdx.x; r < rows_cap; r += (gridDim.x - n) * 256) {
+        row_expert[r] = -1;
+        row_token[r] = 0;
+        row_weight[r] = 0;
+    }
+}
+
+int launch_fat_tables(const int64_t* counts, int n, int cap, const int64_t* token_sorted,
+                      const uint16_t* weight_sorted, int rows_cap, int tile, int max_segs, int* se, int* sr0, int* sr,
+                      int* ns, int* nr, int* row_expert, int64_t* row_token, uint16_t* row_weight, int* sc,
+                      hipStream_t st) {
+    hipLaunchKernelGGL(fat_scan_kernel, dim3(1), dim3(1024), (size_t)2 * n * sizeof(int), st, counts, n, cap, tile,
+                       max_segs, se, sr0, sr, ns, nr, sc);
+    const int tail = std::max(1, std::min(1024, (rows_cap + 255) / 256));
+    hipLaunchKernelGGL(fat_rows_kernel, dim3(n + tail), dim3(256), 0, st, counts, n, cap, token_sorted, weight_sorted,
+                       rows_cap, sc, nr, row_expert, row_token, row_weight);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// The e4m3 extension's plan tables (code/fork/overlay/glm53_moe_e4m3.py:450-477) from a permutation of the routed
+// pairs (launch_route: sorted by local id, sentinel pairs last, pe = -1 for them): per sorted position p the row's
+// token, fp32 weight and local expert (n for the sentinel rows); per pair j its row inv[j] and its local id; the
+// counts [n + 1] widened to int64.
+__global__ __launch_bounds__(256) void route_rows_kernel(RouteArgs a, int* local, int* pos, int64_t* row_token,
+                                                         float* row_weight, int* row_expert, int64_t* counts64) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < max(a.P, a.n + 1); i += gridDim.x * 256) {
+        if (i < a.P) {
+            const int e = a.pe[i];
+            row_token[i] = a.tok[i];
+            row_weight[i] = a.w32[i];
+            row_expert[i] = e >= 0 ? e : a.n;
+            const int p = a.inv[i];
+            const int ep = a.pe[p];
+            pos[i] = p;
+            local[i] = ep >= 0 ? ep : a.n;
+        }
+        if (i <= a.n) counts64[i] = a.counts[i];
+    }
+}
+
+int launch_route_rows(const RouteArgs& a, int* local, int* pos, int64_t* row_token, float* row_weight,
+                      int* row_expert, int64_t* counts64, hipStream_t st) {
+    if (launch_route(a, st)) return -1;
+    const int g = std::max(1, std::min(1024, (std::max(a.P, a.n + 1) + 255) / 256));
+    hipLaunchKernelGGL(route_rows_kernel, dim3(g), dim3(256), 0, st, a, local, pos, row_token, row_weight, row_expert,
+                       counts64);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -10,12 +10,13 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 SO_PATH = os.path.join(_HERE, "libmi355moe.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
 STAGE_ROUTE, STAGE_GATEUP, STAGE_DOWN, STAGE_COMBINE, STAGE_ALL = 1, 2, 4, 8, 15
 PATH_AUTO, PATH_DECODE, PATH_PREFILL = 0, 1, 2
-OPT_ACCUMULATE, OPT_BF16_CONTRIB, OPT_E4M3, OPT_PERSISTENT = 1, 2, 4, 8
+OPT_ACCUMULATE, OPT_BF16_CONTRIB, OPT_E4M3, OPT_PERSISTENT, OPT_DOWN16 = 1, 2, 4, 8, 16
+E4M3_DOWN16, E4M3_TOKEN_ROWS, E4M3_LEAN_MAINLOOP = 16, 2048, 8192
 LAYER_SHARED_W13_SUH = 1
 LAYER_UNIFORM_W13_SUH = 2
 PREFILL_MIN_PAIRS = 5120
@@ -64,6 +65,9 @@ _SIGS = {
     "mi355moe_route_workspace_bytes": (_i64, [_i64, _i64]),
     "mi355moe_route": (_int, [_c_p, _int, _c_p, _int, _i64, _i64, _c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p,
                               _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _sz, _c_p]),
+    "mi355moe_route_rows_workspace_bytes": (_i64, [_i64, _i64]),
+    "mi355moe_route_rows": (_int, [_c_p, _int, _c_p, _int, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                   _c_p, _c_p, _sz, _c_p]),
     "mi355moe_rot_in": (_int, [_c_p, _int, _i64, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p]),
     "mi355moe_moe_workspace_bytes": (_i64, [ctypes.POINTER(Exl3LayerDesc), _i64, _i64]),
     "mi355moe_moe_forward_ids": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int, _c_p,
@@ -90,6 +94,8 @@ _SIGS = {
                                               _c_p, _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _i64, _c_p, _sz,
                                               _c_p]),
     "mi355moe_e3_tile_rows": (_i64, []),
+    "mi355moe_e3_fat_tables": (_int, [_c_p, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _c_p,
+                                      _c_p, _c_p, _c_p, _c_p, _c_p]),
     "mi355moe_e3_gather": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p]),
     "mi355moe_e3_gateup": (_int, [_c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                   _i64, _c_p, _f, _c_p]),
@@ -98,11 +104,19 @@ _SIGS = {
                                 _c_p, _i64, _c_p, _c_p, _sz, _c_p]),
     "mi355moe_e4m3_tile_rows": (_i64, []),
     "mi355moe_e4m3_seg_tables": (_int, [_c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p]),
-    "mi355moe_e4m3_gather2": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p,
-                                     _int, _i64, _c_p]),
-    "mi355moe_e4m3_fused_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
-    "mi355moe_e4m3_fused": (_int, [_c_p, _c_p, _c_p, _int, _i64, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p,
-                                   _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _f, _c_p, _sz, _c_p]),
+    "mi355moe_e4m3_gather2": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p,
+                                     _c_p, _int, _i64, _c_p]),
+    "mi355moe_e4m3_gather_tok": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _int, _i64, _c_p]),
+    "mi355moe_e4m3_stage_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "mi355moe_e4m3_gateup": (_int, [_c_p, _c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                    _i64, _c_p, _f, _i64, _i64, _c_p, _sz, _c_p]),
+    "mi355moe_e4m3_actq": (_int, [_c_p, _i64, _i64, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _i64, _i64,
+                                  _c_p, _sz, _c_p]),
+    "mi355moe_e4m3_down": (_int, [_c_p, _c_p, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _c_p,
+                                  _c_p, _c_p, _i64, _c_p, _i64, _i64, _c_p, _sz, _c_p]),
+    "mi355moe_e4m3_fused": (_int, [_c_p, _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _int, _i64, _i64, _i64, _i64, _i64, _c_p,
+                                   _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _c_p,
+                                   _f, _int, _c_p, _sz, _c_p]),
     "mi355moe_fp8_quant_rows": (_int, [_c_p, _int, _i64, _i64, _i64, _c_p, _c_p, _c_p]),
     "mi355moe_fp8_moe_workspace_bytes": (_i64, [ctypes.POINTER(Fp8LayerDesc), _i64, _i64]),
     "mi355moe_fp8_moe_forward_ids": (_int, [ctypes.POINTER(Fp8LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int, _c_p,

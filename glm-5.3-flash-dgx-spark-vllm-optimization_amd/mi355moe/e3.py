@@ -5,10 +5,10 @@ on device-side row tables, the table builder and the apply that chains them.
                                           exl3_fat_moe.cuh:20-56 (same argument order and meaning)
   exl3_fat_moe_tile_rows_gateup / _down   the segment height the tables must be built with (this library's 256-row
                                           MFMA tiles, both stages)
-  build_grouped_fat_tables                code/fork/docs/prod_exl3_reference.py:1316-1361: fat experts (count > cap)
-                                          back to back in expert order, one segment per tile_rows rows, all on the
-                                          device from capacity-sized tensors (no host synchronisation)
-  apply_exl3_grouped_fat                  prod_exl3_reference.py:1364-1435: out (fp32) += the fat experts' output
+  build_grouped_fat_tables                the table contract of code/fork/docs/prod_exl3_reference.py:1316-1361,
+                                          built by this library's device kernels (mi355moe_e3_fat_tables)
+  apply_exl3_grouped_fat                  the contract of prod_exl3_reference.py:1364-1435: out (fp32) += the fat
+                                          experts' output, tables then the three stages, no host synchronisation
 
 h13 / h2 hold rows in this library's staging order (k permuted within 16-element groups): they are intermediates
 from one stage to the next, not rotated activations in plain order. The down stage sums each token's rows in row
@@ -99,59 +99,59 @@ def exl3_fat_moe_down(h2: torch.Tensor, down_ptrs: torch.Tensor, down_svh_ptrs: 
         seg_expert.numel(), ops._p(num_segs), ops._p(ws), ws.numel(), ops._stream(out.device)))
 
 
-def _excl_cumsum(v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    inc = torch.cumsum(v, 0)
-    return inc - v, inc
-
-
 def build_grouped_fat_tables(counts: torch.Tensor, cap: int, token_sorted: torch.Tensor,
                              weight_sorted: torch.Tensor, rows_cap: int, tile_rows: int) -> dict:
-    """Row and segment tables of the fat experts (code/fork/docs/prod_exl3_reference.py:1316-1361). counts int64 [n]
-    (the sentinel bucket excluded): experts with more than cap rows are laid out back to back in expert order; row r
-    of the fat-row buffer is sorted position sorted_off[e] + (r - row_off[e]) of its expert e; segment s covers
-    tile_rows rows of one expert. Capacity-sized device tensors, no host synchronisation."""
+    """The fat experts' row and segment tables, built on the device by mi355moe_e3_fat_tables (the table contract of
+    code/fork/docs/prod_exl3_reference.py:1316-1361). counts int64 [n] (sentinel bucket excluded) of the pairs
+    sorted by expert (token_sorted int64, weight_sorted fp16, rows_cap entries): the experts with more than cap
+    pairs, back to back in expert order; segments of at most tile_rows rows. Returns the device tensors seg_expert /
+    seg_row0 / seg_rows (int32 [ceil(rows_cap / tile_rows) + n]), num_segs / num_rows (int32 [1]), row_expert (int32
+    [rows_cap], -1 past num_rows), row_token (int64) and row_weight (fp16); nothing is read back to the host."""
+    if not counts.is_cuda or counts.dtype != torch.int64 or counts.dim() != 1:
+        raise ValueError("counts must be an int64 CUDA vector of per-expert pair counts")
     n = int(counts.numel())
     dev = counts.device
-    fat = torch.where(counts > cap, counts, torch.zeros_like(counts))
-    row_off, row_cum = _excl_cumsum(fat)
-    sorted_off, _ = _excl_cumsum(counts)
-    tiles = (fat + tile_rows - 1) // tile_rows
-    tile_off, tile_cum = _excl_cumsum(tiles)
+    cnt = counts.contiguous()
+    tok = token_sorted.to(torch.int64).contiguous()
+    wts = weight_sorted.to(torch.float16).contiguous()
+    if tok.numel() < rows_cap or wts.numel() < rows_cap:
+        raise ValueError("token_sorted / weight_sorted must hold rows_cap entries")
     max_segs = (rows_cap + tile_rows - 1) // tile_rows + n
-    seg = torch.arange(max_segs, device=dev)
-    se = torch.searchsorted(tile_cum, seg, right=True).clamp_(max=n - 1)
-    local_tile = seg - tile_off[se]
-    r = torch.arange(rows_cap, device=dev)
-    re = torch.searchsorted(row_cum, r, right=True).clamp_(max=n - 1)
-    src = (sorted_off[re] + (r - row_off[re])).clamp_(max=max(rows_cap - 1, 0))
-    return {"seg_expert": se.to(torch.int32),
-            "seg_row0": (row_off[se] + local_tile * tile_rows).to(torch.int32),
-            "seg_rows": torch.clamp(fat[se] - local_tile * tile_rows, min=0, max=tile_rows).to(torch.int32),
-            "num_segs": tile_cum[-1:].to(torch.int32), "num_rows": row_cum[-1:].to(torch.int32),
-            "row_expert": re.to(torch.int32),
-            "row_token": token_sorted.index_select(0, src), "row_weight": weight_sorted.index_select(0, src)}
+    i32 = dict(dtype=torch.int32, device=dev)
+    t = {"seg_expert": torch.empty(max_segs, **i32), "seg_row0": torch.empty(max_segs, **i32),
+         "seg_rows": torch.empty(max_segs, **i32), "num_segs": torch.empty(1, **i32),
+         "num_rows": torch.empty(1, **i32), "row_expert": torch.empty(max(rows_cap, 1), **i32),
+         "row_token": torch.empty(max(rows_cap, 1), dtype=torch.int64, device=dev),
+         "row_weight": torch.empty(max(rows_cap, 1), dtype=torch.float16, device=dev)}
+    scratch = torch.empty(2 * n, **i32)
+    _lib.check("mi355moe_e3_fat_tables", _lib.lib().mi355moe_e3_fat_tables(
+        ops._p(cnt), n, int(cap), ops._p(tok), ops._p(wts), int(rows_cap), int(tile_rows), ops._p(t["seg_expert"]),
+        ops._p(t["seg_row0"]), ops._p(t["seg_rows"]), max_segs, ops._p(t["num_segs"]), ops._p(t["num_rows"]),
+        ops._p(t["row_expert"]), ops._p(t["row_token"]), ops._p(t["row_weight"]), ops._p(scratch), ops._stream(dev)))
+    return t
 
 
 def apply_exl3_grouped_fat(xh: torch.Tensor, out: torch.Tensor, counts: torch.Tensor, token_sorted: torch.Tensor,
                            weight_sorted: torch.Tensor, layer, cap: int, limit: float) -> None:
-    """out (fp32 [T, K]) += every fat expert's routed output, three launches and no host synchronisation
-    (code/fork/docs/prod_exl3_reference.py:1364-1435). `layer` carries the pointer tables as production's
-    `_exl3_ptrs` dict, or is an mi355moe.Exl3Experts (its `tables`)."""
+    """Adds every fat expert's (more than cap pairs) routed output to out (fp32 [T, K]): device tables, then the
+    gather, gate/up and down stages; no host synchronisation (the contract of code/fork/docs/
+    prod_exl3_reference.py:1364-1435). `layer` carries the pointer tables as production's `_exl3_ptrs` dict, or is an
+    mi355moe.Exl3Experts (its `tables`)."""
     ptrs = getattr(layer, "_exl3_ptrs", None) or getattr(layer, "tables")
     N = int(getattr(layer, "N", 0) or getattr(layer, "_exl3_intermediate_local"))
     dev = ptrs["gate_trellis"].device
-    if xh.device != dev or out.device != dev or counts.device != dev:
-        raise RuntimeError(f"EXL3 grouped tier: activations on {xh.device}, experts on {dev}")
-    if not (xh.is_contiguous() and out.is_contiguous() and out.dtype == torch.float32):
-        raise RuntimeError("EXL3 grouped tier needs contiguous fp16/bf16 input and fp32 output")
-    rows_cap, K = int(token_sorted.numel()), int(xh.shape[1])
-    tile = exl3_fat_moe_tile_rows_gateup()
-    tg = build_grouped_fat_tables(counts, cap, token_sorted.contiguous(), weight_sorted.contiguous(), rows_cap, tile)
-    h13 = torch.empty(rows_cap, K, dtype=torch.float16, device=dev)
-    h2 = torch.empty(rows_cap, N, dtype=torch.float16, device=dev)
-    exl3_fat_moe_gather(xh, tg["row_token"], tg["row_expert"], ptrs["gate_suh"], h13, tg["num_rows"])
+    for name, t in (("xh", xh), ("out", out), ("counts", counts)):
+        if t.device != dev:
+            raise RuntimeError(f"grouped fat tier: {name} is on {t.device} but the experts' tables are on {dev}")
+    if out.dtype != torch.float32 or not out.is_contiguous() or not xh.is_contiguous():
+        raise RuntimeError("grouped fat tier: out must be contiguous fp32 and xh contiguous fp16 / bf16")
+    rows, K = int(token_sorted.numel()), int(xh.shape[1])
+    tabs = build_grouped_fat_tables(counts, cap, token_sorted, weight_sorted, rows,
+                                    exl3_fat_moe_tile_rows_gateup())
+    h13 = torch.empty(rows, K, dtype=torch.float16, device=dev)
+    h2 = torch.empty(rows, N, dtype=torch.float16, device=dev)
+    segs = (tabs["seg_expert"], tabs["seg_row0"], tabs["seg_rows"], tabs["num_segs"])
+    exl3_fat_moe_gather(xh, tabs["row_token"], tabs["row_expert"], ptrs["gate_suh"], h13, tabs["num_rows"])
     exl3_fat_moe_gateup(h13, ptrs["gate_trellis"], ptrs["up_trellis"], ptrs["gate_svh"], ptrs["up_svh"],
-                        ptrs["down_suh"], h2, tg["seg_expert"], tg["seg_row0"], tg["seg_rows"], tg["num_segs"],
-                        float(limit))
-    exl3_fat_moe_down(h2, ptrs["down_trellis"], ptrs["down_svh"], out, tg["row_token"], tg["row_weight"],
-                      tg["seg_expert"], tg["seg_row0"], tg["seg_rows"], tg["num_segs"])
+                        ptrs["down_suh"], h2, *segs, float(limit))
+    exl3_fat_moe_down(h2, ptrs["down_trellis"], ptrs["down_svh"], out, tabs["row_token"], tabs["row_weight"], *segs)

@@ -120,8 +120,9 @@ def reserve(experts: Exl3Experts, max_tokens: int, topk: int = 8, router_experts
     its persistent scratch at registration (code/fork/tf_exl3_moe.py:391-418): later calls within that size never
     reallocate, so graphs may be captured at any point after this."""
     top = max(1, int(max_tokens))
-    sizes = {top} | {1 << i for i in range(top.bit_length()) if 1 << i <= top}
-    return workspace(experts.device, max(workspace_bytes(experts, t, topk, router_experts) for t in sizes))
+    # every size: the decode plan's split-K partials come and go with T (they exist only while the segments are too
+    # few to fill the chip), so the need is not monotone in T
+    return workspace(experts.device, max(workspace_bytes(experts, t, topk, router_experts) for t in range(1, top + 1)))
 
 
 def dequant(trellis: torch.Tensor) -> torch.Tensor:
@@ -300,12 +301,13 @@ def moe_forward_ids_split(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch
 def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                          limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
                          out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL,
-                         accumulate: bool = False, bf16_contrib: bool = False) -> torch.Tensor:
+                         accumulate: bool = False, bf16_contrib: bool = False, down16: bool = False) -> torch.Tensor:
     """The trellis-sourced e4m3 variant of the routed experts (code/fork/overlay/glm53_moe_e4m3.py:484-592 run(),
-    numerics of spec_ffn :666-674 with DOWN16 off): activations quantized per row to e4m3 after the input rotation,
-    EXL3 weights rounded to e4m3, fp32 sums; output [T, K] written like moe_forward_ids. The layer needs gate and up
-    sharing one suh and hidden <= 4096. accumulate / bf16_contrib: the ACC=bf16 and FOLD_SHARED knobs
-    (code/fork/docs/OPT_MOE.md:9-21) as in moe_forward_ids."""
+    numerics of spec_ffn :666-674): activations quantized per row to e4m3 after the input rotation, EXL3 weights
+    rounded to e4m3, fp32 sums; output [T, K] written like moe_forward_ids. The layer needs gate and up sharing one
+    suh and hidden <= 4096. accumulate / bf16_contrib: the ACC=bf16 and FOLD_SHARED knobs (code/fork/docs/
+    OPT_MOE.md:9-21) as in moe_forward_ids. down16: the down projection on fp16 operands (DOWN16, spec_proj16
+    :660-664) instead of e4m3."""
     if accumulate and out is None:
         raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
@@ -329,9 +331,9 @@ def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.
         raise ValueError("mi355moe_e4m3_moe_workspace_bytes rejected the shape")
     ws = workspace(dev, nb)
     em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
-    if accumulate or bf16_contrib:
+    if accumulate or bf16_contrib or down16:
         opts = (_lib.OPT_E4M3 | (_lib.OPT_ACCUMULATE if accumulate else 0) |
-                (_lib.OPT_BF16_CONTRIB if bf16_contrib else 0))
+                (_lib.OPT_BF16_CONTRIB if bf16_contrib else 0) | (_lib.OPT_DOWN16 if down16 else 0))
         _lib.check("mi355moe_moe_forward_ids_opt", L.mi355moe_moe_forward_ids_opt(
             ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
             ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em),

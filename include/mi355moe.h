@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MI355MOE_ABI_VERSION 1
+#define MI355MOE_ABI_VERSION 2
 
 enum {
     MI355MOE_OK = 0,
@@ -112,6 +112,16 @@ int mi355moe_route(const void* ids, int ids_dtype, const void* weights, int weig
                    int32_t* seg_rows_out, int64_t s_cap, int32_t* nseg, int32_t* counts, void* workspace,
                    size_t workspace_bytes, hipStream_t stream);
 
+/* The e4m3 extension's routing plan (code/fork/overlay/glm53_moe_e4m3.py:450-477) on the device: the permutation
+ * above (local ids by map_topk_to_local, pairs sorted by local id, stable, the sentinel pairs last) returned as its
+ * row tables: per pair j, local[j] (n for a pair with no local expert) and its row pos[j]; per row p, row_token[p]
+ * (int64), row_weight[p] (fp32) and row_expert[p] (n for the sentinel rows); counts int64 [n + 1]. */
+int64_t mi355moe_route_rows_workspace_bytes(int64_t P, int64_t n);
+int mi355moe_route_rows(const void* ids, int ids_dtype, const void* weights, int weights_dtype, int64_t T,
+                        int64_t topk, const int64_t* expert_map, int64_t n_global, int64_t n, int32_t* local,
+                        int32_t* pos, int64_t* row_token, float* row_weight, int32_t* row_expert, int64_t* counts,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Input rotation (stage entry): out[pos] = fp16(H(fp16(x[tok[pos]] * suh[pe[pos]])) * r) for rows with pe >= 0
  * (code/fork/kernels/exl3.cu:321-349; E3 gather code/fork/docs/ref/mia_exl3-fat-kernel/exl3_fat_moe.cu:95-126).
  * x dtype F16 or BF16 [*, K] (row stride x_stride); out fp16 [P][K]. */
@@ -162,12 +172,16 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
  *                             accumulators (relative error about 2^-9 per element). No effect on the decode path.
  *   MI355MOE_OPT_E4M3         the trellis-sourced e4m3 numerics of mi355moe_e4m3_moe_forward_ids (grouped path
  *                             only: path DECODE is refused; hidden <= 4096).
+ *   MI355MOE_OPT_DOWN16       with MI355MOE_OPT_E4M3: the down projection on fp16 operands (the e4m3 extension's
+ *                             variant 16, code/fork/overlay/glm53_moe_e4m3.py:660-674 spec_proj16): the down input
+ *                             h = fp16(H(float(a16) * suh_d) * r) times the fp16 W_q with fp32 sums.
  *   MI355MOE_OPT_PERSISTENT   reserved for a one-launch, ticket-ordered gate/up + down schedule of the grouped path
  *                             (the reference's code/fork/kernels/moe_e4m3.cu:867-897); not available in this library:
  *                             every call with it returns MI355MOE_EUNSUPPORTED before any launch.
  * Unknown bits: MI355MOE_EINVAL. Workspace sizes as mi355moe_moe_workspace_bytes_path (with MI355MOE_OPT_E4M3:
  * mi355moe_e4m3_moe_workspace_bytes). */
-enum { MI355MOE_OPT_ACCUMULATE = 1, MI355MOE_OPT_BF16_CONTRIB = 2, MI355MOE_OPT_E4M3 = 4, MI355MOE_OPT_PERSISTENT = 8 };
+enum { MI355MOE_OPT_ACCUMULATE = 1, MI355MOE_OPT_BF16_CONTRIB = 2, MI355MOE_OPT_E4M3 = 4, MI355MOE_OPT_PERSISTENT = 8,
+       MI355MOE_OPT_DOWN16 = 16 };
 int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
                                  int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
                                  int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,
@@ -249,6 +263,17 @@ int mi355moe_moe_layer_noalloc(const mi355moe_exl3_layer* layer, const void* x, 
  * mi355moe_e3_down_workspace_bytes) holds the raw accumulators and the token row lists. Rows whose token is outside
  * [0, tokens) or whose expert is outside [0, n) are skipped; segment entries outside the row buffer are skipped. */
 int64_t mi355moe_e3_tile_rows(void);
+/* The row and segment tables of the fat experts (the contract of build_grouped_fat_tables, prod_exl3_reference.py:
+ * 1316-1361) from the sorted pairs' counts int64 [n] (sentinel excluded), token_sorted int64 [rows_cap] and
+ * weight_sorted fp16 [rows_cap]: the experts with more than cap pairs are laid out back to back in expert order (row
+ * r of expert e = its sorted position counts-prefix(e) + (r - fat-prefix(e))), segments of at most tile rows (tile <=
+ * mi355moe_e3_tile_rows(), max_segs >= ceil(rows_cap / tile) + n). Rows past num_rows get row_expert -1, token 0 and
+ * weight 0. scratch: int32 [2 n]. */
+int mi355moe_e3_fat_tables(const int64_t* counts, int64_t n, int64_t cap, const int64_t* token_sorted,
+                           const void* weight_sorted, int64_t rows_cap, int64_t tile, int32_t* seg_expert,
+                           int32_t* seg_row0, int32_t* seg_rows, int64_t max_segs, int32_t* num_segs,
+                           int32_t* num_rows, int32_t* row_expert, int64_t* row_token, void* row_weight,
+                           int32_t* scratch, hipStream_t stream);
 int mi355moe_e3_gather(const void* x, int x_dtype, int64_t x_stride, int64_t tokens, int64_t K,
                        const int64_t* row_token, const int32_t* row_expert, int64_t rows_cap, int64_t n,
                        const int64_t* suh_table, void* h13, const int32_t* num_rows, hipStream_t stream);
@@ -266,31 +291,74 @@ int mi355moe_e3_down(const void* h2, int64_t rows_cap, int64_t K, int64_t N, int
 
 /* ---------------------------------------------------------------- the e4m3 extension's stages over row tables */
 
-/* The stage contract of the e4m3 extension the overlay's run() drives (code/fork/overlay/glm53_moe_e4m3.py:450-592
- * -> code/fork/kernels/moe_e4m3.cu seg_tables :3066-3083, gather2 :245-310, fused :2721-2725), trellis-sourced e4m3
- * numerics as mi355moe_e4m3_moe_forward_ids. seg_tables: segments of at most `tile` rows over the rows grouped by
- * expert (counts int64 [n], max_segs >= ceil(rows_cap / tile) + n; tile = mi355moe_e4m3_tile_rows() for the fused
- * stage). gather2: routed pair j = (token j / topk) with local expert local[j] (skipped unless 0 <= local < n) writes
- * row pos[j] of a_rows (fp16 [T*topk][K]: the e4m3 values of the quantised rotated row, this library's staging
- * order) and its scale asc[pos[j]]; a non-null out (fp32 or bf16 [T][out_stride]) is zeroed. fused: gate/up, the
- * down-input quantisation and the down GEMM of every segment's rows, each token's rows (row_token) then ADDED to out
- * in row order with the fp32 row_weight (deterministic); workspace from mi355moe_e4m3_fused_workspace_bytes. K <= 4096.
- */
+/* The stage contract of the e4m3 extension that the overlay's run() drives (code/fork/overlay/glm53_moe_e4m3.py:
+ * 450-592; bindings code/fork/kernels/moe_e4m3.cu:3081-3096), with the trellis-sourced e4m3 numerics of
+ * mi355moe_e4m3_moe_forward_ids. The stages exchange caller-owned buffers in the extension's formats:
+ *   a8  uint8 [rows][K] and a8d uint8 [rows][N]: one e4m3 (OCP E4M3FN) code per element, the columns of every group
+ *       of 16 stored in the order 0,1,8,9,2,3,10,11,4,5,12,13,6,7,14,15 (the extension's perm_pos / perm_cols
+ *       layout, moe_e4m3.cu:18-21,150-156); asc / dsc fp32 [rows]: the rows' scales (q * s is the value);
+ *   a16 fp16 [rows][N]: the SwiGLU output in plain column order;
+ * and the row / segment tables of seg_tables (rows grouped by expert, segments of at most `tile` rows) with the live
+ * counts num_segs / num_rows as int32 [1] device words (read by the kernels: no host synchronisation). Every buffer
+ * pointer must be 16-byte aligned. K (hidden) <= 4096, N (intermediate) <= 4096, multiples of 256 and 128.
+ *
+ * seg_tables (moe_e4m3.cu:3062-3083): counts int64 [n], max_segs >= ceil(rows_cap / tile) + n, 16 <= tile <=
+ *   mi355moe_e4m3_tile_rows() (the GEMMs take segments of at most that many rows).
+ * gather2 (moe_e4m3.cu:2493-2534): routed pair j = (token j / topk, slot j % topk) with local expert local[j] (skipped
+ *   unless 0 <= local[j] < n) writes a8 row pos[j] (pos[j] < a8_rows) and asc[pos[j]]: v = H(fp16(x) * suh) * r in
+ *   fp32, s = amax|v| / 448 (1 if 0), q = e4m3(clamp(v / s)). A non-null out (fp32 or bf16 [T][out_stride]) is zeroed.
+ * gather_tok (moe_e4m3.cu:2536-2571): the same quantisation for one row per token with the suh of expert 0 (valid
+ *   when every expert shares its w13 suh): a8 row t, asc[t] for t < T <= a8_rows; out zeroed if non-null.
+ * gateup (moe_e4m3.cu:2641-2676): a16 rows of the segments of chunk `chunk` of `nchunks` (equal shares of the
+ *   num_segs segments) = fp16(silu(min(g, L)) * clamp(u, -L, L)) (the limit iff L != 0), g = H(acc_g * s) * r * svh_g,
+ *   acc_g = the a8 row's codes times the gate weights rounded to e4m3, summed in fp32; u likewise.
+ * actq (moe_e4m3.cu:2573-2600): the rows of the chunk's segments: v = H(float(a16) * suh_d[row_expert[r]]) * r,
+ *   quantised as in gather2 into a8d row r and dsc[r].
+ * down (moe_e4m3.cu:2678-2719): every token's rows of the chunk's segments, (H(acc_d * dsc) * r) * svh_d * row_weight,
+ *   ADDED to out fp32 [tokens][out_stride] in row order (deterministic; at most 32 rows per token).
+ * fused (moe_e4m3.cu:2721-2725): gateup, actq and down of every segment in one call, out fp32 or bf16 ADDED to.
+ *   a8d / dsc (both or neither) and a16 receive the intermediates when non-null. variant bits:
+ *   MI355MOE_E4M3_TOKEN_ROWS: a8 / asc hold one row per token (gather_tok) and row r reads row row_token[r];
+ *   MI355MOE_E4M3_DOWN16: the down projection on fp16 operands (h = fp16(H(float(a16) * suh_d) * r) times the
+ *   fp16 W_q, the extension's variant 16, spec_proj16 at glm53_moe_e4m3.py:660-664); a8d / dsc are not written;
+ *   MI355MOE_E4M3_LEAN_MAINLOOP (the extension's +8192 schedule variant): accepted, same results.
+ *   The reference's lag / grid / sync arguments schedule its persistent kernel and have no counterpart here.
+ * The stages that take a workspace share one size, mi355moe_e4m3_stage_workspace_bytes(rows_cap, K, N, tokens). */
+enum { MI355MOE_E4M3_DOWN16 = 16, MI355MOE_E4M3_TOKEN_ROWS = 2048, MI355MOE_E4M3_LEAN_MAINLOOP = 8192 };
 int64_t mi355moe_e4m3_tile_rows(void);
 int mi355moe_e4m3_seg_tables(const int64_t* counts, int64_t n, int64_t tile, int64_t rows_cap, int32_t* seg_expert,
                              int32_t* seg_row0, int32_t* seg_rows, int64_t max_segs, int32_t* num_segs,
                              int32_t* num_rows, hipStream_t stream);
 int mi355moe_e4m3_gather2(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K, const int32_t* local,
-                          const int32_t* pos, int64_t topk, int64_t n, const int64_t* gate_suh, void* a_rows,
-                          float* asc, void* out, int out_dtype, int64_t out_stride, hipStream_t stream);
-int64_t mi355moe_e4m3_fused_workspace_bytes(int64_t rows_cap, int64_t K, int64_t N, int64_t tokens);
-int mi355moe_e4m3_fused(const void* a_rows, const float* asc, void* out, int out_dtype, int64_t tokens,
-                        int64_t out_stride, int64_t K, int64_t N, int64_t n, const int64_t* gate_trellis,
-                        const int64_t* up_trellis, const int64_t* gate_svh, const int64_t* up_svh,
-                        const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
-                        const int64_t* row_token, const float* row_weight, int64_t rows_cap,
+                          const int32_t* pos, int64_t topk, int64_t n, const int64_t* gate_suh, uint8_t* a8,
+                          int64_t a8_rows, float* asc, void* out, int out_dtype, int64_t out_stride,
+                          hipStream_t stream);
+int mi355moe_e4m3_gather_tok(const void* x, int x_dtype, int64_t x_stride, int64_t T, int64_t K,
+                             const int64_t* gate_suh, uint8_t* a8, int64_t a8_rows, float* asc, void* out,
+                             int out_dtype, int64_t out_stride, hipStream_t stream);
+int64_t mi355moe_e4m3_stage_workspace_bytes(int64_t rows_cap, int64_t K, int64_t N, int64_t tokens);
+int mi355moe_e4m3_gateup(const uint8_t* a8, const float* asc, int64_t rows_cap, int64_t K, int64_t N, int64_t n,
+                         const int64_t* gate_trellis, const int64_t* up_trellis, const int64_t* gate_svh,
+                         const int64_t* up_svh, void* a16, const int32_t* seg_expert, const int32_t* seg_row0,
+                         const int32_t* seg_rows, int64_t seg_cap, const int32_t* num_segs, float limit, int64_t chunk,
+                         int64_t nchunks, void* workspace, size_t workspace_bytes, hipStream_t stream);
+int mi355moe_e4m3_actq(const void* a16, int64_t rows_cap, int64_t N, const int32_t* row_expert, int64_t n,
+                       const int64_t* down_suh, uint8_t* a8d, float* dsc, const int32_t* seg_row0,
+                       const int32_t* seg_rows, int64_t seg_cap, const int32_t* num_segs, int64_t chunk,
+                       int64_t nchunks, void* workspace, size_t workspace_bytes, hipStream_t stream);
+int mi355moe_e4m3_down(const uint8_t* a8d, const float* dsc, int64_t rows_cap, int64_t K, int64_t N, int64_t n,
+                       const int64_t* down_trellis, const int64_t* down_svh, float* out, int64_t tokens,
+                       int64_t out_stride, const int64_t* row_token, const float* row_weight,
+                       const int32_t* seg_expert, const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap,
+                       const int32_t* num_segs, int64_t chunk, int64_t nchunks, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+int mi355moe_e4m3_fused(const uint8_t* a8, const float* asc, int64_t a8_rows, uint8_t* a8d, float* dsc, void* a16,
+                        void* out, int out_dtype, int64_t tokens, int64_t out_stride, int64_t K, int64_t N, int64_t n,
+                        const int64_t* gate_trellis, const int64_t* up_trellis, const int64_t* gate_svh,
+                        const int64_t* up_svh, const int64_t* down_trellis, const int64_t* down_suh,
+                        const int64_t* down_svh, const int64_t* row_token, const float* row_weight, int64_t rows_cap,
                         const int32_t* seg_expert, const int32_t* seg_row0, const int32_t* seg_rows, int64_t seg_cap,
-                        const int32_t* num_segs, float limit, void* workspace, size_t workspace_bytes,
+                        const int32_t* num_segs, float limit, int variant, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
 
 /* ---------------------------------------------------------------- e4m3 expert variant */
