@@ -268,6 +268,58 @@ void orc_down_epilogue_tf(const float* zd, const uint16_t* svh_d, uint16_t w16, 
     }
 }
 
+/* ---------------------------------------------------------------- the kernel-mode epilogues (modes 0, 1, 4) */
+
+/* Gate/up epilogue of one pair row at the HIP kernels' rounding points, from the fp32 GEMV/GEMM sums zg / zu [N]
+ * (rotated in place, N a multiple of 128): per 128 block g = (H(zg) * r) * svh_g and u likewise in fp32, then
+ *   e3 = 1 (E3, exl3_fat_moe.cu:340-378): g = min(g, L), u = clamp(u, -L, L) iff L != 0, a = sigm(g) * g * u;
+ *   e3 = 0 (decode: exl3.cu's fp32 g / u and SiLU, then the limit as exl3_moe, xl_hadamard_inner.cuh:280-400):
+ *          s = g * sigm(g), s = min(s, L), u = clamp(u, -L, L) iff L != 0, a = s * u;
+ * then fp16(fp16(a) * suh_d) (the fp16 activation and its fp16 product with suh_d, xl_hadamard_inner.cuh:320-400,
+ * exl3_fat_moe.cu:370-375), rotated in fp32 and stored as xd = fp16(H(.) * r). */
+void orc_gateup_epilogue(float* zg, float* zu, const uint16_t* svh_g, const uint16_t* svh_u, const uint16_t* suh_d,
+                         int N, float limit, int e3, uint16_t* xd) {
+    float act[128];
+    for (int b0 = 0; b0 < N; b0 += 128) {
+        orc_fwht128(zg + b0);
+        orc_fwht128(zu + b0);
+        for (int i = 0; i < 128; ++i) {
+            float g = zg[b0 + i] * HAD_R * orc_h2f(svh_g[b0 + i]);
+            float u = zu[b0 + i] * HAD_R * orc_h2f(svh_u[b0 + i]);
+            float a;
+            if (e3) {
+                if (limit != 0.0f) {
+                    g = fminf(g, limit);
+                    u = fminf(fmaxf(u, -limit), limit);
+                }
+                a = sigm(g) * g * u;
+            } else {
+                float sl = g * sigm(g);
+                if (limit != 0.0f) {
+                    sl = fminf(sl, limit);
+                    u = fminf(fmaxf(u, -limit), limit);
+                }
+                a = sl * u;
+            }
+            act[i] = hmul(rh(a), orc_h2f(suh_d[b0 + i]));
+        }
+        orc_fwht128(act);
+        for (int i = 0; i < 128; ++i) xd[b0 + i] = orc_f2h(act[i] * HAD_R);
+    }
+}
+
+/* Down epilogue of one pair row (zd [K] rotated in place) into out [K]: e3 = 1 (exl3_fat_moe.cu:443-457):
+ * ((H(zd) * r) * svh_d) * w; e3 = 0 (exl3.cu:455-496): H(zd) * (r * w) * svh_d. w = the fp16 router weight. */
+void orc_down_epilogue(float* zd, const uint16_t* svh_d, uint16_t w16, int K, int e3, float* out) {
+    const float w = orc_h2f(w16);
+    const float rs = HAD_R * w;
+    for (int b0 = 0; b0 < K; b0 += 128) {
+        orc_fwht128(zd + b0);
+        for (int i = 0; i < 128; ++i)
+            out[b0 + i] = e3 ? zd[b0 + i] * HAD_R * orc_h2f(svh_d[b0 + i]) * w : zd[b0 + i] * rs * orc_h2f(svh_d[b0 + i]);
+    }
+}
+
 /* ---------------------------------------------------------------- one layer of routed experts */
 
 typedef struct {
@@ -356,53 +408,17 @@ int orc_moe_forward(const orc_layer* L, int T, const uint16_t* x16, int P, const
                         const float* ru = wu + (size_t)k * N;
                         for (int c = 0; c < N; ++c) { zg[c] += a * rg[c]; zu[c] += b * ru[c]; }
                     }
-                    float* act = tmp + 2 * N;
                     if (mode == 5) orc_gateup_epilogue_tf(zg, zu, svh_g, svh_u, suh_d, N, limit, xdd);
-                    else for (int b0 = 0; b0 < N; b0 += 128) {
-                        orc_fwht128(zg + b0);
-                        orc_fwht128(zu + b0);
-                        for (int i = 0; i < 128; ++i) {
-                            float g = zg[b0 + i] * HAD_R * orc_h2f(svh_g[b0 + i]);
-                            float u = zu[b0 + i] * HAD_R * orc_h2f(svh_u[b0 + i]);
-                            float a;
-                            if (mode == 1) {
-                                if (limit != 0.0f) {
-                                    g = fminf(g, limit);
-                                    u = fminf(fmaxf(u, -limit), limit);
-                                }
-                                a = sigm(g) * g * u;
-                            } else {
-                                float s = g * sigm(g);
-                                if (limit != 0.0f) {
-                                    s = fminf(s, limit);
-                                    u = fminf(fmaxf(u, -limit), limit);
-                                }
-                                a = s * u;
-                            }
-                            act[b0 + i] = hmul(rh(a), orc_h2f(suh_d[b0 + i]));
-                        }
-                        orc_fwht128(act + b0);
-                        for (int i = 0; i < 128; ++i) xdd[b0 + i] = orc_f2h(act[b0 + i] * HAD_R);
-                    }
+                    else orc_gateup_epilogue(zg, zu, svh_g, svh_u, suh_d, N, limit, mode == 1, xdd);
                     for (int c = 0; c < K; ++c) zd[c] = 0.f;
                     for (int k = 0; k < N; ++k) {
                         const float a = orc_h2f(xdd[k]);
                         const float* rd = wd + (size_t)k * K;
                         for (int c = 0; c < K; ++c) zd[c] += a * rd[c];
                     }
-                    const float w = orc_h2f(pair_w16[j]);
-                    const float rs = HAD_R * w;
                     float* dst = c32 + (size_t)j * K;
                     if (mode == 5) orc_down_epilogue_tf(zd, svh_d, pair_w16[j], K, dst);
-                    else for (int b0 = 0; b0 < K; b0 += 128) {
-                        orc_fwht128(zd + b0);
-                        for (int i = 0; i < 128; ++i) {
-                            float v;
-                            if (mode == 1) v = zd[b0 + i] * HAD_R * orc_h2f(svh_d[b0 + i]) * w;
-                            else v = zd[b0 + i] * rs * orc_h2f(svh_d[b0 + i]);
-                            dst[b0 + i] = v;
-                        }
-                    }
+                    else orc_down_epilogue(zd, svh_d, pair_w16[j], K, mode == 1, dst);
                 } else {
                     /* float64: y = ((((x*suh) H) Wq) H) * svh per projection */
                     const double rr = 1.0 / sqrt(128.0);

@@ -65,6 +65,10 @@ def lib() -> ctypes.CDLL:
         L.orc_gateup_epilogue_tf.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int, ctypes.c_float, ctypes.c_void_p]
         L.orc_down_epilogue_tf.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint16, ctypes.c_int,
                                            ctypes.c_void_p]
+        L.orc_gateup_epilogue.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                                                                  ctypes.c_void_p]
+        L.orc_down_epilogue.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint16, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_void_p]
         L.orc_expf_via_double.argtypes = [ctypes.c_float]
         L.orc_moe_forward.restype = ctypes.c_int
         L.orc_moe_forward.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
@@ -149,6 +153,34 @@ def down_epilogue_tf(zd: np.ndarray, svh_d: np.ndarray, w16) -> np.ndarray:
     out = np.zeros(K, np.float32)
     w = int(np.asarray(w16, np.float16).view(np.uint16))
     lib().orc_down_epilogue_tf(_p(zd), _p(sv), w, K, _p(out))
+    return out
+
+
+def gateup_epilogue(zg: np.ndarray, zu: np.ndarray, svh_g: np.ndarray, svh_u: np.ndarray, suh_d: np.ndarray,
+                    limit: float, mode: str) -> np.ndarray:
+    """One pair row of the kernel modes ("decode" / "decode_x": SiLU then the limit; "e3": the limit then SiLU):
+    fp32 sums zg / zu [N] -> the down input fp16 [N] (orc_gateup_epilogue, the epilogue forward() runs)."""
+    zg = np.array(zg, np.float32, copy=True)
+    zu = np.array(zu, np.float32, copy=True)
+    args = [np.ascontiguousarray(a, np.float16) for a in (svh_g, svh_u, suh_d)]
+    N = zg.size
+    if N % 128 or zu.size != N or any(a.size != N for a in args) or mode not in ("decode", "decode_x", "e3"):
+        raise ValueError("gateup_epilogue: rows of one length (a multiple of 128), mode decode / decode_x / e3")
+    out = np.zeros(N, np.float16)
+    lib().orc_gateup_epilogue(_p(zg), _p(zu), *[_p(a) for a in args], N, float(limit), int(mode == "e3"), _p(out))
+    return out
+
+
+def down_epilogue(zd: np.ndarray, svh_d: np.ndarray, w16, mode: str) -> np.ndarray:
+    """One pair row of the kernel modes: fp32 down sums zd [K] -> the pair's fp32 contribution (orc_down_epilogue)."""
+    zd = np.array(zd, np.float32, copy=True)
+    sv = np.ascontiguousarray(svh_d, np.float16)
+    K = zd.size
+    if K % 128 or sv.size != K or mode not in ("decode", "decode_x", "e3"):
+        raise ValueError("down_epilogue: rows of one length (a multiple of 128), mode decode / decode_x / e3")
+    out = np.zeros(K, np.float32)
+    w = int(np.asarray(w16, np.float16).view(np.uint16))
+    lib().orc_down_epilogue(_p(zd), _p(sv), w, K, int(mode == "e3"), _p(out))
     return out
 
 

@@ -80,19 +80,6 @@ def topk_sigmoid_bias(logits: np.ndarray, bias: np.ndarray, topk: int, scale: fl
     return ids, wts
 
 
-def topk_softmax(logits: np.ndarray, topk: int, renormalize: bool = True) -> tuple[np.ndarray, np.ndarray]:
-    """Softmax router of the dense CPU block: probabilities in float64, topk largest (lower id on ties),
-    renormalised over the picked ones."""
-    z = np.asarray(logits, np.float64)
-    p = np.exp(z - z.max(-1, keepdims=True))
-    p /= p.sum(-1, keepdims=True)
-    order = np.argsort(-p, axis=-1, kind="stable")[:, :topk]
-    w = np.take_along_axis(p, order, -1)
-    if renormalize:
-        w = w / w.sum(-1, keepdims=True)
-    return order.astype(np.int32), w
-
-
 def map_topk_to_local(ids: np.ndarray, n_local: int, expert_map: np.ndarray | None = None) -> np.ndarray:
     """Global ids [T, topk] -> local ids [P]; invalid or non-local -> the sentinel n_local
     (prod_exl3_reference.py:936-958)."""
