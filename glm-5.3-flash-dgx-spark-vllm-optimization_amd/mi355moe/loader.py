@@ -37,7 +37,8 @@ def _slice_tp(t: torch.Tensor, dim: int, tp_rank: int, tp_size: int) -> torch.Te
         raise ValueError(f"tp_rank {tp_rank} outside [0, {tp_size})")
     size = int(t.shape[dim])
     if size % tp_size:
-        raise ValueError(f"EXL3 TP shard: dim {dim} of size {size} is not divisible by tp={tp_size}")
+        raise ValueError(f"cannot cut axis {dim} ({size} entries) into {tp_size} equal tensor-parallel slices: "
+                         "not divisible")
     step = size // tp_size
     return t.narrow(dim, step * tp_rank, step).contiguous()
 
@@ -88,12 +89,12 @@ def load_into(layer: torch.nn.Module, loaded: torch.Tensor, weight_name: str, sh
         part = shard_exl3_row(src, suffix, tp_rank, tp_size)
         dest = getattr(layer, "w2_" + suffix).data[expert_id]
     else:
-        raise ValueError(f"unknown EXL3 shard_id {shard_id!r}")
+        raise ValueError(f"shard_id must be w1, w2 or w3, got {shard_id!r}")
     if suffix == "mcg":
         part = part.reshape(dest.shape)
     if tuple(dest.shape) != tuple(part.shape):
-        raise RuntimeError(f"EXL3 load shape mismatch {weight_name} shard={shard_id} expert={expert_id}: "
-                           f"dest {tuple(dest.shape)} != loaded {tuple(part.shape)}")
+        raise RuntimeError(f"{weight_name} (shard {shard_id}, expert {expert_id}) has shape {tuple(part.shape)} after "
+                           f"tensor-parallel slicing, but the parameter slot holds {tuple(dest.shape)}")
     dest.copy_(part)
     return True
 
@@ -167,7 +168,8 @@ def load_exl3_layer(path: str | Iterable[str], layer_idx: int, num_experts: int,
             h.__exit__(None, None, None)
     for name in ("w13_mcg", "w2_mcg"):
         if not bool(torch.all(getattr(layer, name) == MCG_MARKER)):
-            raise RuntimeError("EXL3 mcg marker is not the MCG int32 0xCBAC1FED; packed ABI mismatch")
+            raise RuntimeError(f"{name}: every entry must be the mcg codebook marker {MCG_MARKER} (0xCBAC1FED as "
+                               "int32); this checkpoint uses another trellis codebook")
     return Exl3Experts(*(getattr(layer, k).data.to(dev) for k in
                          ("w13_trellis", "w13_suh", "w13_svh", "w2_trellis", "w2_suh", "w2_svh")))
 
