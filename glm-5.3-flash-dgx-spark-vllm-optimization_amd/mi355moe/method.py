@@ -140,8 +140,8 @@ class Exl3MoEMethod:
         for name in ("w13_mcg", "w2_mcg"):
             m = getattr(layer, name, None)
             if m is not None and not bool(torch.all(m == MCG_MARKER)):
-                raise RuntimeError("EXL3 mcg marker is not the MCG int32 0xCBAC1FED / "
-                                   f"{MCG_MARKER}; packed ABI mismatch")
+                raise RuntimeError(f"{name}: every entry must be the mcg codebook marker {MCG_MARKER} (0xCBAC1FED "
+                                   "as int32); these weights use another trellis codebook")
         layer._mi355_experts = Exl3Experts.from_module(layer)
         if self.max_num_tokens:
             ops.reserve(layer._mi355_experts, self.max_num_tokens, self.topk)
