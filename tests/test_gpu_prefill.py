@@ -246,16 +246,20 @@ def _hot_ids(T, n, topk, seed, cuda):
     return torch.from_numpy(ids).to(cuda)
 
 
+@pytest.mark.parametrize("uniform", [False, True])
 @pytest.mark.parametrize("numerics,n,K,N,T,topk", [("e3", 16, 1024, 512, 200, 4), ("e4m3", 16, 1024, 512, 200, 4),
                                                    ("e3", 32, 2048, 256, 300, 2), ("e4m3", 8, 4096, 1024, 130, 3)])
-def test_tile_kinds_bit_equal(cuda, monkeypatch, numerics, n, K, N, T, topk):
+def test_tile_kinds_bit_equal(cuda, monkeypatch, numerics, n, K, N, T, topk, uniform):
     """The grouped GEMMs on 64-row tiles and on 128-row tiles (two workgroups per CU; chosen when the routed experts
     average at most 128 rows), on 256-row tiles, and split between small and 256-row tiles by segment size, forced
     with MI355MOE_PREFILL_TILES: bit-identical outputs, including a hot expert whose 130..300 rows span up to four
-    64-row quarters or three 128-row halves of its segments."""
+    64-row quarters or three 128-row halves of its segments. uniform: every expert shares one w13 suh, so the GEMMs
+    read one gathered row per token through the rows' tokens; bit-identical as well to the same layer run with one
+    gathered row per pair (the layer's uniform flag cleared)."""
     from mi355moe import _lib, ops, synthetic
-    _say(f"tile kinds: {numerics} n={n} K={K} N={N} T={T} topk={topk}")
-    ex = synthetic.calibrated_layer(n, K, N, seed=n + K + T, device=cuda)
+    _say(f"tile kinds: {numerics} n={n} K={K} N={N} T={T} topk={topk} uniform_suh={uniform}")
+    ex = synthetic.calibrated_layer(n, K, N, seed=n + K + T, device=cuda, uniform_suh=uniform)
+    assert ex.uniform_suh == uniform
     x = synthetic.activations(T, K, seed=T + 11, device=cuda)
     ids = _hot_ids(T, n, topk, T + 12, cuda)
     w = synthetic.softmax_weights(T, topk, seed=T + 13, device=cuda)
@@ -272,6 +276,16 @@ def test_tile_kinds_bit_equal(cuda, monkeypatch, numerics, n, K, N, T, topk):
     assert torch.equal(outs[0], outs[1])
     assert torch.equal(outs[0], outs[2])
     assert torch.equal(outs[0], outs[3])
+    if uniform:                                                      # per-pair rows, every tile kind
+        ex.desc.flags &= ~_lib.LAYER_UNIFORM_W13_SUH
+        for kind in ("small", "large", "hybrid", "mid"):
+            monkeypatch.setenv("MI355MOE_PREFILL_TILES", kind)
+            if numerics == "e3":
+                o = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+            else:
+                o = ops.moe_forward_ids_e4m3(ex, x, ids, w, out_dtype=torch.float32)
+            torch.cuda.synchronize()
+            assert torch.equal(outs[0], o), kind
 
 
 def test_few_row_tiles_vs_oracle(cuda):

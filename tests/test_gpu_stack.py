@@ -5,10 +5,12 @@ the next layer, the whole forward captured as one HIP graph.
 
 Checks: every graph replay (with eager work and host synchronisation between replays) equals the eager forward bit
 for bit; and for two sampled layers, the router picks of the layer's actual input are bit-exact against the oracle
-router, and two sampled tokens' routed outputs match the float64 oracle (rel_l2 <= 5e-3) and, elementwise within
-rtol 2e-2 / atol 1e-3 on the bf16 output, the oracle at the decode kernels' rounding points (the layer's outputs have
-RMS ~1.7, where the fp16 intermediates those rounding points keep move outputs near zero by more than 1e-3 against
-float64).
+router, and two sampled tokens' routed outputs match the float64 oracle (rel_l2 <= 5e-3), the reference's default
+decode numerics (the oracle's tf_parity mode, TF_PARITY=1) within the reference's own build-vs-production bar E.1
+(rel_l2 <= 2e-3 and per token row <= 1e-2, code/fork/docs/DESIGN.md:520-523), and, elementwise within rtol 2e-2 /
+atol 1e-3 on the bf16 output, the oracle at the decode kernels' rounding points. Elementwise against float64 and
+against tf_parity the layer-41 outputs (RMS ~1.7; the fp16 intermediates of either numerics move outputs near zero by
+more than 1e-3) do not hold that bar everywhere; the share of elements outside it and the worst element are printed.
 """
 from __future__ import annotations
 
@@ -103,10 +105,19 @@ def test_stacked_decode_graph(cuda):
         x16 = x_l[torch.from_numpy(sample).to(cuda)].to(torch.float16).cpu().numpy()
         ref64 = moe.forward(lay, x16, tok, exx, w16, 10.0, "f64")
         ref_k = moe.forward(lay, x16, tok, exx, w16, 10.0, "decode_x")
+        ref_tf = moe.forward(lay, x16, tok, exx, w16, 10.0, "tf_parity")
         got = outs[l][torch.from_numpy(sample).to(cuda)].float().cpu().numpy()
-        r, rk = _rel(got, ref64), _rel(got, ref_k)
-        _say(f"  layer {l}: tokens {sample.tolist()} rel_l2 vs float64 {r:.3e}, vs the kernels' rounding {rk:.3e}")
+        r, rk, rt = _rel(got, ref64), _rel(got, ref_k), _rel(got, ref_tf)
+        rows = max(_rel(got[i], ref_tf[i]) for i in range(sample.size))
+        _say(f"  layer {l}: tokens {sample.tolist()} rel_l2 vs float64 {r:.3e}, vs the kernels' rounding {rk:.3e}, "
+             f"vs the reference's default numerics {rt:.3e} (worst row {rows:.3e})")
         assert r <= 5e-3, (l, r)
+        assert rt <= 2e-3 and rows <= 1e-2, (l, rt, rows)
         assert np.allclose(got, ref_k, rtol=2e-2, atol=1e-3), l
+        for name, rv in (("float64", ref64), ("tf_parity", ref_tf)):
+            bad = ~np.isclose(got, rv, rtol=2e-2, atol=1e-3)
+            i = int(np.argmax(np.abs(got - rv) - 2e-2 * np.abs(rv)))
+            _say(f"    elementwise vs {name}: {bad.mean():.4%} outside rtol 2e-2 / atol 1e-3; worst: token "
+                 f"{sample[i // K]} column {i % K} got {got.flat[i]:.5f} ref {rv.flat[i]:.5f}")
     del graph, layers, routers, xs, outs, ref
     torch.cuda.empty_cache()
