@@ -408,75 +408,87 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
 // ------------------------------------------------------------------------------------------------ top-k + permutation
 
 // Order key of a candidate: the choice key (score + bias; -0 made +0) mapped to an unsigned integer with the same
-// order, above the complement of its id, so the largest 64-bit key is the largest choice key with the lowest id among
-// equal ones (the reference's order).
-__device__ __forceinline__ uint64_t topk_order(float key, int e) {
+// order. Every finite key maps above 0, so 0 marks an empty or taken slot. Among equal keys the lower expert id is
+// picked first (the reference's order).
+__device__ __forceinline__ uint32_t topk_key(float key) {
     const uint32_t b = __builtin_bit_cast(uint32_t, key + 0.0f);
-    const uint32_t u = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// One wave's top-k of one token (E <= 1024 candidates, lane l holding candidates l + 64 j): topk rounds of "largest
-// order key" (the lane-local best, then a butterfly max over the wave); the owner of the winner drops it, so picks
-// come largest first, lower id on ties (the reference's order). Scores s = sigmoid(logit) (through double exp) go to
-// sco [E] for the weights; weights are the picks' scores renormalised over their total (summed sequentially in pick
-// order, + 1e-20, correctly rounded division) and scaled.
-// Maximum of a 64-bit value over the wave, returned in every lane: rotations by 1, 2, 4, 8 inside each 16-lane row
-// (DPP, no LDS), then the four row maxima by readlane.
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, true);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, true);
-    return ((uint64_t)hi << 32) | lo;
+// Maximum / minimum of a 32-bit value over the wave, returned in every lane: rotations by 1, 2, 4, 8 inside each
+// 16-lane row (DPP, no LDS), then the four row results by readlane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xF, 0xF, true));   // row_ror:1
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x122, 0xF, 0xF, true));   // row_ror:2
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true));   // row_ror:4
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true));   // row_ror:8
+    const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+    const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    return max(a, b);
 }
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    uint64_t o = dpp_u64<0x121>(v);                                   // row_ror:1
-    v = o > v ? o : v;
-    o = dpp_u64<0x122>(v);                                            // row_ror:2
-    v = o > v ? o : v;
-    o = dpp_u64<0x124>(v);                                            // row_ror:4
-    v = o > v ? o : v;
-    o = dpp_u64<0x128>(v);                                            // row_ror:8
-    v = o > v ? o : v;
-    uint64_t m = 0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const uint64_t rv = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 16 * r) << 32) |
-                            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
-        m = rv > m ? rv : m;
-    }
-    return m;
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x121, 0xF, 0xF, true));
+    v = min(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x122, 0xF, 0xF, true));
+    v = min(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true));
+    v = min(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true));
+    const uint32_t a = min((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+    const uint32_t b = min((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    return min(a, b);
 }
 
+// One wave's top-k of one token (E <= 1024 candidates, lane l holding candidates l + 64 j). Every load of the row (and
+// of the bias) is issued before the first is used, so the row costs one memory latency. Then topk rounds: each lane's
+// best remaining key (the lower j among equal keys, hence the lower id), the wave maximum, and the winner among the
+// lanes holding it -- the only one, or with equal keys in several lanes the lowest id, by a wave minimum. The winner's
+// owner drops it, so picks come largest first, lower id on ties (the reference's order). Scores s = sigmoid(logit)
+// (through double exp) go to sco [E] for the weights; weights are the picks' scores renormalised over their total
+// (summed sequentially in pick order, + 1e-20, correctly rounded division) and scaled.
 // J >= ceil(E / 64); COH: coherent loads of the row; SCORE: the row holds the scores sigmoid(logit) already
 template <int J, bool COH = false, bool SCORE = false>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E, const float* __restrict__ bias,
                                           int topk, float scale, int renorm, float* sco, int32_t* __restrict__ ids_row,
                                           float* __restrict__ wts_row, int* ids_sh, float* wts_sh) {
     const int lane = threadIdx.x & 63;
-    uint64_t ok[J];
-    const int nj = (E + 63) >> 6;
+    float lv[J], bv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {                                     // clamped addresses: every load in bounds
+        const int e = min(lane + 64 * j, E - 1);
+        lv[j] = COH ? ld_coherent(lrow + e) : lrow[e];
+        bv[j] = bias ? bias[e] : 0.f;
+    }
+    uint32_t key[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        ok[j] = 0;
         const int e = lane + 64 * j;
-        if (j < nj && e < E) {
-            const float lg = COH ? ld_coherent(lrow + e) : lrow[e];
-            const float sv = SCORE ? lg : (float)(1.0 / (1.0 + exp(-(double)lg)));
+        key[j] = 0u;
+        if (e < E) {
+            const float sv = SCORE ? lv[j] : (float)(1.0 / (1.0 + exp(-(double)lv[j])));
             sco[e] = sv;
-            ok[j] = topk_order(sv + (bias ? bias[e] : 0.f), e);
+            key[j] = topk_key(sv + bv[j]);
         }
     }
     int mine_e = 0;                                                   // lane k: the k-th pick
     for (int k = 0; k < topk; ++k) {
-        uint64_t best = 0;
-#pragma unroll
-        for (int j = 0; j < J; ++j) best = ok[j] > best ? ok[j] : best;
-        best = wave_max_u64(best);
-        const int e = (int)(0xFFFFFFFFu - (uint32_t)best);
+        uint32_t bk = 0u;
+        int bj = 0;
 #pragma unroll
         for (int j = 0; j < J; ++j)
-            if (j == (e >> 6) && lane == (e & 63)) ok[j] = 0;
+            if (key[j] > bk) {
+                bk = key[j];
+                bj = j;
+            }
+        const uint32_t m = wave_max_u32(bk);
+        const uint64_t hit = __ballot(bk == m);
+        int e;
+        if (__popcll(hit) == 1) {                                     // uniform: one lane holds the maximum
+            const int wl = __ffsll((long long)hit) - 1;
+            e = 64 * __builtin_amdgcn_readlane(bj, wl) + wl;
+        } else {                                                      // equal keys: the lowest id
+            e = (int)wave_min_u32(bk == m ? (uint32_t)(64 * bj + lane) : 0xFFFFFFFFu);
+        }
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            if (j == (e >> 6) && lane == (e & 63)) key[j] = 0u;
         if (lane == k) mine_e = e;
     }
     // scores of the picks (written by their owners before the rounds), summed in pick order
