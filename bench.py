@@ -384,6 +384,12 @@ def run_prefill(args, torch, dev):
     torch.cuda.synchronize()
     gu_ms = sum(a.elapsed_time(b) for a, b in gu) / len(gu)
 
+    if args.workload == "prefill-uniform":                # the profiling window: these calls only
+        P = sum(pairs) / len(pairs)
+        return {"prefill_ms_per_layer": round(ms, 4), "prefill_gateup_ms": round(gu_ms, 4),
+                "prefill_gateup_frac": round(2.0 * P * K * 2 * N / (gu_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
+                                             4)}
+
     def step_fold(l):
         # bf16 down accumulators, routed sum added into out (which stands for the shared experts' bf16 output)
         ids, wts = ops.router_topk(logits[l], TOPK, None, routed_scale=SCALE)
@@ -751,7 +757,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="all", choices=["all", "decode", "prefill", "zipf", "fp8", "e4m3t", "stack"])
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "decode", "prefill", "prefill-uniform", "zipf", "fp8", "e4m3t", "stack"])
     ap.add_argument("--stack-layers", type=int, default=42)
     ap.add_argument("--prefill-tokens", type=int, default=8192)
     ap.add_argument("--fp8-tokens", type=int, default=2048)
@@ -772,12 +779,12 @@ def main():
     import mi355moe
     mi355moe._lib.lib()
     dev = torch.device("cuda", 0)
-    if args.workload in ("prefill", "zipf", "fp8", "e4m3t", "stack"):
+    if args.workload in ("prefill", "prefill-uniform", "zipf", "fp8", "e4m3t", "stack"):
         args.no_cpu_baseline = True
         res = run_decode(argparse.Namespace(**{**vars(args), "steps": 8, "warmup": 2}), torch, mi355moe, dev)
     else:
         res = run_decode(args, torch, mi355moe, dev)
-    if args.workload in ("all", "prefill"):
+    if args.workload in ("all", "prefill", "prefill-uniform"):
         log("[bench] prefill ...")
         res.update(run_prefill(args, torch, dev))
     if args.workload in ("all", "prefill", "zipf"):

@@ -48,6 +48,10 @@ constexpr size_t PF_LDS_M = (size_t)PF_NSM * (PF_TMM * PF_RB + PF_WSB);  // 73,7
 enum { PF_LARGE = 0, PF_SMALL = 1, PF_MID = 2 };
 __host__ __device__ constexpr int pf_sub_rows(int kind) { return kind == PF_SMALL ? PF_TMS : kind == PF_MID ? PF_TMM : PF_TM; }
 constexpr int PF_CLD = 260;                     // epilogue staging row stride (floats): [32][PF_CLD] fp32
+// Row blocks (32 rows each) the gate/up epilogue stages at once: as many as the kernel's LDS holds.
+__host__ __device__ constexpr int pf_epi_blocks(int kind) {
+    return (int)((kind == PF_SMALL ? PF_LDS_S : kind == PF_MID ? PF_LDS_M : PF_LDS) / (32 * PF_CLD * 4));
+}
 
 // Rotated activations (h13, h2) are stored with k permuted inside every group of 16: storage pair p (halves 2p,
 // 2p+1) holds k pair j with p = 2 (j % 4) + j / 4, i.e. storage order k = 0,1,8,9, 2,3,10,11, 4,5,12,13, 6,7,14,15.
@@ -678,16 +682,23 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
     const int grp0 = cb * 128 + 16 * (c >> 1);                      // the lane's 16-group of the block
     const float L = a.limit;
     const float hr = HAD_R * fwht_sign(lane);                        // r and the sign fwht128_x16s leaves
+    // RBS row blocks are staged per pair of barriers (as many as the kernel's LDS holds), so each wave runs 2 RBS
+    // row passes of independent work between barriers
+    constexpr int RBS = pf_epi_blocks(KIND);
 #pragma unroll
-    for (int rb = 0; rb < SUB / 32; ++rb) {
-        if (32 * rb >= rn) break;                                    // uniform over the workgroup
-        pf_stage_rows(acc, Cs, rb);
+    for (int rb0 = 0; rb0 < SUB / 32; rb0 += RBS) {
+        if (32 * rb0 >= rn) break;                                   // uniform over the workgroup
+#pragma unroll
+        for (int q = 0; q < RBS; ++q)
+            if (rb0 + q < SUB / 32 && 32 * (rb0 + q) < rn) pf_stage_rows(acc, Cs + q * 32 * PF_CLD, rb0 + q);
         __syncthreads();
 #pragma unroll
-        for (int pass = 0; pass < 2; ++pass) {
+        for (int qp = 0; qp < 2 * RBS; ++qp) {
+            const int q = qp >> 1, pass = qp & 1, rb = rb0 + q;
+            if (rb >= SUB / 32 || 32 * rb >= rn) continue;             // uniform
             const int rl = wv * 8 + pass * 4 + rsub;
             const int trow = 32 * rb + rl;
-            const float* cr = Cs + rl * PF_CLD + 8 * c;
+            const float* cr = Cs + (q * 32 + rl) * PF_CLD + 8 * c;
             float g[8], u[8], b[8];
 #pragma unroll
             for (int i = 0; i < 8; i += 4) {
