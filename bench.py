@@ -127,6 +127,20 @@ def _repeat(fn, min_seconds=10.0):
             return el / reps, reps
 
 
+def cpu_threads() -> int:
+    """Threads for the CPU baselines: every host core this process may run on, capped by OMP_NUM_THREADS where the
+    environment sets it (a shared host gives each GPU's jobs a share of its cores and says so there)."""
+    avail = len(os.sched_getaffinity(0))
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(avail, omp) if omp > 0 else avail)
+
+
+def host_cores() -> dict:
+    """The host's core count (os.cpu_count), the cores this process may run on, and OMP_NUM_THREADS."""
+    return {"host_cores": os.cpu_count(), "cores_available": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
 def _sample_pairs(ids, wts, n_tok):
     """The first n_tok tokens' routing as (used experts, local ids [n_tok, topk], weights) with the experts renumbered
     0..len(used)-1 in id order."""
@@ -152,7 +166,7 @@ def cpu_baseline_prefill(torch, layer, x, ids, wts, threads, n_tok=512):
     x16 = x[:n_tok].to(torch.float16).cpu().numpy()
     moe.lib()
     sec, reps = _repeat(lambda: moe.forward(lay, x16, tok, ex, w16, LIMIT, "e3", threads=threads))
-    return {"value": round(n_tok / sec, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(n_tok / sec, 2), "unit": "tokens/s", "cores": threads, **host_cores(), "kind": "port",
             "seconds_per_call": round(sec, 3),
             "sample": f"{reps} repetitions of the first {n_tok} tokens of the T=8192 prefill call ({len(used)} "
                       "distinct experts, each decoded once per repetition) through the oracle's C port "
@@ -171,11 +185,22 @@ def cpu_baseline_fp8(torch, layer, x, ids, wts, threads, n_tok=256):
     tok, ex, pw = e4m3.pairs_fp32(local, w, len(used))
     xs = x[:n_tok].float().cpu().numpy()
     sec, reps = _repeat(lambda: e4m3.forward(lay, xs, tok, ex, pw, LIMIT, "kernel", threads=threads))
-    return {"value": round(n_tok / sec, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(n_tok / sec, 2), "unit": "tokens/s", "cores": threads, **host_cores(), "kind": "port",
             "seconds_per_call": round(sec, 3),
             "sample": f"{reps} repetitions of the first {n_tok} tokens of the T=2048 e4m3 call ({len(used)} distinct "
                       "experts) through the oracle's C port (oracle/csrc/fp8.c: dequantise-then-fp32 GEMM per "
                       f"128-block, OpenMP {threads} threads)"}
+
+
+def _bracket(torch, fn):
+    """(start, end) events around fn()'s launches on the current stream; a spin kernel ahead keeps the stream busy
+    while the host enqueues them, so the start event is stamped right before the first bracketed kernel runs."""
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(HOLD_CYCLES)
+    a.record()
+    fn()
+    b.record()
+    return a, b
 
 
 def run_decode(args, torch, mi355moe, dev):
@@ -264,26 +289,27 @@ def run_decode(args, torch, mi355moe, dev):
     us_per_step = ms * 1000.0 / args.steps
     gbs = total_bytes / (ms / 1000.0) / 1e9
 
-    # dominant kernel alone (grouped gate/up GEMV): route staged untimed, then event-bracketed gate/up launches
-    gu_us, gu_bytes = [], []
+    # the GEMVs alone: route staged untimed, then the gate/up launch and the down launch each event-bracketed
+    gu_t, dn_t, gu_bytes, dn_bytes = [], [], [], []
     for k in range(args.steps):
         c = combos[k % len(combos)]
         d, ids, wts = info[c]
         lay, x = layers[c[0]], xs[c[1]]
-        ops.moe_forward_ids(lay, x, ids, wts, limit=LIMIT, out=bufs[c]["out"], stages=_lib.STAGE_ROUTE)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(HOLD_CYCLES)     # the stream is busy while the host enqueues the bracketed launch
-        a.record()
-        ops.moe_forward_ids(lay, x, ids, wts, limit=LIMIT, out=bufs[c]["out"], stages=_lib.STAGE_GATEUP)
-        b.record()
-        ops.moe_forward_ids(lay, x, ids, wts, limit=LIMIT, out=bufs[c]["out"],
-                            stages=_lib.STAGE_DOWN | _lib.STAGE_COMBINE)
-        gu_us.append((a, b))
-        gu_bytes.append(d * (2 * K * N // 2 + 2 * (2 * K + 3 * N)) + T * TOPK * 0 + T * K * 2)
+        call = lambda st: ops.moe_forward_ids(lay, x, ids, wts, limit=LIMIT, out=bufs[c]["out"], stages=st)
+        call(_lib.STAGE_ROUTE)
+        gu_t.append(_bracket(torch, lambda: call(_lib.STAGE_GATEUP)))
+        dn_t.append(_bracket(torch, lambda: call(_lib.STAGE_DOWN)))
+        call(_lib.STAGE_COMBINE)
+        P = T * TOPK
+        # weights + scales of the d experts, the inputs read, the outputs written
+        gu_bytes.append(d * (2 * K * N // 2 + 2 * (2 * K + 3 * N)) + T * K * 2 + P * N * 2)
+        dn_bytes.append(d * (N * K // 2 + 2 * K) + P * N * 2 + P * K * 4)
     torch.cuda.synchronize()
-    gu_t = [a.elapsed_time(b) * 1000.0 for a, b in gu_us]
-    gu_avg_us = sum(gu_t) / len(gu_t)
+    gu_t = [a.elapsed_time(b) * 1000.0 for a, b in gu_t]
+    dn_t = [a.elapsed_time(b) * 1000.0 for a, b in dn_t]
+    gu_avg_us, dn_avg_us = sum(gu_t) / len(gu_t), sum(dn_t) / len(dn_t)
     gu_gbs = (sum(gu_bytes) / len(gu_bytes)) / (gu_avg_us * 1e-6) / 1e9
+    dn_gbs = (sum(dn_bytes) / len(dn_bytes)) / (dn_avg_us * 1e-6) / 1e9
 
     res = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -299,15 +325,19 @@ def run_decode(args, torch, mi355moe, dev):
         "roofline": {"bound": "hbm", "kernel": "dec_gateup_kernel", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": _traffic(dsum / args.steps), "avg_launch_us": round(gu_avg_us, 2)},
+        "roofline_down": {"bound": "hbm", "kernel": "dec_down_kernel", "achieved": round(dn_gbs, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(dn_gbs / HBM_PEAK_GBS, 4),
+                          "avg_launch_us": round(dn_avg_us, 2)},
         "wall_s": round(wall, 3),
         "settle_ms": SETTLE_MS,
     }
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         c = combos[0]
         sec, reps, d = cpu_baseline(torch, layers[c[0]], xs[c[1]], info[c][1], info[c][2], threads)
         res["cpu_block_a"] = cpu_block_a(torch, threads)
         res["cpu_baseline"] = {"value": round(step_bytes(c) / sec / 1e9, 4), "unit": "GB/s", "cores": threads,
+                               **host_cores(),
                                "kind": "port", "seconds_per_call": round(sec, 4),
                                "sample": f"{reps} repetitions of one full T={T} layer call ({d} distinct experts) "
                                          "through the oracle's C port (oracle/csrc/oracle.c, decode rounding "
@@ -367,28 +397,29 @@ def run_prefill(args, torch, dev):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    # the gate/up grouped GEMM alone (route + gather staged before the bracketed launch)
-    gu = []
+    # the stages alone: route staged untimed, then gather + gate/up, down and combine each event-bracketed
+    gu, dn, cb = [], [], []
     for k in range(steps):
         l = k % n_layers
         ids, wts = info[l]
-        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], stages=_lib.STAGE_ROUTE)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(HOLD_CYCLES)     # the stream is busy while the host enqueues the bracketed launch
-        a.record()
-        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], stages=_lib.STAGE_GATEUP)
-        b.record()
-        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l],
-                            stages=_lib.STAGE_DOWN | _lib.STAGE_COMBINE)
-        gu.append((a, b))
+        call = lambda st: ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], stages=st)
+        call(_lib.STAGE_ROUTE)
+        gu.append(_bracket(torch, lambda: call(_lib.STAGE_GATEUP)))
+        dn.append(_bracket(torch, lambda: call(_lib.STAGE_DOWN)))
+        cb.append(_bracket(torch, lambda: call(_lib.STAGE_COMBINE)))
     torch.cuda.synchronize()
     gu_ms = sum(a.elapsed_time(b) for a, b in gu) / len(gu)
+    dn_ms = sum(a.elapsed_time(b) for a, b in dn) / len(dn)
+    cb_ms = sum(a.elapsed_time(b) for a, b in cb) / len(cb)
 
     if args.workload == "prefill-uniform":                # the profiling window: these calls only
         P = sum(pairs) / len(pairs)
         return {"prefill_ms_per_layer": round(ms, 4), "prefill_gateup_ms": round(gu_ms, 4),
                 "prefill_gateup_frac": round(2.0 * P * K * 2 * N / (gu_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS,
-                                             4)}
+                                             4),
+                "prefill_down_ms": round(dn_ms, 4),
+                "prefill_down_frac": round(2.0 * P * N * K / (dn_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+                "prefill_combine_ms": round(cb_ms, 4)}
 
     def step_fold(l):
         # bf16 down accumulators, routed sum added into out (which stands for the shared experts' bf16 output)
@@ -406,10 +437,13 @@ def run_prefill(args, torch, dev):
     P = sum(pairs) / len(pairs)
     flops = 2.0 * P * (K * 2 * N + N * K)
     gu_flops = 2.0 * P * K * 2 * N
+    dn_flops = 2.0 * P * N * K
+    cb_bytes = int(P * K * 4 + T * K * 2)            # fp32 raw accumulators of every pair read, bf16 out written
+    pe = run_prefill_per_expert_suh(args, torch, dev, x, logits, steps)
     extra = {}
     if not args.no_cpu_baseline:
         extra["cpu_baseline_prefill"] = cpu_baseline_prefill(torch, layers[0], x, info[0][0], info[0][1],
-                                                             min(16, os.cpu_count() or 1))
+                                                             cpu_threads())
     return {**extra, "prefill_tokens_per_s": round(T / (ms / 1000.0), 1), "prefill_ms_per_layer": round(ms, 4),
             "prefill_bf16acc_fold_ms_per_layer": round(ms_fold, 4),
             "prefill_layer_with_router_ms": round(ms_layer, 4),
@@ -419,9 +453,52 @@ def run_prefill(args, torch, dev):
                                  "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                  "frac": round(gu_flops / (gu_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
                                  "avg_launch_us": round(gu_ms * 1000.0, 1)},
+            "roofline_prefill_down": {"bound": "mfma", "kernel": "pf_down_kernel",
+                                      "achieved": round(dn_flops / (dn_ms / 1000.0) / 1e12, 2),
+                                      "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                      "frac": round(dn_flops / (dn_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
+                                      "avg_launch_us": round(dn_ms * 1000.0, 1)},
+            "prefill_combine": {"kernel": "pf_combine_kernel", "avg_launch_us": round(cb_ms * 1000.0, 1),
+                                "gbs": round(cb_bytes / (cb_ms / 1000.0) / 1e9, 1),
+                                "bytes": cb_bytes},
+            **pe,
             "prefill_config": f"T={T}, {E} experts, top-{TOPK}, uniform-random router logits, EXL3 4-bit synthetic "
                               f"experts sharing one w13 suh as the real checkpoints' layers do (one gathered row "
                               f"per token), {n_layers} layers alternated, {steps} timed steps"}
+
+
+def run_prefill_per_expert_suh(args, torch, dev, x, logits, steps):
+    """The T=8192 prefill call on layers whose experts each draw their own w13 input signs (suh): every pair gets its
+    own rotated gate/up input row (T x top-8 rows instead of T)."""
+    from mi355moe import _lib, ops, synthetic
+    n_layers = len(logits)
+    layers = [synthetic.exl3_layer(E, K, N, seed=600 + l, device=dev, uniform_suh=False) for l in range(n_layers)]
+    outs = [torch.empty(x.shape[0], K, dtype=torch.bfloat16, device=dev) for _ in range(n_layers)]
+    info = [ops.router_topk(logits[l], TOPK, None, routed_scale=SCALE) for l in range(n_layers)]
+
+    def step(l):
+        ids, wts = ops.router_topk(logits[l], TOPK, None, routed_scale=SCALE)
+        ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l])
+
+    ms = _time_calls(torch, step, n_layers, 2, steps)
+    gu = []
+    for k in range(steps):
+        l = k % n_layers
+        ids, wts = info[l]
+        call = lambda st: ops.moe_forward_ids(layers[l], x, ids, wts, limit=LIMIT, out=outs[l], stages=st)
+        call(_lib.STAGE_ROUTE)
+        gu.append(_bracket(torch, lambda: call(_lib.STAGE_GATEUP)))
+        call(_lib.STAGE_DOWN | _lib.STAGE_COMBINE)
+    torch.cuda.synchronize()
+    gu_ms = sum(a.elapsed_time(b) for a, b in gu) / len(gu)
+    del layers
+    torch.cuda.empty_cache()
+    return {"prefill_per_expert_suh_ms_per_layer": round(ms, 4),
+            "prefill_per_expert_suh_tokens_per_s": round(x.shape[0] / (ms / 1000.0), 1),
+            "prefill_per_expert_suh_gateup_ms": round(gu_ms, 4),
+            "prefill_per_expert_suh_config": "the same call on layers whose 288 experts each have their own w13 suh "
+                                             "(one rotated gate/up input row per pair; gather and gate/up bracketed "
+                                             "together)"}
 
 
 def run_prefill_zipf(args, torch, dev, caps=(0, 16, 32, 64, 128)):
@@ -544,7 +621,7 @@ def run_fp8(args, torch, dev):
     extra = {}
     if not args.no_cpu_baseline:
         extra["cpu_baseline_fp8"] = cpu_baseline_fp8(torch, layers[0], x, info[0][0], info[0][1],
-                                                     min(16, os.cpu_count() or 1))
+                                                     cpu_threads())
     return {**extra, "fp8_tokens_per_s": round(T / (ms / 1000.0), 1), "fp8_ms_per_layer": round(ms, 4),
             "fp8_gbs": round(layer_bytes / (ms / 1000.0) / 1e9, 1),
             "fp8_tflops": round(2.0 * P * 3 * K * N / (ms / 1000.0) / 1e12, 2),

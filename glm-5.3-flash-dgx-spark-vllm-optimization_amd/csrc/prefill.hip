@@ -882,7 +882,17 @@ __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int pa
         }
         return;
     }
-    float* o = a.contrib + c0;
+    // fp32: lane n holds columns c and c + 8, its partner n ^ 1 columns c + 1 and c + 9 (n even). The pair trades one
+    // value (DPP lane ^ 1) so that the even lane stores (c, c + 1) and the odd lane (c + 8, c + 9), 8 bytes each.
+    const bool odd = n & 1;
+    float* o = a.contrib + c0 + (odd ? 7 : 0);
+    auto pair = [&](int rb, int r) {
+        const float v0 = acc[rb][0][r], v1 = acc[rb][1][r];          // (values first: a select of addresses
+        const float send = odd ? v0 : v1;                             //  would send the array to scratch)
+        const float recv = __builtin_bit_cast(
+            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, true));
+        return make_float2(odd ? recv : v0, odd ? v1 : recv);
+    };
 #pragma unroll
     for (int rb = 0; rb < SUB / 32; ++rb) {
         if (32 * rb >= rn) break;
@@ -890,17 +900,14 @@ __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int pa
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                o[(size_t)trow * K] = acc[rb][0][r];
-                o[(size_t)trow * K + 8] = acc[rb][1][r];
+                *reinterpret_cast<float2*>(o + (size_t)trow * K) = pair(rb, r);
             }
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int trow = 32 * rb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (trow < rn) {
-                    o[(size_t)trow * K] = acc[rb][0][r];
-                    o[(size_t)trow * K + 8] = acc[rb][1][r];
-                }
+                const float2 v = pair(rb, r);                          // (the DPP runs with every lane active)
+                if (trow < rn) *reinterpret_cast<float2*>(o + (size_t)trow * K) = v;
             }
         }
     }
