@@ -31,6 +31,30 @@ __device__ __forceinline__ double xor_lane_f64(double v, int lane) {
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
+// Sums over the 64 lanes of V values per lane (V a power of two <= 64), by halving exchanges: at distance M a lane
+// keeps half of its W live values (the upper half where lane & M), adds its partner's copy of that half and sends the
+// other; after log2(V) such steps (M = 32, 16, ...) each lane holds one value v = lane / (64 / V) in acc[0], and
+// butterflies over the remaining distances finish its sum in every lane of its group (V - 1 exchanges in all instead
+// of 6 V).
+template <int V, int W = V, int M = 32>
+__device__ __forceinline__ void wave_sum_scatter(double (&acc)[V], int lane) {
+    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0 && W >= 1 && W <= V, "a power of two <= 64");
+    if constexpr (M >= 1) {
+        if constexpr (W >= 2) {
+            const bool up = (lane & M) != 0;
+#pragma unroll
+            for (int i = 0; i < W / 2; ++i) {
+                const double lo = acc[i], hi = acc[W / 2 + i];
+                acc[i] = (up ? hi : lo) + xor_lane_f64<M>(up ? lo : hi, lane);
+            }
+            wave_sum_scatter<V, W / 2, M / 2>(acc, lane);
+        } else {
+            acc[0] = acc[0] + xor_lane_f64<M>(acc[0], lane);
+            wave_sum_scatter<V, 1, M / 2>(acc, lane);
+        }
+    }
+}
+
 // The router logit as production returns it: F.linear in bf16 rounds the dot product to bf16, .to(float32) widens
 // it back (code/fork/docs/BF16_GEMV.md:27,38; the reference's router oracle is (X.double() @ W.t()).to(bfloat16),
 // code/fork/tests/router_topk_agreement.py:82, and torch narrows a double to bf16 through fp32). `dot` is the
@@ -78,6 +102,7 @@ __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int6
                     wd[q][2 * i + 1] = (double)__builtin_bit_cast(float, wv[i] & 0xFFFF0000u);
                 }
             }
+            double acc[NE * RL_TCHUNK];                               // value v = q RL_TCHUNK + tt
 #pragma unroll
             for (int tt = 0; tt < RL_TCHUNK; ++tt) {
                 double xd[8];
@@ -88,19 +113,17 @@ __device__ __forceinline__ void logits_body(const uint16_t* __restrict__ x, int6
                 }
 #pragma unroll
                 for (int q = 0; q < NE; ++q) {
-                    double acc = 0.0;
+                    double a = 0.0;
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) acc = __builtin_fma(xd[i], wd[q][i], acc);
-                    // butterfly m = 32, 16, ..., 1, partners by permlane / DPP
-                    acc = acc + xor_lane_f64<32>(acc, lane);
-                    acc = acc + xor_lane_f64<16>(acc, lane);
-                    acc = acc + xor_lane_f64<8>(acc, lane);
-                    acc = acc + xor_lane_f64<4>(acc, lane);
-                    acc = acc + xor_lane_f64<2>(acc, lane);
-                    acc = acc + xor_lane_f64<1>(acc, lane);
-                    if (lane == 0) part[c][q * RL_TCHUNK + tt] = acc;
+                    for (int i = 0; i < 8; ++i) a = __builtin_fma(xd[i], wd[q][i], a);
+                    acc[q * RL_TCHUNK + tt] = a;
                 }
             }
+            // sums over the 64 lanes: value v ends in lane 4 v (for 16 values; see wave_sum_scatter)
+            constexpr int V = NE * RL_TCHUNK;
+            wave_sum_scatter<V>(acc, lane);
+            constexpr int SPREAD = 64 / V;
+            if ((lane & (SPREAD - 1)) == 0) part[c][lane / SPREAD] = acc[0];
         }
         __syncthreads();
         const int q = (int)threadIdx.x / RL_TCHUNK, tt = (int)threadIdx.x % RL_TCHUNK;
@@ -437,10 +460,11 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 }
 
 // One wave's top-k of one token (E <= 1024 candidates, lane l holding candidates l + 64 j). Every load of the row (and
-// of the bias) is issued before the first is used, so the row costs one memory latency. Then topk rounds: each lane's
-// best remaining key (the lower j among equal keys, hence the lower id), the wave maximum, and the winner among the
-// lanes holding it -- the only one, or with equal keys in several lanes the lowest id, by a wave minimum. The winner's
-// owner drops it, so picks come largest first, lower id on ties (the reference's order). Scores s = sigmoid(logit)
+// of the bias) is issued before the first is used, so the row costs one memory latency. Each lane sorts its keys once
+// (descending, the lower j first among equal keys, hence the lower id). Then topk rounds: the wave maximum of the
+// lanes' best keys and the winner among the lanes holding it -- the only one, or with equal keys in several lanes
+// the lowest id, by a wave minimum. The winner's lane drops it, so picks come largest first, lower id on ties (the
+// reference's order). Scores s = sigmoid(logit)
 // (through double exp) go to sco [E] for the weights; weights are the picks' scores renormalised over their total
 // (summed sequentially in pick order, + 1e-20, correctly rounded division) and scaled.
 // J >= ceil(E / 64); COH: coherent loads of the row; SCORE: the row holds the scores sigmoid(logit) already
@@ -457,10 +481,12 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E,
         bv[j] = bias ? bias[e] : 0.f;
     }
     uint32_t key[J];
+    int jo[J];                                                        // key i's candidate index j
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int e = lane + 64 * j;
         key[j] = 0u;
+        jo[j] = j;
         if (e < E) {
             const float sv = SCORE ? lv[j] : (float)(1.0 / (1.0 + exp(-(double)lv[j])));
             sco[e] = sv;
@@ -468,28 +494,66 @@ __device__ __forceinline__ void topk_wave(const float* __restrict__ lrow, int E,
         }
     }
     int mine_e = 0;                                                   // lane k: the k-th pick
-    for (int k = 0; k < topk; ++k) {
-        uint32_t bk = 0u;
-        int bj = 0;
+    if constexpr (J <= 8) {
+        // each lane's keys in descending order, equal keys in ascending j (odd-even transposition: J rounds of
+        // adjacent swaps of strictly smaller keys, which keeps equal keys in their order); its best is key[0]
 #pragma unroll
-        for (int j = 0; j < J; ++j)
-            if (key[j] > bk) {
-                bk = key[j];
-                bj = j;
+        for (int r = 0; r < J; ++r)
+#pragma unroll
+            for (int j = r & 1; j + 1 < J; j += 2)
+                if (key[j + 1] > key[j]) {
+                    const uint32_t tk = key[j];
+                    key[j] = key[j + 1];
+                    key[j + 1] = tk;
+                    const int tj = jo[j];
+                    jo[j] = jo[j + 1];
+                    jo[j + 1] = tj;
+                }
+        for (int k = 0; k < topk; ++k) {
+            const uint32_t m = wave_max_u32(key[0]);
+            const uint64_t hit = __ballot(key[0] == m);
+            int e;
+            if (__popcll(hit) == 1) {                                 // uniform: one lane holds the maximum
+                const int wl = __ffsll((long long)hit) - 1;
+                e = 64 * __builtin_amdgcn_readlane(jo[0], wl) + wl;
+            } else {                                                  // equal keys: the lowest id
+                e = (int)wave_min_u32(key[0] == m ? (uint32_t)(64 * jo[0] + lane) : 0xFFFFFFFFu);
             }
-        const uint32_t m = wave_max_u32(bk);
-        const uint64_t hit = __ballot(bk == m);
-        int e;
-        if (__popcll(hit) == 1) {                                     // uniform: one lane holds the maximum
-            const int wl = __ffsll((long long)hit) - 1;
-            e = 64 * __builtin_amdgcn_readlane(bj, wl) + wl;
-        } else {                                                      // equal keys: the lowest id
-            e = (int)wave_min_u32(bk == m ? (uint32_t)(64 * bj + lane) : 0xFFFFFFFFu);
-        }
+            if (lane == (e & 63)) {                                   // the winner's lane drops its best key
 #pragma unroll
-        for (int j = 0; j < J; ++j)
-            if (j == (e >> 6) && lane == (e & 63)) key[j] = 0u;
-        if (lane == k) mine_e = e;
+                for (int j = 0; j + 1 < J; ++j) {
+                    key[j] = key[j + 1];
+                    jo[j] = jo[j + 1];
+                }
+                key[J - 1] = 0u;
+            }
+            if (lane == k) mine_e = e;
+        }
+    } else {
+        // many keys per lane: each round scans the lane's keys for its best (the lower j among equal keys)
+        for (int k = 0; k < topk; ++k) {
+            uint32_t bk = 0u;
+            int bj = 0;
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (key[j] > bk) {
+                    bk = key[j];
+                    bj = j;
+                }
+            const uint32_t m = wave_max_u32(bk);
+            const uint64_t hit = __ballot(bk == m);
+            int e;
+            if (__popcll(hit) == 1) {
+                const int wl = __ffsll((long long)hit) - 1;
+                e = 64 * __builtin_amdgcn_readlane(bj, wl) + wl;
+            } else {
+                e = (int)wave_min_u32(bk == m ? (uint32_t)(64 * bj + lane) : 0xFFFFFFFFu);
+            }
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (j == (e >> 6) && lane == (e & 63)) key[j] = 0u;
+            if (lane == k) mine_e = e;
+        }
     }
     // scores of the picks (written by their owners before the rounds), summed in pick order
     const float mine = lane < topk ? sco[mine_e] : 0.f;
