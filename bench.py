@@ -842,6 +842,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=8)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--window-only", action="store_true",
+                    help="run only the named workload, without the decode lead-in (a profiling window: the JSON line "
+                         "then carries that workload's fields only)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the workload, copy a tensor of this many MiB three times (counter calibration)")
     args = ap.parse_args()
@@ -856,7 +859,10 @@ def main():
     import mi355moe
     mi355moe._lib.lib()
     dev = torch.device("cuda", 0)
-    if args.workload in ("prefill", "prefill-uniform", "zipf", "fp8", "e4m3t", "stack"):
+    if args.window_only and args.workload not in ("all", "decode"):
+        args.no_cpu_baseline = True
+        res = {"metric": METRIC, "workload": args.workload, "window_only": True}
+    elif args.workload in ("prefill", "prefill-uniform", "zipf", "fp8", "e4m3t", "stack"):
         args.no_cpu_baseline = True
         res = run_decode(argparse.Namespace(**{**vars(args), "steps": 8, "warmup": 2}), torch, mi355moe, dev)
     else:

@@ -208,6 +208,20 @@ void orc_rot_in(const uint16_t* x16, const uint16_t* suh16, int n, uint16_t* out
 /* sigmoid as the HIP kernels define it: 1 / (1 + (float)exp(-(double)g)), IEEE fp32 division */
 static inline float sigm(float g) { return 1.0f / (1.0f + (float)exp(-(double)g)); }
 
+/* sigm over the n floats whose bit patterns are first, first + 1, ... (g_out may be NULL); OpenMP threads (0: the
+ * runtime's default) */
+void orc_sigmoid_bits(uint32_t first, int64_t n, float* g_out, float* s_out, int threads) {
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const uint32_t b = first + (uint32_t)i;
+        float g;
+        memcpy(&g, &b, sizeof g);
+        if (g_out) g_out[i] = g;
+        s_out[i] = sigm(g);
+    }
+}
+
 /* ---------------------------------------------------------------- the reference's default (TF_PARITY=1) epilogues
  * code/fork/kernels/exl3.cu:31-32 (TF_PARITY defaults to 1), :351-357 (fp16 SiLU), :371-436 (gate/up epilogue),
  * :455-496 (down epilogue). fp16 arithmetic is IEEE binary16 with one rounding per operation: a product or a sum of

@@ -70,6 +70,7 @@ def lib() -> ctypes.CDLL:
         L.orc_down_epilogue.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint16, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_void_p]
         L.orc_expf_via_double.argtypes = [ctypes.c_float]
+        L.orc_sigmoid_bits.argtypes = [ctypes.c_uint32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
         L.orc_moe_forward.restype = ctypes.c_int
         L.orc_moe_forward.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float,
@@ -182,6 +183,18 @@ def down_epilogue(zd: np.ndarray, svh_d: np.ndarray, w16, mode: str) -> np.ndarr
     w = int(np.asarray(w16, np.float16).view(np.uint16))
     lib().orc_down_epilogue(_p(zd), _p(sv), w, K, int(mode == "e3"), _p(out))
     return out
+
+
+def sigmoid_bits(first: int, n: int, threads: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """(g, sigmoid(g)) float32 for the n floats whose bit patterns are first, first + 1, ...: the epilogues' sigmoid
+    1 / (1 + (float)exp(-(double)g)) with IEEE float32 add and division, exp from the host's libm
+    (exl3_fat_moe.cu:366-369)."""
+    if n < 0 or first < 0 or first + n > 1 << 32:
+        raise ValueError("sigmoid_bits: a range of 32-bit patterns")
+    g = np.empty(n, np.float32)
+    s = np.empty(n, np.float32)
+    lib().orc_sigmoid_bits(int(first), int(n), _p(g), _p(s), int(threads))
+    return g, s
 
 
 def pairs_from_routing(local: np.ndarray, weights: np.ndarray, n: int, topk: int):

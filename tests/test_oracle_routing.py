@@ -105,6 +105,18 @@ def test_sigmoid_is_correctly_rounded_on_samples():
         assert abs(float(si) - exact) <= abs(float(np.spacing(si))) / 2 + 1e-300
 
 
+def test_sigmoid_bits_is_the_e3_formula():
+    """The oracle's C sigmoid over a range of bit patterns (the GPU test's reference) equals numpy's statement of
+    1 / (1 + (float)exp(-(double)g)) in float32, and its g are the patterns' floats."""
+    from oracle import moe
+    for first in (0x3F000000, 0xC1000000, 0x42AE0000 - (1 << 18)):
+        g, s = moe.sigmoid_bits(first, 1 << 18)
+        assert np.array_equal(g.view(np.uint32), np.arange(first, first + (1 << 18), dtype=np.uint32))
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)
+        ref = (np.float32(1.0) / (np.float32(1.0) + e)).astype(np.float32)
+        assert np.array_equal(s.view(np.uint32), ref.view(np.uint32))
+
+
 def _brute_topk(logits, bias, topk, scale):
     s = routing.sigmoid_f32(logits)
     ids, ws = [], []
