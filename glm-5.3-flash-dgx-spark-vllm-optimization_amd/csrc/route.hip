@@ -612,8 +612,9 @@ __device__ __forceinline__ void topk_route_body(const float* __restrict__ logits
     else route_small_body<int32_t>(b, sh);
 }
 
-template <int J>
-__global__ __launch_bounds__(1024) void topk_route_kernel(const float* __restrict__ logits, int T, int E,
+// MAXT: the launch's threads (512 for J = 16, so that the sixteen keys per lane and their loads fit the registers)
+template <int J, int MAXT = 1024>
+__global__ __launch_bounds__(MAXT) void topk_route_kernel(const float* __restrict__ logits, int T, int E,
                                                           const float* __restrict__ bias, int topk, float scale,
                                                           int renorm, int32_t* __restrict__ ids,
                                                           float* __restrict__ wts, RouteArgs a) {
@@ -627,8 +628,8 @@ constexpr int RR_EXPERTS = 2;   // router experts per workgroup of the one-launc
 // workgroup that finishes last (an arrival counter at a fixed workspace offset, returned to zero by that
 // workgroup) runs topk_route_body over all logits. Logits cross workgroups, and XCDs with their own L2, as device-coherent stores and loads; a workgroup
 // arrives only after its stores have completed.
-template <int J>
-__global__ __launch_bounds__(1024) void router_route_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+template <int J, int MAXT = 1024>
+__global__ __launch_bounds__(MAXT) void router_route_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
                                                             const uint16_t* __restrict__ w, int T, int K, int E,
                                                             float* __restrict__ logits, const float* __restrict__ bias,
                                                             int topk, float scale, int renorm,
@@ -998,7 +999,7 @@ int launch_topk_route(const float* logits, int T, int E, const float* bias, int 
     const size_t shm = (size_t)(3 * a.P + 2 * (a.n + 1)) * sizeof(int) + (size_t)16 * E * sizeof(float);
     static bool attr = false;                                         // up to 45 KB + 64 KB for E = 1024
     if (!attr) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(topk_route_kernel<16>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(topk_route_kernel<16, 512>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024) != hipSuccess)
             return -1;
         attr = true;
@@ -1007,7 +1008,7 @@ int launch_topk_route(const float* logits, int T, int E, const float* bias, int 
         hipLaunchKernelGGL(topk_route_kernel<5>, dim3(1), dim3(1024), shm, st, logits, T, E, bias, topk, scale, renorm,
                            ids, wts, a);
     else
-        hipLaunchKernelGGL(topk_route_kernel<16>, dim3(1), dim3(1024), shm, st, logits, T, E, bias, topk, scale,
+        hipLaunchKernelGGL((topk_route_kernel<16, 512>), dim3(1), dim3(512), shm, st, logits, T, E, bias, topk, scale,
                            renorm, ids, wts, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -1021,6 +1022,8 @@ int launch_router_route(const uint16_t* x, int64_t x_stride, const uint16_t* w, 
     static bool attr = false;
     if (!attr) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(router_route_kernel<16>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024) != hipSuccess ||
+            hipFuncSetAttribute(reinterpret_cast<const void*>(router_route_kernel<16, 512>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024) != hipSuccess)
             return -1;
         attr = true;
@@ -1029,6 +1032,9 @@ int launch_router_route(const uint16_t* x, int64_t x_stride, const uint16_t* w, 
     if (E <= 320)
         hipLaunchKernelGGL(router_route_kernel<5>, grid, dim3(64 * nw), shm, st, x, x_stride, w, T, K, E, logits,
                            bias, topk, scale, renorm, ids, wts, a, arrivals);
+    else if (nw <= 8)                                                 // K <= 4096: at most 512 threads
+        hipLaunchKernelGGL((router_route_kernel<16, 512>), grid, dim3(64 * nw), shm, st, x, x_stride, w, T, K, E,
+                           logits, bias, topk, scale, renorm, ids, wts, a, arrivals);
     else
         hipLaunchKernelGGL(router_route_kernel<16>, grid, dim3(64 * nw), shm, st, x, x_stride, w, T, K, E, logits,
                            bias, topk, scale, renorm, ids, wts, a, arrivals);
