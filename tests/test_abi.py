@@ -136,3 +136,22 @@ def test_workspace_growth_keeps_old_buffer_and_refuses_under_capture(monkeypatch
         ops.workspace(dev, 4 << 20)
     ops._WS.pop(key, None)
     ops._RETIRED.pop(key, None)
+
+
+def test_reserve_covers_every_call_size(monkeypatch):
+    """reserve(experts, max_tokens) asks for at least what every call of 1 .. max_tokens tokens needs (the decode
+    plan's split-K partials make the need non-monotone in T), for the per-call and the whole-layer entries."""
+    import types
+    from mi355moe import ops
+    d = _fake_desc()
+    ex = types.SimpleNamespace(desc=d, K=4096, shared_suh=True, device="cpu")
+    asked = []
+    monkeypatch.setattr(ops, "workspace", lambda dev, n: asked.append(n))
+    for top in (1, 3, 8, 64):
+        for router in (None, 288):
+            asked.clear()
+            ops.reserve(ex, top, router_experts=router)
+            needs = [ops.workspace_bytes(ex, t, 8, router) for t in range(1, top + 1)]
+            assert asked == [max(needs)], (top, router)
+    sizes = [ops.workspace_bytes(ex, t) for t in range(1, 9)]
+    assert any(b > a for a, b in zip(sizes[1:], sizes)), sizes      # the need does fall somewhere: not monotone
