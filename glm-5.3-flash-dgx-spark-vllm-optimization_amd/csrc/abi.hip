@@ -28,8 +28,9 @@ int rc_launch(int r) {
 
 // Every workspace layout starts with a control block of words that keep their value between calls (zero), at the
 // same offset whatever the shapes of the calls sharing the workspace: data of one call never lands on them.
-// Word 0: the arrival counter of the one-launch decode front end.
-constexpr size_t WS_CONTROL_BYTES = 256;
+// Word 0 and words 64, 128, ..., 960: the arrival counters of the one-launch decode front end (its top-level count
+// and its fifteen group counts, 256 bytes apart so that they do not share a cache line).
+constexpr size_t WS_CONTROL_BYTES = 4096;
 
 // Bump allocator over the caller's workspace (or a dry run that only measures), past the control block.
 struct Carve {
@@ -1420,7 +1421,7 @@ void* g_noalloc_ptr[NOALLOC_MAX_DEVICES];          // per device: the address of
 
 // zeroes the control block (the arrival counter words calls expect at zero) of a device's scratch
 __global__ void zero_control_kernel(unsigned* words, int n) {
-    if ((int)threadIdx.x < n) words[threadIdx.x] = 0u;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) words[i] = 0u;
 }
 
 bool g_noalloc_zeroed[NOALLOC_MAX_DEVICES];        // per device: its control block was zeroed outside a capture

@@ -623,10 +623,11 @@ __global__ __launch_bounds__(MAXT) void topk_route_kernel(const float* __restric
 }
 
 constexpr int RR_EXPERTS = 2;   // router experts per workgroup of the one-launch front end (all in one round of CUs)
+constexpr unsigned RR_GROUPS = 15;   // arrival groups (control words 64 (g + 1), g < 15, within a 4 KB control block)
 // The whole decode-size front end in one launch: the router GEMV (RR_EXPERTS experts per workgroup, logits_body, which
 // also applies the sigmoid so the ranking workgroup only loads scores), then the
-// workgroup that finishes last (an arrival counter at a fixed workspace offset, returned to zero by that
-// workgroup) runs topk_route_body over all logits. Logits cross workgroups, and XCDs with their own L2, as device-coherent stores and loads; a workgroup
+// workgroup that finishes last (arrival counters at fixed workspace offsets, returned to zero by the arrivals that
+// complete them) runs topk_route_body over all logits. Logits cross workgroups, and XCDs with their own L2, as device-coherent stores and loads; a workgroup
 // arrives only after its stores have completed.
 template <int J, int MAXT = 1024>
 __global__ __launch_bounds__(MAXT) void router_route_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
@@ -640,10 +641,21 @@ __global__ __launch_bounds__(MAXT) void router_route_kernel(const uint16_t* __re
     logits_body<true, RR_EXPERTS, true>(x, x_stride, w, T, K, E, RR_EXPERTS * blockIdx.x, logits);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    // the last of the grid's arrivals ranks; counted modulo the grid so that a counter left non-zero (a workspace not
-    // zero-filled before its first use) still elects one workgroup per call and the tables are always rebuilt
-    if (threadIdx.x == 0)
-        last = (__hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) % gridDim.x == 0u;
+    // the last of the grid's arrivals ranks. Two levels, so that no counter word queues more than ~16 atomics (one
+    // word took ~8 ns per arrival): workgroup b counts on the word of its group b % G (words 64 (g + 1)), the group's
+    // last arrival on word 0. Each count is taken modulo its number of arrivals, so that a counter left non-zero (a
+    // workspace not zero-filled before its first use) still elects one workgroup per call and the tables are always
+    // rebuilt; the last arrival of each level returns its word to zero.
+    if (threadIdx.x == 0) {
+        const unsigned G = min(RR_GROUPS, gridDim.x), g = blockIdx.x % G, size = (gridDim.x - 1 - g) / G + 1;
+        unsigned* gw = arrivals + 64 * (g + 1);
+        int l = 0;
+        if ((__hip_atomic_fetch_add(gw, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) % size == 0u) {
+            __hip_atomic_store(gw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            l = (__hip_atomic_fetch_add(arrivals, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) % G == 0u;
+        }
+        last = l;
+    }
     __syncthreads();
     if (!last) return;
     acquire_agent();
