@@ -6,6 +6,10 @@ References:
              (TensorFold's restatement of vLLM grouped_topk with n_group = topk_group = 1,
              code/fork/tests/router_topk_agreement.py:58-61). Logits = bf16(x @ W^T) widened to fp32
              (code/fork/docs/BF16_GEMV.md:27,38; code/fork/tests/router_topk_agreement.py:82).
+             Router weights' last ulp: parity unpinned. sigmoid_f32 is the correctly rounded fp32 sigmoid (pinned
+             to that definition); the reference computes 1 / (1 + exp(-x)) in fp32 with the library exp (vLLM's
+             grouped_topk, not importable here; tf_glue.py:381), so its scores, and the renormalised weights built
+             from them, may differ from these in the last ulp. Ids and weights are pinned by the closed form only.
   local ids  map_topk_to_local, code/fork/docs/prod_exl3_reference.py:936-958.
   order      pairs j = t*topk + k grouped by local expert, the sentinel group (id n) last, and inside a group by
              pair index -- torch.argsort(local, stable=True) (code/fork/overlay/glm53_moe_e4m3.py:462;
