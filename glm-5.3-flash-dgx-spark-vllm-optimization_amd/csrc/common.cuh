@@ -131,6 +131,42 @@ __device__ __forceinline__ void fwht128_x16s(float (&v)[8], int lane) {
     MI355_FMAC_DPP8(v, c8, "row_ror:8");
 }
 
+// NV independent fwht128_x16s, stage by stage: every stage issues its NV x 8 independent operations before the next
+// stage reads them, so a single wave per SIMD does not wait on each stage's latency. Each vector's values are those
+// of fwht128_x16s, bit for bit (the same operations in the same order per value).
+template <int NV>
+__device__ __forceinline__ void fwht128_x16s_n(float (&v)[NV][8], int lane) {
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+        for (int n = 0; n < NV; ++n)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (!(i & h)) {
+                    const float a = v[n][i], b = v[n][i + h];
+                    v[n][i] = a + b;
+                    v[n][i + h] = a - b;
+                }
+    }
+    const float c1 = (lane & 1) ? -1.0f : 1.0f, c2 = (lane & 2) ? -1.0f : 1.0f, c4 = (lane & 4) ? -1.0f : 1.0f,
+                c8 = (lane & 8) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int n = 0; n < NV; ++n) MI355_FMAC_DPP8(v[n], c1, "quad_perm:[1,0,3,2]");
+#pragma unroll
+    for (int n = 0; n < NV; ++n) MI355_FMAC_DPP8(v[n], c2, "quad_perm:[2,3,0,1]");
+#pragma unroll
+    for (int n = 0; n < NV; ++n)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {                                 // lane ^ 4, as in fwht128_x16s
+            const int x = __builtin_bit_cast(int, v[n][i]);
+            const int lo = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0xF, true);
+            const float p = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(lo, x, 0x124, 0xF, 0xA, false));
+            v[n][i] = __builtin_fmaf(p, c4, v[n][i]);
+        }
+#pragma unroll
+    for (int n = 0; n < NV; ++n) MI355_FMAC_DPP8(v[n], c8, "row_ror:8");
+}
+
 // The value of lane l ^ M (M = 1, 2, 4, 8, 16, 32) without LDS: quad permutes (1, 2), two row rotations with bank
 // masks (4), a row rotation (8), v_permlane16_swap (16) and v_permlane32_swap (32).
 template <int M>

@@ -693,71 +693,87 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
             if (rb0 + q < SUB / 32 && 32 * (rb0 + q) < rn) pf_stage_rows(acc, Cs + q * 32 * PF_CLD, rb0 + q);
         __syncthreads();
 #pragma unroll
-        for (int qp = 0; qp < 2 * RBS; ++qp) {
-            const int q = qp >> 1, pass = qp & 1, rb = rb0 + q;
+        for (int q = 0; q < RBS; ++q) {
+            const int rb = rb0 + q;
             if (rb >= SUB / 32 || 32 * rb >= rn) continue;             // uniform
-            const int rl = wv * 8 + pass * 4 + rsub;
-            const int trow = 32 * rb + rl;
-            const float* cr = Cs + (q * 32 + rl) * PF_CLD + 8 * c;
-            float g[8], u[8], b[8];
+            // the block's two row passes at once (rows 4 p + rsub of each wave's 8, p = 0, 1): two rows per 16-lane
+            // group, so every Hadamard stage has four (then two) independent vectors of work
+            int trow[2];
+            float gu[4][8], b[2][8];                                  // gu: g of rows 0, 1, then u of rows 0, 1
 #pragma unroll
-            for (int i = 0; i < 8; i += 4) {
-                const float4 g4 = *reinterpret_cast<const float4*>(cr + i);
-                const float4 u4 = *reinterpret_cast<const float4*>(cr + 128 + i);
-                g[i] = g4.x, g[i + 1] = g4.y, g[i + 2] = g4.z, g[i + 3] = g4.w;
-                u[i] = u4.x, u[i + 1] = u4.y, u[i + 2] = u4.z, u[i + 3] = u4.w;
+            for (int p = 0; p < 2; ++p) {
+                const int rl = wv * 8 + p * 4 + rsub;
+                trow[p] = 32 * rb + rl;
+                const float* cr = Cs + (q * 32 + rl) * PF_CLD + 8 * c;
+#pragma unroll
+                for (int i = 0; i < 8; i += 4) {
+                    const float4 g4 = *reinterpret_cast<const float4*>(cr + i);
+                    const float4 u4 = *reinterpret_cast<const float4*>(cr + 128 + i);
+                    gu[p][i] = g4.x, gu[p][i + 1] = g4.y, gu[p][i + 2] = g4.z, gu[p][i + 3] = g4.w;
+                    gu[2 + p][i] = u4.x, gu[2 + p][i + 1] = u4.y, gu[2 + p][i + 2] = u4.z, gu[2 + p][i + 3] = u4.w;
+                }
+                if (E4M3) {                                          // dequantise: times the row's activation scale
+                    const int ar = row0 + min(trow[p], rn - 1);
+                    const float rs = a.asc[a.tok_rows ? a.tok[ar] : ar];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        gu[p][i] *= rs;
+                        gu[2 + p][i] *= rs;
+                    }
+                }
             }
-            if (E4M3) {                                              // dequantise: times the row's activation scale
-                const int ar = row0 + min(trow, rn - 1);
-                const float rs = a.asc[a.tok_rows ? a.tok[ar] : ar];
+            fwht128_x16s_n<4>(gu, lane);
+            _Float16 av[2][8];
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    g[i] *= rs;
-                    u[i] *= rs;
+                    float gv = gu[p][i] * hr * svg[i];
+                    float uv = gu[2 + p][i] * hr * svu[i];
+                    if (L != 0.0f) {
+                        gv = fminf(gv, L);
+                        uv = fminf(fmaxf(uv, -L), L);
+                    }
+                    av[p][i] = (_Float16)(sigmoid_fast(gv) * gv * uv);
+                    b[p][i] = E4M3 ? (float)av[p][i] * (float)sud[i] : (float)(_Float16)(av[p][i] * sud[i]);
                 }
-            }
-            fwht128_x16s(g, lane);
-            fwht128_x16s(u, lane);
-            _Float16 av[8];
+            if (E4M3 && a.a16out) {                                  // the fp16 SwiGLU output, plain column order
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float gv = g[i] * hr * svg[i];
-                float uv = u[i] * hr * svu[i];
-                if (L != 0.0f) {
-                    gv = fminf(gv, L);
-                    uv = fminf(fmaxf(uv, -L), L);
-                }
-                av[i] = (_Float16)(sigmoid_fast(gv) * gv * uv);
-                b[i] = E4M3 ? (float)av[i] * (float)sud[i] : (float)(_Float16)(av[i] * sud[i]);
+                for (int p = 0; p < 2; ++p)
+                    if (trow[p] < rn)
+                        *reinterpret_cast<h8*>(a.a16out + (size_t)(row0 + trow[p]) * N + col) =
+                            h8{av[p][0], av[p][1], av[p][2], av[p][3], av[p][4], av[p][5], av[p][6], av[p][7]};
             }
-            if (E4M3 && a.a16out && trow < rn)                       // the fp16 SwiGLU output, plain column order
-                *reinterpret_cast<h8*>(a.a16out + (size_t)(row0 + trow) * N + col) =
-                    h8{av[0], av[1], av[2], av[3], av[4], av[5], av[6], av[7]};
             if (E4M3 && !a.down16 && !a.vd) continue;                // (uniform) a16 was the only output
-            fwht128_x16s(b, lane);
-            if (E4M3 && !a.down16) {                                 // fp32 down input and its row maximum
-                float m = 0.0f;
+            fwht128_x16s_n<2>(b, lane);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    b[i] = b[i] * hr;
-                    m = fmaxf(m, fabsf(b[i]));
-                }
-                m = fmaxf(m, xor_lane<1>(m, lane));
-                m = fmaxf(m, xor_lane<2>(m, lane));
-                m = fmaxf(m, xor_lane<4>(m, lane));
-                m = fmaxf(m, xor_lane<8>(m, lane));
-                if (trow < rn) {
-                    float* vo = a.vd + (size_t)(row0 + trow) * N + col;
-                    *reinterpret_cast<float4*>(vo) = make_float4(b[0], b[1], b[2], b[3]);
-                    *reinterpret_cast<float4*>(vo + 4) = make_float4(b[4], b[5], b[6], b[7]);
-                    if (c == 0) atomicMax(a.amaxd + row0 + trow, __builtin_bit_cast(unsigned, m));
-                }
-            } else if (trow < rn) {
-                uint32_t wm[4];
+            for (int p = 0; p < 2; ++p) {
+                if (E4M3 && !a.down16) {                             // fp32 down input and its row maximum
+                    float m = 0.0f;
 #pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    wm[m] = __builtin_bit_cast(uint32_t, h2{(_Float16)(b[2 * m] * hr), (_Float16)(b[2 * m + 1] * hr)});
-                pf_store_group(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow) * N + grp0, wm, c);
+                    for (int i = 0; i < 8; ++i) {
+                        b[p][i] = b[p][i] * hr;
+                        m = fmaxf(m, fabsf(b[p][i]));
+                    }
+                    m = fmaxf(m, xor_lane<1>(m, lane));
+                    m = fmaxf(m, xor_lane<2>(m, lane));
+                    m = fmaxf(m, xor_lane<4>(m, lane));
+                    m = fmaxf(m, xor_lane<8>(m, lane));
+                    if (trow[p] < rn) {
+                        float* vo = a.vd + (size_t)(row0 + trow[p]) * N + col;
+                        *reinterpret_cast<float4*>(vo) = make_float4(b[p][0], b[p][1], b[p][2], b[p][3]);
+                        *reinterpret_cast<float4*>(vo + 4) = make_float4(b[p][4], b[p][5], b[p][6], b[p][7]);
+                        if (c == 0) atomicMax(a.amaxd + row0 + trow[p], __builtin_bit_cast(unsigned, m));
+                    }
+                } else {
+                    uint32_t wm[4];
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        wm[m] = __builtin_bit_cast(uint32_t,
+                                                   h2{(_Float16)(b[p][2 * m] * hr), (_Float16)(b[p][2 * m + 1] * hr)});
+                    if (trow[p] < rn)
+                        pf_store_group(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow[p]) * N + grp0, wm, c);
+                }
             }
         }
         __syncthreads();
