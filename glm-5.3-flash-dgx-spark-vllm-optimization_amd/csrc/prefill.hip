@@ -1011,6 +1011,49 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) sv[k][i] = *reinterpret_cast<const uint32_t*>(svp + 2 * i);
         }
+        bool any_thin = false;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) any_thin |= thin[k];
+        if (!any_thin) {                                             // (uniform) four slots' rotations at a time
+#pragma unroll
+            for (int k0h = 0; k0h < 8; k0h += 4) {
+                float v[4][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int k = k0h + j;
+                    if (a.contrib_bf16) {
+                        const u32x4 rb16 = __builtin_bit_cast(u32x4, raw[k][0]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            v[j][2 * i] = bf16_to_f32((uint16_t)(rb16[i] & 0xFFFFu));
+                            v[j][2 * i + 1] = bf16_to_f32((uint16_t)(rb16[i] >> 16));
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            v[j][i] = raw[k][0][i];
+                            v[j][4 + i] = raw[k][1][i];
+                        }
+                    }
+                    if (a.dsc) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) v[j][i] *= ds[k];
+                    }
+                }
+                fwht128_x16s_n<4>(v, lane);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {                        // slot order, as below
+                    const int k = k0h + j;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const uint32_t s2 = sv[k][i >> 1];
+                        const float svf = (float)u16_as_h((i & 1) ? s2 >> 16 : s2 & 0xFFFFu);
+                        if (ok[k]) sum[i] += v[j][i] * hr * svf * w[k];
+                    }
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             float v[8];
