@@ -77,6 +77,48 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const void* __restrict_
     }
 }
 
+// The same quantisation with one wave per row and the row held in registers (4 rows per 256-thread workgroup): one
+// read of the row, a wave maximum, K / 64 divisions per lane. G = K / 256 groups of four values per lane (lane l
+// takes k = 256 g + 4 l .. + 3, so every wave load and store is contiguous). Same values as quant_rows_kernel.
+template <int G>
+__global__ __launch_bounds__(256) void quant_rows_wave_kernel(const void* __restrict__ x, int xdt, int64_t stride,
+                                                              int rows, int K, uint8_t* __restrict__ q,
+                                                              float* __restrict__ s) {
+    const int r = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const size_t base = (size_t)r * stride;
+    float v[G][4];
+    float m = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const size_t i0 = base + 256 * g + 4 * lane;
+        if (xdt == DT_F32) {
+            const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + i0);
+            v[g][0] = f.x, v[g][1] = f.y, v[g][2] = f.z, v[g][3] = f.w;
+        } else {
+            const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(x) + i0);
+            const uint32_t hv[2] = {h.x, h.y};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint16_t b = (uint16_t)(hv[i >> 1] >> (16 * (i & 1)));
+                v[g][i] = xdt == DT_BF16 ? bf16_to_f32(b) : (float)u16_as_h(b);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(v[g][i]));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float sc = __fdiv_rn(m, E4M3_MAX);
+    sc = sc > 0.f ? sc : 1.f;
+    if (lane == 0) s[r] = sc;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        *reinterpret_cast<uint32_t*>(q + (size_t)r * K + 256 * g + 4 * lane) =
+            e4m3x4(__fdiv_rn(v[g][0], sc), __fdiv_rn(v[g][1], sc), __fdiv_rn(v[g][2], sc), __fdiv_rn(v[g][3], sc));
+}
+
 // Staging of one 128-k block of a workgroup tile in LDS: row R of the tile holds its 128 bytes as eight 16-byte
 // chunks, chunk g at slot g ^ swz(R). The swizzle is applied through the load addresses (global_load_lds writes
 // lane l of a wave instruction to slot l % 8 of row l / 8), so every wave instruction reads eight whole 128-byte
@@ -331,19 +373,32 @@ __global__ __launch_bounds__(128) void fp8_combine_kernel(Fp8Args a) {
 
 // ------------------------------------------------------------------------------------------------ launchers
 
+// Rows of K = 256, 512, 1024, 2048 or 4096 values (and a 16-byte aligned source for fp32, 8-byte otherwise) take
+// the one-wave-per-row kernel; other shapes the one-workgroup-per-row kernel.
+static void quant_rows(const void* x, int xdt, int64_t stride, int rows, int K, uint8_t* q, float* s, hipStream_t st) {
+    if (rows <= 0) return;
+    const int align = xdt == DT_F32 ? 16 : 8;
+    const bool wave = (reinterpret_cast<uintptr_t>(x) % align) == 0 && stride % 4 == 0;
+    const dim3 grid((rows + 3) / 4);
+    if (wave && K == 4096) hipLaunchKernelGGL(quant_rows_wave_kernel<16>, grid, dim3(256), 0, st, x, xdt, stride, rows, K, q, s);
+    else if (wave && K == 2048) hipLaunchKernelGGL(quant_rows_wave_kernel<8>, grid, dim3(256), 0, st, x, xdt, stride, rows, K, q, s);
+    else if (wave && K == 1024) hipLaunchKernelGGL(quant_rows_wave_kernel<4>, grid, dim3(256), 0, st, x, xdt, stride, rows, K, q, s);
+    else if (wave && K == 512) hipLaunchKernelGGL(quant_rows_wave_kernel<2>, grid, dim3(256), 0, st, x, xdt, stride, rows, K, q, s);
+    else if (wave && K == 256) hipLaunchKernelGGL(quant_rows_wave_kernel<1>, grid, dim3(256), 0, st, x, xdt, stride, rows, K, q, s);
+    else hipLaunchKernelGGL(quant_rows_kernel, dim3(rows), dim3(256), 0, st, x, xdt, stride, K, q, s);
+}
+
 int launch_quant_rows(const void* x, int xdt, int64_t stride, int rows, int K, uint8_t* q, float* s, hipStream_t st) {
-    if (rows > 0) hipLaunchKernelGGL(quant_rows_kernel, dim3(rows), dim3(256), 0, st, x, xdt, stride, K, q, s);
+    quant_rows(x, xdt, stride, rows, K, q, s, st);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_fp8(const Fp8Args& a, hipStream_t st, int kernels) {
     if (kernels & 1)
-        if (a.T > 0) hipLaunchKernelGGL(quant_rows_kernel, dim3(a.T), dim3(256), 0, st, a.x, a.xdt, a.x_stride, a.K,
-                                        a.qx, a.sx);
+        quant_rows(a.x, a.xdt, a.x_stride, a.T, a.K, a.qx, a.sx, st);
     if (kernels & 2) hipLaunchKernelGGL(fp8_gateup_kernel, dim3(a.N / 64, a.S_cap), dim3(256), 0, st, a);
     if (kernels & 4) {
-        hipLaunchKernelGGL(quant_rows_kernel, dim3(a.P), dim3(256), 0, st, (const void*)a.a16, (int)DT_F16,
-                           (int64_t)a.N, a.N, a.qa, a.sa);
+        quant_rows(a.a16, DT_F16, a.N, a.P, a.N, a.qa, a.sa, st);
         hipLaunchKernelGGL(fp8_down_kernel, dim3(a.K / 128, a.S_cap), dim3(256), 0, st, a);
     }
     if (kernels & 8) hipLaunchKernelGGL(fp8_combine_kernel, dim3(a.T, a.K / 256), dim3(128), 0, st, a);

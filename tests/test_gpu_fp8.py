@@ -34,11 +34,12 @@ def _host_layer(ex, experts=None):
             "w2": ex.w2[sel].cpu().numpy(), "w2_scale": ex.w2_scale[sel].cpu().numpy()}
 
 
+@pytest.mark.parametrize("K", [1024, 4096, 256, 384])   # one wave per row (256 .. 4096), one workgroup per row (384)
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
-def test_quant_rows_bit_exact(cuda, dt):
+def test_quant_rows_bit_exact(cuda, dt, K):
     from mi355moe import fp8
     g = torch.Generator(device="cuda").manual_seed(7)
-    x = torch.randn(37, 1024, generator=g, device="cuda")
+    x = torch.randn(37, K, generator=g, device="cuda")
     x *= torch.logspace(-3, 3, 37, device="cuda")[:, None]
     x[5] = 0
     x[9, 100] = 3e4
