@@ -347,27 +347,48 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
     }
 }
 
-// grid (T, K/256), 128 threads x 2 columns: out[t] = sum over the token's slots k (in order) of the valid pairs'
-// contributions, converted to the output dtype (deterministic: no atomics).
-__global__ __launch_bounds__(128) void fp8_combine_kernel(Fp8Args a) {
-    const int t = blockIdx.x;
-    const int col = blockIdx.y * 256 + 2 * threadIdx.x;
-    float s0 = 0.f, s1 = 0.f;
-    for (int k = 0; k < a.topk; ++k) {
-        const int pos = a.inv[t * a.topk + k];
-        if (a.pe[pos] < 0) continue;
-        const float2 c = *reinterpret_cast<const float2*>(a.contrib + (size_t)pos * a.K + col);
-        s0 += c.x;
-        s1 += c.y;
+// grid (ceil(T/4), K/256), 256 threads: one wave per (token t, 256 columns), 4 columns per lane. out[t] = sum over
+// the token's slots k (in order) of the valid pairs' contributions, converted to the output dtype (deterministic:
+// no atomics).
+__global__ __launch_bounds__(256) void fp8_combine_kernel(Fp8Args a) {
+    const int t = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+    if (t >= a.T) return;
+    const int lane = threadIdx.x & 63;
+    const int col = blockIdx.y * 256 + 4 * lane;
+    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < a.topk; k0 += 8) {
+        // lanes 0..7 read slot k0 + lane's position and validity (broadcast by readlane); every slot's row is then
+        // loaded before the first is added
+        const int lk = k0 + (lane & 7);
+        const int pl = a.inv[t * a.topk + min(lk, a.topk - 1)];
+        const int okl = (int)(lk < a.topk && a.pe[pl] >= 0);
+        float4 c[8];
+        bool ok[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int pos = __builtin_amdgcn_readlane(pl, k);
+            ok[k] = __builtin_amdgcn_readlane(okl, k) != 0;
+            c[k] = *reinterpret_cast<const float4*>(a.contrib + (size_t)pos * a.K + col);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (ok[k]) {                                               // slot order
+                sum[0] += c[k].x;
+                sum[1] += c[k].y;
+                sum[2] += c[k].z;
+                sum[3] += c[k].w;
+            }
     }
     const size_t o = (size_t)t * a.out_stride + col;
     if (a.odt == DT_F32) {
-        *reinterpret_cast<float2*>(reinterpret_cast<float*>(a.out) + o) = make_float2(s0, s1);
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + o) = make_float4(sum[0], sum[1], sum[2], sum[3]);
     } else if (a.odt == DT_BF16) {
-        const uint32_t v = pack_bf16x2(s0, s1);
-        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.out) + o) = v;
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + o) =
+            make_uint2(pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3]));
     } else {
-        *reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o) = h2{(_Float16)s0, (_Float16)s1};
+        h2* op = reinterpret_cast<h2*>(reinterpret_cast<uint16_t*>(a.out) + o);
+        op[0] = h2{(_Float16)sum[0], (_Float16)sum[1]};
+        op[1] = h2{(_Float16)sum[2], (_Float16)sum[3]};
     }
 }
 
@@ -401,7 +422,7 @@ int launch_fp8(const Fp8Args& a, hipStream_t st, int kernels) {
         quant_rows(a.a16, DT_F16, a.N, a.P, a.N, a.qa, a.sa, st);
         hipLaunchKernelGGL(fp8_down_kernel, dim3(a.K / 128, a.S_cap), dim3(256), 0, st, a);
     }
-    if (kernels & 8) hipLaunchKernelGGL(fp8_combine_kernel, dim3(a.T, a.K / 256), dim3(128), 0, st, a);
+    if (kernels & 8) hipLaunchKernelGGL(fp8_combine_kernel, dim3((a.T + 3) / 4, a.K / 256), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
