@@ -175,9 +175,11 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     __shared__ __align__(16) unsigned char st1[GU_ROWS * 128];
     __shared__ __align__(16) unsigned char st2[GU_ROWS * 128];
     __shared__ float scl[2 * FP8_MAX_KB];
+    __shared__ float rsx[64];                                        // the segment rows' activation scales
     const int cb = blockIdx.x, s = blockIdx.y;
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
+    if (rn <= 0) return;                                             // (no rows: nothing to stage or store)
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, N = a.N;
@@ -207,6 +209,7 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     // loop reads no global memory of its own
     for (int i = threadIdx.x; i < 2 * nkb; i += 256)
         scl[i] = a.w13s[((size_t)e * (2 * N / 128) + (i < nkb ? 0 : N / 128) + cb / 2) * nkb + (i < nkb ? i : i - nkb)];
+    if (threadIdx.x < 64) rsx[threadIdx.x] = a.sx[a.tok[row0 + min((int)threadIdx.x, rn - 1)]];
     __syncthreads();
     const int h = lane >> 5, c = lane & 31;
     const int rt = wv >> 1, ct = wv & 1;
@@ -244,22 +247,21 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
         if (kb + 2 < nkb) step(st2, st1, kb + 2);
     }
 
+    // epilogue: every row computed (rows past rn repeat row rn - 1, not stored), so the 16 rows' work is one block of
+    // independent operations; the row scales come from LDS
     const float L = a.limit;
     const int col = cb * 64 + ct * 32 + c;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int row = 32 * rt + tile_row(r, lane);
-        if (row < rn) {
-            const int pos = row0 + row;
-            const float sxv = a.sx[a.tok[pos]];
-            float gv = g0[r] * sxv, uv = u0[r] * sxv;
-            if (L != 0.0f) {
-                gv = fminf(gv, L);
-                uv = fminf(fmaxf(uv, -L), L);
-            }
-            const float act = __fdiv_rn(gv, 1.0f + (float)exp(-(double)gv)) * uv;
-            a.a16[(size_t)pos * N + col] = (uint16_t)h_as_u16((_Float16)act);
+        const float sxv = rsx[min(row, rn - 1)];
+        float gv = g0[r] * sxv, uv = u0[r] * sxv;
+        if (L != 0.0f) {
+            gv = fminf(gv, L);
+            uv = fminf(fmaxf(uv, -L), L);
         }
+        const float act = __fdiv_rn(gv, 1.0f + (float)exp(-(double)gv)) * uv;
+        if (row < rn) a.a16[(size_t)(row0 + row) * N + col] = (uint16_t)h_as_u16((_Float16)act);
     }
 }
 
@@ -271,9 +273,12 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
     __shared__ __align__(16) unsigned char st1[DN_ROWS * 128];
     __shared__ __align__(16) unsigned char st2[DN_ROWS * 128];
     __shared__ float scl[FP8_MAX_KB];
+    __shared__ float rsa[64], rw[64];                                // the segment rows' scales and router weights
+    __shared__ int rok[64];                                          // and whether they hold a valid pair
     const int cb = blockIdx.x, s = blockIdx.y;
     if (s >= a.nseg[0]) return;
     const int e = a.seg_expert[s], row0 = a.seg_row0[s], rn = a.seg_rows[s];
+    if (rn <= 0) return;                                             // (no rows: nothing to stage or store)
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, N = a.N;
@@ -297,6 +302,12 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
         }
     };
     for (int i = threadIdx.x; i < nkb; i += 256) scl[i] = a.w2s[((size_t)e * (K / 128) + cb) * nkb + i];
+    if (threadIdx.x < 64) {
+        const int pos = row0 + min((int)threadIdx.x, rn - 1);
+        rsa[threadIdx.x] = a.sa[pos];
+        rw[threadIdx.x] = a.w32[pos];
+        rok[threadIdx.x] = (int)threadIdx.x < rn && a.pe[pos] >= 0;  // (a pair whose token id was out of range: no row)
+    }
     __syncthreads();
     const int h = lane >> 5, c = lane & 31;
     f32x16 d0 = {}, d1 = {};
@@ -331,18 +342,17 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
         if (kb + 2 < nkb) step(st2, st1, kb + 2);
     }
 
+    // epilogue: every row computed from the LDS row factors, stored where the row holds a valid pair
     const int col = cb * 128 + wv * 32 + c;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = 32 * t + tile_row(r, lane);
-            if (row < rn) {
-                const int pos = row0 + row;
-                if (a.pe[pos] < 0) continue;                         // a row whose token id was out of range
-                const float y = (t ? d1[r] : d0[r]) * a.sa[pos];
-                a.contrib[(size_t)pos * K + col] = a.w32[pos] * y;
-            }
+            const int rr = min(row, 63);
+            const float y = (t ? d1[r] : d0[r]) * rsa[rr];
+            const float v = rw[rr] * y;
+            if (rok[rr]) a.contrib[(size_t)(row0 + row) * K + col] = v;
         }
     }
 }
