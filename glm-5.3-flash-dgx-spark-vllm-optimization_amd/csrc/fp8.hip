@@ -249,19 +249,29 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
 
     // epilogue: every row computed (rows past rn repeat row rn - 1, not stored), so the 16 rows' work is one block of
     // independent operations; the row scales come from LDS
+    // Lanes c and c ^ 1 then trade one fp16 of each register pair r, r + 1 (DPP lane ^ 1): the even lane stores
+    // columns (c, c + 1) of row(r), the odd lane those of row(r + 1), 4 bytes each.
     const float L = a.limit;
-    const int col = cb * 64 + ct * 32 + c;
+    const bool odd = c & 1;
+    const int col = cb * 64 + ct * 32 + (c & ~1);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = 32 * rt + tile_row(r, lane);
-        const float sxv = rsx[min(row, rn - 1)];
-        float gv = g0[r] * sxv, uv = u0[r] * sxv;
-        if (L != 0.0f) {
-            gv = fminf(gv, L);
-            uv = fminf(fmaxf(uv, -L), L);
+    for (int r = 0; r < 16; r += 2) {
+        uint32_t hv[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float sxv = rsx[min(32 * rt + tile_row(r + i, lane), rn - 1)];
+            float gv = g0[r + i] * sxv, uv = u0[r + i] * sxv;
+            if (L != 0.0f) {
+                gv = fminf(gv, L);
+                uv = fminf(fmaxf(uv, -L), L);
+            }
+            const float act = __fdiv_rn(gv, 1.0f + (float)exp(-(double)gv)) * uv;
+            hv[i] = h_as_u16((_Float16)act);
         }
-        const float act = __fdiv_rn(gv, 1.0f + (float)exp(-(double)gv)) * uv;
-        if (row < rn) a.a16[(size_t)(row0 + row) * N + col] = (uint16_t)h_as_u16((_Float16)act);
+        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)(odd ? hv[0] : hv[1]), 0xB1, 0xF, 0xF, true);
+        const int row = 32 * rt + tile_row(r + (odd ? 1 : 0), lane);     // (r even: rows r, r + 1 are adjacent)
+        const uint32_t pv = odd ? (recv | (hv[1] << 16)) : (hv[0] | (recv << 16));
+        if (row < rn) *reinterpret_cast<uint32_t*>(a.a16 + (size_t)(row0 + row) * N + col) = pv;
     }
 }
 
@@ -342,17 +352,27 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
         if (kb + 2 < nkb) step(st2, st1, kb + 2);
     }
 
-    // epilogue: every row computed from the LDS row factors, stored where the row holds a valid pair
-    const int col = cb * 128 + wv * 32 + c;
+    // epilogue: every row computed from the LDS row factors, stored where the row holds a valid pair. Lanes c and
+    // c ^ 1 (same rows, adjacent columns) trade one value of each register pair r, r + 1 (DPP lane ^ 1): the even
+    // lane stores columns (c, c + 1) of row(r), the odd lane those of row(r + 1), 8 bytes each.
+    const bool odd = c & 1;
+    const int col = cb * 128 + wv * 32 + (c & ~1);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = 32 * t + tile_row(r, lane);
-            const int rr = min(row, 63);
-            const float y = (t ? d1[r] : d0[r]) * rsa[rr];
-            const float v = rw[rr] * y;
-            if (rok[rr]) a.contrib[(size_t)(row0 + row) * K + col] = v;
+        for (int r = 0; r < 16; r += 2) {
+            float v[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int rr = min(32 * t + tile_row(r + i, lane), 63);
+                v[i] = rw[rr] * ((t ? d1[r + i] : d0[r + i]) * rsa[rr]);
+            }
+            const float send = odd ? v[0] : v[1];
+            const float recv = __builtin_bit_cast(
+                float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, true));
+            const int row = 32 * t + tile_row(r + (odd ? 1 : 0), lane);   // (r even: rows r, r + 1 are adjacent)
+            const float2 pv = odd ? make_float2(recv, v[1]) : make_float2(v[0], recv);
+            if (rok[min(row, 63)]) *reinterpret_cast<float2*>(a.contrib + (size_t)(row0 + row) * K + col) = pv;
         }
     }
 }
