@@ -185,15 +185,25 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     const int K = a.K, N = a.N;
     const int nkb = K >> 7;
 
-    // this lane's source rows for its six stage instructions (swizzled chunk offset included)
+    // thread i < 64: the token of segment row i (its activation scale goes to LDS at the first step)
+    const int ti = threadIdx.x;
+    const int tk = a.tok[row0 + min(ti & 63, rn - 1)];
+    // this lane's source rows for its six stage instructions (swizzled chunk offset included); the token ids of the
+    // activation rows (stage rows 128 ..) are all loaded before any is used (one memory latency, not one per row)
     const uint8_t* src[GU_INST];
+    int rtok[GU_INST];
+#pragma unroll
+    for (int j = 0; j < GU_INST; ++j) {
+        const int R = wv * (GU_INST * 8) + j * 8 + (lane >> 3);
+        rtok[j] = a.tok[row0 + min(max(R - 128, 0), rn - 1)];
+    }
 #pragma unroll
     for (int j = 0; j < GU_INST; ++j) {
         const int R = wv * (GU_INST * 8) + j * 8 + (lane >> 3);
         const uint8_t* rowp;
         if (R < 64) rowp = a.w13 + ((size_t)e * 2 * N + cb * 64 + R) * K;
         else if (R < 128) rowp = a.w13 + ((size_t)e * 2 * N + N + cb * 64 + (R - 64)) * K;
-        else rowp = a.qx + (size_t)a.tok[row0 + min(R - 128, rn - 1)] * K;
+        else rowp = a.qx + (size_t)rtok[j] * K;
         src[j] = rowp + (((lane & 7) ^ swz(R)) << 4);
     }
     const int ldsw = wv * (GU_INST * 8) * 128;                       // this wave's first stage row
@@ -205,12 +215,14 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
         }
     };
 
-    // the block scales of this column block (gate then up) go to LDS before any staged load is issued, so the
-    // loop reads no global memory of its own
-    for (int i = threadIdx.x; i < 2 * nkb; i += 256)
-        scl[i] = a.w13s[((size_t)e * (2 * N / 128) + (i < nkb ? 0 : N / 128) + cb / 2) * nkb + (i < nkb ? i : i - nkb)];
-    if (threadIdx.x < 64) rsx[threadIdx.x] = a.sx[a.tok[row0 + min((int)threadIdx.x, rn - 1)]];
-    __syncthreads();
+    // the block scales of this column block (gate then up; thread i < 2 nkb <= 256) and the rows' activation scales
+    // (thread i < 64) are loaded before the first staged loads and written to LDS at the first step: loads return in
+    // issue order, so the first step's wait covers them, and the loop reads no global memory of its own
+    // (unconditional loads at clamped indices: a conditional one would be waited for where its value is selected)
+    const int tsc = min(ti, 2 * nkb - 1);
+    const float scv = a.w13s[((size_t)e * (2 * N / 128) + (tsc < nkb ? 0 : N / 128) + cb / 2) * nkb +
+                             (tsc < nkb ? tsc : tsc - nkb)];
+    const float sxv = a.sx[tk];
     const int h = lane >> 5, c = lane & 31;
     const int rt = wv >> 1, ct = wv & 1;
     f32x16 g0 = {}, u0 = {};
@@ -235,6 +247,10 @@ __global__ __launch_bounds__(256) void fp8_gateup_kernel(Fp8Args a) {
     auto step = [&](unsigned char* cur, unsigned char* nxt, int kb) {
         if (kb + 1 < nkb) WAIT_VM(GU_INST);
         else WAIT_VM(0);
+        if (kb == 0) {                                               // (uniform) the scales, published by the barrier
+            if (ti < 2 * nkb) scl[ti] = scv;
+            if (ti < 64) rsx[ti] = sxv;
+        }
         LDS_BARRIER();
         if (kb + 2 < nkb) issue(nxt, kb + 2);
         compute(cur, kb);
@@ -311,14 +327,14 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
             else dma16(src[j] + (size_t)kb * 128, st + ldsw + j * 1024);
         }
     };
-    for (int i = threadIdx.x; i < nkb; i += 256) scl[i] = a.w2s[((size_t)e * (K / 128) + cb) * nkb + i];
-    if (threadIdx.x < 64) {
-        const int pos = row0 + min((int)threadIdx.x, rn - 1);
-        rsa[threadIdx.x] = a.sa[pos];
-        rw[threadIdx.x] = a.w32[pos];
-        rok[threadIdx.x] = (int)threadIdx.x < rn && a.pe[pos] >= 0;  // (a pair whose token id was out of range: no row)
-    }
-    __syncthreads();
+    // the block scales (thread i < nkb) and the rows' scales, router weights and validity (thread i < 64) are loaded
+    // before the first staged loads and written to LDS at the first step (loads return in issue order)
+    const int ti = threadIdx.x;
+    // (unconditional loads at clamped indices: a conditional one would be waited for where its value is selected)
+    const float scv = a.w2s[((size_t)e * (K / 128) + cb) * nkb + min(ti, nkb - 1)];
+    const int rpos = row0 + min(ti & 63, rn - 1);
+    const float sav = a.sa[rpos], rwv = a.w32[rpos];
+    const int pev = a.pe[rpos];
     const int h = lane >> 5, c = lane & 31;
     f32x16 d0 = {}, d1 = {};
     auto compute = [&](const unsigned char* st, int kb) {
@@ -340,6 +356,14 @@ __global__ __launch_bounds__(256) void fp8_down_kernel(Fp8Args a) {
     auto step = [&](unsigned char* cur, unsigned char* nxt, int kb) {
         if (kb + 1 < nkb) WAIT_VM(DN_INST);
         else WAIT_VM(0);
+        if (kb == 0) {                                               // (uniform) published by the barrier
+            if (ti < nkb) scl[ti] = scv;
+            if (ti < 64) {
+                rsa[ti] = sav;
+                rw[ti] = rwv;
+                rok[ti] = ti < rn && pev >= 0;                      // (a pair whose token id was out of range: no row)
+            }
+        }
         LDS_BARRIER();
         if (kb + 2 < nkb) issue(nxt, kb + 2);
         compute(cur, kb);
