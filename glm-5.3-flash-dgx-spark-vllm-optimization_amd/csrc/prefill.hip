@@ -682,6 +682,23 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
     const int grp0 = cb * 128 + 16 * (c >> 1);                      // the lane's 16-group of the block
     const float L = a.limit;
     const float hr = HAD_R * fwht_sign(lane);                        // r and the sign fwht128_x16s leaves
+    // E4M3: the activation scales of the rows this lane's passes take (block rb, pass p: row 32 rb + 8 wv + 4 p +
+    // rsub), loaded in one batch (token ids, then scales) instead of two dependent loads per pass
+    float rsc[SUB / 32][2];
+    if (E4M3) {
+        int ri[SUB / 32][2];
+#pragma unroll
+        for (int rb = 0; rb < SUB / 32; ++rb)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const int ar = row0 + min(32 * rb + wv * 8 + p * 4 + rsub, rn - 1);
+                ri[rb][p] = a.tok_rows ? a.tok[ar] : ar;
+            }
+#pragma unroll
+        for (int rb = 0; rb < SUB / 32; ++rb)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) rsc[rb][p] = a.asc[ri[rb][p]];
+    }
     // RBS row blocks are staged per pair of barriers (as many as the kernel's LDS holds), so each wave runs 2 RBS
     // row passes of independent work between barriers
     constexpr int RBS = pf_epi_blocks(KIND);
@@ -713,8 +730,7 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
                     gu[2 + p][i] = u4.x, gu[2 + p][i + 1] = u4.y, gu[2 + p][i + 2] = u4.z, gu[2 + p][i + 3] = u4.w;
                 }
                 if (E4M3) {                                          // dequantise: times the row's activation scale
-                    const int ar = row0 + min(trow[p], rn - 1);
-                    const float rs = a.asc[a.tok_rows ? a.tok[ar] : ar];
+                    const float rs = rsc[rb][p];
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         gu[p][i] *= rs;
