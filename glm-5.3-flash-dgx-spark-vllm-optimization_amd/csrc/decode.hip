@@ -435,6 +435,17 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
         }
     }
 
+    // the epilogue's column scales (waves with rows to finish) are loaded here, so their latency overlaps the
+    // exchange of the K halves and any split-K reduction below (with DEPTH 2 -- short K ranges -- where they are
+    // used: there the registers they would hold are the loop's)
+    u32x4 svg = {}, svu = {}, sud = {};
+    auto load_scales = [&]() {
+        const int colb = cb * 128 + 8 * (opaque_lane() & 15);
+        svg = ld_g128(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + colb);
+        svu = ld_g128(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + colb);
+        sud = ld_g128(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + colb);
+    };
+    if (DEPTH == 4 && wv * 4 < rn) load_scales();
     // the two K halves: kh = 1 hands its accumulators to kh = 0 through LDS, which writes the row sums
     __syncthreads();                                                 // the staged inputs are no longer read
     float* red = reinterpret_cast<float*>(smem);                    // [4][64][16]
@@ -490,9 +501,7 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
         const int ln = opaque_lane(), eg4 = ln >> 4, el16 = ln & 15;
         const int rr = wv * 4 + eg4, r = min(rr, rn - 1);
         const int colb = cb * 128 + 8 * el16;
-        const u32x4 svg = ld_g128(reinterpret_cast<const _Float16*>(a.wt.g_svh[e]) + colb);
-        const u32x4 svu = ld_g128(reinterpret_cast<const _Float16*>(a.wt.u_svh[e]) + colb);
-        const u32x4 sud = ld_g128(reinterpret_cast<const _Float16*>(a.wt.d_suh[e]) + colb);
+        if (DEPTH != 4) load_scales();
         auto half = [](const u32x4& v, int i) { return u16_as_h(v[i >> 1] >> (16 * (i & 1))); };
         const float L = a.limit;
         float g[8], u[8], bv[8];
@@ -635,6 +644,20 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int s, in
             pu = pun;
         }
     }
+    // this wave's first epilogue task (below): its column scales and row factors are loaded here, so their latency
+    // overlaps the staging of the sums and any split-N reduction
+    const int ncol = min(DN_COLS, K - cb * DN_COLS);                // 256 or 512
+    const int NBLK = ncol / 128, ntk = rn * NBLK;
+    u32x4 svd0 = {};
+    uint16_t w16_0 = 0;
+    int pe_0 = -1;
+    if (4 * wv < ntk) {
+        const int l = opaque_lane(), tc = min(4 * wv + (l >> 4), ntk - 1), r = tc / NBLK;
+        svd0 = ld_g128(reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + cb * DN_COLS + (tc - r * NBLK) * 128 +
+                       8 * (l & 15));
+        w16_0 = a.w16[row0 + r];
+        pe_0 = a.pe[row0 + r];
+    }
     __syncthreads();                                                 // the staged inputs are no longer read
     float* zs = reinterpret_cast<float*>(smem);                     // [ZS_ROWS][DN_COLS]
     {
@@ -651,7 +674,6 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int s, in
     __syncthreads();
 
     const size_t P = a.P;
-    const int ncol = min(DN_COLS, K - cb * DN_COLS);                // 256 or 512
     unsigned long long* cnt = a.cnt_dn + (size_t)s * ((K + DN_COLS - 1) / DN_COLS) + cb;
     const bool part = kc1 - kc0 < NC;
     if (part) {
@@ -675,22 +697,24 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int s, in
 
     // epilogue: (row, 128-column block) tasks, four per wave at a time (one per 16-lane row, 8 columns per lane);
     // output Hadamard, scale, then atomics or the per-pair contribution
-    const int NBLK = ncol / 128, ntk = rn * NBLK;
     const int ln = opaque_lane(), g4 = ln >> 4, l16 = ln & 15;
     for (int t0 = 4 * wv; t0 < ntk; t0 += 4 * DN_WAVES) {
         const int task = t0 + g4, tc = min(task, ntk - 1);
         const int r = tc / NBLK, hb = tc - r * NBLK;
         const size_t row = row0 + r;
         const int col = cb * DN_COLS + hb * 128 + 8 * l16;
-        const u32x4 svd = ld_g128(reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + col);
+        const bool first = t0 == 4 * wv;                             // (uniform) its loads were issued above
+        const u32x4 svd = first ? svd0 : ld_g128(reinterpret_cast<const _Float16*>(a.wt.d_svh[e]) + col);
+        const uint16_t w16v = first ? w16_0 : a.w16[row];
+        const int pev = first ? pe_0 : a.pe[row];
         float v[8];
         *reinterpret_cast<float4*>(v) = *reinterpret_cast<const float4*>(zs + r * DN_COLS + hb * 128 + 8 * l16);
         *reinterpret_cast<float4*>(v + 4) = *reinterpret_cast<const float4*>(zs + r * DN_COLS + hb * 128 + 8 * l16 + 4);
         fwht128_x16s(v, ln);
-        const float rs = HAD_R * fwht_sign(ln) * (float)u16_as_h(a.w16[row]);   // with the sign fwht128_x16s leaves
+        const float rs = HAD_R * fwht_sign(ln) * (float)u16_as_h(w16v);   // with the sign fwht128_x16s leaves
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = v[i] * rs * (float)u16_as_h(svd[i >> 1] >> (16 * (i & 1)));
-        if (task < ntk && a.pe[row] >= 0) {                          // pe < 0: a row whose token id was out of range
+        if (task < ntk && pev >= 0) {                                // pe < 0: a row whose token id was out of range
             if (a.accumulate) {
                 float* o = reinterpret_cast<float*>(a.out) + (size_t)a.tok[row] * a.out_stride + col;
 #pragma unroll
