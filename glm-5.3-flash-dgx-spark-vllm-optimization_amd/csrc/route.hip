@@ -946,6 +946,51 @@ __global__ __launch_bounds__(1024) void route_scan_lds_kernel(RouteArgs a, int n
     build_segments(cnt, start, a.n, a.R, a.seg, a.S_cap, a.seg_expert, a.seg_row0, a.seg_rows, a.nseg, tot, a.Rmin);
 }
 
+// route_place_kernel with the ranks from ballots (n + 1 <= ROUTE_MATCH_MAX_IDS): in each wave the lanes holding the
+// same id are the AND over the id's bits of the ballots of lanes agreeing on that bit, so a lane's rank in its wave
+// is a popcount; the earlier waves' pairs of an id come from per-wave counts (written by each id's first lane) summed
+// in wave order. Same ranks as route_place_kernel (pairs of an id in pair-index order), without its O(block) scan.
+constexpr int ROUTE_MATCH_MAX_IDS = 1024;
+__global__ __launch_bounds__(ROUTE_BLK) void route_place_match_kernel(RouteArgs a) {
+    extern __shared__ int wh[];                                       // [ROUTE_BLK / 64 waves][n + 1]
+    constexpr int NW = ROUTE_BLK / 64;
+    const int n1 = a.n + 1;
+    const int j0 = blockIdx.x * ROUTE_BLK;
+    const int j = j0 + threadIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const bool valid = j < a.P;
+    for (int i = threadIdx.x; i < NW * n1; i += ROUTE_BLK) wh[i] = 0;
+    const int l = valid ? a.loc[j] : 0;
+    uint64_t same = __ballot(valid);
+    const int nbits = 32 - __builtin_clz((unsigned)max(a.n, 1));       // ids 0 .. n
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = (l >> b) & 1;
+        const uint64_t m = __ballot(bit);
+        same &= bit ? m : ~m;
+    }
+    const int wrank = __popcll(same & ((1ull << lane) - 1));
+    __syncthreads();                                                  // (the zeroed counts)
+    if (valid && wrank == 0) wh[wv * n1 + l] = __popcll(same);
+    __syncthreads();
+    for (int e = threadIdx.x; e < n1; e += ROUTE_BLK) {               // counts -> earlier waves' pairs of id e
+        int run = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int c = wh[w * n1 + e];
+            wh[w * n1 + e] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    if (!valid) return;
+    const int pos = a.blk_cnt[(size_t)blockIdx.x * n1 + l] + wh[wv * n1 + l] + wrank;
+    a.tok[pos] = j / a.topk;
+    a.w16[pos] = weight_f16(a.w, a.wdt, j);
+    if (a.w32) a.w32[pos] = weight_f32(a.w, a.wdt, j);
+    a.pe[pos] = (l < a.n && a.cnt_out[l] <= a.R && a.cnt_out[l] > a.Rmin) ? l : -1;
+    a.inv[j] = pos;
+}
+
 __global__ __launch_bounds__(ROUTE_BLK) void route_place_kernel(RouteArgs a) {
     __shared__ __align__(16) int loc[ROUTE_BLK];
     const int j0 = blockIdx.x * ROUTE_BLK;
@@ -1083,7 +1128,11 @@ int launch_route(const RouteArgs& a, hipStream_t st) {
         hipLaunchKernelGGL(route_scan_lds_kernel, dim3(1), dim3(1024), shm_lds, st, a, nblk);
     else
         hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(1024), 2 * shm1, st, a, nblk);
-    hipLaunchKernelGGL(route_place_kernel, dim3(nblk), dim3(ROUTE_BLK), 0, st, a);
+    if (a.n + 1 <= ROUTE_MATCH_MAX_IDS)
+        hipLaunchKernelGGL(route_place_match_kernel, dim3(nblk), dim3(ROUTE_BLK),
+                           (size_t)(ROUTE_BLK / 64) * (a.n + 1) * sizeof(int), st, a);
+    else
+        hipLaunchKernelGGL(route_place_kernel, dim3(nblk), dim3(ROUTE_BLK), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
