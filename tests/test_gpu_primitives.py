@@ -175,11 +175,15 @@ def test_router_topk_bit_exact(cuda, T, E, topk):
 @pytest.mark.parametrize("T,topk,n,seg,ids64,emap", [(8, 8, 288, 8, False, False), (1, 8, 288, 1, True, False),
                                                      (64, 8, 288, 16, False, True), (2048, 8, 288, 256, False, False),
                                                      (8192, 8, 288, 256, True, False), (130, 8, 64, 16, True, True),
-                                                     (2048, 8, 4000, 64, False, False)])
+                                                     (2048, 8, 4000, 64, False, False),
+                                                     # per-block placement by ballots up to 1024 ids, the scan beyond
+                                                     (2048, 8, 1023, 64, False, False), (2048, 8, 1024, 64, False, False),
+                                                     # few ids: long runs of one id inside every wave and block
+                                                     (1024, 8, 3, 256, False, False)])
 def test_route_bit_exact(cuda, T, topk, n, seg, ids64, emap):
     from mi355moe import ops
     _say(f"route T={T} topk={topk} n={n} seg={seg}")
-    g = torch.Generator().manual_seed(T)
+    g = torch.Generator().manual_seed(T + n)
     ids = torch.randint(-1, n + 2, (T, topk), generator=g)
     ids = ids.to(torch.int64 if ids64 else torch.int32)
     w = torch.rand(T, topk, generator=g)
