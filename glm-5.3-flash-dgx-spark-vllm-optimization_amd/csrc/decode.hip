@@ -243,6 +243,23 @@ __device__ __forceinline__ void step_mfma2_dup(const u32x4& wg, uint32_t pwg, co
     }
 }
 
+// Issue priority by progress through the K loop: 3 in the first quarter of the steps, down to 0 in the last (the
+// loops run as four quarters, so no branch sits inside the step loop). The arbiter favours a CU's oldest waves, so
+// the waves of a workgroup drift apart (its last wave finishing ~13 µs after its first at T = 8) and the last ones
+// then run with few others to hide their latency; waves behind now issue first, so a workgroup's waves finish
+// closer together.
+__device__ __forceinline__ void prio_for_quarter(int q) {
+    if (q == 0) __builtin_amdgcn_s_setprio(3);
+    else if (q == 1) __builtin_amdgcn_s_setprio(2);
+    else if (q == 2) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
+// The end of quarter q of a loop of `steps` steps taken DEPTH at a time.
+template <int DEPTH>
+__device__ __forceinline__ int quarter_end(int q, int steps) {
+    return q == 3 ? steps : ((q + 1) * steps / 4) / DEPTH * DEPTH;
+}
+
 // Streamed weight load: a global-address-space 16-byte load marked non-temporal (read once per call).
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
     return __builtin_nontemporal_load(reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(p)));
@@ -374,7 +391,9 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
         u32x4 xa[4], xn[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) xa[i] = reinterpret_cast<const u32x4*>(xr)[i];
-        for (int st = 0; st < steps; st += DEPTH) {
+        for (int q = 0, st = 0; q < 4; ++q) {
+          prio_for_quarter(q);
+          for (const int st1 = quarter_end<DEPTH>(q, steps); st < st1; st += DEPTH) {
 #pragma unroll
             for (int j = 0; j < DEPTH; ++j) {
                 const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
@@ -392,6 +411,7 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
                 pg = pgn;
                 pu = pun;
             }
+          }
         }
     } else {
         const uint16_t* xg = xs + (size_t)arow * RSH + kh * KH + (t >> 1) * 16;
@@ -403,7 +423,9 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
             xc[1][0] = reinterpret_cast<const u32x4*>(xu)[0];
             xc[1][1] = reinterpret_cast<const u32x4*>(xu)[1];
         }
-        for (int st = 0; st < steps; st += DEPTH) {
+        for (int q = 0, st = 0; q < 4; ++q) {
+          prio_for_quarter(q);
+          for (const int st1 = quarter_end<DEPTH>(q, steps); st < st1; st += DEPTH) {
 #pragma unroll
             for (int j = 0; j < DEPTH; ++j) {
                 const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
@@ -432,9 +454,11 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
                 pg = pgn;
                 pu = pun;
             }
+          }
         }
     }
 
+    __builtin_amdgcn_s_setprio(0);
     // the epilogue's column scales (waves with rows to finish) are loaded here, so their latency overlaps the
     // exchange of the K halves and any split-K reduction below (with DEPTH 2 -- short K ranges -- where they are
     // used: there the registers they would hold are the loop's)
@@ -625,7 +649,9 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int s, in
 #pragma unroll
     for (int i = 0; i < 4; ++i) xa[i] = reinterpret_cast<const u32x4*>(xr)[i];
     uint32_t pg = prev_word(gb[0][3], lane), pu = prev_word(ub[0][3], lane);
-    for (int st = 0; live && st < steps; st += DEPTH) {
+    for (int q = 0, st = 0; live && q < 4; ++q) {
+      prio_for_quarter(q);
+      for (const int st1 = quarter_end<DEPTH>(q, steps); st < st1; st += DEPTH) {
 #pragma unroll
         for (int j = 0; j < DEPTH; ++j) {
             const size_t nx = idx0 + (size_t)min(st + DEPTH + j, steps - 1) * sstr;
@@ -643,7 +669,9 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int s, in
             pg = pgn;
             pu = pun;
         }
+      }
     }
+    __builtin_amdgcn_s_setprio(0);
     // this wave's first epilogue task (below): its column scales and row factors are loaded here, so their latency
     // overlaps the staging of the sums and any split-N reduction
     const int ncol = min(DN_COLS, K - cb * DN_COLS);                // 256 or 512
