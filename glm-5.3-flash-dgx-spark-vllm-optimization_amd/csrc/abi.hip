@@ -1,5 +1,6 @@
 // C-ABI entry points: argument checks (all before the first launch), launch planning and workspace layout.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -50,6 +51,14 @@ int shared_flag(const mi355moe_exl3_layer* L) { return (L->flags & MI355MOE_LAYE
 // one w13 suh for every expert (and gate == up): the grouped path gathers one row per token
 int tok_rows_flag(const mi355moe_exl3_layer* L) {
     return (L->flags & MI355MOE_LAYER_SHARED_W13_SUH) && (L->flags & MI355MOE_LAYER_UNIFORM_W13_SUH) ? 1 : 0;
+}
+
+// The one-launch schedule's lag in segments of one ticket queue (pf_sched_item): MI355MOE_SCHED_LAG, default 0 = all
+// of a queue's gate/up items before its first down item (a down item then rarely waits; small lags make down items
+// wait for gate/up items still running).
+int sched_lag() {
+    const char* v = getenv("MI355MOE_SCHED_LAG");
+    return v ? std::max(0, atoi(v)) : 0;
 }
 
 struct DecodePlan {
@@ -416,6 +425,7 @@ namespace {
 struct PrefillWs {
     RouteArgs ra;
     PrefillArgs pa;
+    int* sched;             // the one-launch schedule's control words [PF_SCHED_HEAD + S_cap]
     size_t bytes;
 };
 
@@ -442,6 +452,7 @@ void carve_prefill(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t
     d.h13 = c.take<uint16_t>((size_t)P * K);
     d.h2 = c.take<uint16_t>((size_t)P * N);
     d.contrib = c.take<float>((size_t)P * K);
+    w.sched = c.take<int>((size_t)PF_SCHED_HEAD + S_cap);
     if (e4m3) {
         r.w32 = c.take<float>(P);
         d.w32 = r.w32;
@@ -477,6 +488,20 @@ int64_t mi355moe_moe_workspace_bytes_path(const mi355moe_exl3_layer* layer, int6
     DecodeWs w;
     carve_decode(nullptr, P, layer->n, layer->hidden, layer->intermediate, p, true, w);
     return (int64_t)w.bytes;
+}
+
+int mi355moe_sched_item(int64_t ticket, int64_t segments, int64_t lag, int64_t gateup_items, int64_t down_items,
+                        int* kind, int* segment, int* block) {
+    if (!kind || !segment || !block) return MI355MOE_EINVAL;
+    if (segments < 0 || segments > (1 << 24) || gateup_items < 1 || gateup_items > 1024 || down_items < 1 ||
+        down_items > 1024 || lag < 0)
+        return MI355MOE_EINVAL;
+    const PfSchedItem r = pf_sched_item(ticket, (int)segments, (int)std::min<int64_t>(lag, 1 << 24), (int)gateup_items,
+                                        (int)down_items);
+    *kind = r.kind;
+    *segment = r.seg;
+    *block = r.block;
+    return 0;
 }
 
 int64_t mi355moe_moe_workspace_bytes(const mi355moe_exl3_layer* layer, int64_t T, int64_t topk) {
@@ -587,6 +612,10 @@ static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     d.tok_rows = tok_rows_flag(layer);
     d.contrib_bf16 = (options & MI355MOE_OPT_BF16_CONTRIB) ? 1 : 0;
     d.out_accumulate = (options & MI355MOE_OPT_ACCUMULATE) ? 1 : 0;
+    if ((options & MI355MOE_OPT_PERSISTENT) && (stages & MI355MOE_STAGE_GATEUP) && (stages & MI355MOE_STAGE_DOWN)) {
+        d.sched = w.sched;                            // gate/up and down tiles in one launch
+        d.sched_lag = sched_lag();
+    }
     if (e4m3 && (options & MI355MOE_OPT_DOWN16)) {   // fp16 down operands: no down-input quantisation or its scale
         d.down16 = 1;
         d.dsc = nullptr;
@@ -635,7 +664,7 @@ int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x
         return MI355MOE_EINVAL;
     const bool e4m3 = (options & MI355MOE_OPT_E4M3) != 0;
     if ((options & MI355MOE_OPT_DOWN16) && !e4m3) return MI355MOE_EINVAL;
-    if (options & MI355MOE_OPT_PERSISTENT) return MI355MOE_EUNSUPPORTED;      // switched off (see the header)
+    if ((options & MI355MOE_OPT_PERSISTENT) && e4m3) return MI355MOE_EUNSUPPORTED;   // E3 numerics only
     if (e4m3 && path == MI355MOE_PATH_DECODE) return MI355MOE_EINVAL;      // e4m3 numerics run on the grouped tier
     if (e4m3 && layer && layer->hidden > 4096) return MI355MOE_EUNSUPPORTED;
     if (dt_act(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;

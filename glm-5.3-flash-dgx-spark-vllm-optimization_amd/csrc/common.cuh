@@ -82,6 +82,14 @@ __device__ __forceinline__ int opaque_lane() {
     return l;
 }
 
+// threadIdx.x through an opaque instruction: the same use-where-defined effect for code that runs once per work item
+// inside a persistent loop (values derived from it are not hoisted out of the loop and kept live across items).
+__device__ __forceinline__ int opaque_tid() {
+    int t;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+    return t;
+}
+
 // v[i] += c * v[i] of lane l ^ m for the 8 values, one v_fmac_f32 with a DPP source per value (control CTL:
 // quad_perm [1,0,3,2] for m = 1, [2,3,0,1] for m = 2, row_ror:8 for m = 8). s_nop 1 gives the two wait states a DPP
 // read needs after a VALU write of its source; inside the block each source was written eight instructions earlier.
@@ -294,6 +302,13 @@ __device__ __forceinline__ void dma16(const void* src_lane, unsigned char* lds_w
 __device__ __forceinline__ void dma16_nt(const void* src_lane, unsigned char* lds_wave) {
     const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(m0), "v"(src_lane)
+                 : "memory", "m0");
+}
+// The same as a device-coherent load (agent scope, sc1: the data comes from the device coherence point, not from a
+// line another XCD's stores left stale in this CU's or XCD's caches).
+__device__ __forceinline__ void dma16_coh(const void* src_lane, unsigned char* lds_wave) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off sc1" ::"s"(m0), "v"(src_lane)
                  : "memory", "m0");
 }
 // The same with 4 bytes per lane: lane l -> LDS bytes lds_wave + 4 l (global_load_lds_dword).

@@ -152,8 +152,56 @@ struct PrefillArgs {
     int chunk, nchunks;     // nchunks > 1: the GEMMs and row kernels take only the segments
                             // [ns chunk / nchunks, ns (chunk + 1) / nchunks) of the ns = nseg[0] live ones
     const int* row_expert;  // optional: the row-table setup marks row r with row_expert[r] instead of its segment's
+    // one-launch schedule (nullptr: separate gate/up and down launches): control words [PF_SCHED_HEAD + S_cap] --
+    // the next ticket of queue q at [PF_SCHED_QSTRIDE q] (q < PF_SCHED_QUEUES), the give-up word after them (set
+    // when a down item gave up waiting), then from PF_SCHED_HEAD per segment the gate/up items finished -- zeroed by
+    // the gather that starts the call; sched_lag: the schedule's lag in segments of a queue (0: all of them)
+    int* sched;
+    int sched_lag;
 };
 constexpr int PREFILL_TM = 256;
+constexpr int PF_SCHED_QUEUES = 8;      // ticket queues (one per XCD; segment s in queue s % 8)
+constexpr int PF_SCHED_QSTRIDE = 32;    // words between queue counters (one 128-byte line each)
+constexpr int PF_SCHED_HEAD = PF_SCHED_QUEUES * PF_SCHED_QSTRIDE + PF_SCHED_QSTRIDE;
+
+// Item t of the one-launch gate/up -> down schedule over ns segments with ncg gate/up and ncd down items each
+// (column blocks), lag L = min(lag, ns) (lag <= 0: ns): the gate/up items of segments 0 .. L - 1, then for
+// r = 0 .. ns - L - 1 the gate/up items of segment L + r followed by the down items of segment r, then the down items
+// of segments ns - L .. ns - 1 (the reference's item order, code/fork/kernels/moe_e4m3.cu:867-872, 931-959).
+// Every down item of a segment comes after all of that segment's gate/up items, so a down item only waits for items
+// with smaller tickets, which workgroups already running hold. kind: 0 gate/up, 1 down, -1 past the last item.
+struct PfSchedItem {
+    int kind, seg, block;
+};
+__host__ __device__ inline PfSchedItem pf_sched_item(int64_t t, int ns, int lag, int ncg, int ncd) {
+    PfSchedItem r{-1, 0, 0};
+    if (t < 0 || ns <= 0 || ncg <= 0 || ncd <= 0) return r;
+    const int64_t L = (lag <= 0 || lag > ns) ? ns : lag;
+    const int64_t round = ncg + ncd;
+    const int64_t lead = L * ncg, mid = (ns - L) * round;
+    if (t < lead) {
+        r.kind = 0;
+        r.seg = (int)(t / ncg);
+        r.block = (int)(t % ncg);
+    } else if (t < lead + mid) {
+        const int64_t u = t - lead, q = u / round, w = u % round;
+        if (w < ncg) {
+            r.kind = 0;
+            r.seg = (int)(L + q);
+            r.block = (int)w;
+        } else {
+            r.kind = 1;
+            r.seg = (int)q;
+            r.block = (int)(w - ncg);
+        }
+    } else if (t < lead + mid + L * ncd) {
+        const int64_t u = t - lead - mid;
+        r.kind = 1;
+        r.seg = (int)(ns - L + u / ncd);
+        r.block = (int)(u % ncd);
+    }
+    return r;
+}
 constexpr int PF_ROWS_PER_TOKEN = 32;   // rows of one token the row-table combine handles (topk <= 32)
 
 // kernels: bit 0 gather, bit 1 gate/up, bit 2 down (e4m3: the down-input quantization, then the down GEMM), bit 3

@@ -63,13 +63,23 @@ __device__ __forceinline__ int pf_kperm_pair(int j) { return 2 * (j & 3) + (j >>
 // with one 16-byte store: the lanes c, c ^ 1 of a group own its 32 bytes interleaved (storage pair 2m + h = the lane's
 // pair m), so they swap two pairs (DPP lane ^ 1) and lane h then writes storage pairs 4h .. 4h + 3 contiguously.
 // grp: the 16-group's first element.
+// COH: written as two device-coherent 8-byte stores (agent-scope relaxed atomics, written through to the device
+// coherence point), for rows that workgroups on other XCDs read in the same launch.
+template <bool COH = false>
 __device__ __forceinline__ void pf_store_group(_Float16* grp, const uint32_t (&wm)[4], int c) {
     const bool hi = c & 1;
     const uint32_t s0 = hi ? wm[0] : wm[2], s1 = hi ? wm[1] : wm[3];
     const uint32_t r0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s0, 0xB1, 0xF, 0xF, true);   // lane ^ 1
     const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s1, 0xB1, 0xF, 0xF, true);
     const u32x4 v = hi ? u32x4{r0, wm[2], r1, wm[3]} : u32x4{wm[0], r0, wm[1], r1};
-    *reinterpret_cast<u32x4*>(grp + 8 * (c & 1)) = v;
+    if (COH) {
+        uint64_t* d = reinterpret_cast<uint64_t*>(grp + 8 * (c & 1));
+        __hip_atomic_store(d, (uint64_t)v[0] | ((uint64_t)v[1] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(d + 1, (uint64_t)v[2] | ((uint64_t)v[3] << 32), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *reinterpret_cast<u32x4*>(grp + 8 * (c & 1)) = v;
+    }
 }
 // The same placement for one byte per element (e4m3 codes): q[m] holds the lane's pair m as two codes in its low 16
 // bits; lane h of the pair of lanes writes storage pairs 4h .. 4h + 3 as 8 contiguous bytes. grp: the 16-group's
@@ -125,6 +135,8 @@ __device__ __forceinline__ int pf_gather_items(const PrefillArgs& a) {
 // DPP Hadamard); the loads of all passes of the row are issued before the first rotation.
 constexpr int PF_GATHER_PASSES = 8;                 // passes of 4 blocks in flight (K up to 4096 in one round)
 __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
+    if (a.sched && blockIdx.x == 0)                                   // the one-launch schedule's control words
+        for (int i = threadIdx.x; i < PF_SCHED_HEAD + a.S_cap; i += 256) a.sched[i] = 0;
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
     const int nb = a.K >> 7;
@@ -463,7 +475,7 @@ __device__ __forceinline__ uint32_t pf_decode_pair(const uint32_t (&w)[3], int p
 // MFMAs and A reads of the other blocks, whose accumulators stay zero and are never stored; the decode is the same).
 // TM: the A rows staged per step (256; 128 or 64 for the mid- and small-tile kernels). NS: staged steps (loads of
 // step it + NS - 1 are issued while step it is multiplied).
-template <bool E4M3 = false, int NRB = 8, int TM = PF_TM, int NS = PF_NS>
+template <bool E4M3 = false, int NRB = 8, int TM = PF_TM, int NS = PF_NS, bool ACOH = false>
 __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f16v (&acc)[8][2]) {
     static_assert(32 * NRB <= TM && TM % 32 == 0, "the multiplied row blocks are staged");
     constexpr int ASB = TM * PF_RB;                                   // one A stage
@@ -474,7 +486,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     constexpr int NDMA = NA + PF_KT / 2;                              // DMA instructions per wave per step
     unsigned char* Ast = smem;                                        // [NS][TM rows][PF_RB]
     unsigned char* Wst = smem + NS * ASB;                          // [NS][4 waves][PF_KT k tiles][4 tiles][128 B]
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = opaque_tid(), lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int steps = t.kdim / (16 * PF_KT);
     // A DMA sources: instruction i of this wave = rows RPW wv + RPI i + lane / CPR, slot lane % CPR
@@ -498,7 +510,9 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
     auto issue_one = [&](int k, int sa, int sw) {                     // DMA instruction k of the batch (A(sa), W(sw))
         sa = min(sa, steps - 1);
         sw = min(sw, steps - 1);
-        if (k < NA)
+        if (k < NA && ACOH)
+            dma16_coh(asrc[k] + (size_t)sa * 16 * PF_KT, Ast + (sa % NS) * ASB + wv * RPW * PF_RB + k * 1024);
+        else if (k < NA)
             dma16(asrc[k] + (size_t)sa * 16 * PF_KT, Ast + (sa % NS) * ASB + wv * RPW * PF_RB + k * 1024);
         else
             dma16(wsrc + (size_t)sw * wstep + (k - NA) * wins, Wst + (sw % NS) * PF_WSB + wv * PF_WWB + (k - NA) * 1024);
@@ -597,8 +611,8 @@ __device__ __forceinline__ void pf_gemm(const PfTile& t, unsigned char* smem, f1
 
 // Stage the accumulators of row block rb (32 rows x 256 columns of the tile) into Cs [32][PF_CLD] fp32.
 __device__ __forceinline__ void pf_stage_rows(const f16v (&acc)[8][2], float* Cs, int rb) {
-    const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = opaque_tid() & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(opaque_tid() >> 6);
     const int n = lane & 31;
     const int col = 64 * wv + 16 * (n >> 3) + (n & 7);
 #pragma unroll
@@ -642,7 +656,7 @@ __device__ __forceinline__ void pf_seg_range(const PrefillArgs& a, int& lo, int&
 // activation scale before the output Hadamard; the down input H(a16 * suh_d) * r kept in fp32 in vd, its row maxima
 // gathered in amaxd for pf_quantd_kernel). code/fork/overlay/glm53_moe_e4m3.py:654-674 (spec_proj, spec_ffn).
 // KIND: the tile is part `part` of the segment's rows in pf_sub_rows(KIND)-row parts (PF_LARGE: the whole segment).
-template <bool E4M3, int KIND>
+template <bool E4M3, int KIND, bool COH = false>
 __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int part, int cb, unsigned char* smem) {
     constexpr int SUB = pf_sub_rows(KIND);
     const int e = a.seg_expert[s];
@@ -653,7 +667,7 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
     }
     if (rn <= 0 || row0 < 0 || row0 + rn > a.P || e < 0 || e >= a.n) return;   // (caller-built tables)
     const int K = a.K, N = a.N;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(opaque_tid() >> 6);
     PfTile t;                                                        // waves 0, 1: gate columns; 2, 3: up columns
     t.a_rows = a.tok_rows ? a.h13 : a.h13 + (size_t)row0 * K;       // tok_rows: the rows' tokens index h13
     t.a_tok = a.tok_rows ? a.tok + row0 : nullptr;
@@ -672,7 +686,7 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
     // epilogue, 32 rows at a time through LDS; a wave finishes 4 rows at once: 16 lanes per row, lane c holding
     // columns 8c .. 8c + 7 (the 128-point Hadamards run across the 16 lanes by DPP)
     float* Cs = reinterpret_cast<float*>(smem);
-    const int lane = threadIdx.x & 63;
+    const int lane = opaque_tid() & 63;
     const int c = lane & 15, rsub = lane >> 4;
     const int col = cb * 128 + 8 * c;
     float svg[8], svu[8];
@@ -798,7 +812,8 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
                         wm[m] = __builtin_bit_cast(uint32_t,
                                                    h2{(_Float16)(b[p][2 * m] * hr), (_Float16)(b[p][2 * m + 1] * hr)});
                     if (trow[p] < rn)
-                        pf_store_group(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow[p]) * N + grp0, wm, c);
+                        pf_store_group<COH>(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow[p]) * N + grp0, wm,
+                                            c);
                 }
             }
         }
@@ -858,7 +873,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 
 // ------------------------------------------------------------------------------------------------ down
 
-template <bool E4M3, int KIND>
+template <bool E4M3, int KIND, bool ACOH = false>
 __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int part, int cb, unsigned char* smem) {
     constexpr int SUB = pf_sub_rows(KIND);
     const int e = a.seg_expert[s];
@@ -869,7 +884,7 @@ __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int pa
     }
     if (rn <= 0 || row0 < 0 || row0 + rn > a.P || e < 0 || e >= a.n) return;   // (caller-built tables)
     const int K = a.K, N = a.N;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(opaque_tid() >> 6);
     PfTile t;
     t.a_rows = a.h2 + (size_t)row0 * N;
     t.a_tok = nullptr;
@@ -882,13 +897,13 @@ __device__ __forceinline__ void pf_down_tile(const PrefillArgs& a, int s, int pa
     if (KIND == PF_SMALL) pf_gemm<E4M3, 2, PF_TMS>(t, smem, acc);
     else if (KIND == PF_MID && rn <= 64) pf_gemm<E4M3, 2, PF_TMM, PF_NSM>(t, smem, acc);
     else if (KIND == PF_MID) pf_gemm<E4M3, 4, PF_TMM, PF_NSM>(t, smem, acc);
-    else if (rn <= 64) pf_gemm<E4M3, 2>(t, smem, acc);
-    else pf_gemm<E4M3, 8>(t, smem, acc);
+    else if (rn <= 64) pf_gemm<E4M3, 2, PF_TM, PF_NS, ACOH>(t, smem, acc);
+    else pf_gemm<E4M3, 8, PF_TM, PF_NS, ACOH>(t, smem, acc);
 
     // epilogue: the raw accumulators (rows < rn) straight from registers into contrib; the output rotation, svh and
     // router weight are applied by the combine (the VALU work runs there, beside its memory traffic, instead of after
     // this kernel's MFMAs). Lane n of block s holds column 16 (n / 8) + n % 8 + 8 s of the wave.
-    const int lane = threadIdx.x & 63;
+    const int lane = opaque_tid() & 63;
     const int n = lane & 31;
     const size_t c0 = (size_t)row0 * K + cb * 256 + 64 * wv + 16 * (n >> 3) + (n & 7);
     // row blocks wholly inside the segment store unguarded (uniform test); only the block holding row rn is masked
@@ -983,6 +998,80 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     int s, half, cb;
     if (!pf_part_tile_of(a, a.K >> 8, 2, s, half, cb)) return;
     pf_down_tile<E4M3, PF_MID>(a, s, half, cb, smem);
+}
+
+// ------------------------------------------------------------------------------------------------ one-launch schedule
+
+// Every gate/up and down tile of a call (256-row kind, E3 numerics) in one launch of one workgroup per CU. The
+// segments are dealt to eight ticket queues (segment s to queue s % 8, as the separate launches deal them to the
+// XCDs), each ordered by pf_sched_item over its own segments; a workgroup takes tickets from its own XCD's queue
+// (the XCC_ID register), so a segment's column blocks share that XCD's L2 for their A rows, and once that queue is
+// empty from the other queues in turn. A gate/up item stores its h2 rows device-coherent (written through to the
+// device coherence point, so no L2 write-back fence is needed), and once every wave's stores have completed
+// (s_waitcnt, then a barrier) one lane raises the segment's count. A down item waits until the count reaches the
+// segment's ncg gate/up items (one lane polls with agent-scope atomic loads, sleeping between polls) and loads the
+// h2 rows device-coherent (so no cache invalidation is needed). The gate/up items a down item waits for have smaller
+// tickets of the same queue, so running workgroups hold them, and they never wait themselves: every wait ends. A
+// wait is still bounded (PF_SCHED_POLLS polls): one that runs out sets the give-up word, skips its tile, and every
+// later wait gives up at once, so a broken table costs a wrong result, never a hung launch. The tiles run the
+// separate launches' code on the same rows, so the results are bit-identical to theirs.
+constexpr int PF_SCHED_POLLS = 1 << 20;
+__global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    // The item's ticket and whether its wait ran out sit in the first LDS words between tiles (the tiles' stages
+    // take the whole LDS): written by one lane, read by every wave after a barrier, and overwritten by the tile's
+    // loads only after a second barrier.
+    int* s_ctl = reinterpret_cast<int*>(smem);
+    int lo, hi;
+    pf_seg_range(a, lo, hi);
+    const int ns = hi - lo, ncg = a.N >> 7, ncd = a.K >> 8;
+    int* ctl = a.sched;
+    int* gave_up_word = ctl + PF_SCHED_QUEUES * PF_SCHED_QSTRIDE;
+    int* ready = ctl + PF_SCHED_HEAD;
+    const int xq = __builtin_amdgcn_s_getreg((2 << 11) | 20) & (PF_SCHED_QUEUES - 1);   // XCC_ID bits 2:0
+    for (int d = 0; d < PF_SCHED_QUEUES; ++d) {
+        const int q = (xq + d) & (PF_SCHED_QUEUES - 1);
+        const int nq = ns > q ? (ns - q + PF_SCHED_QUEUES - 1) / PF_SCHED_QUEUES : 0;   // the queue's segments
+        int* ticket = ctl + q * PF_SCHED_QSTRIDE;
+        while (nq > 0) {
+            WAIT_VM(0);                                               // the last item's stores have completed
+            __syncthreads();                                          // and every wave is done with LDS
+            if (threadIdx.x == 0) {
+                s_ctl[0] = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_ctl[1] = 0;
+            }
+            __syncthreads();
+            const PfSchedItem it = pf_sched_item(__builtin_amdgcn_readfirstlane(s_ctl[0]), nq, a.sched_lag, ncg, ncd);
+            if (it.kind < 0) break;                                   // (uniform) the queue is empty
+            const int s = lo + q + PF_SCHED_QUEUES * it.seg;          // < hi
+            if (it.kind == 0) {
+                __syncthreads();                                      // every wave has read s_ctl
+                pf_gateup_tile<false, PF_LARGE, true>(a, s, 0, it.block, smem);   // h2 stored device-coherent
+                WAIT_VM(0);                                           // this wave's h2 stores have completed
+                __syncthreads();
+                if (threadIdx.x == 0)
+                    __hip_atomic_fetch_add(ready + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                continue;
+            }
+            if (threadIdx.x == 0) {
+                for (int polls = 0;
+                     __hip_atomic_load(ready + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ncg; ++polls) {
+                    if (polls >= PF_SCHED_POLLS ||
+                        __hip_atomic_load(gave_up_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                        __hip_atomic_store(gave_up_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        s_ctl[1] = 1;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(4);
+                }
+            }
+            __syncthreads();
+            const int gave_up = __builtin_amdgcn_readfirstlane(s_ctl[1]);
+            __syncthreads();                                          // every wave has read s_ctl
+            if (gave_up) continue;                                    // (uniform) the tile is skipped
+            pf_down_tile<false, PF_LARGE, true>(a, s, 0, it.block, smem);   // h2 loaded device-coherent
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ combine
@@ -1326,6 +1415,19 @@ __global__ __launch_bounds__(256) void pf_combine_rows_kernel(PrefillArgs a, con
 
 static bool g_pf_attr = false;
 
+// Compute units of the current device (the one-launch schedule's grid: one workgroup per CU), cached per device.
+static int pf_device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] <= 0) {
+        int v = 0;
+        cus[dev] = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v
+                                                                                                               : 256;
+    }
+    return cus[dev];
+}
+
 int prefill_setup() {
     if (g_pf_attr) return 0;
     const void* ks[4] = {reinterpret_cast<const void*>(pf_gateup_kernel<false>),
@@ -1346,6 +1448,9 @@ int prefill_setup() {
                           reinterpret_cast<const void*>(pf_down_mid_kernel<true>)};
     for (const void* k : ksm)
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_M) != hipSuccess) return -1;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(pf_sched_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)PF_LDS) != hipSuccess)
+        return -1;
     g_pf_attr = true;
     return 0;
 }
@@ -1401,6 +1506,14 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     const dim3 gum(8 * (a.N / 128) * sgm), dnm(8 * (a.K / 256) * sgm);
     const int tiles = pf_tiles(a0);
     a.small_rows = tiles == PF_TILES_BOTH ? PF_SMALL_ROWS : 0;
+    if (a.sched && (f8 || (kernels & 7) != 7)) return -1;           // E3 numerics, after this call's gather
+    if (a.sched) {
+        a.small_rows = 0;
+        const int64_t items = (int64_t)std::max(a.S_cap, 0) * ((a.N >> 7) + (a.K >> 8));
+        const int grid = (int)std::min<int64_t>(pf_device_cus(), items);
+        if (grid > 0) hipLaunchKernelGGL(pf_sched_kernel, dim3(grid), dim3(PF_THREADS), PF_LDS, st, a);
+        kernels &= ~6;
+    }
     if (kernels & 2) {
         if (tiles & PF_TILES_LARGE) {
             if (f8) hipLaunchKernelGGL(pf_gateup_kernel<true>, gu, dim3(PF_THREADS), PF_LDS, st, a);

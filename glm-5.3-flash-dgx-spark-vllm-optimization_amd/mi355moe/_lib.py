@@ -121,6 +121,8 @@ _SIGS = {
     "mi355moe_fp8_moe_workspace_bytes": (_i64, [ctypes.POINTER(Fp8LayerDesc), _i64, _i64]),
     "mi355moe_fp8_moe_forward_ids": (_int, [ctypes.POINTER(Fp8LayerDesc), _c_p, _int, _i64, _i64, _c_p, _int, _c_p,
                                             _int, _i64, _c_p, _i64, _f, _c_p, _int, _i64, _c_p, _sz, _int, _c_p]),
+    "mi355moe_sched_item": (_int, [_i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_int), ctypes.POINTER(_int),
+                                   ctypes.POINTER(_int)]),
     "mi355moe_exl3_moe": (_int, [ctypes.POINTER(Exl3LayerDesc), _c_p, _i64, _c_p, _c_p, _c_p, _c_p, _i64, _i64,
                                  _int, _int, _int, _int, _int, _int, _int, _int, _int, _int, _f, _c_p, _sz, _c_p]),
 }

@@ -231,8 +231,9 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
     path: _lib.PATH_AUTO (decode kernels for few pairs, the grouped MFMA prefill kernels for many), or forced.
     stages: a subset of the call's launches (_lib.STAGE_*), for timing one kernel; the default runs them all.
     bf16_contrib: the grouped path keeps its per-pair down accumulators in bf16 (half the contribution traffic;
-    code/fork/docs/OPT_MOE.md:13). persistent: the one-launch ticket-ordered schedule of the grouped path
-    (code/fork/kernels/moe_e4m3.cu:867-897); not available (the library refuses it)."""
+    code/fork/docs/OPT_MOE.md:13). persistent: the grouped path's gate/up and down tiles in one launch, taken in
+    ticket order with per-segment dataflow counts (code/fork/kernels/moe_e4m3.cu:867-897; E3 numerics; results
+    bit-identical to the separate launches)."""
     if accumulate and out is None:
         raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
@@ -264,6 +265,17 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
         float(limit), _p(out), weight_dtype_code(out.dtype), out.stride(0), _p(ws), ws.numel(), int(path),
         int(stages), opts, _stream(dev)))
     return out
+
+
+def sched_item(ticket: int, segments: int, lag: int, gateup_items: int, down_items: int) -> tuple[int, int, int]:
+    """(kind, segment, block) of item `ticket` of the one-launch schedule (kind 0 gate/up, 1 down, -1 past the last
+    item): the library's own item order, evaluated on the host (code/fork/kernels/moe_e4m3.cu:931-959)."""
+    k, s, b = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.check("mi355moe_sched_item", _lib.lib().mi355moe_sched_item(int(ticket), int(segments), int(lag),
+                                                                     int(gateup_items), int(down_items),
+                                                                     ctypes.byref(k), ctypes.byref(s),
+                                                                     ctypes.byref(b)))
+    return k.value, s.value, b.value
 
 
 def moe_forward_ids_split(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor,

@@ -175,13 +175,27 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
  *   MI355MOE_OPT_DOWN16       with MI355MOE_OPT_E4M3: the down projection on fp16 operands (the e4m3 extension's
  *                             variant 16, code/fork/overlay/glm53_moe_e4m3.py:660-674 spec_proj16): the down input
  *                             h = fp16(H(float(a16) * suh_d) * r) times the fp16 W_q with fp32 sums.
- *   MI355MOE_OPT_PERSISTENT   reserved for a one-launch, ticket-ordered gate/up + down schedule of the grouped path
- *                             (the reference's code/fork/kernels/moe_e4m3.cu:867-897); not available in this library:
- *                             every call with it returns MI355MOE_EUNSUPPORTED before any launch.
+ *   MI355MOE_OPT_PERSISTENT   the grouped path's gate/up and down tiles in one launch of one workgroup per compute
+ *                             unit, ticket-ordered with per-segment dataflow counts (the reference's fused schedule,
+ *                             code/fork/kernels/moe_e4m3.cu:867-897; item order: mi355moe_sched_item). Applies when
+ *                             the call runs both stages (MI355MOE_STAGE_GATEUP and MI355MOE_STAGE_DOWN) on the grouped
+ *                             path; results are bit-identical to the separate launches. E3 numerics only: with
+ *                             MI355MOE_OPT_E4M3 the call returns MI355MOE_EUNSUPPORTED before any launch. The lag (in
+ *                             segments) is read from the environment variable MI355MOE_SCHED_LAG (default 0 = every
+ *                             segment's gate/up items first).
  * Unknown bits: MI355MOE_EINVAL. Workspace sizes as mi355moe_moe_workspace_bytes_path (with MI355MOE_OPT_E4M3:
  * mi355moe_e4m3_moe_workspace_bytes). */
 enum { MI355MOE_OPT_ACCUMULATE = 1, MI355MOE_OPT_BF16_CONTRIB = 2, MI355MOE_OPT_E4M3 = 4, MI355MOE_OPT_PERSISTENT = 8,
        MI355MOE_OPT_DOWN16 = 16 };
+
+/* Item `ticket` of the one-launch schedule (MI355MOE_OPT_PERSISTENT) over `segments` row segments with gateup_items /
+ * down_items column blocks per segment (intermediate / 128 and hidden / 256) and lag L = min(lag, segments) (lag 0:
+ * segments): the gate/up items of segments 0 .. L - 1, then for r = 0, 1, ... the gate/up items of segment L + r
+ * followed by the down items of segment r, then the down items of the last L segments
+ * (code/fork/kernels/moe_e4m3.cu:867-872 and 931-959, make_job). *kind = 0 gate/up, 1 down, -1 past the last item;
+ * *segment and *block name the tile. A host-side query (no device work): 0, or MI355MOE_EINVAL. */
+int mi355moe_sched_item(int64_t ticket, int64_t segments, int64_t lag, int64_t gateup_items, int64_t down_items,
+                        int* kind, int* segment, int* block);
 int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x, int x_dtype, int64_t x_stride,
                                  int64_t T, const void* ids, int ids_dtype, const void* weights, int weights_dtype,
                                  int64_t topk, const int64_t* expert_map, int64_t n_global, float limit, void* out,

@@ -89,8 +89,7 @@ def test_forward_options_are_checked_before_any_launch():
             p, 1 << 30]
     assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_AUTO, _lib.STAGE_ALL, 16, None) == 1         # unknown bit
     assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_AUTO, _lib.STAGE_ALL,
-                                          _lib.OPT_E4M3 | _lib.OPT_PERSISTENT, None) == 6                # unsupported
-    assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_AUTO, _lib.STAGE_ALL, _lib.OPT_PERSISTENT, None) == 6
+                                          _lib.OPT_E4M3 | _lib.OPT_PERSISTENT, None) == 6   # one-launch: E3 only
     assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_DECODE, _lib.STAGE_ALL, _lib.OPT_E4M3, None) == 1
 
 

@@ -1,17 +1,14 @@
-"""GPU checks of the one-launch ticket-ordered schedule of the grouped path (MI355MOE_OPT_PERSISTENT): gate/up and
-down tiles taken from per-XCD ticket queues, a down tile waiting on its segment's gate/up count. Same kernels per
-tile, so the output equals the separate launches' bit for bit: uniform and Zipf routing, full size, fewer segments
-than queues, one-block routing, bf16 accumulators, and stage-split calls that rely on the control words being left at
-zero."""
+"""GPU checks of the one-launch schedule of the grouped path (MI355MOE_OPT_PERSISTENT): gate/up and down tiles taken
+from one ticket counter, a down tile waiting on its segment's gate/up count. Same tile code, so the output equals
+the separate launches' bit for bit: uniform and Zipf routing, full size, fewer segments than compute units, one-block
+routing, bf16 accumulators, lags that make down tiles wait, and stage-split calls (the call's gather zeroes the
+control words)."""
 from __future__ import annotations
 
 import pytest
 import torch
 
-pytestmark = [pytest.mark.gpu,
-              pytest.mark.skip(reason="the one-launch schedule took a GPU memory fault on its first run and no cause "
-                                      "was found by reading it; the library refuses MI355MOE_OPT_PERSISTENT until "
-                                      "one is")]
+pytestmark = pytest.mark.gpu
 
 
 def _say(*a):
@@ -45,9 +42,27 @@ def test_persistent_equals_separate_launches(cuda, n, K, N, T, routing, uniform)
         assert torch.equal(again, ref)
 
 
+@pytest.mark.parametrize("lag", [1, 3, 12])
+def test_persistent_lag_waits(cuda, lag, monkeypatch):
+    """Small lags put a segment's down tiles right behind its gate/up tiles, so down tiles wait on the counts."""
+    from mi355moe import _lib, ops, synthetic
+    _say(f"persistent schedule, lag {lag}")
+    monkeypatch.setenv("MI355MOE_SCHED_LAG", str(lag))
+    n, K, N, T = 64, 2048, 512, 3000
+    ex = synthetic.calibrated_layer(n, K, N, seed=11, device=cuda, uniform_suh=True)
+    x = synthetic.activations(T, K, seed=12, device=cuda)
+    ids = synthetic.zipf_ids(T, n, 8, seed=13, device=cuda)
+    w = synthetic.softmax_weights(T, 8, seed=14, device=cuda)
+    ref = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+    for _ in range(2):
+        got = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL, persistent=True)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), (got - ref).abs().max().item()
+
+
 def test_persistent_stage_split_calls(cuda):
-    """Route once, then the gate/up + down + combine stages twice with new activations: the second launch finds its
-    tickets and segment counts back at zero (left so by the first) and equals the separate launches."""
+    """Route once, then the gate/up + down + combine stages twice with new activations: each call's gather zeroes the
+    ticket and segment counts the previous launch left, and the result equals the separate launches."""
     from mi355moe import _lib, ops, synthetic
     _say("persistent schedule, stage-split calls")
     n, K, N, T = 32, 1024, 512, 1500
