@@ -612,9 +612,10 @@ static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     d.tok_rows = tok_rows_flag(layer);
     d.contrib_bf16 = (options & MI355MOE_OPT_BF16_CONTRIB) ? 1 : 0;
     d.out_accumulate = (options & MI355MOE_OPT_ACCUMULATE) ? 1 : 0;
-    if ((options & MI355MOE_OPT_PERSISTENT) && (stages & MI355MOE_STAGE_GATEUP) && (stages & MI355MOE_STAGE_DOWN)) {
-        d.sched = w.sched;                            // gate/up and down tiles in one launch
-        d.sched_lag = sched_lag();
+    if (!e4m3 && (stages & MI355MOE_STAGE_GATEUP) && (stages & MI355MOE_STAGE_DOWN)) {
+        d.sched = w.sched;                            // gate/up and down tiles in one launch: forced, or chosen
+        d.sched_lag = sched_lag();                    // by launch_prefill for calls on the 256-row tiles
+        d.sched_force = (options & MI355MOE_OPT_PERSISTENT) ? 1 : 0;
     }
     if (e4m3 && (options & MI355MOE_OPT_DOWN16)) {   // fp16 down operands: no down-input quantisation or its scale
         d.down16 = 1;

@@ -155,9 +155,11 @@ struct PrefillArgs {
     // one-launch schedule (nullptr: separate gate/up and down launches): control words [PF_SCHED_HEAD + S_cap] --
     // the next ticket of queue q at [PF_SCHED_QSTRIDE q] (q < PF_SCHED_QUEUES), the give-up word after them (set
     // when a down item gave up waiting), then from PF_SCHED_HEAD per segment the gate/up items finished -- zeroed by
-    // the gather that starts the call; sched_lag: the schedule's lag in segments of a queue (0: all of them)
+    // the gather that starts the call; sched_lag: the schedule's lag in segments of a queue (0: all of them);
+    // sched_force: always (otherwise launch_prefill takes the schedule for calls on the 256-row tiles only)
     int* sched;
     int sched_lag;
+    int sched_force;
 };
 constexpr int PREFILL_TM = 256;
 constexpr int PF_SCHED_QUEUES = 8;      // ticket queues (one per XCD; segment s in queue s % 8)

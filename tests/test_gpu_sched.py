@@ -11,6 +11,13 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _separate_by_default(monkeypatch):
+    """The reference calls run the separate launches (the library would take the schedule by itself for calls on
+    the 256-row tiles); the calls under test force it with persistent=True."""
+    monkeypatch.setenv("MI355MOE_SCHED", "separate")
+
+
 def _say(*a):
     print(*a, flush=True)
 
@@ -97,3 +104,20 @@ def test_persistent_refused_with_e4m3(cuda):
         ops._p(w), _lib.F32, 4, None, 0, 10.0, ops._p(out), _lib.F32, out.stride(0), ops._p(ws), ws.numel(),
         _lib.PATH_PREFILL, _lib.STAGE_ALL, _lib.OPT_E4M3 | _lib.OPT_PERSISTENT, ops._stream(cuda))
     assert rc == 6                                                # MI355MOE_EUNSUPPORTED, before any launch
+
+
+def test_automatic_choice_equals_separate_launches(cuda, monkeypatch):
+    """Without the option, a call on the 256-row tiles takes the schedule by itself; MI355MOE_SCHED=separate turns
+    that off. Both give the same bits."""
+    from mi355moe import _lib, ops, synthetic
+    _say("automatic one-launch choice")
+    n, K, N, T = 32, 1024, 512, 4000
+    ex = synthetic.calibrated_layer(n, K, N, seed=21, device=cuda, uniform_suh=True)
+    x = synthetic.activations(T, K, seed=22, device=cuda)
+    ids = synthetic.random_ids(T, n, 8, seed=23, device=cuda)
+    w = synthetic.softmax_weights(T, 8, seed=24, device=cuda)
+    ref = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+    monkeypatch.delenv("MI355MOE_SCHED")
+    got = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
