@@ -612,7 +612,7 @@ static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     d.tok_rows = tok_rows_flag(layer);
     d.contrib_bf16 = (options & MI355MOE_OPT_BF16_CONTRIB) ? 1 : 0;
     d.out_accumulate = (options & MI355MOE_OPT_ACCUMULATE) ? 1 : 0;
-    if (!e4m3 && (stages & MI355MOE_STAGE_GATEUP) && (stages & MI355MOE_STAGE_DOWN)) {
+    if ((stages & MI355MOE_STAGE_GATEUP) && (stages & MI355MOE_STAGE_DOWN)) {
         d.sched = w.sched;                            // gate/up and down tiles in one launch: forced, or chosen
         d.sched_lag = sched_lag();                    // by launch_prefill for calls on the 256-row tiles
         d.sched_force = (options & MI355MOE_OPT_PERSISTENT) ? 1 : 0;
@@ -665,7 +665,6 @@ int mi355moe_moe_forward_ids_opt(const mi355moe_exl3_layer* layer, const void* x
         return MI355MOE_EINVAL;
     const bool e4m3 = (options & MI355MOE_OPT_E4M3) != 0;
     if ((options & MI355MOE_OPT_DOWN16) && !e4m3) return MI355MOE_EINVAL;
-    if ((options & MI355MOE_OPT_PERSISTENT) && e4m3) return MI355MOE_EUNSUPPORTED;   // E3 numerics only
     if (e4m3 && path == MI355MOE_PATH_DECODE) return MI355MOE_EINVAL;      // e4m3 numerics run on the grouped tier
     if (e4m3 && layer && layer->hidden > 4096) return MI355MOE_EUNSUPPORTED;
     if (dt_act(x_dtype) < 0 || dt_w(weights_dtype) < 0 || dt_w(out_dtype) < 0) return MI355MOE_EDTYPE;

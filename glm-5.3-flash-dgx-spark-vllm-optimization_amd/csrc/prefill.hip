@@ -81,6 +81,24 @@ __device__ __forceinline__ void pf_store_group(_Float16* grp, const uint32_t (&w
         *reinterpret_cast<u32x4*>(grp + 8 * (c & 1)) = v;
     }
 }
+// Four floats as two device-coherent 8-byte stores / loads (agent-scope relaxed atomics), for rows that
+// workgroups on other XCDs read or wrote in the same launch.
+__device__ __forceinline__ void st_coh_f4(float* p, float x, float y, float z, float w) {
+    uint64_t* d = reinterpret_cast<uint64_t*>(p);
+    __hip_atomic_store(d, (uint64_t)__builtin_bit_cast(uint32_t, x) | ((uint64_t)__builtin_bit_cast(uint32_t, y) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(d + 1,
+                       (uint64_t)__builtin_bit_cast(uint32_t, z) | ((uint64_t)__builtin_bit_cast(uint32_t, w) << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4 ld_coh_f4(const float* p) {
+    uint64_t* d = reinterpret_cast<uint64_t*>(const_cast<float*>(p));
+    const uint64_t v0 = __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t v1 = __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(__builtin_bit_cast(float, (uint32_t)v0), __builtin_bit_cast(float, (uint32_t)(v0 >> 32)),
+                       __builtin_bit_cast(float, (uint32_t)v1), __builtin_bit_cast(float, (uint32_t)(v1 >> 32)));
+}
+
 // The same placement for one byte per element (e4m3 codes): q[m] holds the lane's pair m as two codes in its low 16
 // bits; lane h of the pair of lanes writes storage pairs 4h .. 4h + 3 as 8 contiguous bytes. grp: the 16-group's
 // first byte.
@@ -235,6 +253,8 @@ __device__ __forceinline__ float e4m3_row_scale(float amax) {
 // one byte each, in that order), asc[pos] = s; the row's down-input maximum amaxd[pos] is zeroed for the gate/up
 // epilogue. One wave per row; the whole row (K <= 4096) stays in registers between the amax and the quantization.
 __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
+    if (a.sched && blockIdx.x == 0)                                   // the one-launch schedule's control words
+        for (int i = threadIdx.x; i < PF_SCHED_HEAD + a.S_cap; i += 256) a.sched[i] = 0;
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
     const int nb = a.K >> 7;
@@ -321,41 +341,47 @@ __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
 // The e4m3 variant's down-input quantization: per row, s = amaxd / 448 (the maximum over the whole row, gathered by
 // the gate/up epilogues), h2 = the fp16 of e4m3(clamp(vd / s)) in the permuted order (a8dout: also the codes, one
 // byte each, in that order), dsc[pos] = s. One wave per row, four 128-blocks per pass.
+// One row of it, by one wave. COH: vd and amaxd were written in the same launch (possibly on other XCDs) and h2 is read
+// there: device-coherent loads and stores.
+template <bool COH>
+__device__ __forceinline__ void pf_quantd_row(const PrefillArgs& a, int pos, int lane) {
+    const int c = lane & 15, q = lane >> 4;
+    // the row's expert, maximum and first values are loaded together (a row without an expert is read, not
+    // written), so the row costs one memory latency instead of three
+    const int pe = a.pe[pos];
+    const float amax = __builtin_bit_cast(
+        float, COH ? __hip_atomic_load(a.amaxd + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : a.amaxd[pos]);
+    const float* src = a.vd + (size_t)pos * a.N + 8 * c;
+    const int nb = a.N >> 7;
+    auto ld4 = [&](const float* p) { return COH ? ld_coh_f4(p) : *reinterpret_cast<const float4*>(p); };
+    float4 lo0 = {}, hi0 = {};
+    if (q < nb) {
+        lo0 = ld4(src + q * 128);
+        hi0 = ld4(src + q * 128 + 4);
+    }
+    if (pe < 0) return;
+    const float sc = e4m3_row_scale(amax);
+    _Float16* dst0 = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos * a.N + 16 * (c >> 1);
+    uint8_t* dst8 = a.a8dout + (size_t)pos * a.N + 16 * (c >> 1);
+    for (int blk = q; blk < nb; blk += 4) {
+        const float4 lo = blk == q ? lo0 : ld4(src + blk * 128);
+        const float4 hi = blk == q ? hi0 : ld4(src + blk * 128 + 4);
+        const float w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        uint32_t f8[4], wm[4];
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            f8[mm] = e4m3_quant_f8(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
+            wm[mm] = e4m3_h2(f8[mm]);
+        }
+        pf_store_group<COH>(dst0 + blk * 128, wm, c);
+        if (a.a8dout) pf_store_group8(dst8 + blk * 128, f8, c);
+    }
+    if (lane == 0) a.dsc[pos] = sc;
+}
 __global__ __launch_bounds__(256) void pf_quantd_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
-    const int c = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
-    for (int pos = wave; pos < a.P; pos += gridDim.x * 4) {
-        // the row's expert, maximum and first values are loaded together (a row without an expert is read, not
-        // written), so the row costs one memory latency instead of three
-        const int pe = a.pe[pos];
-        const float amax = __builtin_bit_cast(float, a.amaxd[pos]);
-        const float* src = a.vd + (size_t)pos * a.N + 8 * c;
-        const int nb = a.N >> 7;
-        float4 lo0 = {}, hi0 = {};
-        if (q < nb) {
-            lo0 = *reinterpret_cast<const float4*>(src + q * 128);
-            hi0 = *reinterpret_cast<const float4*>(src + q * 128 + 4);
-        }
-        if (pe < 0) continue;
-        const float sc = e4m3_row_scale(amax);
-        _Float16* dst0 = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos * a.N + 16 * (c >> 1);
-        uint8_t* dst8 = a.a8dout + (size_t)pos * a.N + 16 * (c >> 1);
-        for (int blk = q; blk < nb; blk += 4) {
-            const float4 lo = blk == q ? lo0 : *reinterpret_cast<const float4*>(src + blk * 128);
-            const float4 hi = blk == q ? hi0 : *reinterpret_cast<const float4*>(src + blk * 128 + 4);
-            const float w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-            uint32_t f8[4], wm[4];
-#pragma unroll
-            for (int mm = 0; mm < 4; ++mm) {
-                f8[mm] = e4m3_quant_f8(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
-                wm[mm] = e4m3_h2(f8[mm]);
-            }
-            pf_store_group(dst0 + blk * 128, wm, c);
-            if (a.a8dout) pf_store_group8(dst8 + blk * 128, f8, c);
-        }
-        if (lane == 0) a.dsc[pos] = sc;
-    }
+    for (int pos = wave; pos < a.P; pos += gridDim.x * 4) pf_quantd_row<false>(a, pos, lane);
 }
 
 // ------------------------------------------------------------------------------------------------ GEMM core
@@ -801,8 +827,13 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
                     m = fmaxf(m, xor_lane<8>(m, lane));
                     if (trow[p] < rn) {
                         float* vo = a.vd + (size_t)(row0 + trow[p]) * N + col;
-                        *reinterpret_cast<float4*>(vo) = make_float4(b[p][0], b[p][1], b[p][2], b[p][3]);
-                        *reinterpret_cast<float4*>(vo + 4) = make_float4(b[p][4], b[p][5], b[p][6], b[p][7]);
+                        if (COH) {
+                            st_coh_f4(vo, b[p][0], b[p][1], b[p][2], b[p][3]);
+                            st_coh_f4(vo + 4, b[p][4], b[p][5], b[p][6], b[p][7]);
+                        } else {
+                            *reinterpret_cast<float4*>(vo) = make_float4(b[p][0], b[p][1], b[p][2], b[p][3]);
+                            *reinterpret_cast<float4*>(vo + 4) = make_float4(b[p][4], b[p][5], b[p][6], b[p][7]);
+                        }
                         if (c == 0) atomicMax(a.amaxd + row0 + trow[p], __builtin_bit_cast(unsigned, m));
                     }
                 } else {
@@ -1002,7 +1033,7 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 
 // ------------------------------------------------------------------------------------------------ one-launch schedule
 
-// Every gate/up and down tile of a call (256-row kind, E3 numerics) in one launch of one workgroup per CU. The
+// Every gate/up and down tile of a call (256-row kind) in one launch of one workgroup per CU. The
 // segments are dealt to eight ticket queues (segment s to queue s % 8, as the separate launches deal them to the
 // XCDs), each ordered by pf_sched_item over its own segments; a workgroup takes tickets from its own XCD's queue
 // (the XCC_ID register), so a segment's column blocks share that XCD's L2 for their A rows, and once that queue is
@@ -1015,7 +1046,14 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 // wait is still bounded (PF_SCHED_POLLS polls): one that runs out sets the give-up word, skips its tile, and every
 // later wait gives up at once, so a broken table costs a wrong result, never a hung launch. The tiles run the
 // separate launches' code on the same rows, so the results are bit-identical to theirs.
+// MODE: PF_SCHED_E3 (E3 numerics), PF_SCHED_E4M3_16 (trellis-sourced e4m3 gate/up writing the fp16 down input h2,
+// fp16 down GEMM) or PF_SCHED_E4M3 (the e4m3 gate/up writes the fp32 down input vd and its row maxima amaxd, both
+// device-coherent; the workgroup whose gate/up item completes a segment -- its count reaches ncg -- quantises the
+// segment's rows to h2 and dsc (device-coherent) and adds one more, and the segment's down items, e4m3 GEMMs, wait
+// for ncg + 1: the reference's dataflow, code/fork/kernels/moe_e4m3.cu:867-872).
+enum { PF_SCHED_E3 = 0, PF_SCHED_E4M3_16 = 1, PF_SCHED_E4M3 = 2 };
 constexpr int PF_SCHED_POLLS = 1 << 20;
+template <int MODE>
 __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     // The item's ticket and whether its wait ran out sit in the first LDS words between tiles (the tiles' stages
@@ -1025,6 +1063,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
     int lo, hi;
     pf_seg_range(a, lo, hi);
     const int ns = hi - lo, ncg = a.N >> 7, ncd = a.K >> 8;
+    const int ready_at = ncg + (MODE == PF_SCHED_E4M3 ? 1 : 0);      // a down item's segment count to wait for
     int* ctl = a.sched;
     int* gave_up_word = ctl + PF_SCHED_QUEUES * PF_SCHED_QSTRIDE;
     int* ready = ctl + PF_SCHED_HEAD;
@@ -1046,8 +1085,27 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
             const int s = lo + q + PF_SCHED_QUEUES * it.seg;          // < hi
             if (it.kind == 0) {
                 __syncthreads();                                      // every wave has read s_ctl
-                pf_gateup_tile<false, PF_LARGE, true>(a, s, 0, it.block, smem);   // h2 stored device-coherent
-                WAIT_VM(0);                                           // this wave's h2 stores have completed
+                // h2 (or vd and amaxd) stored device-coherent
+                pf_gateup_tile<MODE != PF_SCHED_E3, PF_LARGE, true>(a, s, 0, it.block, smem);
+                WAIT_VM(0);                                           // this wave's stores have completed
+                __syncthreads();
+                if (MODE != PF_SCHED_E4M3) {
+                    if (threadIdx.x == 0)
+                        __hip_atomic_fetch_add(ready + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    continue;
+                }
+                if (threadIdx.x == 0)
+                    s_ctl[1] = __hip_atomic_fetch_add(ready + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                               ncg - 1;
+                __syncthreads();
+                if (!__builtin_amdgcn_readfirstlane(s_ctl[1])) continue;   // (uniform) not the segment's last
+                // the segment's last gate/up item: every other one's stores completed before its count; quantise
+                // the segment's rows (one wave per row) and publish them with one more count
+                const int r0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
+                if (r0 >= 0 && rn > 0 && r0 + rn <= a.P)             // (caller-built tables)
+                    for (int r = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); r < rn; r += PF_THREADS / 64)
+                        pf_quantd_row<true>(a, r0 + r, threadIdx.x & 63);
+                WAIT_VM(0);
                 __syncthreads();
                 if (threadIdx.x == 0)
                     __hip_atomic_fetch_add(ready + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1055,7 +1113,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
             }
             if (threadIdx.x == 0) {
                 for (int polls = 0;
-                     __hip_atomic_load(ready + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ncg; ++polls) {
+                     __hip_atomic_load(ready + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ready_at; ++polls) {
                     if (polls >= PF_SCHED_POLLS ||
                         __hip_atomic_load(gave_up_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
                         __hip_atomic_store(gave_up_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1069,7 +1127,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
             const int gave_up = __builtin_amdgcn_readfirstlane(s_ctl[1]);
             __syncthreads();                                          // every wave has read s_ctl
             if (gave_up) continue;                                    // (uniform) the tile is skipped
-            pf_down_tile<false, PF_LARGE, true>(a, s, 0, it.block, smem);   // h2 loaded device-coherent
+            pf_down_tile<MODE == PF_SCHED_E4M3, PF_LARGE, true>(a, s, 0, it.block, smem);   // h2 device-coherent
         }
     }
 }
@@ -1448,9 +1506,11 @@ int prefill_setup() {
                           reinterpret_cast<const void*>(pf_down_mid_kernel<true>)};
     for (const void* k : ksm)
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_M) != hipSuccess) return -1;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(pf_sched_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)PF_LDS) != hipSuccess)
-        return -1;
+    const void* ksc[3] = {reinterpret_cast<const void*>(pf_sched_kernel<PF_SCHED_E3>),
+                          reinterpret_cast<const void*>(pf_sched_kernel<PF_SCHED_E4M3_16>),
+                          reinterpret_cast<const void*>(pf_sched_kernel<PF_SCHED_E4M3>)};
+    for (const void* k : ksc)
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS) != hipSuccess) return -1;
     g_pf_attr = true;
     return 0;
 }
@@ -1506,18 +1566,27 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     const dim3 gum(8 * (a.N / 128) * sgm), dnm(8 * (a.K / 256) * sgm);
     const int tiles = pf_tiles(a0);
     a.small_rows = tiles == PF_TILES_BOTH ? PF_SMALL_ROWS : 0;
-    if (a.sched && a.sched_force && (f8 || (kernels & 7) != 7)) return -1;   // E3, after this call's gather
-    // The one-launch schedule: when forced, or for E3 calls on the 256-row tiles that run gather, gate/up and down
-    // (measured at T = 8192, 288 experts: 0-3 % faster than the separate launches with uniform routing, within
-    // +-0.7 % with Zipf routing; bit-identical). MI355MOE_SCHED=separate turns the automatic choice off.
+    // The one-launch schedule, for calls that run gather, gate/up and down (and, e4m3, the down-input quantisation):
+    // when forced, or for E3 and e4m3-DOWN16 calls on the 256-row tiles (measured at T = 8192, 288 experts: E3 0-3 %
+    // faster than the separate launches with uniform routing, within +-0.7 % with Zipf routing; DOWN16 4 % faster;
+    // bit-identical). Not chosen by itself for the e4m3 down GEMM, whose in-launch quantisation (one workgroup per
+    // segment) made the T = 8192 call 2 % slower. MI355MOE_SCHED=separate turns the automatic choice off.
+    const bool sched_ok = (kernels & 7) == 7 && !(kernels & PF_NO_QUANTD);
+    if (a.sched && a.sched_force && !sched_ok) return -1;
     const char* sched_env = getenv("MI355MOE_SCHED");
-    const bool sched = a.sched && (a.sched_force || (!f8 && (kernels & 7) == 7 && tiles == PF_TILES_LARGE &&
-                                                     !(sched_env && !strcmp(sched_env, "separate"))));
+    const bool sched_auto = tiles == PF_TILES_LARGE && !(f8 && !a.down16) &&
+                            !(sched_env && !strcmp(sched_env, "separate"));
+    const bool sched = a.sched && sched_ok && (a.sched_force || sched_auto);
     if (sched) {
         a.small_rows = 0;
         const int64_t items = (int64_t)std::max(a.S_cap, 0) * ((a.N >> 7) + (a.K >> 8));
         const int grid = (int)std::min<int64_t>(pf_device_cus(), items);
-        if (grid > 0) hipLaunchKernelGGL(pf_sched_kernel, dim3(grid), dim3(PF_THREADS), PF_LDS, st, a);
+        if (grid > 0) {
+            if (!f8) hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E3>, dim3(grid), dim3(PF_THREADS), PF_LDS, st, a);
+            else if (a.down16)
+                hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E4M3_16>, dim3(grid), dim3(PF_THREADS), PF_LDS, st, a);
+            else hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E4M3>, dim3(grid), dim3(PF_THREADS), PF_LDS, st, a);
+        }
         kernels &= ~6;
     }
     if (kernels & 2) {

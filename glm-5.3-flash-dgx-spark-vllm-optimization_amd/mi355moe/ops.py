@@ -232,8 +232,8 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
     stages: a subset of the call's launches (_lib.STAGE_*), for timing one kernel; the default runs them all.
     bf16_contrib: the grouped path keeps its per-pair down accumulators in bf16 (half the contribution traffic;
     code/fork/docs/OPT_MOE.md:13). persistent: the grouped path's gate/up and down tiles in one launch, taken in
-    ticket order with per-segment dataflow counts (code/fork/kernels/moe_e4m3.cu:867-897; E3 numerics; results
-    bit-identical to the separate launches)."""
+    ticket order with per-segment dataflow counts (code/fork/kernels/moe_e4m3.cu:867-897), whatever the call's size
+    (calls on the 256-row tiles take it by themselves); results bit-identical to the separate launches."""
     if accumulate and out is None:
         raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
@@ -313,13 +313,16 @@ def moe_forward_ids_split(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch
 def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
                          limit: float = 10.0, expert_map: torch.Tensor | None = None, out: torch.Tensor | None = None,
                          out_dtype: torch.dtype | None = None, stages: int = _lib.STAGE_ALL,
-                         accumulate: bool = False, bf16_contrib: bool = False, down16: bool = False) -> torch.Tensor:
+                         accumulate: bool = False, bf16_contrib: bool = False, down16: bool = False,
+                         persistent: bool = False) -> torch.Tensor:
     """The trellis-sourced e4m3 variant of the routed experts (code/fork/overlay/glm53_moe_e4m3.py:484-592 run(),
     numerics of spec_ffn :666-674): activations quantized per row to e4m3 after the input rotation, EXL3 weights
     rounded to e4m3, fp32 sums; output [T, K] written like moe_forward_ids. The layer needs gate and up sharing one
     suh and hidden <= 4096. accumulate / bf16_contrib: the ACC=bf16 and FOLD_SHARED knobs (code/fork/docs/
     OPT_MOE.md:9-21) as in moe_forward_ids. down16: the down projection on fp16 operands (DOWN16, spec_proj16
-    :660-664) instead of e4m3."""
+    :660-664) instead of e4m3. persistent: the one-launch ticket-ordered gate/up -> down schedule (SCHED mode
+    "fused", code/fork/kernels/moe_e4m3.cu:867-897) whatever the call's size (calls on the 256-row tiles take it by
+    themselves); bit-identical to the separate launches."""
     if accumulate and out is None:
         raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
@@ -343,9 +346,10 @@ def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.
         raise ValueError("mi355moe_e4m3_moe_workspace_bytes rejected the shape")
     ws = workspace(dev, nb)
     em = None if expert_map is None else expert_map.to(torch.int64).contiguous()
-    if accumulate or bf16_contrib or down16:
+    if accumulate or bf16_contrib or down16 or persistent:
         opts = (_lib.OPT_E4M3 | (_lib.OPT_ACCUMULATE if accumulate else 0) |
-                (_lib.OPT_BF16_CONTRIB if bf16_contrib else 0) | (_lib.OPT_DOWN16 if down16 else 0))
+                (_lib.OPT_BF16_CONTRIB if bf16_contrib else 0) | (_lib.OPT_DOWN16 if down16 else 0) |
+                (_lib.OPT_PERSISTENT if persistent else 0))
         _lib.check("mi355moe_moe_forward_ids_opt", L.mi355moe_moe_forward_ids_opt(
             ctypes.byref(experts.desc), _p(x), act_dtype_code(x.dtype), x.stride(0), T, _p(ids),
             ids_dtype_code(ids.dtype), _p(w), weight_dtype_code(w.dtype), topk, _p(em),

@@ -178,11 +178,12 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
  *   MI355MOE_OPT_PERSISTENT   the grouped path's gate/up and down tiles in one launch of one workgroup per compute
  *                             unit, ticket-ordered with per-segment dataflow counts (the reference's fused schedule,
  *                             code/fork/kernels/moe_e4m3.cu:867-897; item order: mi355moe_sched_item), whatever the
- *                             call's size. Without the option the library takes this schedule by itself for E3 calls
- *                             on the 256-row tiles (the environment variable MI355MOE_SCHED=separate turns that off).
- *                             Applies when the call runs both stages (MI355MOE_STAGE_GATEUP and MI355MOE_STAGE_DOWN)
- *                             on the grouped path; results are bit-identical to the separate launches. E3 numerics
- *                             only: with MI355MOE_OPT_E4M3 the call returns MI355MOE_EUNSUPPORTED before any launch.
+ *                             call's size. Without the option the library takes this schedule by itself for E3 and
+ *                             MI355MOE_OPT_DOWN16 calls on the 256-row tiles (the environment variable
+ *                             MI355MOE_SCHED=separate turns that off). Applies when the call runs both stages
+ *                             (MI355MOE_STAGE_GATEUP and MI355MOE_STAGE_DOWN) on the grouped path; results are
+ *                             bit-identical to the separate launches. With MI355MOE_OPT_E4M3 (e4m3 down GEMM) the
+ *                             workgroup finishing a segment's gate/up items quantises its down inputs in the launch.
  *                             The lag (in segments of one of its eight queues) is read from the environment variable
  *                             MI355MOE_SCHED_LAG (default 0 = all of a queue's gate/up items first).
  * Unknown bits: MI355MOE_EINVAL. Workspace sizes as mi355moe_moe_workspace_bytes_path (with MI355MOE_OPT_E4M3:

@@ -88,8 +88,6 @@ def test_forward_options_are_checked_before_any_launch():
     args = [ctypes.byref(d), p, _lib.BF16, 1024, 4, p, _lib.I32, p, _lib.F32, 8, None, 0, 10.0, p, _lib.BF16, 1024,
             p, 1 << 30]
     assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_AUTO, _lib.STAGE_ALL, 16, None) == 1         # unknown bit
-    assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_AUTO, _lib.STAGE_ALL,
-                                          _lib.OPT_E4M3 | _lib.OPT_PERSISTENT, None) == 6   # one-launch: E3 only
     assert L.mi355moe_moe_forward_ids_opt(*args, _lib.PATH_DECODE, _lib.STAGE_ALL, _lib.OPT_E4M3, None) == 1
 
 

@@ -1,8 +1,8 @@
 """GPU checks of the one-launch schedule of the grouped path (MI355MOE_OPT_PERSISTENT): gate/up and down tiles taken
 from one ticket counter, a down tile waiting on its segment's gate/up count. Same tile code, so the output equals
 the separate launches' bit for bit: uniform and Zipf routing, full size, fewer segments than compute units, one-block
-routing, bf16 accumulators, lags that make down tiles wait, and stage-split calls (the call's gather zeroes the
-control words)."""
+routing, bf16 accumulators, lags that make down tiles wait, stage-split calls (the call's gather zeroes the
+control words), and the trellis-sourced e4m3 variant with its down-input quantisation inside the launch."""
 from __future__ import annotations
 
 import pytest
@@ -89,21 +89,45 @@ def test_persistent_stage_split_calls(cuda):
         assert torch.equal(out, ref)
 
 
-def test_persistent_refused_with_e4m3(cuda):
-    from mi355moe import _lib, ops, synthetic
-    ex = synthetic.calibrated_layer(8, 1024, 256, seed=1, device=cuda)
-    x = synthetic.activations(64, 1024, seed=2, device=cuda)
-    ids = synthetic.random_ids(64, 8, 4, seed=3, device=cuda)
-    w = synthetic.softmax_weights(64, 4, seed=4, device=cuda)
-    out = torch.empty(64, 1024, dtype=torch.float32, device=cuda)
-    L = _lib.lib()
-    import ctypes
-    ws = ops.workspace(cuda, L.mi355moe_e4m3_moe_workspace_bytes(ctypes.byref(ex.desc), 64, 4))
-    rc = L.mi355moe_moe_forward_ids_opt(
-        ctypes.byref(ex.desc), ops._p(x), ops.act_dtype_code(x.dtype), x.stride(0), 64, ops._p(ids), _lib.I32,
-        ops._p(w), _lib.F32, 4, None, 0, 10.0, ops._p(out), _lib.F32, out.stride(0), ops._p(ws), ws.numel(),
-        _lib.PATH_PREFILL, _lib.STAGE_ALL, _lib.OPT_E4M3 | _lib.OPT_PERSISTENT, ops._stream(cuda))
-    assert rc == 6                                                # MI355MOE_EUNSUPPORTED, before any launch
+@pytest.mark.parametrize("n,K,N,T,routing,down16", [(16, 1024, 512, 700, "uniform", False),
+                                                    (16, 1024, 512, 700, "uniform", True),
+                                                    (64, 1024, 512, 4096, "zipf", False),
+                                                    (4, 1024, 256, 20, "uniform", False),
+                                                    (288, 4096, 1024, 8192, "uniform", False)])
+def test_persistent_e4m3_equals_separate_launches(cuda, n, K, N, T, routing, down16):
+    """The trellis-sourced e4m3 variant: the segment's last gate/up item quantises its rows' down inputs in the same
+    launch (or, DOWN16, the gate/up items write the fp16 down input directly)."""
+    from mi355moe import ops, synthetic
+    _say(f"persistent schedule e4m3 n={n} K={K} N={N} T={T} {routing} down16={down16}")
+    ex = synthetic.calibrated_layer(n, K, N, seed=n + T + 1, device=cuda, uniform_suh=True)
+    topk = min(8, n)
+    x = synthetic.activations(T, K, seed=T + 5, device=cuda)
+    ids = (synthetic.zipf_ids(T, n, topk, seed=T + 6, device=cuda) if routing == "zipf" else
+           synthetic.random_ids(T, n, topk, seed=T + 6, device=cuda))
+    w = synthetic.softmax_weights(T, topk, seed=T + 7, device=cuda)
+    ref = ops.moe_forward_ids_e4m3(ex, x, ids, w, out_dtype=torch.float32, down16=down16)
+    for _ in range(2):
+        got = ops.moe_forward_ids_e4m3(ex, x, ids, w, out_dtype=torch.float32, down16=down16, persistent=True)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got).all()
+        assert torch.equal(got, ref), (got - ref).abs().max().item()
+
+
+@pytest.mark.parametrize("lag", [1, 4])
+def test_persistent_e4m3_lag_waits(cuda, lag, monkeypatch):
+    """Small lags make the down items wait on segments whose quantisation runs in the same launch."""
+    from mi355moe import ops, synthetic
+    _say(f"persistent schedule e4m3, lag {lag}")
+    monkeypatch.setenv("MI355MOE_SCHED_LAG", str(lag))
+    n, K, N, T = 48, 2048, 512, 3000
+    ex = synthetic.calibrated_layer(n, K, N, seed=31, device=cuda, uniform_suh=True)
+    x = synthetic.activations(T, K, seed=32, device=cuda)
+    ids = synthetic.zipf_ids(T, n, 8, seed=33, device=cuda)
+    w = synthetic.softmax_weights(T, 8, seed=34, device=cuda)
+    ref = ops.moe_forward_ids_e4m3(ex, x, ids, w, out_dtype=torch.float32)
+    got = ops.moe_forward_ids_e4m3(ex, x, ids, w, out_dtype=torch.float32, persistent=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref), (got - ref).abs().max().item()
 
 
 def test_automatic_choice_equals_separate_launches(cuda, monkeypatch):
