@@ -378,6 +378,56 @@ __device__ __forceinline__ void pf_quantd_row(const PrefillArgs& a, int pos, int
     }
     if (lane == 0) a.dsc[pos] = sc;
 }
+// Rows pos0, pos0 + step, ... (R of them, below end) by one wave, device-coherent, with every row's maximum and values
+// loaded before the first is quantised (one memory latency for the R rows; N <= 1024: two 128-blocks per lane).
+template <int R>
+__device__ __forceinline__ void pf_quantd_rows_coh(const PrefillArgs& a, int pos0, int step, int end, int lane) {
+    const int c = lane & 15, q = lane >> 4;
+    const int nb = a.N >> 7;
+    int pos[R], pe[R];
+    float amax[R];
+    float4 v[R][4];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        pos[r] = min(pos0 + r * step, end - 1);
+        pe[r] = pos0 + r * step < end ? a.pe[pos[r]] : -1;
+        amax[r] = __builtin_bit_cast(float, __hip_atomic_load(a.amaxd + pos[r], __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT));
+        const float* src = a.vd + (size_t)pos[r] * a.N + 8 * c;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int blk = q + 4 * j;
+            v[r][2 * j] = v[r][2 * j + 1] = float4{};
+            if (blk < nb) {
+                v[r][2 * j] = ld_coh_f4(src + blk * 128);
+                v[r][2 * j + 1] = ld_coh_f4(src + blk * 128 + 4);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (pe[r] < 0) continue;                                      // (uniform)
+        const float sc = e4m3_row_scale(amax[r]);
+        _Float16* dst0 = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos[r] * a.N + 16 * (c >> 1);
+        uint8_t* dst8 = a.a8dout + (size_t)pos[r] * a.N + 16 * (c >> 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int blk = q + 4 * j;
+            if (blk >= nb) continue;
+            const float w[8] = {v[r][2 * j].x, v[r][2 * j].y, v[r][2 * j].z, v[r][2 * j].w,
+                                v[r][2 * j + 1].x, v[r][2 * j + 1].y, v[r][2 * j + 1].z, v[r][2 * j + 1].w};
+            uint32_t f8[4], wm[4];
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) {
+                f8[mm] = e4m3_quant_f8(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
+                wm[mm] = e4m3_h2(f8[mm]);
+            }
+            pf_store_group<true>(dst0 + blk * 128, wm, c);
+            if (a.a8dout) pf_store_group8(dst8 + blk * 128, f8, c);
+        }
+        if (lane == 0) a.dsc[pos[r]] = sc;
+    }
+}
 __global__ __launch_bounds__(256) void pf_quantd_kernel(PrefillArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
@@ -1102,9 +1152,15 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
                 // the segment's last gate/up item: every other one's stores completed before its count; quantise
                 // the segment's rows (one wave per row) and publish them with one more count
                 const int r0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
-                if (r0 >= 0 && rn > 0 && r0 + rn <= a.P)             // (caller-built tables)
-                    for (int r = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); r < rn; r += PF_THREADS / 64)
-                        pf_quantd_row<true>(a, r0 + r, threadIdx.x & 63);
+                constexpr int QR = 4;                                 // rows in flight per wave
+                const int w0 = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+                if (r0 >= 0 && rn > 0 && r0 + rn <= a.P) {           // (caller-built tables)
+                    if (a.N <= 1024)
+                        for (int r = w0; r < rn; r += QR * (PF_THREADS / 64))
+                            pf_quantd_rows_coh<QR>(a, r0 + r, PF_THREADS / 64, r0 + rn, threadIdx.x & 63);
+                    else
+                        for (int r = w0; r < rn; r += PF_THREADS / 64) pf_quantd_row<true>(a, r0 + r, threadIdx.x & 63);
+                }
                 WAIT_VM(0);
                 __syncthreads();
                 if (threadIdx.x == 0)
@@ -1570,7 +1626,7 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     // when forced, or for E3 and e4m3-DOWN16 calls on the 256-row tiles (measured at T = 8192, 288 experts: E3 0-3 %
     // faster than the separate launches with uniform routing, within +-0.7 % with Zipf routing; DOWN16 4 % faster;
     // bit-identical). Not chosen by itself for the e4m3 down GEMM, whose in-launch quantisation (one workgroup per
-    // segment) made the T = 8192 call 2 % slower. MI355MOE_SCHED=separate turns the automatic choice off.
+    // segment) made the T = 8192 call 1.5 % slower. MI355MOE_SCHED=separate turns the automatic choice off.
     const bool sched_ok = (kernels & 7) == 7 && !(kernels & PF_NO_QUANTD);
     if (a.sched && a.sched_force && !sched_ok) return -1;
     const char* sched_env = getenv("MI355MOE_SCHED");

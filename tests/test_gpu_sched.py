@@ -93,6 +93,7 @@ def test_persistent_stage_split_calls(cuda):
                                                     (16, 1024, 512, 700, "uniform", True),
                                                     (64, 1024, 512, 4096, "zipf", False),
                                                     (4, 1024, 256, 20, "uniform", False),
+                                                    (8, 1024, 2048, 600, "uniform", False),
                                                     (288, 4096, 1024, 8192, "uniform", False)])
 def test_persistent_e4m3_equals_separate_launches(cuda, n, K, N, T, routing, down16):
     """The trellis-sourced e4m3 variant: the segment's last gate/up item quantises its rows' down inputs in the same
