@@ -627,8 +627,8 @@ constexpr unsigned RR_GROUPS = 15;   // arrival groups (control words 64 (g + 1)
 // The whole decode-size front end in one launch: the router GEMV (RR_EXPERTS experts per workgroup, logits_body, which
 // also applies the sigmoid so the ranking workgroup only loads scores), then the
 // workgroup that finishes last (arrival counters at fixed workspace offsets, returned to zero by the arrivals that
-// complete them) runs topk_route_body over all logits. Logits cross workgroups, and XCDs with their own L2, as device-coherent stores and loads; a workgroup
-// arrives only after its stores have completed.
+// complete them) runs topk_route_body over all logits. Logits cross workgroups, and XCDs with their own L2, as
+// device-coherent stores and loads; a workgroup arrives only after its stores have completed.
 template <int J, int MAXT = 1024>
 __global__ __launch_bounds__(MAXT) void router_route_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
                                                             const uint16_t* __restrict__ w, int T, int K, int E,
@@ -658,7 +658,9 @@ __global__ __launch_bounds__(MAXT) void router_route_kernel(const uint16_t* __re
     }
     __syncthreads();
     if (!last) return;
-    acquire_agent();
+    // no acquire fence: the only data other workgroups wrote here are the scores, stored device-coherent and complete
+    // before their arrivals, and the ranking loads them device-coherent (from the coherence point, never from a line
+    // this CU's or XCD's caches hold)
     if (threadIdx.x == 0) *arrivals = 0u;
     topk_route_body<J, true, true>(logits, T, E, bias, topk, scale, renorm, ids, wts, a, sh);
 }
