@@ -269,25 +269,6 @@ __device__ __forceinline__ int ld_coherent(const int* p) {
     return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Acquire side of a last-arrival election, run by every thread of the elected workgroup after the barrier that
-// published the election: agent-scope acquire (invalidates this CU's and XCD's non-coherent cached lines), so the
-// loads that follow observe every store the other workgroups completed before they arrived.
-__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
-
-// Returns true in the workgroup that completes counter `c` (the `total`-th arrival); it then resets the counter.
-// Every thread's coherent stores are complete (s_waitcnt) before its workgroup arrives, and the elected workgroup
-// acquires before it reads them.
-__device__ __forceinline__ bool arrive_last(unsigned* c, unsigned total, int* flag) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        *flag = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
-    __syncthreads();
-    if (*flag == 0) return false;
-    acquire_agent();
-    return true;
-}
-
 // ---------------------------------------------------------------------------------------------- LDS staging
 
 // Wave instruction: 64 lanes x 16 bytes, lane l -> LDS bytes lds_wave + 16 l (global_load_lds_dwordx4). Written as

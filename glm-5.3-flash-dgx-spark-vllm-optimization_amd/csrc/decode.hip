@@ -275,8 +275,8 @@ constexpr int ZS_ROWS = 16;
 
 // Arrival of a tile fragment of `len` chunks whose partial sums went to slot `slot`: one 64-bit atomic adds len to
 // the tile's chunk count (bits 0-31) and the slot's bit (bits 32-63). Returns true in the workgroup whose fragment
-// completes the tile's `total` chunks, with *mask = the slots of every fragment (every fragment's stores completed
-// before it arrived; the elected workgroup acquires before reading them).
+// completes the tile's `total` chunks, with *mask = the slots of every fragment (every fragment's device-coherent
+// stores completed before it arrived, and the elected workgroup loads them device-coherent, so no fence is needed).
 __device__ __forceinline__ bool arrive_fragment(unsigned long long* c, unsigned len, int slot, unsigned total,
                                                 unsigned* mask, int* flag) {
     __builtin_amdgcn_s_waitcnt(0);
@@ -289,9 +289,7 @@ __device__ __forceinline__ bool arrive_fragment(unsigned long long* c, unsigned 
         *mask = (unsigned)(now >> 32);
     }
     __syncthreads();
-    if (*flag == 0) return false;
-    acquire_agent();
-    return true;
+    return *flag != 0;
 }
 
 // 512 threads: workgroup = 128 gate and up columns of one segment over one K range [kc0, kc1) in chunks of kch_gu;
