@@ -1083,6 +1083,7 @@ struct RowsWs {
     float* dsc;
     int* tok32;
     uint16_t* h13;
+    int* sched;             // e4m3: the one-launch schedule's control words [PF_SCHED_HEAD + rows] (segments <= rows)
     size_t bytes;
 };
 RowsWs carve_rows(void* ws, int64_t rows, int64_t K, int64_t N, int64_t tokens, bool e4m3) {
@@ -1100,6 +1101,7 @@ RowsWs carve_rows(void* ws, int64_t rows, int64_t K, int64_t N, int64_t tokens, 
         w.dsc = c.take<float>(std::max<int64_t>(1, rows));
         w.tok32 = c.take<int>(std::max<int64_t>(1, rows));
         w.h13 = c.take<uint16_t>((size_t)std::max<int64_t>(1, std::max(rows, tokens)) * K);
+        w.sched = c.take<int>((size_t)PF_SCHED_HEAD + std::max<int64_t>(1, rows));
     }
     w.bytes = c.off;
     return w;
@@ -1430,6 +1432,10 @@ int mi355moe_e4m3_fused(const uint8_t* a8, const float* asc, int64_t a8_rows, ui
     rp.a8_all = tok_rows ? 1 : 0;
     rp.a8_dst = w.h13;
     rp.kernels = 2 | 4;
+    if (seg_cap <= rows_cap) {                        // the one-launch schedule where the tile choice takes it
+        a.sched = w.sched;                            // (zeroed by the row-table setup)
+        a.sched_lag = sched_lag();
+    }
     return rc_launch(launch_prefill_rows(a, rp, stream));
 }
 

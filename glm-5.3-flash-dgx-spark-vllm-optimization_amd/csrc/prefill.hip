@@ -1357,6 +1357,8 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
 // tok32 (optional): tok32[r] = row_token[r] as int32, 0 where it lies outside [0, tokens).
 __global__ __launch_bounds__(256) void pf_rows_init_kernel(PrefillArgs a, int* pe, int* cnt, int tokens, int* tok32,
                                                            const int64_t* row_token) {
+    if (a.sched && blockIdx.x == 0)                                   // the one-launch schedule's control words
+        for (int i = threadIdx.x; i < PF_SCHED_HEAD + a.S_cap; i += 256) a.sched[i] = 0;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < max(a.P, tokens); i += gridDim.x * 256) {
         if (i < a.P) {
             pe[i] = -1;
@@ -1622,12 +1624,13 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     const dim3 gum(8 * (a.N / 128) * sgm), dnm(8 * (a.K / 256) * sgm);
     const int tiles = pf_tiles(a0);
     a.small_rows = tiles == PF_TILES_BOTH ? PF_SMALL_ROWS : 0;
-    // The one-launch schedule, for calls that run gather, gate/up and down (and, e4m3, the down-input quantisation):
+    // The one-launch schedule, for calls that run gate/up and down (and, e4m3, the down-input quantisation):
     // when forced, or for E3 and e4m3-DOWN16 calls on the 256-row tiles (measured at T = 8192, 288 experts: E3 0-3 %
     // faster than the separate launches with uniform routing, within +-0.7 % with Zipf routing; DOWN16 4 % faster;
     // bit-identical). Not chosen by itself for the e4m3 down GEMM, whose in-launch quantisation (one workgroup per
     // segment) made the T = 8192 call 1.5 % slower. MI355MOE_SCHED=separate turns the automatic choice off.
-    const bool sched_ok = (kernels & 7) == 7 && !(kernels & PF_NO_QUANTD);
+    // (the control words are zeroed by the call's gather or, on row tables, by the row-table setup)
+    const bool sched_ok = (kernels & 6) == 6 && !(kernels & PF_NO_QUANTD);
     if (a.sched && a.sched_force && !sched_ok) return -1;
     const char* sched_env = getenv("MI355MOE_SCHED");
     const bool sched_auto = tiles == PF_TILES_LARGE && !(f8 && !a.down16) &&

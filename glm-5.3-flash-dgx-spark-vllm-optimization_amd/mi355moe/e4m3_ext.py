@@ -18,7 +18,8 @@ fp16 staging copies of the code rows live in the library's scratch workspace for
   fused                    gateup + actq + down of every segment; a8d / dsc / a16 written when given
   plan / run               the overlay's routing tables (on the device) and its schedule on an Exl3Experts layer
 
-Schedule knobs of the reference's persistent kernel (lag, grid, sync) have no counterpart and are accepted unused.
+The per-call knobs of the reference's persistent kernel (lag, grid, sync) are accepted unused: fused() takes the
+library's one-launch schedule by itself where it pays (its lag from the environment variable MI355MOE_SCHED_LAG).
 """
 from __future__ import annotations
 
@@ -230,7 +231,9 @@ def fused(a8, asc, a8d, dsc, a16, out, gate_ptrs, up_ptrs, gate_svh, up_svh, dow
     """Gate/up, the down input's per-row quantisation and the down GEMM of every segment, then out[token] += the
     token's rows in row order (moe_e4m3.cu:2721-2725; out fp32 or bf16). a8d / dsc and a16 receive the intermediates
     when given (a16 also gives the intermediate size, else `intermediate`). variant: TOKEN_ROWS (a8 / asc from
-    gather_tok), DOWN16 (fp16 down operands; a8d / dsc not written), LEAN_MAINLOOP (accepted)."""
+    gather_tok), DOWN16 (fp16 down operands; a8d / dsc not written), LEAN_MAINLOOP (accepted). Calls on the 256-row
+    tiles with DOWN16 run gate/up and down as one ticket-ordered launch by themselves (lag: the environment variable
+    MI355MOE_SCHED_LAG); the reference's per-call sync, lag and grid are accepted unused."""
     del sync, lag, grid
     N = int(intermediate) if intermediate else (int(a16.shape[1]) if a16 is not None else 0)
     if N <= 0:

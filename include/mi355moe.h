@@ -339,7 +339,9 @@ int mi355moe_e3_down(const void* h2, int64_t rows_cap, int64_t K, int64_t N, int
  *   MI355MOE_E4M3_DOWN16: the down projection on fp16 operands (h = fp16(H(float(a16) * suh_d) * r) times the
  *   fp16 W_q, the extension's variant 16, spec_proj16 at glm53_moe_e4m3.py:660-664); a8d / dsc are not written;
  *   MI355MOE_E4M3_LEAN_MAINLOOP (the extension's +8192 schedule variant): accepted, same results.
- *   The reference's lag / grid / sync arguments schedule its persistent kernel and have no counterpart here.
+ *   mi355moe_e4m3_fused runs gate/up and down as one ticket-ordered launch (MI355MOE_OPT_PERSISTENT's schedule) by
+ *   itself when the row tables pick the 256-row tiles, DOWN16 is set and seg_cap <= rows_cap; the lag comes from
+ *   MI355MOE_SCHED_LAG. The reference's per-call lag / grid / sync arguments have no counterpart.
  * The stages that take a workspace share one size, mi355moe_e4m3_stage_workspace_bytes(rows_cap, K, N, tokens). */
 enum { MI355MOE_E4M3_DOWN16 = 16, MI355MOE_E4M3_TOKEN_ROWS = 2048, MI355MOE_E4M3_LEAN_MAINLOOP = 8192 };
 int64_t mi355moe_e4m3_tile_rows(void);

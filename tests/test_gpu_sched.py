@@ -146,3 +146,22 @@ def test_automatic_choice_equals_separate_launches(cuda, monkeypatch):
     got = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("down16", [False, True])
+def test_e4m3_extension_fused_takes_the_schedule(cuda, monkeypatch, down16):
+    """The e4m3 extension's fused entry over its row tables: a call on the 256-row tiles runs the one-launch schedule
+    by itself (DOWN16) and gives the separate launches' bits; the e4m3 down GEMM keeps the separate launches."""
+    from mi355moe import e4m3_ext, synthetic
+    _say(f"e4m3 extension fused, one-launch schedule, down16={down16}")
+    n, K, N, T = 8, 1024, 512, 600
+    ex = synthetic.calibrated_layer(n, K, N, seed=41, device=cuda, uniform_suh=True)
+    x = synthetic.activations(T, K, seed=42, device=cuda)
+    ids = synthetic.random_ids(T, n, 8, seed=43, device=cuda)
+    w = synthetic.softmax_weights(T, 8, seed=44, device=cuda)
+    ref = e4m3_ext.run(x, ids, w, ex, 10.0, sched={"down16": down16})
+    monkeypatch.delenv("MI355MOE_SCHED")
+    for _ in range(2):
+        got = e4m3_ext.run(x, ids, w, ex, 10.0, sched={"down16": down16})
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
