@@ -165,3 +165,43 @@ def test_e4m3_extension_fused_takes_the_schedule(cuda, monkeypatch, down16):
         got = e4m3_ext.run(x, ids, w, ex, 10.0, sched={"down16": down16})
         torch.cuda.synchronize()
         assert torch.equal(got, ref)
+
+
+def _random_cases(count=14, seed=2026):
+    import random
+    rnd = random.Random(seed)
+    out = []
+    for i in range(count):
+        n = rnd.choice([2, 3, 5, 8, 13, 24, 40, 64])
+        K = 256 * rnd.randint(1, 8)
+        N = 128 * rnd.randint(1, 8)
+        T = rnd.randint(1, 1500)
+        out.append((i, n, K, N, T, rnd.choice(["uniform", "zipf"]), rnd.choice(["e3", "e4m3", "down16"]),
+                    rnd.random() < 0.3, rnd.choice([0, 1, 2, 5])))
+    return out
+
+
+@pytest.mark.parametrize("i,n,K,N,T,routing,numerics,b16,lag", _random_cases())
+def test_persistent_random_shapes(cuda, monkeypatch, i, n, K, N, T, routing, numerics, b16, lag):
+    """Seeded ragged shapes (hidden 256..2048, intermediate 128..1024, 1..1500 tokens, 2..64 experts, lags 0..5):
+    the forced one-launch schedule gives the separate launches' bits in every numerics."""
+    from mi355moe import _lib, ops, synthetic
+    _say(f"random case {i}: n={n} K={K} N={N} T={T} {routing} {numerics} bf16={b16} lag={lag}")
+    monkeypatch.setenv("MI355MOE_SCHED_LAG", str(lag))
+    ex = synthetic.calibrated_layer(n, K, N, seed=100 + i, device=cuda, uniform_suh=(i % 2 == 0))
+    topk = min(8, n)
+    x = synthetic.activations(T, K, seed=200 + i, device=cuda)
+    ids = (synthetic.zipf_ids(T, n, topk, seed=300 + i, device=cuda) if routing == "zipf" else
+           synthetic.random_ids(T, n, topk, seed=300 + i, device=cuda))
+    w = synthetic.softmax_weights(T, topk, seed=400 + i, device=cuda)
+    if numerics == "e3":
+        call = lambda pers: ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL,
+                                                bf16_contrib=b16, persistent=pers)
+    else:
+        call = lambda pers: ops.moe_forward_ids_e4m3(ex, x, ids, w, out_dtype=torch.float32, bf16_contrib=b16,
+                                                     down16=numerics == "down16", persistent=pers)
+    ref = call(False)
+    got = call(True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, ref), (got - ref).abs().max().item()
