@@ -205,3 +205,35 @@ def test_persistent_random_shapes(cuda, monkeypatch, i, n, K, N, T, routing, num
     torch.cuda.synchronize()
     assert torch.isfinite(got).all()
     assert torch.equal(got, ref), (got - ref).abs().max().item()
+
+
+def test_schedule_in_a_replayed_graph(cuda, monkeypatch):
+    """A grouped call on the 256-row tiles (the one-launch schedule, taken by itself) captured in a HIP graph: every
+    replay, with eager calls between replays, equals the separate launches (the gather re-zeroes the control words
+    inside the graph)."""
+    from mi355moe import _lib, ops, synthetic
+    _say("one-launch schedule, graph replays")
+    n, K, N, T = 16, 1024, 512, 700
+    ex = synthetic.calibrated_layer(n, K, N, seed=51, device=cuda, uniform_suh=True)
+    x = synthetic.activations(T, K, seed=52, device=cuda)
+    ids = synthetic.random_ids(T, n, 8, seed=53, device=cuda)
+    w = synthetic.softmax_weights(T, 8, seed=54, device=cuda)
+    ref = ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)
+    monkeypatch.delenv("MI355MOE_SCHED")
+    ops.reserve(ex, T)
+    out = torch.empty(T, K, dtype=torch.float32, device=cuda)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.moe_forward_ids(ex, x, ids, w, out=out, path=_lib.PATH_PREFILL)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.moe_forward_ids(ex, x, ids, w, out=out, path=_lib.PATH_PREFILL)
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), i
+        ops.moe_forward_ids(ex, x, ids, w, out_dtype=torch.float32, path=_lib.PATH_PREFILL)   # eager between
+        torch.cuda.synchronize()
