@@ -398,7 +398,7 @@ def run_prefill(args, torch, dev):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     # the stages alone: route staged untimed, then gather + gate/up, down and combine each event-bracketed
-    gu, dn, cb = [], [], []
+    gu, dn, cb, one = [], [], [], []
     for k in range(steps):
         l = k % n_layers
         ids, wts = info[l]
@@ -407,10 +407,13 @@ def run_prefill(args, torch, dev):
         gu.append(_bracket(torch, lambda: call(_lib.STAGE_GATEUP)))
         dn.append(_bracket(torch, lambda: call(_lib.STAGE_DOWN)))
         cb.append(_bracket(torch, lambda: call(_lib.STAGE_COMBINE)))
+        # gather + the one-launch gate/up -> down kernel (both GEMM stages in one call)
+        one.append(_bracket(torch, lambda: call(_lib.STAGE_GATEUP | _lib.STAGE_DOWN)))
     torch.cuda.synchronize()
     gu_ms = sum(a.elapsed_time(b) for a, b in gu) / len(gu)
     dn_ms = sum(a.elapsed_time(b) for a, b in dn) / len(dn)
     cb_ms = sum(a.elapsed_time(b) for a, b in cb) / len(cb)
+    one_ms = sum(a.elapsed_time(b) for a, b in one) / len(one)
 
     if args.workload == "prefill-uniform":                # the profiling window: these calls only
         P = sum(pairs) / len(pairs)
@@ -419,7 +422,7 @@ def run_prefill(args, torch, dev):
                                              4),
                 "prefill_down_ms": round(dn_ms, 4),
                 "prefill_down_frac": round(2.0 * P * N * K / (dn_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
-                "prefill_combine_ms": round(cb_ms, 4)}
+                "prefill_combine_ms": round(cb_ms, 4), "prefill_one_launch_ms": round(one_ms, 4)}
 
     def step_fold(l):
         # bf16 down accumulators, routed sum added into out (which stands for the shared experts' bf16 output)
@@ -469,6 +472,13 @@ def run_prefill(args, torch, dev):
                                       "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                       "frac": round(dn_flops / (dn_ms / 1000.0) / 1e12 / MFMA_FP16_PEAK_TFLOPS, 4),
                                       "avg_launch_us": round(dn_ms * 1000.0, 1)},
+            "roofline_prefill_one_launch": {"bound": "mfma",
+                                            "kernel": "pf_sched_kernel (includes the gather launch)",
+                                            "achieved": round((gu_flops + dn_flops) / (one_ms / 1000.0) / 1e12, 2),
+                                            "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                            "frac": round((gu_flops + dn_flops) / (one_ms / 1000.0) / 1e12 /
+                                                          MFMA_FP16_PEAK_TFLOPS, 4),
+                                            "avg_launch_us": round(one_ms * 1000.0, 1)},
             "prefill_combine": {"kernel": "pf_combine_kernel", "avg_launch_us": round(cb_ms * 1000.0, 1),
                                 "gbs": round(cb_bytes / (cb_ms / 1000.0) / 1e9, 1),
                                 "bytes": cb_bytes},
