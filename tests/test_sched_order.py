@@ -116,3 +116,40 @@ def test_query_rejects_bad_arguments():
     assert k.value == -1
     assert L.mi355moe_sched_item(5, 0, 0, 8, 4, ctypes.byref(k), ctypes.byref(s), ctypes.byref(b)) == 0
     assert k.value == -1
+
+
+QUEUES, QSTRIDE = 8, 32                       # the kernel's ticket queues and their word stride
+HEAD = QUEUES * QSTRIDE + QSTRIDE             # queue counters, the give-up word, then one count per segment
+
+
+@pytest.mark.parametrize("S_cap,ncg,ncd", _gpu_shapes())
+def test_queue_and_count_indexing_in_bounds(S_cap, ncg, ncd):
+    """The kernel's indexing, emulated on the host for every shape of the GPU tests: segment s of a call with ns live
+    segments goes to queue s % 8 as its unit s // 8; every ticket a queue hands out names a segment below ns, every
+    word the kernel touches (queue counter, give-up word, the segment's count) lies inside the carved
+    PF_SCHED_HEAD + S_cap words, and every (segment, tile) is taken exactly once over the eight queues."""
+    words = HEAD + S_cap
+    for ns in sorted({1, 2, 7, 8, 9, S_cap // 2, S_cap} - {0}):
+        if ns > S_cap:
+            continue
+        seen = []
+        for q in range(QUEUES):
+            assert q * QSTRIDE < HEAD - QSTRIDE and QUEUES * QSTRIDE < HEAD     # counter and give-up word
+            nq = (ns - q + QUEUES - 1) // QUEUES if ns > q else 0
+            if nq == 0:
+                continue
+            for t in range(nq * (ncg + ncd) + 4):
+                k, j, b = _library_order_one(t, nq, ncg, ncd)
+                if k < 0:
+                    assert t >= nq * (ncg + ncd)
+                    continue
+                s = q + QUEUES * j
+                assert 0 <= s < ns <= S_cap and HEAD + s < words
+                seen.append((k, s, b))
+        assert sorted(seen) == sorted([(0, s, b) for s in range(ns) for b in range(ncg)] +
+                                      [(1, s, b) for s in range(ns) for b in range(ncd)])
+
+
+def _library_order_one(t, nq, ncg, ncd):
+    from mi355moe import ops
+    return ops.sched_item(t, nq, 0, ncg, ncd)
