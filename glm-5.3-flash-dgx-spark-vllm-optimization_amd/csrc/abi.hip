@@ -425,7 +425,7 @@ namespace {
 struct PrefillWs {
     RouteArgs ra;
     PrefillArgs pa;
-    int* sched;             // the one-launch schedule's control words [PF_SCHED_HEAD + S_cap]
+    int* sched;             // the one-launch schedule's control words [PF_SCHED_WORDS(S_cap)]
     size_t bytes;
 };
 
@@ -452,7 +452,7 @@ void carve_prefill(void* ws, int64_t P, int64_t T, int64_t n, int64_t K, int64_t
     d.h13 = c.take<uint16_t>((size_t)P * K);
     d.h2 = c.take<uint16_t>((size_t)P * N);
     d.contrib = c.take<float>((size_t)P * K);
-    w.sched = c.take<int>((size_t)PF_SCHED_HEAD + S_cap);
+    w.sched = c.take<int>((size_t)PF_SCHED_WORDS(S_cap));
     if (e4m3) {
         r.w32 = c.take<float>(P);
         d.w32 = r.w32;
@@ -614,7 +614,7 @@ static int run_grouped(const mi355moe_exl3_layer* layer, const void* x, int x_dt
     d.out_accumulate = (options & MI355MOE_OPT_ACCUMULATE) ? 1 : 0;
     if ((stages & MI355MOE_STAGE_GATEUP) && (stages & MI355MOE_STAGE_DOWN)) {
         d.sched = w.sched;                            // gate/up and down tiles in one launch: forced, or chosen
-        d.sched_lag = sched_lag();                    // by launch_prefill for calls on the 256-row tiles
+        d.sched_lag = sched_lag();                    // by launch_prefill where it measured faster
         d.sched_force = (options & MI355MOE_OPT_PERSISTENT) ? 1 : 0;
     }
     if (e4m3 && (options & MI355MOE_OPT_DOWN16)) {   // fp16 down operands: no down-input quantisation or its scale
@@ -1083,7 +1083,7 @@ struct RowsWs {
     float* dsc;
     int* tok32;
     uint16_t* h13;
-    int* sched;             // e4m3: the one-launch schedule's control words [PF_SCHED_HEAD + rows] (segments <= rows)
+    int* sched;             // e4m3: the one-launch schedule's control words [PF_SCHED_WORDS(rows)] (segments <= rows)
     size_t bytes;
 };
 RowsWs carve_rows(void* ws, int64_t rows, int64_t K, int64_t N, int64_t tokens, bool e4m3) {
@@ -1101,7 +1101,7 @@ RowsWs carve_rows(void* ws, int64_t rows, int64_t K, int64_t N, int64_t tokens, 
         w.dsc = c.take<float>(std::max<int64_t>(1, rows));
         w.tok32 = c.take<int>(std::max<int64_t>(1, rows));
         w.h13 = c.take<uint16_t>((size_t)std::max<int64_t>(1, std::max(rows, tokens)) * K);
-        w.sched = c.take<int>((size_t)PF_SCHED_HEAD + std::max<int64_t>(1, rows));
+        w.sched = c.take<int>((size_t)PF_SCHED_WORDS(std::max<int64_t>(1, rows)));
     }
     w.bytes = c.off;
     return w;

@@ -152,9 +152,9 @@ struct PrefillArgs {
     int chunk, nchunks;     // nchunks > 1: the GEMMs and row kernels take only the segments
                             // [ns chunk / nchunks, ns (chunk + 1) / nchunks) of the ns = nseg[0] live ones
     const int* row_expert;  // optional: the row-table setup marks row r with row_expert[r] instead of its segment's
-    // one-launch schedule (nullptr: separate gate/up and down launches): control words [PF_SCHED_HEAD + S_cap] --
+    // one-launch schedule (nullptr: separate gate/up and down launches): control words [PF_SCHED_WORDS(S_cap)] --
     // the next ticket of queue q at [PF_SCHED_QSTRIDE q] (q < PF_SCHED_QUEUES), the give-up word after them (set
-    // when a down item gave up waiting), then from PF_SCHED_HEAD per segment the gate/up items finished -- zeroed by
+    // when a down item gave up waiting), then from PF_SCHED_HEAD per (segment, part) the gate/up items finished -- zeroed by
     // the gather that starts the call; sched_lag: the schedule's lag in segments of a queue (0: all of them);
     // sched_force: always (otherwise launch_prefill takes the schedule for calls on the 256-row tiles only)
     int* sched;
@@ -165,6 +165,8 @@ constexpr int PREFILL_TM = 256;
 constexpr int PF_SCHED_QUEUES = 8;      // ticket queues (one per XCD; segment s in queue s % 8)
 constexpr int PF_SCHED_QSTRIDE = 32;    // words between queue counters (one 128-byte line each)
 constexpr int PF_SCHED_HEAD = PF_SCHED_QUEUES * PF_SCHED_QSTRIDE + PF_SCHED_QSTRIDE;
+// control words of a call with S_cap segments: the head, then a count per (segment, part), up to four 64-row parts
+__host__ __device__ constexpr int64_t PF_SCHED_WORDS(int64_t S_cap) { return PF_SCHED_HEAD + 4 * S_cap; }
 
 // Item t of the one-launch gate/up -> down schedule over ns segments with ncg gate/up and ncd down items each
 // (column blocks), lag L = min(lag, ns) (lag <= 0: ns): the gate/up items of segments 0 .. L - 1, then for

@@ -154,7 +154,7 @@ __device__ __forceinline__ int pf_gather_items(const PrefillArgs& a) {
 constexpr int PF_GATHER_PASSES = 8;                 // passes of 4 blocks in flight (K up to 4096 in one round)
 __global__ __launch_bounds__(256) void pf_gather_kernel(PrefillArgs a) {
     if (a.sched && blockIdx.x == 0)                                   // the one-launch schedule's control words
-        for (int i = threadIdx.x; i < PF_SCHED_HEAD + a.S_cap; i += 256) a.sched[i] = 0;
+        for (int i = threadIdx.x; i < PF_SCHED_WORDS(a.S_cap); i += 256) a.sched[i] = 0;
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
     const int nb = a.K >> 7;
@@ -254,7 +254,7 @@ __device__ __forceinline__ float e4m3_row_scale(float amax) {
 // epilogue. One wave per row; the whole row (K <= 4096) stays in registers between the amax and the quantization.
 __global__ __launch_bounds__(256) void pf_gather8_kernel(PrefillArgs a) {
     if (a.sched && blockIdx.x == 0)                                   // the one-launch schedule's control words
-        for (int i = threadIdx.x; i < PF_SCHED_HEAD + a.S_cap; i += 256) a.sched[i] = 0;
+        for (int i = threadIdx.x; i < PF_SCHED_WORDS(a.S_cap); i += 256) a.sched[i] = 0;
     const int lane = threadIdx.x & 63;
     const int c = lane & 15, q = lane >> 4;
     const int nb = a.K >> 7;
@@ -1083,8 +1083,8 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 
 // ------------------------------------------------------------------------------------------------ one-launch schedule
 
-// Every gate/up and down tile of a call (256-row kind) in one launch of one workgroup per CU. The
-// segments are dealt to eight ticket queues (segment s to queue s % 8, as the separate launches deal them to the
+// Every gate/up and down tile of a call in one launch of one workgroup per CU (256-row tiles; two per CU for the
+// 128- and 64-row part tiles, KIND below). The segments are dealt to eight ticket queues (segment s to queue s % 8, as the separate launches deal them to the
 // XCDs), each ordered by pf_sched_item over its own segments; a workgroup takes tickets from its own XCD's queue
 // (the XCC_ID register), so a segment's column blocks share that XCD's L2 for their A rows, and once that queue is
 // empty from the other queues in turn. A gate/up item stores its h2 rows device-coherent (written through to the
@@ -1103,9 +1103,14 @@ __global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 // for ncg + 1: the reference's dataflow, code/fork/kernels/moe_e4m3.cu:867-872).
 enum { PF_SCHED_E3 = 0, PF_SCHED_E4M3_16 = 1, PF_SCHED_E4M3 = 2 };
 constexpr int PF_SCHED_POLLS = 1 << 20;
-template <int MODE>
-__global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) {
-    extern __shared__ __align__(16) unsigned char smem[];
+// KIND: the call's tile kind (PF_LARGE: 256-row segments, one workgroup per CU; PF_MID / PF_SMALL: the segments'
+// 128- or 64-row parts, two workgroups per CU). A queue's units are its (segment, part) pairs, every segment's first
+// part first; a part past its segment's rows holds no tile, so its items only take their tickets. Each unit has its
+// own count (segment s, part p: word PF_SCHED_HEAD + s * parts + p).
+template <int MODE, int KIND>
+__device__ __forceinline__ void pf_sched_body(const PrefillArgs& a, unsigned char* smem) {
+    constexpr int PARTS = KIND == PF_SMALL ? 4 : KIND == PF_MID ? 2 : 1;
+    constexpr int SUB = pf_sub_rows(KIND);
     // The item's ticket and whether its wait ran out sit in the first LDS words between tiles (the tiles' stages
     // take the whole LDS): written by one lane, read by every wave after a barrier, and overwritten by the tile's
     // loads only after a second barrier.
@@ -1113,7 +1118,7 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
     int lo, hi;
     pf_seg_range(a, lo, hi);
     const int ns = hi - lo, ncg = a.N >> 7, ncd = a.K >> 8;
-    const int ready_at = ncg + (MODE == PF_SCHED_E4M3 ? 1 : 0);      // a down item's segment count to wait for
+    const int ready_at = ncg + (MODE == PF_SCHED_E4M3 ? 1 : 0);      // a down item's unit count to wait for
     int* ctl = a.sched;
     int* gave_up_word = ctl + PF_SCHED_QUEUES * PF_SCHED_QSTRIDE;
     int* ready = ctl + PF_SCHED_HEAD;
@@ -1130,28 +1135,29 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
                 s_ctl[1] = 0;
             }
             __syncthreads();
-            const PfSchedItem it = pf_sched_item(__builtin_amdgcn_readfirstlane(s_ctl[0]), nq, a.sched_lag, ncg, ncd);
+            const PfSchedItem it =
+                pf_sched_item(__builtin_amdgcn_readfirstlane(s_ctl[0]), nq * PARTS, a.sched_lag, ncg, ncd);
             if (it.kind < 0) break;                                   // (uniform) the queue is empty
-            const int s = lo + q + PF_SCHED_QUEUES * it.seg;          // < hi
+            const int part = it.seg / nq, s = lo + q + PF_SCHED_QUEUES * (it.seg - part * nq);   // s < hi
+            if (PARTS > 1 && __builtin_amdgcn_readfirstlane(a.seg_rows[s]) <= SUB * part) continue;   // no tile
+            int* cnt = ready + s * PARTS + part;
             if (it.kind == 0) {
                 __syncthreads();                                      // every wave has read s_ctl
                 // h2 (or vd and amaxd) stored device-coherent
-                pf_gateup_tile<MODE != PF_SCHED_E3, PF_LARGE, true>(a, s, 0, it.block, smem);
+                pf_gateup_tile<MODE != PF_SCHED_E3, KIND, true>(a, s, part, it.block, smem);
                 WAIT_VM(0);                                           // this wave's stores have completed
                 __syncthreads();
                 if (MODE != PF_SCHED_E4M3) {
-                    if (threadIdx.x == 0)
-                        __hip_atomic_fetch_add(ready + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     continue;
                 }
                 if (threadIdx.x == 0)
-                    s_ctl[1] = __hip_atomic_fetch_add(ready + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                               ncg - 1;
+                    s_ctl[1] = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ncg - 1;
                 __syncthreads();
-                if (!__builtin_amdgcn_readfirstlane(s_ctl[1])) continue;   // (uniform) not the segment's last
-                // the segment's last gate/up item: every other one's stores completed before its count; quantise
-                // the segment's rows (one wave per row) and publish them with one more count
-                const int r0 = a.seg_row0[s], rn = min(a.seg_rows[s], PF_TM);
+                if (!__builtin_amdgcn_readfirstlane(s_ctl[1])) continue;   // (uniform) not the unit's last
+                // the unit's last gate/up item: every other one's stores completed before its count; quantise the
+                // unit's rows (one wave per row) and publish them with one more count
+                const int r0 = a.seg_row0[s] + SUB * part, rn = min(a.seg_rows[s] - SUB * part, SUB);
                 constexpr int QR = 4;                                 // rows in flight per wave
                 const int w0 = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
                 if (r0 >= 0 && rn > 0 && r0 + rn <= a.P) {           // (caller-built tables)
@@ -1163,13 +1169,12 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
                 }
                 WAIT_VM(0);
                 __syncthreads();
-                if (threadIdx.x == 0)
-                    __hip_atomic_fetch_add(ready + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 continue;
             }
             if (threadIdx.x == 0) {
-                for (int polls = 0;
-                     __hip_atomic_load(ready + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ready_at; ++polls) {
+                for (int polls = 0; __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ready_at;
+                     ++polls) {
                     if (polls >= PF_SCHED_POLLS ||
                         __hip_atomic_load(gave_up_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
                         __hip_atomic_store(gave_up_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1183,9 +1188,20 @@ __global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) 
             const int gave_up = __builtin_amdgcn_readfirstlane(s_ctl[1]);
             __syncthreads();                                          // every wave has read s_ctl
             if (gave_up) continue;                                    // (uniform) the tile is skipped
-            pf_down_tile<MODE == PF_SCHED_E4M3, PF_LARGE, true>(a, s, 0, it.block, smem);   // h2 device-coherent
+            pf_down_tile<MODE == PF_SCHED_E4M3, KIND, true>(a, s, part, it.block, smem);   // h2 device-coherent
         }
     }
+}
+template <int MODE>
+__global__ __launch_bounds__(PF_THREADS, 1) void pf_sched_kernel(PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    pf_sched_body<MODE, PF_LARGE>(a, smem);
+}
+template <int MODE, int KIND>
+__global__ __launch_bounds__(PF_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void pf_sched_part_kernel(
+    PrefillArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    pf_sched_body<MODE, KIND>(a, smem);
 }
 
 // ------------------------------------------------------------------------------------------------ combine
@@ -1358,7 +1374,7 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(PrefillArgs a) {
 __global__ __launch_bounds__(256) void pf_rows_init_kernel(PrefillArgs a, int* pe, int* cnt, int tokens, int* tok32,
                                                            const int64_t* row_token) {
     if (a.sched && blockIdx.x == 0)                                   // the one-launch schedule's control words
-        for (int i = threadIdx.x; i < PF_SCHED_HEAD + a.S_cap; i += 256) a.sched[i] = 0;
+        for (int i = threadIdx.x; i < PF_SCHED_WORDS(a.S_cap); i += 256) a.sched[i] = 0;
     for (int i = blockIdx.x * 256 + threadIdx.x; i < max(a.P, tokens); i += gridDim.x * 256) {
         if (i < a.P) {
             pe[i] = -1;
@@ -1569,6 +1585,16 @@ int prefill_setup() {
                           reinterpret_cast<const void*>(pf_sched_kernel<PF_SCHED_E4M3>)};
     for (const void* k : ksc)
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS) != hipSuccess) return -1;
+    const void* kscm[3] = {reinterpret_cast<const void*>(pf_sched_part_kernel<PF_SCHED_E3, PF_MID>),
+                           reinterpret_cast<const void*>(pf_sched_part_kernel<PF_SCHED_E4M3_16, PF_MID>),
+                           reinterpret_cast<const void*>(pf_sched_part_kernel<PF_SCHED_E4M3, PF_MID>)};
+    for (const void* k : kscm)
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_M) != hipSuccess) return -1;
+    const void* kscs[3] = {reinterpret_cast<const void*>(pf_sched_part_kernel<PF_SCHED_E3, PF_SMALL>),
+                           reinterpret_cast<const void*>(pf_sched_part_kernel<PF_SCHED_E4M3_16, PF_SMALL>),
+                           reinterpret_cast<const void*>(pf_sched_part_kernel<PF_SCHED_E4M3, PF_SMALL>)};
+    for (const void* k : kscs)
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)PF_LDS_S) != hipSuccess) return -1;
     g_pf_attr = true;
     return 0;
 }
@@ -1624,27 +1650,44 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     const dim3 gum(8 * (a.N / 128) * sgm), dnm(8 * (a.K / 256) * sgm);
     const int tiles = pf_tiles(a0);
     a.small_rows = tiles == PF_TILES_BOTH ? PF_SMALL_ROWS : 0;
-    // The one-launch schedule, for calls that run gate/up and down (and, e4m3, the down-input quantisation):
-    // when forced, or for E3 and e4m3-DOWN16 calls on the 256-row tiles (measured at T = 8192, 288 experts: E3 0-3 %
-    // faster than the separate launches with uniform routing, within +-0.7 % with Zipf routing; DOWN16 4 % faster;
-    // bit-identical). Not chosen by itself for the e4m3 down GEMM, whose in-launch quantisation (one workgroup per
-    // segment) made the T = 8192 call 1.5 % slower. MI355MOE_SCHED=separate turns the automatic choice off.
-    // (the control words are zeroed by the call's gather or, on row tables, by the row-table setup)
-    const bool sched_ok = (kernels & 6) == 6 && !(kernels & PF_NO_QUANTD);
+    // The one-launch schedule, for calls that run gate/up and down (and, e4m3, the down-input quantisation) on one
+    // tile kind: when forced, or by itself where it measured faster than the separate launches (288 experts,
+    // bit-identical): E3 and e4m3-DOWN16 calls on every tile kind (T = 8192 256-row tiles: 0-3 % with uniform
+    // routing, within +-0.7 % with Zipf routing; T = 2048 / 4096 128-row tiles -0.5 / -1.7 %; DOWN16 -3 to -4 %), and
+    // e4m3 calls on the 64-row tiles (T = 2048 -1.2 %), whose in-launch quantisation of 64-row units costs less than
+    // the 128- and 256-row units' (+0.6 % at T = 4096, +1.5 % at T = 8192). MI355MOE_SCHED=separate turns the
+    // automatic choice off. (The control words are zeroed by the call's gather or, on row tables, by the row-table
+    // setup.)
+    const bool sched_ok = (kernels & 6) == 6 && !(kernels & PF_NO_QUANTD) && tiles != PF_TILES_BOTH;
     if (a.sched && a.sched_force && !sched_ok) return -1;
     const char* sched_env = getenv("MI355MOE_SCHED");
-    const bool sched_auto = tiles == PF_TILES_LARGE && !(f8 && !a.down16) &&
+    const bool sched_auto = (!f8 || a.down16 || tiles == PF_TILES_SMALL) &&
                             !(sched_env && !strcmp(sched_env, "separate"));
     const bool sched = a.sched && sched_ok && (a.sched_force || sched_auto);
     if (sched) {
         a.small_rows = 0;
-        const int64_t items = (int64_t)std::max(a.S_cap, 0) * ((a.N >> 7) + (a.K >> 8));
-        const int grid = (int)std::min<int64_t>(pf_device_cus(), items);
-        if (grid > 0) {
-            if (!f8) hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E3>, dim3(grid), dim3(PF_THREADS), PF_LDS, st, a);
-            else if (a.down16)
-                hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E4M3_16>, dim3(grid), dim3(PF_THREADS), PF_LDS, st, a);
-            else hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E4M3>, dim3(grid), dim3(PF_THREADS), PF_LDS, st, a);
+        const int parts = tiles == PF_TILES_SMALL ? 4 : tiles == PF_TILES_MID ? 2 : 1;
+        const int per_cu = parts > 1 ? 2 : 1;
+        const int64_t items = (int64_t)std::max(a.S_cap, 0) * parts * ((a.N >> 7) + (a.K >> 8));
+        const dim3 grid((unsigned)std::min<int64_t>((int64_t)per_cu * pf_device_cus(), items)), blk(PF_THREADS);
+        const int mode = !f8 ? 0 : a.down16 ? 1 : 2;
+        if (grid.x > 0) {
+            if (parts == 1) {
+                if (mode == 0) hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E3>, grid, blk, PF_LDS, st, a);
+                else if (mode == 1) hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E4M3_16>, grid, blk, PF_LDS, st, a);
+                else hipLaunchKernelGGL(pf_sched_kernel<PF_SCHED_E4M3>, grid, blk, PF_LDS, st, a);
+            } else if (parts == 2) {
+                if (mode == 0) hipLaunchKernelGGL((pf_sched_part_kernel<PF_SCHED_E3, PF_MID>), grid, blk, PF_LDS_M, st, a);
+                else if (mode == 1)
+                    hipLaunchKernelGGL((pf_sched_part_kernel<PF_SCHED_E4M3_16, PF_MID>), grid, blk, PF_LDS_M, st, a);
+                else hipLaunchKernelGGL((pf_sched_part_kernel<PF_SCHED_E4M3, PF_MID>), grid, blk, PF_LDS_M, st, a);
+            } else {
+                if (mode == 0)
+                    hipLaunchKernelGGL((pf_sched_part_kernel<PF_SCHED_E3, PF_SMALL>), grid, blk, PF_LDS_S, st, a);
+                else if (mode == 1)
+                    hipLaunchKernelGGL((pf_sched_part_kernel<PF_SCHED_E4M3_16, PF_SMALL>), grid, blk, PF_LDS_S, st, a);
+                else hipLaunchKernelGGL((pf_sched_part_kernel<PF_SCHED_E4M3, PF_SMALL>), grid, blk, PF_LDS_S, st, a);
+            }
         }
         kernels &= ~6;
     }

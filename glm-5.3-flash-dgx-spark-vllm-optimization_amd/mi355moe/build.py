@@ -3,7 +3,9 @@
     python -m mi355moe.build        (from the package's parent directory)
 
 Flags: -O3, no FMA contraction (epilogues round exactly as written), and no packed-fp32 instructions
-(``-Xclang -target-feature -Xclang -packed-fp32-ops``): hipcc is asked never to emit v_pk_*_f32.
+(``-Xclang -target-feature -Xclang -packed-fp32-ops``): hipcc is asked never to emit v_pk_*_f32. A larger budget for
+promoting private arrays to registers (``-mllvm -amdgpu-promote-alloca-to-vector-limit=2048``) keeps the GEMM loops'
+per-lane arrays out of scratch.
 """
 from __future__ import annotations
 
@@ -21,7 +23,11 @@ OUT = os.path.join(_HERE, "libmi355moe.so")
 ARCH = "gfx950"
 
 FLAGS = ["-O3", f"--offload-arch={ARCH}", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # private arrays of the GEMM loops (decoded weight pairs, B operands) kept in registers: without it the
+         # default promotion budget leaves some of them in scratch in the larger kernels (the 128- and 64-row tile
+         # kernels, the one-launch schedule)
+         "-mllvm", "-amdgpu-promote-alloca-to-vector-limit=2048"]
 
 
 def hipcc() -> str:

@@ -178,9 +178,9 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
  *   MI355MOE_OPT_PERSISTENT   the grouped path's gate/up and down tiles in one launch of one workgroup per compute
  *                             unit, ticket-ordered with per-segment dataflow counts (the reference's fused schedule,
  *                             code/fork/kernels/moe_e4m3.cu:867-897; item order: mi355moe_sched_item), whatever the
- *                             call's size. Without the option the library takes this schedule by itself for E3 and
- *                             MI355MOE_OPT_DOWN16 calls on the 256-row tiles (the environment variable
- *                             MI355MOE_SCHED=separate turns that off). Applies when the call runs both stages
+ *                             call's size, on the tile kind the call picks. Without the option the library takes
+ *                             this schedule by itself for E3 and MI355MOE_OPT_DOWN16 calls, and for e4m3 calls on the
+ *                             64-row tiles (the environment variable MI355MOE_SCHED=separate turns that off). Applies when the call runs both stages
  *                             (MI355MOE_STAGE_GATEUP and MI355MOE_STAGE_DOWN) on the grouped path; results are
  *                             bit-identical to the separate launches. With MI355MOE_OPT_E4M3 (e4m3 down GEMM) the
  *                             workgroup finishing a segment's gate/up items quantises its down inputs in the launch.
@@ -340,7 +340,7 @@ int mi355moe_e3_down(const void* h2, int64_t rows_cap, int64_t K, int64_t N, int
  *   fp16 W_q, the extension's variant 16, spec_proj16 at glm53_moe_e4m3.py:660-664); a8d / dsc are not written;
  *   MI355MOE_E4M3_LEAN_MAINLOOP (the extension's +8192 schedule variant): accepted, same results.
  *   mi355moe_e4m3_fused runs gate/up and down as one ticket-ordered launch (MI355MOE_OPT_PERSISTENT's schedule) by
- *   itself when the row tables pick the 256-row tiles, DOWN16 is set and seg_cap <= rows_cap; the lag comes from
+ *   itself where that choice applies (DOWN16, or the 64-row tiles) and seg_cap <= rows_cap; the lag comes from
  *   MI355MOE_SCHED_LAG. The reference's per-call lag / grid / sync arguments have no counterpart.
  * The stages that take a workspace share one size, mi355moe_e4m3_stage_workspace_bytes(rows_cap, K, N, tokens). */
 enum { MI355MOE_E4M3_DOWN16 = 16, MI355MOE_E4M3_TOKEN_ROWS = 2048, MI355MOE_E4M3_LEAN_MAINLOOP = 8192 };

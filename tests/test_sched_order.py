@@ -122,13 +122,16 @@ QUEUES, QSTRIDE = 8, 32                       # the kernel's ticket queues and t
 HEAD = QUEUES * QSTRIDE + QSTRIDE             # queue counters, the give-up word, then one count per segment
 
 
+@pytest.mark.parametrize("parts", [1, 2, 4])
 @pytest.mark.parametrize("S_cap,ncg,ncd", _gpu_shapes())
-def test_queue_and_count_indexing_in_bounds(S_cap, ncg, ncd):
-    """The kernel's indexing, emulated on the host for every shape of the GPU tests: segment s of a call with ns live
-    segments goes to queue s % 8 as its unit s // 8; every ticket a queue hands out names a segment below ns, every
-    word the kernel touches (queue counter, give-up word, the segment's count) lies inside the carved
-    PF_SCHED_HEAD + S_cap words, and every (segment, tile) is taken exactly once over the eight queues."""
-    words = HEAD + S_cap
+def test_queue_and_count_indexing_in_bounds(S_cap, ncg, ncd, parts):
+    """The kernel's indexing, emulated on the host for every shape of the GPU tests and every tile kind (1, 2 or 4
+    parts per segment): segment s of a call with ns live segments goes to queue s % 8 as its unit s // 8, a queue's
+    units are (segment, part) pairs with every first part first; every ticket a queue hands out names a segment below
+    ns and a part below `parts`, every word the kernel touches (queue counter, give-up word, the unit's count
+    PF_SCHED_HEAD + s * parts + part) lies inside the carved PF_SCHED_HEAD + 4 S_cap words, and every (segment, part,
+    tile) is taken exactly once over the eight queues."""
+    words = HEAD + 4 * S_cap
     for ns in sorted({1, 2, 7, 8, 9, S_cap // 2, S_cap} - {0}):
         if ns > S_cap:
             continue
@@ -138,16 +141,17 @@ def test_queue_and_count_indexing_in_bounds(S_cap, ncg, ncd):
             nq = (ns - q + QUEUES - 1) // QUEUES if ns > q else 0
             if nq == 0:
                 continue
-            for t in range(nq * (ncg + ncd) + 4):
-                k, j, b = _library_order_one(t, nq, ncg, ncd)
+            for t in range(nq * parts * (ncg + ncd) + 4):
+                k, u, b = _library_order_one(t, nq * parts, ncg, ncd)
                 if k < 0:
-                    assert t >= nq * (ncg + ncd)
+                    assert t >= nq * parts * (ncg + ncd)
                     continue
+                part, j = divmod(u, nq)
                 s = q + QUEUES * j
-                assert 0 <= s < ns <= S_cap and HEAD + s < words
-                seen.append((k, s, b))
-        assert sorted(seen) == sorted([(0, s, b) for s in range(ns) for b in range(ncg)] +
-                                      [(1, s, b) for s in range(ns) for b in range(ncd)])
+                assert 0 <= s < ns <= S_cap and 0 <= part < parts and HEAD + s * parts + part < words
+                seen.append((k, s, part, b))
+        assert sorted(seen) == sorted([(0, s, p, b) for s in range(ns) for p in range(parts) for b in range(ncg)] +
+                                      [(1, s, p, b) for s in range(ns) for p in range(parts) for b in range(ncd)])
 
 
 def _library_order_one(t, nq, ncg, ncd):
