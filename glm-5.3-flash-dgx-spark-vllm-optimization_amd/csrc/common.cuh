@@ -292,6 +292,22 @@ __device__ __forceinline__ void dma16_coh(const void* src_lane, unsigned char* l
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off sc1" ::"s"(m0), "v"(src_lane)
                  : "memory", "m0");
 }
+// Device-coherent 16-byte accesses (sc1: agent scope, served by the device coherence point, the cache policy
+// agent-scope relaxed atomics take) through a buffer resource over a wave-uniform base address: one instruction
+// where an atomic access moves at most 8 bytes. Offsets are in bytes from the base, below 2^31.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const void* base) {
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p) |
+                       ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32)) << 32);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)u, (short)0, 0x7FFFFFFF, 0x00020000);
+}
+constexpr int COH_SC1 = 16;                       // the buffer instructions' cache-policy bit for sc1
+__device__ __forceinline__ u32x4 ld_coh16(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, COH_SC1));
+}
+__device__ __forceinline__ void st_coh16(__amdgpu_buffer_rsrc_t r, int off, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, COH_SC1);
+}
 // The same with 4 bytes per lane: lane l -> LDS bytes lds_wave + 4 l (global_load_lds_dword).
 __device__ __forceinline__ void dma4(const void* src_lane, unsigned char* lds_wave) {
     const uint32_t m0 = (uint32_t)(uintptr_t)lds_wave;

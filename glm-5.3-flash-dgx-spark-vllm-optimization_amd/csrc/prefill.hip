@@ -63,40 +63,25 @@ __device__ __forceinline__ int pf_kperm_pair(int j) { return 2 * (j & 3) + (j >>
 // with one 16-byte store: the lanes c, c ^ 1 of a group own its 32 bytes interleaved (storage pair 2m + h = the lane's
 // pair m), so they swap two pairs (DPP lane ^ 1) and lane h then writes storage pairs 4h .. 4h + 3 contiguously.
 // grp: the 16-group's first element.
-// COH: written as two device-coherent 8-byte stores (agent-scope relaxed atomics, written through to the device
-// coherence point), for rows that workgroups on other XCDs read in the same launch.
-template <bool COH = false>
-__device__ __forceinline__ void pf_store_group(_Float16* grp, const uint32_t (&wm)[4], int c) {
+__device__ __forceinline__ u32x4 pf_group_vec(const uint32_t (&wm)[4], int c) {
     const bool hi = c & 1;
     const uint32_t s0 = hi ? wm[0] : wm[2], s1 = hi ? wm[1] : wm[3];
     const uint32_t r0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s0, 0xB1, 0xF, 0xF, true);   // lane ^ 1
     const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)s1, 0xB1, 0xF, 0xF, true);
-    const u32x4 v = hi ? u32x4{r0, wm[2], r1, wm[3]} : u32x4{wm[0], r0, wm[1], r1};
-    if (COH) {
-        uint64_t* d = reinterpret_cast<uint64_t*>(grp + 8 * (c & 1));
-        __hip_atomic_store(d, (uint64_t)v[0] | ((uint64_t)v[1] << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(d + 1, (uint64_t)v[2] | ((uint64_t)v[3] << 32), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-        *reinterpret_cast<u32x4*>(grp + 8 * (c & 1)) = v;
-    }
+    return hi ? u32x4{r0, wm[2], r1, wm[3]} : u32x4{wm[0], r0, wm[1], r1};
 }
-// Four floats as two device-coherent 8-byte stores / loads (agent-scope relaxed atomics), for rows that
-// workgroups on other XCDs read or wrote in the same launch.
-__device__ __forceinline__ void st_coh_f4(float* p, float x, float y, float z, float w) {
-    uint64_t* d = reinterpret_cast<uint64_t*>(p);
-    __hip_atomic_store(d, (uint64_t)__builtin_bit_cast(uint32_t, x) | ((uint64_t)__builtin_bit_cast(uint32_t, y) << 32),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(d + 1,
-                       (uint64_t)__builtin_bit_cast(uint32_t, z) | ((uint64_t)__builtin_bit_cast(uint32_t, w) << 32),
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void pf_store_group(_Float16* grp, const uint32_t (&wm)[4], int c) {
+    *reinterpret_cast<u32x4*>(grp + 8 * (c & 1)) = pf_group_vec(wm, c);
 }
-__device__ __forceinline__ float4 ld_coh_f4(const float* p) {
-    uint64_t* d = reinterpret_cast<uint64_t*>(const_cast<float*>(p));
-    const uint64_t v0 = __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t v1 = __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float4(__builtin_bit_cast(float, (uint32_t)v0), __builtin_bit_cast(float, (uint32_t)(v0 >> 32)),
-                       __builtin_bit_cast(float, (uint32_t)v1), __builtin_bit_cast(float, (uint32_t)(v1 >> 32)));
+// The same as one device-coherent store, for rows that workgroups on other XCDs read in the same launch: r over the
+// row block, grp_off the 16-group's byte offset in it.
+__device__ __forceinline__ void pf_store_group_coh(__amdgpu_buffer_rsrc_t r, int grp_off, const uint32_t (&wm)[4],
+                                                   int c) {
+    st_coh16(r, grp_off + 16 * (c & 1), pf_group_vec(wm, c));
+}
+__device__ __forceinline__ float4 f4_of(u32x4 v) {
+    const f32x4 f = __builtin_bit_cast(f32x4, v);
+    return make_float4(f[0], f[1], f[2], f[3]);
 }
 
 // The same placement for one byte per element (e4m3 codes): q[m] holds the lane's pair m as two codes in its low 16
@@ -353,19 +338,24 @@ __device__ __forceinline__ void pf_quantd_row(const PrefillArgs& a, int pos, int
         float, COH ? __hip_atomic_load(a.amaxd + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : a.amaxd[pos]);
     const float* src = a.vd + (size_t)pos * a.N + 8 * c;
     const int nb = a.N >> 7;
-    auto ld4 = [&](const float* p) { return COH ? ld_coh_f4(p) : *reinterpret_cast<const float4*>(p); };
+    // pos is wave-uniform: the coherent accesses go through buffer resources over the row
+    const __amdgpu_buffer_rsrc_t rv = coh_rsrc(a.vd + (size_t)pos * a.N);
+    const __amdgpu_buffer_rsrc_t rh = coh_rsrc(reinterpret_cast<_Float16*>(a.h2) + (size_t)pos * a.N);
+    auto ld4 = [&](int e) {                                   // the lane's floats e .. e + 3
+        return COH ? f4_of(ld_coh16(rv, 4 * (8 * c + e))) : *reinterpret_cast<const float4*>(src + e);
+    };
     float4 lo0 = {}, hi0 = {};
     if (q < nb) {
-        lo0 = ld4(src + q * 128);
-        hi0 = ld4(src + q * 128 + 4);
+        lo0 = ld4(q * 128);
+        hi0 = ld4(q * 128 + 4);
     }
     if (pe < 0) return;
     const float sc = e4m3_row_scale(amax);
     _Float16* dst0 = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos * a.N + 16 * (c >> 1);
     uint8_t* dst8 = a.a8dout + (size_t)pos * a.N + 16 * (c >> 1);
     for (int blk = q; blk < nb; blk += 4) {
-        const float4 lo = blk == q ? lo0 : ld4(src + blk * 128);
-        const float4 hi = blk == q ? hi0 : ld4(src + blk * 128 + 4);
+        const float4 lo = blk == q ? lo0 : ld4(blk * 128);
+        const float4 hi = blk == q ? hi0 : ld4(blk * 128 + 4);
         const float w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         uint32_t f8[4], wm[4];
 #pragma unroll
@@ -373,7 +363,10 @@ __device__ __forceinline__ void pf_quantd_row(const PrefillArgs& a, int pos, int
             f8[mm] = e4m3_quant_f8(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
             wm[mm] = e4m3_h2(f8[mm]);
         }
-        pf_store_group<COH>(dst0 + blk * 128, wm, c);
+        if (COH)
+            pf_store_group_coh(rh, 2 * (16 * (c >> 1) + blk * 128), wm, c);
+        else
+            pf_store_group(dst0 + blk * 128, wm, c);
         if (a.a8dout) pf_store_group8(dst8 + blk * 128, f8, c);
     }
     if (lane == 0) a.dsc[pos] = sc;
@@ -393,14 +386,14 @@ __device__ __forceinline__ void pf_quantd_rows_coh(const PrefillArgs& a, int pos
         pe[r] = pos0 + r * step < end ? a.pe[pos[r]] : -1;
         amax[r] = __builtin_bit_cast(float, __hip_atomic_load(a.amaxd + pos[r], __ATOMIC_RELAXED,
                                                               __HIP_MEMORY_SCOPE_AGENT));
-        const float* src = a.vd + (size_t)pos[r] * a.N + 8 * c;
+        const __amdgpu_buffer_rsrc_t rv = coh_rsrc(a.vd + (size_t)pos[r] * a.N);   // (pos0, step: wave-uniform)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int blk = q + 4 * j;
             v[r][2 * j] = v[r][2 * j + 1] = float4{};
             if (blk < nb) {
-                v[r][2 * j] = ld_coh_f4(src + blk * 128);
-                v[r][2 * j + 1] = ld_coh_f4(src + blk * 128 + 4);
+                v[r][2 * j] = f4_of(ld_coh16(rv, 4 * (8 * c + blk * 128)));
+                v[r][2 * j + 1] = f4_of(ld_coh16(rv, 4 * (8 * c + blk * 128 + 4)));
             }
         }
     }
@@ -408,7 +401,7 @@ __device__ __forceinline__ void pf_quantd_rows_coh(const PrefillArgs& a, int pos
     for (int r = 0; r < R; ++r) {
         if (pe[r] < 0) continue;                                      // (uniform)
         const float sc = e4m3_row_scale(amax[r]);
-        _Float16* dst0 = reinterpret_cast<_Float16*>(a.h2) + (size_t)pos[r] * a.N + 16 * (c >> 1);
+        const __amdgpu_buffer_rsrc_t rh = coh_rsrc(reinterpret_cast<_Float16*>(a.h2) + (size_t)pos[r] * a.N);
         uint8_t* dst8 = a.a8dout + (size_t)pos[r] * a.N + 16 * (c >> 1);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -422,7 +415,7 @@ __device__ __forceinline__ void pf_quantd_rows_coh(const PrefillArgs& a, int pos
                 f8[mm] = e4m3_quant_f8(__fdiv_rn(w[2 * mm], sc), __fdiv_rn(w[2 * mm + 1], sc));
                 wm[mm] = e4m3_h2(f8[mm]);
             }
-            pf_store_group<true>(dst0 + blk * 128, wm, c);
+            pf_store_group_coh(rh, 2 * (16 * (c >> 1) + blk * 128), wm, c);
             if (a.a8dout) pf_store_group8(dst8 + blk * 128, f8, c);
         }
         if (lane == 0) a.dsc[pos[r]] = sc;
@@ -877,9 +870,11 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
                     m = fmaxf(m, xor_lane<8>(m, lane));
                     if (trow[p] < rn) {
                         float* vo = a.vd + (size_t)(row0 + trow[p]) * N + col;
-                        if (COH) {
-                            st_coh_f4(vo, b[p][0], b[p][1], b[p][2], b[p][3]);
-                            st_coh_f4(vo + 4, b[p][4], b[p][5], b[p][6], b[p][7]);
+                        if (COH) {                           // buffer over the tile's rows (row0: uniform)
+                            const __amdgpu_buffer_rsrc_t rv = coh_rsrc(a.vd + (size_t)row0 * N);
+                            const int off = 4 * (trow[p] * N + col);
+                            st_coh16(rv, off, __builtin_bit_cast(u32x4, f32x4{b[p][0], b[p][1], b[p][2], b[p][3]}));
+                            st_coh16(rv, off + 16, __builtin_bit_cast(u32x4, f32x4{b[p][4], b[p][5], b[p][6], b[p][7]}));
                         } else {
                             *reinterpret_cast<float4*>(vo) = make_float4(b[p][0], b[p][1], b[p][2], b[p][3]);
                             *reinterpret_cast<float4*>(vo + 4) = make_float4(b[p][4], b[p][5], b[p][6], b[p][7]);
@@ -892,9 +887,13 @@ __device__ __forceinline__ void pf_gateup_tile(const PrefillArgs& a, int s, int 
                     for (int m = 0; m < 4; ++m)
                         wm[m] = __builtin_bit_cast(uint32_t,
                                                    h2{(_Float16)(b[p][2 * m] * hr), (_Float16)(b[p][2 * m + 1] * hr)});
-                    if (trow[p] < rn)
-                        pf_store_group<COH>(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow[p]) * N + grp0, wm,
-                                            c);
+                    if (trow[p] < rn) {
+                        if (COH)
+                            pf_store_group_coh(coh_rsrc(reinterpret_cast<_Float16*>(a.h2) + (size_t)row0 * N),
+                                               2 * (trow[p] * N + grp0), wm, c);
+                        else
+                            pf_store_group(reinterpret_cast<_Float16*>(a.h2) + (size_t)(row0 + trow[p]) * N + grp0, wm, c);
+                    }
                 }
             }
         }
@@ -1651,18 +1650,15 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     const int tiles = pf_tiles(a0);
     a.small_rows = tiles == PF_TILES_BOTH ? PF_SMALL_ROWS : 0;
     // The one-launch schedule, for calls that run gate/up and down (and, e4m3, the down-input quantisation) on one
-    // tile kind: when forced, or by itself where it measured faster than the separate launches (288 experts,
-    // bit-identical): E3 and e4m3-DOWN16 calls on every tile kind (T = 8192 256-row tiles: 0-3 % with uniform
-    // routing, within +-0.7 % with Zipf routing; T = 2048 / 4096 128-row tiles -0.5 / -1.7 %; DOWN16 -3 to -4 %), and
-    // e4m3 calls on the 64-row tiles (T = 2048 -1.2 %), whose in-launch quantisation of 64-row units costs less than
-    // the 128- and 256-row units' (+0.6 % at T = 4096, +1.5 % at T = 8192). MI355MOE_SCHED=separate turns the
-    // automatic choice off. (The control words are zeroed by the call's gather or, on row tables, by the row-table
-    // setup.)
+    // tile kind: when forced, or by itself, where it measured faster than the separate launches on every tile kind
+    // and numerics (288 experts, bit-identical; T = 8192 256-row tiles: E3 -1 to -4 % with uniform routing, within
+    // +-0.7 % with Zipf routing, DOWN16 -1.6 %, e4m3 -1.2 %; T = 2048 / 4096 128-row tiles: E3 0 to -1.7 %, DOWN16
+    // -3.5 %, e4m3 -3.6 / -2.3 %). MI355MOE_SCHED=separate turns the automatic choice off. (The control words are
+    // zeroed by the call's gather or, on row tables, by the row-table setup.)
     const bool sched_ok = (kernels & 6) == 6 && !(kernels & PF_NO_QUANTD) && tiles != PF_TILES_BOTH;
     if (a.sched && a.sched_force && !sched_ok) return -1;
     const char* sched_env = getenv("MI355MOE_SCHED");
-    const bool sched_auto = (!f8 || a.down16 || tiles == PF_TILES_SMALL) &&
-                            !(sched_env && !strcmp(sched_env, "separate"));
+    const bool sched_auto = !(sched_env && !strcmp(sched_env, "separate"));
     const bool sched = a.sched && sched_ok && (a.sched_force || sched_auto);
     if (sched) {
         a.small_rows = 0;

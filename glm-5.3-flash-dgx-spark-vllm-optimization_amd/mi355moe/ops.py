@@ -233,7 +233,7 @@ def moe_forward_ids(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.Tenso
     bf16_contrib: the grouped path keeps its per-pair down accumulators in bf16 (half the contribution traffic;
     code/fork/docs/OPT_MOE.md:13). persistent: the grouped path's gate/up and down tiles in one launch, taken in
     ticket order with per-segment dataflow counts (code/fork/kernels/moe_e4m3.cu:867-897), whatever the call's size
-    (E3 calls take it by themselves); results bit-identical to the separate launches."""
+    (calls running both stages take it by themselves); results bit-identical to the separate launches."""
     if accumulate and out is None:
         raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)
@@ -321,8 +321,8 @@ def moe_forward_ids_e4m3(experts: Exl3Experts, x: torch.Tensor, topk_ids: torch.
     suh and hidden <= 4096. accumulate / bf16_contrib: the ACC=bf16 and FOLD_SHARED knobs (code/fork/docs/
     OPT_MOE.md:9-21) as in moe_forward_ids. down16: the down projection on fp16 operands (DOWN16, spec_proj16
     :660-664) instead of e4m3. persistent: the one-launch ticket-ordered gate/up -> down schedule (SCHED mode
-    "fused", code/fork/kernels/moe_e4m3.cu:867-897) whatever the call's size (DOWN16 calls and calls on the 64-row
-    tiles take it by themselves); bit-identical to the separate launches."""
+    "fused", code/fork/kernels/moe_e4m3.cu:867-897) whatever the call's size (calls running both stages take it by
+    themselves); bit-identical to the separate launches."""
     if accumulate and out is None:
         raise ValueError("accumulate needs out")
     dev = _need_cuda(x, topk_ids, topk_weights, expert_map)

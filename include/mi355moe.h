@@ -179,8 +179,8 @@ int mi355moe_moe_forward_ids_ex(const mi355moe_exl3_layer* layer, const void* x,
  *                             unit, ticket-ordered with per-segment dataflow counts (the reference's fused schedule,
  *                             code/fork/kernels/moe_e4m3.cu:867-897; item order: mi355moe_sched_item), whatever the
  *                             call's size, on the tile kind the call picks. Without the option the library takes
- *                             this schedule by itself for E3 and MI355MOE_OPT_DOWN16 calls, and for e4m3 calls on the
- *                             64-row tiles (the environment variable MI355MOE_SCHED=separate turns that off). Applies when the call runs both stages
+ *                             this schedule by itself in every numerics (the environment variable
+ *                             MI355MOE_SCHED=separate turns that off). Applies when the call runs both stages
  *                             (MI355MOE_STAGE_GATEUP and MI355MOE_STAGE_DOWN) on the grouped path; results are
  *                             bit-identical to the separate launches. With MI355MOE_OPT_E4M3 (e4m3 down GEMM) the
  *                             workgroup finishing a segment's gate/up items quantises its down inputs in the launch.

@@ -151,7 +151,8 @@ def test_automatic_choice_equals_separate_launches(cuda, monkeypatch):
 @pytest.mark.parametrize("down16", [False, True])
 def test_e4m3_extension_fused_takes_the_schedule(cuda, monkeypatch, down16):
     """The e4m3 extension's fused entry over its row tables: a call on the 256-row tiles runs the one-launch schedule
-    by itself (DOWN16) and gives the separate launches' bits; the e4m3 down GEMM keeps the separate launches."""
+    by itself (the e4m3 down GEMM with its in-launch quantisation, and DOWN16) and gives the separate launches'
+    bits."""
     from mi355moe import e4m3_ext, synthetic
     _say(f"e4m3 extension fused, one-launch schedule, down16={down16}")
     n, K, N, T = 8, 1024, 512, 600
