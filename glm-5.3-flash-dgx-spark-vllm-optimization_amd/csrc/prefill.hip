@@ -1651,9 +1651,9 @@ int launch_prefill(const PrefillArgs& a0, hipStream_t st, int kernels) {
     a.small_rows = tiles == PF_TILES_BOTH ? PF_SMALL_ROWS : 0;
     // The one-launch schedule, for calls that run gate/up and down (and, e4m3, the down-input quantisation) on one
     // tile kind: when forced, or by itself, where it measured faster than the separate launches on every tile kind
-    // and numerics (288 experts, bit-identical; T = 8192 256-row tiles: E3 -1 to -4 % with uniform routing, within
-    // +-0.7 % with Zipf routing, DOWN16 -1.6 %, e4m3 -1.2 %; T = 2048 / 4096 128-row tiles: E3 0 to -1.7 %, DOWN16
-    // -3.5 %, e4m3 -3.6 / -2.3 %). MI355MOE_SCHED=separate turns the automatic choice off. (The control words are
+    // and numerics (288 experts, bit-identical; T = 8192 256-row tiles, uniform routing: E3 -1 to -4 %, DOWN16
+    // -1.6 %, e4m3 -1.2 %; Zipf(1.2) routing: E3 -2.1 %, DOWN16 -0.7 %, e4m3 -0.9 %; T = 2048 / 4096 128- and 64-row
+    // tiles: E3 0 to -1.7 %, DOWN16 -3.5 %, e4m3 -3.6 / -2.3 %, e4m3 T = 4096 Zipf -4.9 %). MI355MOE_SCHED=separate turns the automatic choice off. (The control words are
     // zeroed by the call's gather or, on row tables, by the row-table setup.)
     const bool sched_ok = (kernels & 6) == 6 && !(kernels & PF_NO_QUANTD) && tiles != PF_TILES_BOTH;
     if (a.sched && a.sched_force && !sched_ok) return -1;
