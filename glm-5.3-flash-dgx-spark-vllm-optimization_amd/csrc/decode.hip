@@ -499,20 +499,26 @@ __device__ __forceinline__ void gateup_tile(const DecodeArgs& a, int cb, int s, 
     unsigned long long* cnt = a.cnt_gu + (size_t)s * (N >> 7) + cb;
     const bool part = kc1 - kc0 < KC;
     if (part) {
-        for (int i = tid; i < 2 * rn * 128; i += GU_WAVES * 64) {
-            const int mat = i / (rn * 128), rem = i - mat * rn * 128, r = rem >> 7, c = rem & 127;
-            st_coherent(a.zg + ((size_t)(slot * 2 + mat) * P + row0 + r) * N + cb * 128 + c,
-                        zs[(mat * ZS_ROWS + r) * 128 + c]);
-        }
+        // four columns per thread: one device-coherent 16-byte store / load each, through a buffer resource over the
+        // (slot, matrix) block's first row (uniform), offsets (r N + c) * 4
+        for (int mat = 0; mat < 2; ++mat)
+            for (int i = tid; i < rn * 32; i += GU_WAVES * 64) {
+                const int r = i >> 5, c = (i & 31) * 4;
+                st_coh16(coh_rsrc(a.zg + ((size_t)(slot * 2 + mat) * P + row0) * N + cb * 128), 4 * (r * N + c),
+                         __builtin_bit_cast(u32x4, *reinterpret_cast<const f32x4*>(zs + (mat * ZS_ROWS + r) * 128 + c)));
+            }
         if (!arrive_fragment(cnt, (unsigned)(kc1 - kc0), slot, (unsigned)KC, &slot_mask, &last_flag)) return;
         const unsigned mask = slot_mask;
-        for (int i = tid; i < 2 * rn * 128; i += GU_WAVES * 64) {
-            const int mat = i / (rn * 128), rem = i - mat * rn * 128, r = rem >> 7, c = rem & 127;
-            float v = 0.f;
-            for (unsigned m = mask; m; m &= m - 1)                  // the slots in order (the chunks in K order)
-                v += ld_coherent(a.zg + ((size_t)(__builtin_ctz(m) * 2 + mat) * P + row0 + r) * N + cb * 128 + c);
-            zs[(mat * ZS_ROWS + r) * 128 + c] = v;
-        }
+        for (int mat = 0; mat < 2; ++mat)
+            for (int i = tid; i < rn * 32; i += GU_WAVES * 64) {
+                const int r = i >> 5, c = (i & 31) * 4;
+                f32x4 v = {0.f, 0.f, 0.f, 0.f};
+                for (unsigned m = mask; m; m &= m - 1)              // the slots in order (the chunks in K order)
+                    v += __builtin_bit_cast(
+                        f32x4, ld_coh16(coh_rsrc(a.zg + ((size_t)(__builtin_ctz(m) * 2 + mat) * P + row0) * N + cb * 128),
+                                        4 * (r * N + c)));
+                *reinterpret_cast<f32x4*>(zs + (mat * ZS_ROWS + r) * 128 + c) = v;
+            }
         __syncthreads();
     }
 
@@ -703,20 +709,24 @@ __device__ __forceinline__ void down_tile(const DecodeArgs& a, int cb, int s, in
     unsigned long long* cnt = a.cnt_dn + (size_t)s * ((K + DN_COLS - 1) / DN_COLS) + cb;
     const bool part = kc1 - kc0 < NC;
     if (part) {
-        for (int i = tid; i < rn * DN_COLS; i += DN_WAVES * 64) {
-            const int r = i / DN_COLS, c = i % DN_COLS;
+        // four columns per thread (ncol is a multiple of 4), as in the gate/up kernel
+        for (int i = tid; i < rn * (DN_COLS / 4); i += DN_WAVES * 64) {
+            const int r = i / (DN_COLS / 4), c = (i % (DN_COLS / 4)) * 4;
             if (c < ncol)
-                st_coherent(a.zd + ((size_t)slot * P + row0 + r) * K + cb * DN_COLS + c, zs[r * DN_COLS + c]);
+                st_coh16(coh_rsrc(a.zd + ((size_t)slot * P + row0) * K + cb * DN_COLS), 4 * (r * K + c),
+                         __builtin_bit_cast(u32x4, *reinterpret_cast<const f32x4*>(zs + r * DN_COLS + c)));
         }
         if (!arrive_fragment(cnt, (unsigned)(kc1 - kc0), slot, (unsigned)NC, &slot_mask, &last_flag)) return;
         const unsigned mask = slot_mask;
-        for (int i = tid; i < rn * DN_COLS; i += DN_WAVES * 64) {
-            const int r = i / DN_COLS, c = i % DN_COLS;
+        for (int i = tid; i < rn * (DN_COLS / 4); i += DN_WAVES * 64) {
+            const int r = i / (DN_COLS / 4), c = (i % (DN_COLS / 4)) * 4;
             if (c >= ncol) continue;
-            float v = 0.f;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
             for (unsigned m = mask; m; m &= m - 1)                  // the slots in order (the chunks in N order)
-                v += ld_coherent(a.zd + ((size_t)__builtin_ctz(m) * P + row0 + r) * K + cb * DN_COLS + c);
-            zs[r * DN_COLS + c] = v;
+                v += __builtin_bit_cast(
+                    f32x4, ld_coh16(coh_rsrc(a.zd + ((size_t)__builtin_ctz(m) * P + row0) * K + cb * DN_COLS),
+                                    4 * (r * K + c)));
+            *reinterpret_cast<f32x4*>(zs + r * DN_COLS + c) = v;
         }
         __syncthreads();
     }
